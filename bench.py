@@ -1,0 +1,222 @@
+"""Benchmark: paged-attention decode over an int8 KV cache, 14B shape, one MI355X.
+
+Workload (the configuration the headline metric is quoted on): Qwen2.5-14B-
+shaped decode attention, 64 sequences x 4096 tokens of context, 40 query heads
+over 8 KV heads, head_dim 128, page 16, in a 48-layer pool of 16384 pages
+(25.8 GB of int8 codes + per-token fp32 scales).  K/V are bf16 N(0, 1) with 2
+of 128 channels per head scaled by 20, quantized to int8 with one scale per
+(token, head).  One step = one layer-step: every sequence attends once for one
+new query token over one layer.  Steps rotate over 4 filled layers so that the
+working set (4 x 556 MB) does not fit the 256 MB Infinity Cache.
+
+Prints one JSON line.  value = microseconds per layer-step (lower is better);
+the line also carries the achieved HBM bandwidth on algorithmic bytes, the
+tokens/s this implies for a 48-layer model, the roofline of the dominant
+kernel (the split-K partition pass, timed alone with events on its stream)
+and the reference's CPU path (the oracle restatement) timed on a sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from vramancer_amd import _lib, kv_quant, workloads  # noqa: E402
+from vramancer_amd.paged_attention_cuda import decode_workspace  # noqa: E402
+
+METRIC = "paged-attn decode µs/layer-step + HBM GB/s (% of peak), 14B-shape quantized KV"
+PEAK_HBM_GBPS = 8000.0
+LAYERS_FILLED = (0, 12, 24, 36)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_14b_int8.json")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_events(fn, steps):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / steps  # microseconds per call
+
+
+def cpu_baseline(inp, layer, n_seq, reps):
+    """The reference's PyTorch decode path (restated in oracle/) on the host
+    cores, over the first n_seq sequences of the same workload."""
+    from oracle import paged_decode as PD
+
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    threads = torch.get_num_threads()
+    table = inp["page_table"][:n_seq]
+    pages = torch.unique(table[table >= 0]).long()
+    # copy only the pages the sample reads, relabelled 0..n-1
+    remap = torch.full((inp["num_pages"],), -1, dtype=torch.long, device=pages.device)
+    remap[pages] = torch.arange(pages.numel(), device=pages.device)
+    pool = inp["kv_pool"][pages][:, layer:layer + 1].cpu()
+    scales = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
+    tbl = remap[table.long()].to(torch.int32).cpu()
+    q = inp["query"][:n_seq].cpu()
+    lens = inp["context_lens"][:n_seq].cpu()
+    PD.paged_attention_decode(q, pool, tbl, lens, 0, kv_scales=scales)  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        PD.paged_attention_decode(q, pool, tbl, lens, 0, kv_scales=scales)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    per_seq_us = times[len(times) // 2] / n_seq * 1e6
+    return per_seq_us, threads
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seqs", type=int, default=4, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(sharding of the decode is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cfg = workloads.CONFIGS["14b-int8"]
+    log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {LAYERS_FILLED})")
+    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=LAYERS_FILLED)
+    torch.cuda.synchronize()
+    q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
+    B, H, D = q.shape
+    P, L, _, KH, PS, _ = pool.shape
+    max_pp = table.shape[1]
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws = decode_workspace(B, H, KH, D, max_pp, dev, PS)
+    nsplit = lib.vrm_paged_decode_num_splits(B, H, KH, max_pp, PS)
+    stream = _lib.stream_of(q)
+    code = _lib.VRM_KV_I8
+    lens_list = lens.tolist()
+    ab = workloads.algorithmic_bytes(cfg, lens_list)
+    log(f"pool {P} pages, {nsplit} partitions/sequence, algorithmic bytes/layer-step {ab['total'] / 1e6:.2f} MB")
+
+    def full(i):
+        layer = LAYERS_FILLED[i % len(LAYERS_FILLED)]
+        rc = lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(), lens.data_ptr(),
+                                  out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp, layer,
+                                  scale, code, stream)
+        if rc:
+            _lib.check(rc, "decode")
+
+    def partitions(i):
+        layer = LAYERS_FILLED[i % len(LAYERS_FILLED)]
+        rc = lib.vrm_paged_decode_partitions(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(),
+                                             lens.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P,
+                                             max_pp, layer, scale, code, stream)
+        if rc:
+            _lib.check(rc, "partitions")
+
+    for i in range(args.warmup):
+        full(i)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} layer-steps")
+    us_step = time_events(full, args.steps)
+    us_part = time_events(partitions, args.steps)
+    log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
+
+    # append one token per sequence (quantize-on-append), timed separately
+    kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+    vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+    last = (lens - 1).clamp(min=0)
+    pid = table.gather(1, (last // PS).long()[:, None]).squeeze(1).contiguous()
+    slot = (last % PS).to(torch.int32).contiguous()
+
+    def append(i):
+        rc = lib.vrm_kv_quant_append(kn.data_ptr(), vn.data_ptr(), _lib.VRM_SRC_BF16, pid.data_ptr(),
+                                     slot.data_ptr(), B, pool.data_ptr(), sc.data_ptr(), code, KH, D, PS, L, P,
+                                     LAYERS_FILLED[0], stream)
+        if rc:
+            _lib.check(rc, "append")
+
+    for i in range(5):
+        append(i)
+    us_append = time_events(append, 50)
+
+    achieved = ab["total"] / (us_part * 1e-6) / 1e9
+    overall = ab["total"] / (us_step * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline on {args.cpu_seqs} sequences")
+        per_seq_us, threads = cpu_baseline(inp, LAYERS_FILLED[0], args.cpu_seqs, args.cpu_reps)
+        cpu = {
+            "value": round(per_seq_us * B, 1),
+            "unit": "us/layer-step",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle restatement of the reference's PyTorch decode (int8 dequant + gather + "
+                       f"repeat_interleave + bmm/softmax/bmm, fp32) over {args.cpu_seqs} of the {B} sequences, "
+                       f"median of {args.cpu_reps}, scaled to the full batch"),
+        }
+    result = {
+        "metric": METRIC,
+        "value": round(us_step, 3),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
+                         "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
+            "batch": B, "num_heads": H, "num_kv_heads": KH, "head_dim": D, "context": 4096, "page_size": PS,
+            "num_layers": L, "num_pages": P, "partitions": nsplit, "layers_rotated": list(LAYERS_FILLED),
+        },
+        "hbm_gbps": round(overall, 1),
+        "pct_of_peak": round(100 * overall / PEAK_HBM_GBPS, 2),
+        "tokens_per_s": round(B / (us_step * 1e-6 * L), 1),
+        "append_us": round(us_append, 2),
+        "algorithmic_bytes": int(ab["total"]),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "decode_split_kernel<K_I8,128,5>",
+            "kernel_us": round(us_part, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

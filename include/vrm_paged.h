@@ -1,0 +1,227 @@
+/*
+ * vrm_paged.h — C ABI of libvrm_paged.so, the gfx950 (MI355X) implementation of
+ * VRAMancer's paged-attention decode over a quantized KV cache.
+ *
+ * Every entry point takes raw device pointers, explicit sizes and a HIP stream,
+ * never allocates or frees device memory, and returns an int status:
+ *      0              success (the kernels are enqueued on `stream`)
+ *      < 0            invalid argument, detected on the host before any launch
+ *      > 0            a hipError_t reported by the launch
+ * vrm_last_error() returns a thread-local description of the last failure.
+ * The library keeps no per-call state, so calls are reentrant; calls on one
+ * stream are ordered by that stream.
+ *
+ * Pool layout (the reference's, core/paged_attention.py:321-330):
+ *      kv_pool[P][L][2][KH][PS][D]    (index 2 selects K=0 / V=1)
+ * with PS = 16 tokens per page.  A sequence's logical page i lives in physical
+ * page page_table[b][i]; tokens t < context_lens[b] are attended.
+ */
+#ifndef VRM_PAGED_H
+#define VRM_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VRM_ABI_VERSION 1
+
+/* Status codes (negative: rejected on the host, nothing was launched). */
+#define VRM_OK 0
+#define VRM_ERR_ARG (-1)          /* bad size, pointer, dtype or layer index */
+#define VRM_ERR_UNSUPPORTED (-2)  /* valid request outside the compiled shapes */
+#define VRM_ERR_WORKSPACE (-3)    /* workspace smaller than required */
+
+/* Element type of the KV pool. */
+typedef enum vrm_kv_dtype {
+  VRM_KV_F32 = 0,      /* float32 pool                                        */
+  VRM_KV_F16 = 1,      /* float16 pool                                        */
+  VRM_KV_BF16 = 2,     /* bfloat16 pool                                       */
+  VRM_KV_I8 = 3,       /* int8 codes, float32 scale per (page,layer,kv,head,token) */
+  VRM_KV_FP8E4M3 = 4   /* OCP e4m3fn codes, float32 scale per (page,layer,kv,head) */
+} vrm_kv_dtype;
+
+/* Element type of new K/V rows handed to the quantizers. */
+typedef enum vrm_src_dtype {
+  VRM_SRC_F32 = 0,
+  VRM_SRC_F16 = 1,
+  VRM_SRC_BF16 = 2
+} vrm_src_dtype;
+
+typedef struct ihipStream_t* vrm_stream_t; /* == hipStream_t */
+
+/* ABI version of the loaded library (== VRM_ABI_VERSION it was built with). */
+int vrm_abi_version(void);
+
+/* Thread-local text of the last error ("" when none). */
+const char* vrm_last_error(void);
+
+/* --------------------------------------------------------------------------
+ * Paged decode attention.
+ * -------------------------------------------------------------------------- */
+
+/* Number of token partitions (split-K) vrm_paged_decode will use for a call of
+ * this shape, and the workspace bytes it needs.  Both depend only on the
+ * arguments (no device state).  max_pp is the page-table width. */
+int vrm_paged_decode_num_splits(int B, int H, int KH, int max_pp, int page_size);
+size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit);
+
+/*
+ * out[b][h][:] = softmax(scale * q[b][h] . K[b,kvh]^T) V[b,kvh] for one decode
+ * token per sequence, kvh = h / (H / KH), reading K/V straight from the pages.
+ *
+ * Replaces the pybind entry `paged_attention_decode(query, kv_pool, page_table,
+ * context_lens, layer_idx, scale)` of csrc/paged_attention_kernel.cu:445-499,
+ * called from core/paged_attention_cuda.py:170-177; the int8 and fp8 pools
+ * (kv_scales != NULL) have no counterpart in the reference and follow the
+ * same signature with one extra scale pointer.
+ *
+ *   query        [B][H][D] float32
+ *   kv_pool      [P][L][2][KH][PS][D] of kv_dtype
+ *   kv_scales    VRM_KV_I8:      [P][L][2][KH][PS] float32 (per token)
+ *                VRM_KV_FP8E4M3: [P][L][2][KH]     float32 (per page)
+ *                float pools:    NULL
+ *   page_table   [B][max_pp] int32; entries < 0 or >= P mark absent pages,
+ *                whose tokens are skipped
+ *   context_lens [B] int32; ctx <= 0 gives an all-zero output row
+ *   out          [B][H][D] float32
+ *   workspace    >= vrm_paged_decode_workspace_bytes(B, H, D, nsplit) bytes,
+ *                nsplit = vrm_paged_decode_num_splits(...); may be NULL when
+ *                that size is 0
+ * Supported: D in {64, 128, 256}, PS == 16, H % KH == 0.
+ */
+int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_scales,
+                     const int32_t* page_table, const int32_t* context_lens,
+                     float* out, void* workspace, size_t workspace_bytes,
+                     int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                     int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
+
+/*
+ * The two passes of vrm_paged_decode, for callers that schedule them
+ * separately (and for timing the dominant pass on its own):
+ * vrm_paged_decode_partitions writes per-partition (max, sum, unnormalised
+ * accumulator) into the workspace; vrm_paged_decode_merge combines them into
+ * out.  Same arguments and workspace contract as vrm_paged_decode; merge only
+ * reads query/kv_pool/kv_scales for argument checks, never their contents.
+ * No counterpart in the reference, whose kernel is single-pass.
+ */
+int vrm_paged_decode_partitions(const float* query, const void* kv_pool, const float* kv_scales,
+                                const int32_t* page_table, const int32_t* context_lens,
+                                void* workspace, size_t workspace_bytes,
+                                int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
+int vrm_paged_decode_merge(const int32_t* context_lens, float* out,
+                           const void* workspace, size_t workspace_bytes,
+                           int B, int H, int KH, int D, int PS, int max_pp, vrm_stream_t stream);
+
+/*
+ * Same attention over the reference's asymmetric 4-bit pool:
+ *   value(d) = (nibble(d) - zero[g]) * scale[g],  g = d / 32,
+ *   byte j of a row holds d = 2j in its low nibble and d = 2j+1 in its high one.
+ * Replaces the pybind entry `paged_attention_decode_q4` of
+ * csrc/paged_attention_kernel.cu:502-549 (wrapper core/paged_attention_cuda.py:238-288).
+ *   kv_pool_q4  [P][L][2][KH][PS][D/2] uint8
+ *   kv_scales, kv_zeros [P][L][2][KH][PS][D/32] float16 (passed as uint16 bits)
+ */
+int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4,
+                        const uint16_t* kv_scales, const uint16_t* kv_zeros,
+                        const int32_t* page_table, const int32_t* context_lens,
+                        float* out, void* workspace, size_t workspace_bytes,
+                        int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                        int layer_idx, float scale, vrm_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Quantize-on-append into int8 / fp8 pools.  No counterpart exists in the
+ * reference (core/kv_quantizer.py is TurboQuant-only); the write itself
+ * replaces the raw index-put of PagedKVCacheManager.write_kv
+ * (core/paged_attention.py:611-612: pool[page, layer, 0|1, :, slot, :] = k|v).
+ * -------------------------------------------------------------------------- */
+
+/*
+ * Writes N new tokens.  Token n goes to (page_ids[n], slots[n]) of layer
+ * layer_idx; key/value are [N][KH][D] of src_dtype.
+ *   VRM_KV_I8:      per (token, head) amax over D; scale = amax / 127;
+ *                   code = clamp(round_half_even(x / scale), -127, 127);
+ *                   amax == 0 gives scale 0 and codes 0.
+ *   VRM_KV_FP8E4M3: the page's per-head scale only grows.  With old scale s
+ *                   (taken as 0 when slots[n] == 0) and a = amax(x) / 448:
+ *                   s' = max(s, a); codes already in slots < slots[n] are
+ *                   re-encoded as e4m3(fp32(e4m3 code) * s / s') when s' > s,
+ *                   then the new row is e4m3(x / s') (round to nearest even).
+ *                   Several tokens of one call must not share a page.
+ * kv_pool/kv_scales as in vrm_paged_decode.
+ */
+int vrm_kv_quant_append(const void* key, const void* value, int src_dtype,
+                        const int32_t* page_ids, const int32_t* slots, int N,
+                        void* kv_pool, float* kv_scales, int kv_dtype,
+                        int KH, int D, int PS, int L, int P, int layer_idx,
+                        vrm_stream_t stream);
+
+/*
+ * Bulk (prefill) write of whole pages.  key/value are [NP][KH][PS][D] of
+ * src_dtype; page n goes to physical page page_ids[n] and holds n_valid[n]
+ * tokens (slots >= n_valid are written as code 0).
+ *   VRM_KV_I8:      as vrm_kv_quant_append, per token.
+ *   VRM_KV_FP8E4M3: scale = amax over the valid tokens of the page-head / 448.
+ */
+int vrm_kv_quant_pages(const void* key, const void* value, int src_dtype,
+                       const int32_t* page_ids, const int32_t* n_valid, int NP,
+                       void* kv_pool, float* kv_scales, int kv_dtype,
+                       int KH, int D, int PS, int L, int P, int layer_idx,
+                       vrm_stream_t stream);
+
+/*
+ * Dequantizes pages of a quantized pool to float32: for each n,
+ * out[n][2][KH][PS][D] = codes of (page_ids[n], layer_idx) * scale.
+ * Debug/offload helper; decode never materializes this.
+ */
+int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales, int kv_dtype,
+                         const int32_t* page_ids, int NP, float* out,
+                         int KH, int D, int PS, int L, int P, int layer_idx,
+                         vrm_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * TurboQuant (randomized Hadamard + PolarQuant + QJL) codec.
+ * -------------------------------------------------------------------------- */
+
+/*
+ * Compresses N rows of head_dim values, following the CPU path of
+ * KVCacheCompressor.compress (core/kv_quantizer.py:391-417): pad to
+ * padded_dim, rotate, 7-level polar encode, bin angles, decode with the fp32
+ * radius, QJL-sign the residual.  Replaces the pybind entry `compress` of
+ * csrc/turboquant_kernel.cu:410-450 (wrapper core/turboquant_cuda.py:124-174).
+ *   kv          [N][head_dim] of src_dtype
+ *   signs       [padded_dim] float32 (+-1), jl [qjl_dim][padded_dim] float32
+ *   angle_lut   [2][2][2^bits] float32: {cos, sin} of the bin centres of
+ *               level 0 and of levels >= 1, as the host computes them
+ *   radius      [N] float16 bits; angles [N][padded_dim-1] uint8, level-major
+ *               (level 0 first); qjl_signs [N][qjl_dim] uint8 (0/1);
+ *               qjl_norms [N] float16 bits
+ * Supported: padded_dim in {64, 128, 256}, 1 <= bits <= 8, qjl_dim <= 256.
+ */
+int vrm_turboquant_compress(const void* kv, int src_dtype, int N, int head_dim,
+                            int padded_dim, int n_levels, int bits, int qjl_dim,
+                            const float* signs, const float* jl, const float* angle_lut,
+                            uint16_t* radius, uint8_t* angles, uint8_t* qjl_signs,
+                            uint16_t* qjl_norms, vrm_stream_t stream);
+
+/*
+ * out[N][head_dim] float32 = unrotate(polar_decode(radius, angles)), no QJL
+ * (core/kv_quantizer.py:481-500).  Replaces the pybind entry `decompress` of
+ * csrc/turboquant_kernel.cu:453-481.  With rotated != 0 the inverse rotation
+ * is skipped and out is [N][padded_dim] = polar_decode(radius, angles), the
+ * key reconstruction that KVCacheCompressor.attention_score dots with the
+ * rotated query (core/kv_quantizer.py:523-527).
+ */
+int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* angles, int N,
+                              int head_dim, int padded_dim, int n_levels, int bits,
+                              const float* signs, const float* angle_lut, float* out,
+                              int rotated, vrm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VRM_PAGED_H */

@@ -1,0 +1,136 @@
+"""Restatement of the reference's PyTorch decode path (test oracle only).
+
+``paged_attention_decode`` follows ``_pytorch_paged_attention_decode``
+(core/paged_attention_cuda.py:187-231) op for op: per-sequence loop, page
+gather -> [KH, ctx, D] float32, repeat_interleave for GQA (head h reads kv-head
+h // (H / KH)), bmm -> softmax -> bmm.  Quantized pools are dequantized first
+(int8: code * per-token scale; fp8: float(code) * per-page scale), as the
+reference's fused-dequant contract implies.  ``paged_attention_decode_q4``
+follows core/paged_attention_cuda.py:291-348.  ``dense_attention`` is an
+independent fp64 closed form used to pin the restatement.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+
+def _dequant_pages(kv_pool, kv_scales, page_ids, layer_idx, kv):
+    pages = kv_pool[page_ids, layer_idx, kv]  # [n, KH, PS, D]
+    if kv_pool.dtype == torch.int8:
+        return pages.float() * kv_scales[page_ids, layer_idx, kv].unsqueeze(-1)
+    if kv_pool.dtype == torch.float8_e4m3fn:
+        return pages.float() * kv_scales[page_ids, layer_idx, kv][:, :, None, None]
+    return pages.float()
+
+
+def paged_attention_decode(query, kv_pool, page_table, context_lens, layer_idx, scale=None, kv_scales=None):
+    """[B, H, D] float32 attention output; core/paged_attention_cuda.py:187-231."""
+    batch_size, num_heads, head_dim = query.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    query = query.float()
+    num_kv_heads = kv_pool.shape[3]
+    page_size = kv_pool.shape[4]
+    kv_head_ratio = num_heads // num_kv_heads
+    outputs = []
+    for b in range(batch_size):
+        ctx_len = int(context_lens[b].item())
+        if ctx_len <= 0:
+            outputs.append(torch.zeros(num_heads, head_dim))
+            continue
+        num_pages = (ctx_len + page_size - 1) // page_size
+        page_ids = page_table[b, :num_pages].long()
+        k_pages = _dequant_pages(kv_pool, kv_scales, page_ids, layer_idx, 0)
+        v_pages = _dequant_pages(kv_pool, kv_scales, page_ids, layer_idx, 1)
+        k_flat = k_pages.permute(1, 0, 2, 3).reshape(num_kv_heads, -1, head_dim)[:, :ctx_len, :]
+        v_flat = v_pages.permute(1, 0, 2, 3).reshape(num_kv_heads, -1, head_dim)[:, :ctx_len, :]
+        if kv_head_ratio > 1:
+            k_flat = k_flat.repeat_interleave(kv_head_ratio, dim=0)
+            v_flat = v_flat.repeat_interleave(kv_head_ratio, dim=0)
+        q = query[b].unsqueeze(1)
+        scores = torch.bmm(q, k_flat.transpose(1, 2)) * scale
+        weights = torch.softmax(scores, dim=-1)
+        outputs.append(torch.bmm(weights, v_flat).squeeze(1))
+    return torch.stack(outputs)
+
+
+def dequant_q4_page(packed, scales, zeros, group_size: int = 32):
+    """[..., D/2] nibbles -> [..., D] float32; core/paged_attention_cuda.py:303-313."""
+    lo = (packed & 0x0F).float()
+    hi = ((packed >> 4) & 0x0F).float()
+    vals = torch.stack([lo, hi], dim=-1).reshape(*packed.shape[:-1], -1)
+    sc = scales.float().repeat_interleave(group_size, dim=-1)[..., :vals.shape[-1]]
+    zp = zeros.float().repeat_interleave(group_size, dim=-1)[..., :vals.shape[-1]]
+    return (vals - zp) * sc
+
+
+def paged_attention_decode_q4(query, kv_pool_q4, kv_scales, kv_zeros, page_table, context_lens, layer_idx,
+                              scale=None):
+    """core/paged_attention_cuda.py:291-348."""
+    batch_size, num_heads, head_dim = query.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    query = query.float()
+    num_kv_heads = kv_pool_q4.shape[3]
+    page_size = kv_pool_q4.shape[4]
+    ratio = num_heads // num_kv_heads
+    outputs = []
+    for b in range(batch_size):
+        ctx_len = int(context_lens[b].item())
+        if ctx_len <= 0:
+            outputs.append(torch.zeros(num_heads, head_dim))
+            continue
+        num_pages = (ctx_len + page_size - 1) // page_size
+        page_ids = page_table[b, :num_pages].long()
+        k_pages = dequant_q4_page(kv_pool_q4[page_ids, layer_idx, 0], kv_scales[page_ids, layer_idx, 0],
+                                  kv_zeros[page_ids, layer_idx, 0])
+        v_pages = dequant_q4_page(kv_pool_q4[page_ids, layer_idx, 1], kv_scales[page_ids, layer_idx, 1],
+                                  kv_zeros[page_ids, layer_idx, 1])
+        k_flat = k_pages.permute(1, 0, 2, 3).reshape(num_kv_heads, -1, head_dim)[:, :ctx_len, :]
+        v_flat = v_pages.permute(1, 0, 2, 3).reshape(num_kv_heads, -1, head_dim)[:, :ctx_len, :]
+        if ratio > 1:
+            k_flat = k_flat.repeat_interleave(ratio, dim=0)
+            v_flat = v_flat.repeat_interleave(ratio, dim=0)
+        q = query[b].unsqueeze(1)
+        scores = torch.bmm(q, k_flat.transpose(1, 2)) * scale
+        weights = torch.softmax(scores, dim=-1)
+        outputs.append(torch.bmm(weights, v_flat).squeeze(1))
+    return torch.stack(outputs)
+
+
+def gather_sequence(pool_f32, page_table_row, ctx_len, layer_idx, skip_invalid: bool = False):
+    """K, V of one sequence as [KH, n, D] float64 from a dequantized [P, L, 2,
+    KH, PS, D] pool, token by token; with skip_invalid, tokens on pages whose
+    id is < 0 or >= P are dropped."""
+    P = pool_f32.shape[0]
+    PS = pool_f32.shape[4]
+    ks, vs = [], []
+    for t in range(ctx_len):
+        pid = int(page_table_row[t // PS])
+        if not (0 <= pid < P):
+            if skip_invalid:
+                continue
+            pid = pid % P
+        ks.append(pool_f32[pid, layer_idx, 0, :, t % PS, :].double())
+        vs.append(pool_f32[pid, layer_idx, 1, :, t % PS, :].double())
+    if not ks:
+        return None, None
+    return torch.stack(ks, dim=1), torch.stack(vs, dim=1)
+
+
+def dense_attention(q, K, V, scale):
+    """fp64 softmax(scale q K^T) V for one sequence; q [H, D], K/V [KH, n, D];
+    query head h uses kv-head h // (H / KH).  Independent of the restatement."""
+    H, D = q.shape
+    KH = K.shape[0]
+    out = torch.zeros(H, D, dtype=torch.float64)
+    for h in range(H):
+        kh = h // (H // KH)
+        s = (K[kh] @ q[h].double()) * scale
+        s = s - s.max()
+        w = torch.exp(s)
+        out[h] = (w[:, None] * V[kh]).sum(0) / w.sum()
+    return out

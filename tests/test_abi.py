@@ -1,0 +1,103 @@
+"""The C-ABI library loads on a host without a GPU, exports every function
+include/vrm_paged.h declares, and rejects bad arguments on the host (these
+paths return before any HIP call, so no device is touched)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from vramancer_amd import _lib
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "vrm_paged.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vrm_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_abi_version(lib):
+    assert lib.vrm_abi_version() == _lib.VRM_ABI_VERSION == 1
+
+
+def test_split_geometry_is_host_only(lib):
+    # 14B int8 shape: 64 sequences x 8 kv heads, 256 pages each
+    ns = lib.vrm_paged_decode_num_splits(64, 40, 8, 256, 16)
+    assert ns >= 1
+    assert lib.vrm_paged_decode_workspace_bytes(64, 40, 128, ns) == 64 * 40 * ns * 130 * 4
+    assert lib.vrm_paged_decode_num_splits(1, 3, 2, 4, 16) == 0  # H % KH != 0
+
+
+def _decode(lib, **kw):
+    a = dict(q=1, pool=1, sc=None, pt=1, cl=1, out=1, ws=1, wsb=1 << 30, B=2, H=8, KH=2, D=128, PS=16, L=1, P=4,
+             max_pp=2, layer=0, scale=0.1, dt=_lib.VRM_KV_BF16)
+    a.update(kw)
+    return lib.vrm_paged_decode(a["q"], a["pool"], a["sc"], a["pt"], a["cl"], a["out"], a["ws"], a["wsb"], a["B"],
+                                a["H"], a["KH"], a["D"], a["PS"], a["L"], a["P"], a["max_pp"], a["layer"],
+                                a["scale"], a["dt"], None)
+
+
+def test_decode_rejects_bad_arguments(lib):
+    assert _decode(lib, q=None) == -1 and b"null" in lib.vrm_last_error()
+    assert _decode(lib, H=7) == -1 and b"multiple" in lib.vrm_last_error()
+    assert _decode(lib, layer=1) == -1 and b"layer_idx" in lib.vrm_last_error()
+    assert _decode(lib, D=96) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert _decode(lib, PS=32) == -2 and b"page_size" in lib.vrm_last_error()
+    assert _decode(lib, dt=99) == -1 and b"kv_dtype" in lib.vrm_last_error()
+    assert _decode(lib, dt=_lib.VRM_KV_I8) == -1 and b"kv_scales" in lib.vrm_last_error()
+    assert _decode(lib, sc=1) == -1 and b"float pool" in lib.vrm_last_error()
+    assert _decode(lib, wsb=16) == -3 and b"workspace" in lib.vrm_last_error()
+    assert _decode(lib, scale=float("nan")) == -1
+
+
+def test_quant_rejects_bad_arguments(lib):
+    f = lib.vrm_kv_quant_append
+    ok = dict(k=1, v=1, src=_lib.VRM_SRC_BF16, pid=1, sl=1, N=4, pool=1, sc=1, dt=_lib.VRM_KV_I8, KH=8, D=128, PS=16,
+              L=2, P=10, layer=0)
+
+    def call(**kw):
+        a = dict(ok)
+        a.update(kw)
+        return f(a["k"], a["v"], a["src"], a["pid"], a["sl"], a["N"], a["pool"], a["sc"], a["dt"], a["KH"], a["D"],
+                 a["PS"], a["L"], a["P"], a["layer"], None)
+
+    assert call(k=None) == -1
+    assert call(dt=_lib.VRM_KV_BF16) == -1 and b"quantized" in lib.vrm_last_error()
+    assert call(src=7) == -1
+    assert call(layer=2) == -1
+    assert call(D=100) == -2
+    assert call(N=0) == 0  # nothing to do, nothing launched
+
+
+def test_turboquant_rejects_bad_arguments(lib):
+    c = lib.vrm_turboquant_compress
+    assert c(1, 0, 4, 128, 128, 6, 3, 64, 1, 1, 1, 1, 1, 1, 1, None) == -1  # levels mismatch
+    assert c(1, 0, 4, 128, 128, 7, 9, 64, 1, 1, 1, 1, 1, 1, 1, None) == -1  # bits
+    assert c(1, 0, 4, 100, 100, 7, 3, 64, 1, 1, 1, 1, 1, 1, 1, None) == -2  # padded_dim
+    assert c(1, 0, 0, 128, 128, 7, 3, 64, 1, 1, 1, 1, 1, 1, 1, None) == 0   # N == 0
+
+
+def test_python_api_refuses_cpu_tensors():
+    import torch
+    from vramancer_amd.paged_attention_cuda import paged_attention_decode
+
+    q = torch.randn(1, 4, 64)
+    pool = torch.randn(2, 1, 2, 4, 16, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        paged_attention_decode(q, pool, torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32), 0)

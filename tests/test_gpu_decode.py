@@ -1,0 +1,226 @@
+"""GPU parity of the split-K paged decode against the CPU oracle.
+
+Tolerance (attention outputs): |gpu - oracle| <= 2e-3 + 1e-2 * |oracle|
+elementwise (max-abs 2e-3 / rel 1e-2), the oracle being the reference's
+PyTorch decode path restated in oracle/paged_decode.py, evaluated on the very
+same pool contents (for quantized pools, on the same codes and scales).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import paged_decode as PD
+from vramancer_amd import _lib, workloads
+from vramancer_amd.paged_attention_cuda import paged_attention_decode, paged_attention_decode_q4
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-3, 1e-2
+DEV = "cuda:0"
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _assert_close(got, want, what):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    err = (got - want).abs()
+    bound = ATOL + RTOL * want.abs()
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.numel()} outside tolerance, "
+                          f"max abs err {err.max().item():.3e}")
+
+
+def _oracle(inp, layer):
+    pool = inp["kv_pool"].cpu()
+    sc = inp["kv_scales"].cpu() if inp["kv_scales"] is not None else None
+    return PD.paged_attention_decode(inp["query"].cpu(), pool, inp["page_table"].cpu(),
+                                     inp["context_lens"].cpu(), layer, kv_scales=sc)
+
+
+CASES = [
+    ("fp32-plumbing", dict()),
+    ("7b-bf16", dict(batch=4, ctx_div=4)),
+    ("14b-int8", dict(batch=4, ctx_div=8, num_layers=3)),
+    ("mixed-fp8", dict(batch=6, ctx_div=32)),
+]
+
+
+@pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
+def test_decode_matches_oracle_on_benchmark_shapes(name, kw):
+    cfg = workloads.scaled(workloads.CONFIGS[name], **kw)
+    layer = cfg.num_layers - 1
+    _say(f"{name} scaled {kw} layer {layer}")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=11, layers=(layer,))
+    out = paged_attention_decode(inp["query"], inp["kv_pool"], inp["page_table"], inp["context_lens"], layer,
+                                 kv_scales=inp["kv_scales"])
+    torch.cuda.synchronize()
+    _assert_close(out, _oracle(inp, layer), name)
+
+
+def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pad=1):
+    g = torch.Generator().manual_seed(seed)
+    PS = 16
+    npages = [(max(c, 0) + PS - 1) // PS for c in ctxs]
+    P = sum(npages) + spare
+    base = torch.randn(P, L, 2, KH, PS, D, generator=g)
+    scales = None
+    if dtype == torch.int8:
+        from oracle.kv_codecs import quantize_int8
+        pool, scales = quantize_int8(base)
+    elif dtype == torch.float8_e4m3fn:
+        amax = base.abs().amax(dim=(-2, -1))
+        scales = amax / 448
+        pool = (base / scales[..., None, None]).to(torch.float8_e4m3fn)
+    else:
+        pool = base.to(dtype)
+    perm = torch.randperm(P, generator=g)
+    table = torch.full((B, max(max(npages), 1) + table_pad), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = torch.randn(B, H, D, generator=g)
+    return q, pool, scales, table, torch.tensor(ctxs, dtype=torch.int32)
+
+
+def _run_both(q, pool, scales, table, lens, layer, scale=None):
+    out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), layer, scale=scale,
+                                 kv_scales=None if scales is None else scales.to(DEV))
+    torch.cuda.synchronize()
+    ref = PD.paged_attention_decode(q, pool, table, lens, layer, scale=scale, kv_scales=scales)
+    return out.cpu(), ref
+
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16, torch.int8, torch.float8_e4m3fn]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("H,KH,D", [(12, 12, 64), (32, 8, 128), (40, 8, 128), (28, 4, 128), (64, 8, 128),
+                                    (16, 1, 128), (8, 2, 256), (6, 3, 64)])
+def test_decode_dtypes_gqa_and_head_dims(dtype, H, KH, D):
+    _say(f"dtype {dtype} H {H} KH {KH} D {D}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, H, KH, D, [37, 160, 1], seed=H + D)
+    out, ref = _run_both(q, pool, sc, table, lens, 1)
+    _assert_close(out, ref, f"{dtype} H{H} KH{KH} D{D}")
+
+
+def test_decode_zero_and_single_token_contexts():
+    _say("ctx 0 and 1")
+    q, pool, sc, table, lens = _pool_case(torch.bfloat16, 4, 8, 2, 128, [0, 1, 16, 0], seed=3)
+    out, ref = _run_both(q, pool, sc, table, lens, 1)
+    assert (out[0] == 0).all() and (out[3] == 0).all()
+    _assert_close(out, ref, "ctx 0/1")
+    # a single token returns its V row for every head of the group
+    pid = int(table[1, 0])
+    for h in range(8):
+        torch.testing.assert_close(out[1, h], pool[pid, 1, 1, h // 4, 0].float(), atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.int8, torch.float8_e4m3fn],
+                         ids=lambda d: str(d).split(".")[-1])
+def test_decode_long_context_many_partitions(dtype):
+    _say(f"long context {dtype}")
+    q, pool, sc, table, lens = _pool_case(dtype, 2, 16, 2, 128, [20011, 3000], L=1, layer=0, seed=5)
+    out, ref = _run_both(q, pool, sc, table, lens, 0)
+    _assert_close(out, ref, "long context")
+
+
+def test_decode_custom_scale_and_layer():
+    _say("custom scale")
+    q, pool, sc, table, lens = _pool_case(torch.float32, 2, 8, 8, 64, [100, 33], L=3, layer=2, seed=8)
+    out, ref = _run_both(q, pool, sc, table, lens, 2, scale=0.37)
+    _assert_close(out, ref, "scale 0.37")
+
+
+def test_decode_absent_pages_are_skipped():
+    _say("absent pages")
+    q, pool, sc, table, lens = _pool_case(torch.float32, 2, 4, 2, 64, [64, 48], L=1, layer=0, seed=9)
+    P = pool.shape[0]
+    table[0, 1] = -1       # negative id
+    table[1, 2] = P + 5    # out of range id
+    out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), 0)
+    torch.cuda.synchronize()
+    for b in range(2):
+        K, V = PD.gather_sequence(pool, table[b], int(lens[b]), 0, skip_invalid=True)
+        ref = PD.dense_attention(q[b], K, V, 1 / 8)
+        _assert_close(out[b].cpu(), ref, f"absent pages b{b}")
+
+
+def test_partitions_then_merge_equals_fused_call():
+    _say("partitions + merge")
+    q, pool, sc, table, lens = _pool_case(torch.int8, 3, 40, 8, 128, [300, 2000, 17], L=1, layer=0, seed=4)
+    q, pool, sc, table, lens = (t.to(DEV) for t in (q, pool, sc, table, lens))
+    out = paged_attention_decode(q, pool, table, lens, 0, kv_scales=sc)
+    lib = _lib.load()
+    B, H, D = q.shape
+    P, L, _, KH, PS, _ = pool.shape
+    from vramancer_amd.paged_attention_cuda import decode_workspace
+    ws = decode_workspace(B, H, KH, D, table.shape[1], q.device)
+    out2 = torch.empty_like(out)
+    s = _lib.stream_of(q)
+    rc = lib.vrm_paged_decode_partitions(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(),
+                                         lens.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P,
+                                         table.shape[1], 0, 1 / math.sqrt(D), _lib.VRM_KV_I8, s)
+    _lib.check(rc, "partitions")
+    rc = lib.vrm_paged_decode_merge(lens.data_ptr(), out2.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS,
+                                    table.shape[1], s)
+    _lib.check(rc, "merge")
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_decode_q4_matches_oracle():
+    _say("q4")
+    g = torch.Generator().manual_seed(12)
+    B, H, KH, D, PS, L = 3, 16, 4, 128, 16, 2
+    ctxs = [70, 1, 400]
+    npages = [(c + PS - 1) // PS for c in ctxs]
+    P = sum(npages) + 2
+    packed = torch.randint(0, 256, (P, L, 2, KH, PS, D // 2), generator=g, dtype=torch.uint8)
+    sc = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 0.1 + 0.01).half()
+    zp = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 15).half()
+    perm = torch.randperm(P, generator=g)
+    table = torch.full((B, max(npages)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = torch.randn(B, H, D, generator=g)
+    lens = torch.tensor(ctxs, dtype=torch.int32)
+    out = paged_attention_decode_q4(q.to(DEV), packed.to(DEV), sc.to(DEV), zp.to(DEV), table.to(DEV), lens.to(DEV), 1)
+    torch.cuda.synchronize()
+    ref = PD.paged_attention_decode_q4(q, packed, sc, zp, table, lens, 1)
+    _assert_close(out.cpu(), ref, "q4")
+
+
+def test_decode_full_size_int8_sampled_parity_and_relabel_invariance():
+    """14B int8 at its full size (B=64, context 4096, 16384 pages): the output of
+    a sample of sequences matches the oracle, and relabelling the physical pages
+    (pool rows permuted, table remapped) leaves the output bit-identical."""
+    cfg = workloads.scaled(workloads.CONFIGS["14b-int8"], num_layers=2)
+    _say("14b-int8 full size, L=2")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=21, layers=(1,))
+    q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
+    out = paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc)
+    torch.cuda.synchronize()
+    for b in (0, 37, 63):
+        pages = table[b].long()
+        sub_pool = pool[pages].cpu()
+        sub_sc = sc[pages].cpu()
+        sub_table = torch.arange(pages.numel(), dtype=torch.int32)[None]
+        ref = PD.paged_attention_decode(q[b:b + 1].cpu(), sub_pool, sub_table, lens[b:b + 1].cpu(), 1,
+                                        kv_scales=sub_sc)
+        _assert_close(out[b:b + 1], ref, f"full-size seq {b}")
+    P = pool.shape[0]
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(3)).to(DEV)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(P, device=DEV)
+    pool2 = pool[perm]       # new page i holds old page perm[i]
+    sc2 = sc[perm]
+    table2 = inv[table.long()].to(torch.int32)
+    out2 = paged_attention_decode(q, pool2, table2, lens, 1, kv_scales=sc2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)

@@ -1,0 +1,136 @@
+"""GPU TurboQuant codec against the oracle (the reference's CPU path).
+
+Bit-exact: polar angle bins, fp16 radius, packed bytes, decompressed rows.
+QJL signs: bit-exact except where the reference's float32 BLAS projection is
+within its own rounding of zero (|p| <= 2^-18 * sum_i |r_i * jl_ji|); the GPU
+takes the sign of a float64 dot product.  QJL norms (fp16): bit-exact on the
+host where the eight-lane reduction order matches PyTorch's, otherwise within
+one fp16 ulp.  Scores: float32 tolerance.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import turboquant as TQ
+from vramancer_amd.kv_quantizer import KVCacheCompressor
+from vramancer_amd.turboquant_cuda import CUDATurboQuantOps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "turboquant_golden.npz")
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _student_t(rows, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(rows, d, generator=g)
+    chi2 = sum(torch.randn(rows, d, generator=g) ** 2 for _ in range(3))
+    return (z / torch.sqrt(chi2 / 3) / math.sqrt(3.0)).to(torch.bfloat16)
+
+
+def _compare(p, kv_cpu, gpu, tag):
+    ref, proj, residual = TQ.compress(p, kv_cpu, pack=False, return_projection=True)
+    assert torch.equal(gpu["radius"].cpu().view(torch.int16), ref["radius"].reshape(-1).view(torch.int16)), tag
+    ga = torch.cat([a.cpu() for a in gpu["angles"]], -1)
+    ra = torch.cat(ref["angles"], -1)
+    assert torch.equal(ga, ra), f"{tag}: {(ga != ra).sum().item()} angle bins differ"
+    gs = gpu["qjl_signs"].cpu()
+    diff = gs != ref["qjl_signs"]
+    if diff.any():
+        mag = residual.abs() @ p.jl_matrix.abs().t()
+        ties = proj.abs() <= mag * 2.0 ** -18
+        assert (ties | ~diff).all(), f"{tag}: {int((diff & ~ties).sum())} QJL signs differ outside ties"
+    print(f"[{tag}] qjl sign tie flips: {int(diff.sum())} of {diff.numel()}", flush=True)
+    gn = gpu["qjl_norms"].cpu().reshape(-1).float()
+    rn = ref["qjl_norms"].reshape(-1).float()
+    exact = torch.equal(gn, rn)
+    if not exact:
+        ulp = rn.abs() * 2.0 ** -10
+        assert ((gn - rn).abs() <= ulp).all(), tag
+    print(f"[{tag}] qjl norms bit-exact: {exact}", flush=True)
+    return ref
+
+
+def test_compress_matches_reference_goldens():
+    g = np.load(GOLDEN, allow_pickle=False)
+    for case in sorted({k.split("/")[0] for k in g.files}):
+        _say(f"golden {case}")
+        hd, bits, seed, rows = (int(v) for v in g[case + "/meta"])
+        torch.manual_seed(seed)
+        comp = KVCacheCompressor(hd, bits).to(DEV)
+        assert np.array_equal(comp._hadamard_signs.cpu().numpy(), g[case + "/signs"])
+        kv = torch.from_numpy(g[case + "/kv"])
+        if bool(g[case + "/kv_is_bf16"]):
+            kv = kv.to(torch.bfloat16)
+        raw = comp.compress(kv.to(DEV), pack=False)
+        assert np.array_equal(raw["radius"].cpu().view(torch.int16).numpy().reshape(-1),
+                              g[case + "/radius"].reshape(-1)), case
+        assert np.array_equal(torch.cat([a.cpu() for a in raw["angles"]], -1).numpy(), g[case + "/angles"]), case
+        packed = comp.compress(kv.to(DEV))
+        assert np.array_equal(packed["angles_packed"].cpu().numpy(), g[case + "/angles_packed"]), case
+        dec = comp.decompress(raw).cpu().numpy()
+        assert np.array_equal(dec, g[case + "/decompress"]), case
+        p = TQ.make_params(hd, bits, seed=seed)
+        _compare(p, kv, raw, case)
+        score = comp.attention_score(torch.from_numpy(g[case + "/q"]).to(DEV), raw).cpu()
+        torch.testing.assert_close(score, torch.from_numpy(g[case + "/score"]), atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_compress_large_student_t_bit_exact(bits):
+    _say(f"student-t 16384 rows bits {bits}")
+    p = TQ.make_params(128, bits, seed=2026)
+    kv = _student_t(16384, 128, 77 + bits)
+    gpu = CUDATurboQuantOps.compress_gpu(kv.to(DEV), 128, 128, 7, bits, p.signs.to(DEV), p.jl_matrix.to(DEV))
+    torch.cuda.synchronize()
+    ref = _compare(p, kv, gpu, f"t3 b{bits}")
+    dec = CUDATurboQuantOps.decompress_gpu(gpu, 128, 128, 7, bits, p.signs.to(DEV)).cpu()
+    assert torch.equal(dec, TQ.decompress(p, ref))
+
+
+@pytest.mark.parametrize("head_dim,bits", [(96, 3), (64, 8), (256, 4), (128, 1)])
+def test_compress_other_shapes(head_dim, bits):
+    _say(f"shape d{head_dim} b{bits}")
+    p = TQ.make_params(head_dim, bits, seed=head_dim + bits)
+    kv = torch.randn(513, head_dim, generator=torch.Generator().manual_seed(1))
+    gpu = CUDATurboQuantOps.compress_gpu(kv.to(DEV), head_dim, p.padded_dim, p.n_levels, bits, p.signs.to(DEV),
+                                         p.jl_matrix.to(DEV))
+    ref = _compare(p, kv, gpu, f"d{head_dim} b{bits}")
+    dec = CUDATurboQuantOps.decompress_gpu(gpu, head_dim, p.padded_dim, p.n_levels, bits, p.signs.to(DEV)).cpu()
+    assert torch.equal(dec, TQ.decompress(p, ref))
+
+
+def test_compressor_api_roundtrip_and_batch():
+    _say("compressor api")
+    torch.manual_seed(42)
+    comp = KVCacheCompressor(128, 4).to(DEV)
+    p = TQ.make_params(128, 4, seed=42)
+    k = torch.randn(3, 8, 128, device=DEV)
+    v = torch.randn(5, 128, device=DEV)
+    packed = comp.compress(k)
+    assert packed["shape"] == (3, 8, 128)
+    assert comp.decompress(packed).shape == (3, 8, 128)
+    refs = comp.compress_batch([k, v])
+    raw_k = comp.compress(k, pack=False)
+    assert torch.equal(refs[0]["qjl_signs"], raw_k["qjl_signs"])
+    assert torch.equal(torch.cat(refs[1]["angles"], -1), torch.cat(comp.compress(v, pack=False)["angles"], -1))
+    single = comp.compress_batch([v])
+    assert "angles_packed" in single[0]  # the reference's single-item quirk
+    # sparse V attention against the oracle on the same codes
+    q = torch.randn(1, 128)
+    keys = torch.randn(40, 128)
+    values = torch.randn(40, 128)
+    ck_g = comp.compress(keys.to(DEV), pack=False)
+    cv_g = [comp.compress(values[i:i + 1].to(DEV), pack=False) for i in range(40)]
+    out = comp.sparse_v_attend(q.to(DEV), ck_g, cv_g, sparse_v_ratio=0.25).cpu()
+    ck_r = TQ.compress(p, keys, pack=False)
+    cv_r = [TQ.compress(p, values[i:i + 1], pack=False) for i in range(40)]
+    ref = TQ.sparse_v_attend(p, q, ck_r, cv_r, sparse_v_ratio=0.25)
+    torch.testing.assert_close(out, ref, atol=1e-4, rtol=1e-4)
+    assert comp.bits_per_dim() == TQ.bits_per_dim(p)

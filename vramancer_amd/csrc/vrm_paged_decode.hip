@@ -1,0 +1,681 @@
+// Split-K paged decode attention for gfx950.
+//
+// Semantics follow the reference's decode path (core/paged_attention_cuda.py:
+// 187-231 and csrc/paged_attention_kernel.cu:61-174): per sequence b and query
+// head h, out = softmax(scale * q . K^T) V over the first context_lens[b]
+// tokens of the sequence's pages, with GQA head h reading kv-head h / (H/KH).
+//
+// Design (MI355X-first, not the reference's one-warp-per-head loop):
+//  * one 64-lane wavefront per (sequence, kv-head, head group, token
+//    partition); the query heads that share a kv-head are packed into the same
+//    wavefront, so every K/V byte is read from HBM once per partition instead
+//    of once per query head;
+//  * each lane issues 16-byte loads of the contiguous [PS][D] page slice; the
+//    page ids of a partition are fetched with one vector load up front and the
+//    next page is loaded while the current one is consumed;
+//  * dequantization happens in registers (int8 * per-token scale, e4m3 *
+//    per-page scale, (nibble - zero) * scale for the 4-bit pool);
+//  * phase 1 writes all scores of the partition to LDS, phase 2 takes the
+//    exact partition maximum, phase 3 streams V once with fixed weights, so no
+//    running rescale of the accumulators is needed;
+//  * partitions leave (max, sum, unnormalised acc) in the workspace and a
+//    second kernel merges them with log-sum-exp weights.
+#include "vrm_common.h"
+
+#include <math.h>
+
+namespace vrm {
+namespace {
+
+constexpr int kPS = 16;               // tokens per page (the reference's default)
+constexpr int kMaxPagesPerSplit = 64;  // one page id per lane
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum KvKind { K_F32 = 0, K_F16 = 1, K_BF16 = 2, K_I8 = 3, K_FP8 = 4, K_Q4 = 5 };
+
+template <int KIND> struct Kv;
+template <> struct Kv<K_F32> { static constexpr int kElems = 4; };   // elements per 16 B
+template <> struct Kv<K_F16> { static constexpr int kElems = 8; };
+template <> struct Kv<K_BF16> { static constexpr int kElems = 8; };
+template <> struct Kv<K_I8> { static constexpr int kElems = 16; };
+template <> struct Kv<K_FP8> { static constexpr int kElems = 16; };
+template <> struct Kv<K_Q4> { static constexpr int kElems = 32; };
+
+template <int KIND>
+__device__ __forceinline__ void unpack16(const uint4 r, float* x) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+  if constexpr (KIND == K_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(w[i]);
+  } else if constexpr (KIND == K_F16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+      x[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  } else if constexpr (KIND == K_BF16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else if constexpr (KIND == K_I8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * i + j] = (float)(int8_t)(w[i] >> (8 * j));
+    }
+  } else if constexpr (KIND == K_FP8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * i + j] = e4m3fn_to_f32((w[i] >> (8 * j)) & 0xffu);
+    }
+  } else {  // K_Q4: raw nibbles; byte j holds d = 2j (low) and 2j + 1 (high)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t byte = (w[i] >> (8 * j)) & 0xffu;
+        x[8 * i + 2 * j] = (float)(byte & 0xfu);
+        x[8 * i + 2 * j + 1] = (float)(byte >> 4);
+      }
+    }
+  }
+}
+
+struct DecodeArgs {
+  const float* query;
+  const uint8_t* pool;
+  const float* scales;        // int8 / fp8 scale arrays
+  const uint16_t* q4_scale;   // 4-bit pool group scales (fp16 bits)
+  const uint16_t* q4_zero;    // 4-bit pool group zeros (fp16 bits)
+  const int32_t* page_table;
+  const int32_t* ctx_lens;
+  float* part_acc;            // [B][H][nsplit][D]
+  float* part_ml;             // [B][H][nsplit][2]
+  int H, KH, L, P, max_pp, layer;
+  float qscale;               // scale * log2(e): scores live in the log2 domain
+  int pages_per_split, nsplit;
+};
+
+// Registers holding one page of K or V for this lane, plus its dequant factors.
+template <int KIND, int LPP>
+struct PageRegs {
+  uint4 data[LPP];
+  float s0[LPP];  // K: key scale of the lane's token / V: value scale (int8, q4)
+  float s1[LPP];  // K: value scale of the lane's token (int8) / V, q4: zero point
+};
+
+// One wavefront per (split, kv head x head chunk, sequence).
+template <int KIND, int D, int G>
+__global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
+  constexpr int E = Kv<KIND>::kElems;         // elements per 16-byte lane chunk
+  constexpr int RB = D * 16 / E;              // bytes per token row
+  constexpr int LPT = RB / 16;                // lanes per token
+  constexpr int TPL = 64 / LPT;               // tokens per wave load
+  constexpr int LPP = (kPS + TPL - 1) / TPL;  // wave loads per page
+  constexpr int HEAD_BYTES = kPS * RB;        // one (page, layer, kv, head) slice
+  constexpr int Q4G = D / 32;                 // 4-bit groups per row
+  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "lane mapping");
+  static_assert(TPL <= kPS || (TPL % kPS) == 0, "page mapping");
+  static_assert(LPP * TPL * RB == (TPL <= kPS ? HEAD_BYTES : TPL * RB), "load coverage");
+
+  extern __shared__ float lds[];
+  const int TS = a.pages_per_split * kPS;
+  float* s_lds = lds;                 // [G][TS] scores, then weights * V scale
+  float* v_scale_lds = lds + G * TS;  // [TS] per-token V dequant factor (int8)
+
+  const int lane = threadIdx.x;
+  const int split = blockIdx.x;
+  const int b = blockIdx.z;
+  const int group = a.H / a.KH;
+  const int chunks = group / G;
+  const int kvh = blockIdx.y / chunks;
+  const int h0 = kvh * group + (blockIdx.y % chunks) * G;
+
+  const int ctx = a.ctx_lens[b];
+  const int num_pages = ctx > 0 ? min((ctx + kPS - 1) / kPS, a.max_pp) : 0;
+  const int p_begin = split * a.pages_per_split;
+  const int p_end = min(p_begin + a.pages_per_split, num_pages);
+  float* ml_base = a.part_ml + (((size_t)b * a.H + h0) * a.nsplit + split) * 2;
+  if (p_begin >= p_end) {
+    if (lane < G) {
+      ml_base[(size_t)lane * a.nsplit * 2] = -INFINITY;
+      ml_base[(size_t)lane * a.nsplit * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  const int n_pages = p_end - p_begin;
+  const int tok_end = min(p_end * kPS, ctx) - p_begin * kPS;  // valid tokens in split
+
+  // Page ids of this split: lane i holds logical page p_begin + i.
+  int my_pid = -1;
+  if (lane < n_pages) my_pid = a.page_table[(size_t)b * a.max_pp + p_begin + lane];
+
+  const int c = lane % LPT;   // which 16-byte chunk of a token row
+  const int tl = lane / LPT;  // which token of a wave load
+  const bool lane_live = (TPL <= kPS) || (tl < kPS);
+
+  const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
+  const size_t page_stride = kv_stride * 2 * a.L;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
+
+  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+  // Index of (page, layer, kv, kvh) in units of heads.
+  auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
+
+  // Loads page `pid` of K (kv = 0) or V (kv = 1) and the factors this lane needs.
+  auto load_page = [&](PageRegs<KIND, LPP>& r, int pid, int kv) {
+    const bool ok = page_ok(pid);
+    const uint8_t* base = layer_base + (size_t)(ok ? pid : 0) * page_stride + (size_t)kv * kv_stride;
+#pragma unroll
+    for (int j = 0; j < LPP; ++j) {
+      const int tp = j * TPL + tl;
+      const bool live = ok && lane_live;
+      r.data[j] = live ? *reinterpret_cast<const uint4*>(base + (size_t)j * 1024 + (size_t)lane * 16)
+                       : make_uint4(0, 0, 0, 0);
+      r.s0[j] = 1.f;
+      r.s1[j] = 0.f;
+      if constexpr (KIND == K_I8) {
+        if (live) {
+          const size_t ts = head_index(pid, kv) * kPS + tp;
+          r.s0[j] = a.scales[ts];
+          if (kv == 0) r.s1[j] = a.scales[ts + (size_t)a.KH * kPS];  // V scale of the same token
+        }
+      } else if constexpr (KIND == K_FP8) {
+        if (live) {
+          r.s0[j] = a.scales[head_index(pid, kv)];
+          if (kv == 0) r.s1[j] = a.scales[head_index(pid, 1)];
+        }
+      } else if constexpr (KIND == K_Q4) {
+        if (live) {
+          const size_t rs = (head_index(pid, kv) * kPS + tp) * Q4G + c;  // lane chunk c == group c
+          r.s0[j] = f16_bits_to_f32(a.q4_scale[rs]);
+          r.s1[j] = f16_bits_to_f32(a.q4_zero[rs]);
+        }
+      }
+    }
+  };
+
+  // Query chunk of every head of the group, pre-scaled into the log2 domain.
+  float qr[G][E];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* qh = a.query + ((size_t)b * a.H + h0 + g) * D;
+#pragma unroll
+    for (int e = 0; e < E; ++e) qr[g][e] = qh[c * E + e] * a.qscale;
+  }
+
+  // ---------------- phase 1: scores ----------------
+  {
+    PageRegs<KIND, LPP> cur;
+    int pid_cur = __builtin_amdgcn_readlane(my_pid, 0);
+    load_page(cur, pid_cur, 0);
+    for (int pi = 0; pi < n_pages; ++pi) {
+      PageRegs<KIND, LPP> nxt;
+      const int pid_nxt = (pi + 1 < n_pages) ? __builtin_amdgcn_readlane(my_pid, pi + 1) : -1;
+      if (pi + 1 < n_pages) load_page(nxt, pid_nxt, 0);
+      const bool ok = page_ok(pid_cur);
+#pragma unroll
+      for (int j = 0; j < LPP; ++j) {
+        const int tp = j * TPL + tl;  // token within page
+        const int t = pi * kPS + tp;  // token within split
+        const bool valid = ok && lane_live && tp < kPS && t < tok_end;
+        float x[E];
+        unpack16<KIND>(cur.data[j], x);
+        if constexpr (KIND == K_Q4) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) x[e] = (x[e] - cur.s1[j]) * cur.s0[j];
+        }
+        float part[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float s = 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) s = fmaf(qr[g][e], x[e], s);
+          part[g] = group_sum<LPT>(s);
+        }
+        if (c == 0 && lane_live && tp < kPS && t < TS) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float sc = part[g];
+            if constexpr (KIND == K_I8 || KIND == K_FP8) sc *= cur.s0[j];
+            s_lds[g * TS + t] = valid ? sc : -INFINITY;
+          }
+          v_scale_lds[t] = (KIND == K_I8 || KIND == K_FP8) ? cur.s1[j] : 1.f;
+        }
+      }
+      cur = nxt;
+      pid_cur = pid_nxt;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- phase 2: exact softmax statistics ----------------
+  float m_g[G], l_g[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mx = -INFINITY;
+    for (int t = lane; t < tok_end; t += 64) mx = fmaxf(mx, s_lds[g * TS + t]);
+    mx = group_max<64>(mx);
+    float sum = 0.f;
+    for (int t = lane; t < tok_end; t += 64) {
+      const float s = s_lds[g * TS + t];
+      const float p = (s == -INFINITY) ? 0.f : exp2f(s - mx);
+      sum += p;
+      s_lds[g * TS + t] = p * v_scale_lds[t];
+    }
+    m_g[g] = mx;
+    l_g[g] = group_sum<64>(sum);
+  }
+  __syncthreads();
+
+  // ---------------- phase 3: weighted V ----------------
+  float acc[G][E];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+  {
+    PageRegs<KIND, LPP> cur;
+    int pid_cur = __builtin_amdgcn_readlane(my_pid, 0);
+    load_page(cur, pid_cur, 1);
+    for (int pi = 0; pi < n_pages; ++pi) {
+      PageRegs<KIND, LPP> nxt;
+      const int pid_nxt = (pi + 1 < n_pages) ? __builtin_amdgcn_readlane(my_pid, pi + 1) : -1;
+      if (pi + 1 < n_pages) load_page(nxt, pid_nxt, 1);
+      const bool ok = page_ok(pid_cur);
+#pragma unroll
+      for (int j = 0; j < LPP; ++j) {
+        const int tp = j * TPL + tl;
+        const int t = pi * kPS + tp;
+        const bool valid = ok && lane_live && tp < kPS && t < tok_end;
+        if (valid) {
+          float x[E];
+          unpack16<KIND>(cur.data[j], x);
+          if constexpr (KIND == K_Q4) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = (x[e] - cur.s1[j]) * cur.s0[j];
+          }
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float w = s_lds[g * TS + t];
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[g][e] = fmaf(w, x[e], acc[g][e]);
+          }
+        }
+      }
+      cur = nxt;
+      pid_cur = pid_nxt;
+    }
+  }
+
+  // Lanes that hold the same chunk c (different tokens) sum their partials.
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = strided_sum<LPT>(acc[g][e]);
+
+  if (tl == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float* dst = a.part_acc + ((((size_t)b * a.H + h0 + g) * a.nsplit + split) * D) + c * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) dst[e] = acc[g][e];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      ml_base[(size_t)g * a.nsplit * 2] = m_g[g];
+      ml_base[(size_t)g * a.nsplit * 2 + 1] = l_g[g];
+    }
+  }
+}
+
+// Merges the partitions of one (sequence, head): out = sum_s w_s acc_s / sum_s w_s l_s
+// with w_s = 2^(m_s - max_s m_s).
+template <int D>
+__global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restrict__ part_acc,
+                                                           const float* __restrict__ part_ml,
+                                                           const int32_t* __restrict__ ctx_lens,
+                                                           float* __restrict__ out, int H, int nsplit,
+                                                           int pages_per_split, int max_pp) {
+  constexpr int PER = D / 64;
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int ctx = ctx_lens[b];
+  float* o = out + ((size_t)b * H + h) * D;
+  const int num_pages = ctx > 0 ? min((ctx + kPS - 1) / kPS, max_pp) : 0;
+  const int nact = min(nsplit, (num_pages + pages_per_split - 1) / pages_per_split);
+  const float* ml = part_ml + ((size_t)b * H + h) * nsplit * 2;
+  const float* acc = part_acc + ((size_t)b * H + h) * nsplit * D;
+  float M = -INFINITY;
+  for (int s = 0; s < nact; ++s) M = fmaxf(M, ml[2 * s]);
+  float res[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) res[i] = 0.f;
+  float Lsum = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < nact; ++s) {
+      const float m = ml[2 * s];
+      if (m == -INFINITY) continue;
+      const float w = exp2f(m - M);
+      Lsum = fmaf(w, ml[2 * s + 1], Lsum);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, acc[(size_t)s * D + i * 64 + lane], res[i]);
+    }
+  }
+  const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) o[i * 64 + lane] = res[i] * inv;
+}
+
+// Largest divisor of the GQA group size that fits the register budget.
+int pick_group_tile(int group, int max_tile) {
+  for (int g = max_tile; g >= 1; --g)
+    if (group % g == 0) return g;
+  return 1;
+}
+
+template <int KIND, int D, int G>
+hipError_t launch_split(const DecodeArgs& a, int B, hipStream_t st) {
+  const int chunks = (a.H / a.KH) / G;
+  dim3 grid(a.nsplit, a.KH * chunks, B);
+  const size_t lds = (size_t)(G + 1) * a.pages_per_split * kPS * sizeof(float);
+  hipLaunchKernelGGL((decode_split_kernel<KIND, D, G>), grid, dim3(64), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int KIND, int D>
+hipError_t dispatch_g(const DecodeArgs& a, int B, int G, hipStream_t st) {
+  if constexpr (KIND == K_Q4) {  // 32 elements per lane chunk: at most 4 heads per wave
+    switch (G) {
+      case 1: return launch_split<KIND, D, 1>(a, B, st);
+      case 2: return launch_split<KIND, D, 2>(a, B, st);
+      case 3: return launch_split<KIND, D, 3>(a, B, st);
+      default: return launch_split<KIND, D, 4>(a, B, st);
+    }
+  } else {
+    switch (G) {
+      case 1: return launch_split<KIND, D, 1>(a, B, st);
+      case 2: return launch_split<KIND, D, 2>(a, B, st);
+      case 3: return launch_split<KIND, D, 3>(a, B, st);
+      case 4: return launch_split<KIND, D, 4>(a, B, st);
+      case 5: return launch_split<KIND, D, 5>(a, B, st);
+      case 6: return launch_split<KIND, D, 6>(a, B, st);
+      case 7: return launch_split<KIND, D, 7>(a, B, st);
+      default: return launch_split<KIND, D, 8>(a, B, st);
+    }
+  }
+}
+
+template <int KIND>
+hipError_t dispatch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
+  switch (D) {
+    case 64: return dispatch_g<KIND, 64>(a, B, G, st);
+    case 128: return dispatch_g<KIND, 128>(a, B, G, st);
+    default: return dispatch_g<KIND, 256>(a, B, G, st);
+  }
+}
+
+hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStream_t st) {
+  dim3 grid(a.H, B);
+  switch (D) {
+    case 64:
+      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
+                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      break;
+    case 128:
+      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
+                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      break;
+    default:
+      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
+                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      break;
+  }
+  return hipGetLastError();
+}
+
+// Pages per partition: enough partitions to give the chip >= ~4 waves per
+// SIMD of work, each partition at most 64 pages (1024 tokens).
+int pages_per_split_for(int B, int H, int KH, int max_pp, int max_tile) {
+  const long units = (long)B * KH * ((H / KH) / pick_group_tile(H / KH, max_tile));
+  const long target = 4096;
+  long want_splits = (target + units - 1) / units;
+  if (want_splits < 1) want_splits = 1;
+  long pps = (max_pp + want_splits - 1) / want_splits;
+  if (pps < 4) pps = 4;
+  if (pps > kMaxPagesPerSplit) pps = kMaxPagesPerSplit;
+  return (int)pps;
+}
+
+int check_common(const float* query, const void* pool, const int32_t* page_table, const int32_t* ctx, float* out,
+                 int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx, float scale) {
+  if (!query || !pool || !page_table || !ctx || !out) {
+    set_error("vrm_paged_decode: null pointer argument");
+    return VRM_ERR_ARG;
+  }
+  if (B <= 0 || H <= 0 || KH <= 0 || D <= 0 || PS <= 0 || L <= 0 || P <= 0 || max_pp <= 0) {
+    set_error("vrm_paged_decode: sizes must be positive (B=%d H=%d KH=%d D=%d PS=%d L=%d P=%d max_pp=%d)", B, H, KH,
+              D, PS, L, P, max_pp);
+    return VRM_ERR_ARG;
+  }
+  if (H % KH != 0) {
+    set_error("vrm_paged_decode: num_heads %d is not a multiple of num_kv_heads %d", H, KH);
+    return VRM_ERR_ARG;
+  }
+  if (layer_idx < 0 || layer_idx >= L) {
+    set_error("vrm_paged_decode: layer_idx %d outside [0, %d)", layer_idx, L);
+    return VRM_ERR_ARG;
+  }
+  if (!(scale == scale)) {
+    set_error("vrm_paged_decode: scale is NaN");
+    return VRM_ERR_ARG;
+  }
+  if (PS != kPS) {
+    set_error("vrm_paged_decode: page_size %d unsupported (compiled for %d)", PS, kPS);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (D != 64 && D != 128 && D != 256) {
+    set_error("vrm_paged_decode: head_dim %d unsupported (64, 128, 256)", D);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if ((long)B * H > 65535L * 65535L) {
+    set_error("vrm_paged_decode: batch too large");
+    return VRM_ERR_UNSUPPORTED;
+  }
+  return VRM_OK;
+}
+
+// Which passes run_decode enqueues.
+enum Passes { kBoth = 3, kPartitionsOnly = 1, kMergeOnly = 2 };
+
+int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D,
+               float scale, hipStream_t st, int passes) {
+  const int max_tile = kind == K_Q4 ? 4 : 8;
+  const int G = pick_group_tile(a.H / a.KH, max_tile);
+  a.pages_per_split = pages_per_split_for(B, a.H, a.KH, a.max_pp, max_tile);
+  a.nsplit = (a.max_pp + a.pages_per_split - 1) / a.pages_per_split;
+  if (a.nsplit > 65535) {
+    set_error("vrm_paged_decode: page table too wide (%d pages)", a.max_pp);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  const size_t need = vrm_paged_decode_workspace_bytes(B, a.H, D, a.nsplit);
+  if (!workspace || workspace_bytes < need) {
+    set_error("vrm_paged_decode: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+    return VRM_ERR_WORKSPACE;
+  }
+  a.part_acc = reinterpret_cast<float*>(workspace);
+  a.part_ml = a.part_acc + (size_t)B * a.H * a.nsplit * D;
+  a.qscale = scale * kLog2e;
+  hipError_t e = hipSuccess;
+  if (passes & kPartitionsOnly) {
+    switch (kind) {
+      case K_F32: e = dispatch_d<K_F32>(a, B, D, G, st); break;
+      case K_F16: e = dispatch_d<K_F16>(a, B, D, G, st); break;
+      case K_BF16: e = dispatch_d<K_BF16>(a, B, D, G, st); break;
+      case K_I8: e = dispatch_d<K_I8>(a, B, D, G, st); break;
+      case K_FP8: e = dispatch_d<K_FP8>(a, B, D, G, st); break;
+      default: e = dispatch_d<K_Q4>(a, B, D, G, st); break;
+    }
+    if (e != hipSuccess) {
+      set_error("vrm_paged_decode: partition kernel launch failed: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  if (passes & kMergeOnly) {
+    e = launch_reduce(a, out, B, D, st);
+    if (e != hipSuccess) {
+      set_error("vrm_paged_decode: merge kernel launch failed: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+  }
+  clear_error();
+  return VRM_OK;
+}
+
+int kind_of(int kv_dtype) {
+  switch (kv_dtype) {
+    case VRM_KV_F32: return K_F32;
+    case VRM_KV_F16: return K_F16;
+    case VRM_KV_BF16: return K_BF16;
+    case VRM_KV_I8: return K_I8;
+    case VRM_KV_FP8E4M3: return K_FP8;
+    default: return -1;
+  }
+}
+
+int decode_entry(const float* query, const void* kv_pool, const float* kv_scales, const int32_t* page_table,
+                 const int32_t* context_lens, float* out, void* workspace, size_t workspace_bytes, int B, int H,
+                 int KH, int D, int PS, int L, int P, int max_pp, int layer_idx, float scale, int kv_dtype,
+                 vrm_stream_t stream, int passes) {
+  int rc = check_common(query, kv_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  const int kind = kind_of(kv_dtype);
+  if (kind < 0) {
+    set_error("vrm_paged_decode: unknown kv_dtype %d", kv_dtype);
+    return VRM_ERR_ARG;
+  }
+  if ((kind == K_I8 || kind == K_FP8) && !kv_scales) {
+    set_error("vrm_paged_decode: quantized pool needs kv_scales");
+    return VRM_ERR_ARG;
+  }
+  if ((kind != K_I8 && kind != K_FP8) && kv_scales) {
+    set_error("vrm_paged_decode: kv_scales given for a float pool");
+    return VRM_ERR_ARG;
+  }
+  DecodeArgs a{};
+  a.query = query;
+  a.pool = static_cast<const uint8_t*>(kv_pool);
+  a.scales = kv_scales;
+  a.page_table = page_table;
+  a.ctx_lens = context_lens;
+  a.H = H;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.max_pp = max_pp;
+  a.layer = layer_idx;
+  return run_decode(a, kind, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
+                    passes);
+}
+
+}  // namespace
+}  // namespace vrm
+
+using namespace vrm;
+
+extern "C" int vrm_paged_decode_num_splits(int B, int H, int KH, int max_pp, int page_size) {
+  (void)page_size;
+  if (B <= 0 || H <= 0 || KH <= 0 || max_pp <= 0 || H % KH) return 0;
+  const int pps = pages_per_split_for(B, H, KH, max_pp, 8);
+  return (max_pp + pps - 1) / pps;
+}
+
+extern "C" size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit) {
+  if (B <= 0 || H <= 0 || D <= 0 || nsplit <= 0) return 0;
+  return (size_t)B * H * nsplit * (D + 2) * sizeof(float);
+}
+
+extern "C" int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_scales,
+                                const int32_t* page_table, const int32_t* context_lens, float* out, void* workspace,
+                                size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                int layer_idx, float scale, int kv_dtype, vrm_stream_t stream) {
+  return decode_entry(query, kv_pool, kv_scales, page_table, context_lens, out, workspace, workspace_bytes, B, H, KH,
+                      D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth);
+}
+
+extern "C" int vrm_paged_decode_partitions(const float* query, const void* kv_pool, const float* kv_scales,
+                                           const int32_t* page_table, const int32_t* context_lens, void* workspace,
+                                           size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,
+                                           int max_pp, int layer_idx, float scale, int kv_dtype,
+                                           vrm_stream_t stream) {
+  // `out` is not touched by the partition pass; pass a non-null placeholder for the checks.
+  return decode_entry(query, kv_pool, kv_scales, page_table, context_lens, reinterpret_cast<float*>(workspace),
+                      workspace, workspace_bytes, B, H, KH, D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream,
+                      kPartitionsOnly);
+}
+
+extern "C" int vrm_paged_decode_merge(const int32_t* context_lens, float* out, const void* workspace,
+                                      size_t workspace_bytes, int B, int H, int KH, int D, int PS, int max_pp,
+                                      vrm_stream_t stream) {
+  if (!context_lens || !out || !workspace) {
+    set_error("vrm_paged_decode_merge: null pointer argument");
+    return VRM_ERR_ARG;
+  }
+  if (B <= 0 || H <= 0 || KH <= 0 || H % KH || max_pp <= 0) {
+    set_error("vrm_paged_decode_merge: bad sizes");
+    return VRM_ERR_ARG;
+  }
+  if (PS != kPS || (D != 64 && D != 128 && D != 256)) {
+    set_error("vrm_paged_decode_merge: unsupported page_size %d / head_dim %d", PS, D);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  DecodeArgs a{};
+  a.ctx_lens = context_lens;
+  a.H = H;
+  a.KH = KH;
+  a.max_pp = max_pp;
+  a.L = 1;
+  a.P = 1;
+  // The merge only depends on the partition geometry, which is the same for every dtype except
+  // the 4-bit pool; callers of the 4-bit pool use vrm_paged_decode_q4.
+  return run_decode(a, K_I8, out, const_cast<void*>(workspace), workspace_bytes, B, D, 1.f,
+                    reinterpret_cast<hipStream_t>(stream), kMergeOnly);
+}
+
+extern "C" int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4, const uint16_t* kv_scales,
+                                   const uint16_t* kv_zeros, const int32_t* page_table, const int32_t* context_lens,
+                                   float* out, void* workspace, size_t workspace_bytes, int B, int H, int KH, int D,
+                                   int PS, int L, int P, int max_pp, int layer_idx, float scale,
+                                   vrm_stream_t stream) {
+  int rc = check_common(query, kv_pool_q4, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  if (!kv_scales || !kv_zeros) {
+    set_error("vrm_paged_decode_q4: null scales/zeros");
+    return VRM_ERR_ARG;
+  }
+  if (D % 32) {
+    set_error("vrm_paged_decode_q4: head_dim %d is not a multiple of the group size 32", D);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  DecodeArgs a{};
+  a.query = query;
+  a.pool = kv_pool_q4;
+  a.q4_scale = kv_scales;
+  a.q4_zero = kv_zeros;
+  a.page_table = page_table;
+  a.ctx_lens = context_lens;
+  a.H = H;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.max_pp = max_pp;
+  a.layer = layer_idx;
+  return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
+                    kBoth);
+}

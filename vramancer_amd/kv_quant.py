@@ -1,0 +1,164 @@
+"""int8 / fp8-e4m3 paged KV pools: allocation, quantize-on-append, bulk page
+writes and dequantization, all on the GPU.
+
+VRAMancer has no int8 or fp8 KV codec (core/kv_quantizer.py is
+TurboQuant-only and fp8 exists only as vLLM's kv_cache_dtype); this module
+defines them in the style of the reference's pool API:
+
+* the pool keeps the reference layout ``[P, L, 2, KH, PS, D]``
+  (core/paged_attention.py:321-330) with int8 or float8_e4m3fn elements;
+* int8 uses one float32 scale per (page, layer, K/V, kv-head, token):
+  ``scale = amax / 127``, ``code = clamp(round_half_even(x / scale), -127, 127)``
+  (amax == 0 gives scale 0 and codes 0);
+* fp8 uses one float32 scale per (page, layer, K/V, kv-head):
+  ``scale = amax / 448``, ``code = e4m3fn(x / scale)`` rounded to nearest even.
+  On append the page scale only grows; when it grows, codes already in the
+  page are re-encoded as ``e4m3fn(float(code) * old / new)``;
+* the write itself replaces the raw index-put of
+  ``PagedKVCacheManager.write_kv`` (core/paged_attention.py:611-612).
+"""
+from __future__ import annotations
+
+from typing import Any, Optional, Tuple
+
+from . import _lib
+
+__all__ = [
+    "allocate_pool",
+    "quantize_append",
+    "quantize_pages",
+    "dequantize_pages",
+]
+
+CODECS = ("int8", "fp8")
+
+
+def _codec_dtype(codec: str):
+    import torch
+
+    if codec == "int8":
+        return torch.int8
+    if codec == "fp8":
+        return torch.float8_e4m3fn
+    raise ValueError(f"unknown codec {codec!r}; expected one of {CODECS}")
+
+
+def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, head_dim: int, codec: str,
+                  page_size: int = 16, device: Any = "cuda") -> Tuple[Any, Any]:
+    """Zero-initialised (codes, scales) for a quantized pool."""
+    import torch
+
+    dtype = _codec_dtype(codec)
+    pool = torch.zeros((num_pages, num_layers, 2, num_kv_heads, page_size, head_dim), dtype=torch.uint8,
+                       device=device).view(dtype)
+    if codec == "int8":
+        scales = torch.zeros((num_pages, num_layers, 2, num_kv_heads, page_size), dtype=torch.float32, device=device)
+    else:
+        scales = torch.zeros((num_pages, num_layers, 2, num_kv_heads), dtype=torch.float32, device=device)
+    return pool, scales
+
+
+def _check_pool(kv_pool, kv_scales):
+    import torch
+
+    code = _lib.kv_dtype_code(kv_pool.dtype)
+    if code not in (_lib.VRM_KV_I8, _lib.VRM_KV_FP8E4M3):
+        raise RuntimeError(f"kv_pool dtype {kv_pool.dtype} is not a quantized pool (int8, float8_e4m3fn)")
+    P, L, two, KH, PS, D = kv_pool.shape
+    want = (P, L, 2, KH, PS) if code == _lib.VRM_KV_I8 else (P, L, 2, KH)
+    if tuple(kv_scales.shape) != want or kv_scales.dtype != torch.float32:
+        raise RuntimeError(f"kv_scales must be float32 of shape {want}")
+    if not (kv_pool.is_contiguous() and kv_scales.is_contiguous()):
+        raise RuntimeError("kv_pool and kv_scales must be contiguous (they are written in place)")
+    return code, P, L, KH, PS, D
+
+
+def quantize_append(kv_pool: Any, kv_scales: Any, layer_idx: int, page_ids: Any, slots: Any,
+                    key: Any, value: Any) -> None:
+    """Quantizes N new tokens into their (page, slot) of layer ``layer_idx``.
+
+    ``key``/``value`` are [N, KH, D] float32/float16/bfloat16 on the pool's
+    device; ``page_ids``/``slots`` are [N] integer tensors (as returned by the
+    reference's ``append_token``, core/paged_attention.py:431-459).  For fp8
+    pools, tokens of one call must go to distinct pages.
+    """
+    import torch
+
+    _lib.require_cuda(kv_pool, kv_scales, page_ids, slots, key, value)
+    code, P, L, KH, PS, D = _check_pool(kv_pool, kv_scales)
+    if key.shape != value.shape or key.dim() != 3 or key.shape[1:] != (KH, D):
+        raise RuntimeError(f"key/value must be [N, {KH}, {D}], got {tuple(key.shape)} / {tuple(value.shape)}")
+    if key.dtype != value.dtype:
+        raise RuntimeError("key and value must share a dtype")
+    N = key.shape[0]
+    page_ids = page_ids.to(torch.int32).contiguous()
+    slots = slots.to(torch.int32).contiguous()
+    if page_ids.shape != (N,) or slots.shape != (N,):
+        raise RuntimeError("page_ids and slots must be [N]")
+    key = key.contiguous()
+    value = value.contiguous()
+    rc = _lib.load().vrm_kv_quant_append(
+        _lib.ptr(key), _lib.ptr(value), _lib.src_dtype_code(key.dtype), _lib.ptr(page_ids), _lib.ptr(slots), N,
+        _lib.ptr(kv_pool), _lib.ptr(kv_scales), code, KH, D, PS, L, P, int(layer_idx), _lib.stream_of(kv_pool),
+    )
+    _lib.check(rc, "quantize_append")
+
+
+def quantize_pages(kv_pool: Any, kv_scales: Any, layer_idx: int, page_ids: Any, key_pages: Any, value_pages: Any,
+                   n_valid: Optional[Any] = None) -> None:
+    """Bulk (prefill) write of whole pages.
+
+    ``key_pages``/``value_pages`` are [NP, KH, PS, D]; page n is written to
+    physical page ``page_ids[n]`` and holds ``n_valid[n]`` tokens (default: a
+    full page).  Slots past ``n_valid`` get code 0; the fp8 page scale is taken
+    over the valid tokens only.
+    """
+    import torch
+
+    _lib.require_cuda(kv_pool, kv_scales, page_ids, key_pages, value_pages, n_valid)
+    code, P, L, KH, PS, D = _check_pool(kv_pool, kv_scales)
+    if key_pages.shape != value_pages.shape or key_pages.dim() != 4 or key_pages.shape[1:] != (KH, PS, D):
+        raise RuntimeError(f"key/value pages must be [NP, {KH}, {PS}, {D}], got {tuple(key_pages.shape)}")
+    if key_pages.dtype != value_pages.dtype:
+        raise RuntimeError("key and value pages must share a dtype")
+    NP = key_pages.shape[0]
+    page_ids = page_ids.to(torch.int32).contiguous()
+    if n_valid is None:
+        n_valid = torch.full((NP,), PS, dtype=torch.int32, device=kv_pool.device)
+    n_valid = n_valid.to(torch.int32).contiguous()
+    if page_ids.shape != (NP,) or n_valid.shape != (NP,):
+        raise RuntimeError("page_ids and n_valid must be [NP]")
+    key_pages = key_pages.contiguous()
+    value_pages = value_pages.contiguous()
+    lib = _lib.load()
+    # The kernels index rows with a 16-bit grid dimension; split large writes.
+    step = 65535
+    for s in range(0, NP, step):
+        e = min(NP, s + step)
+        rc = lib.vrm_kv_quant_pages(
+            _lib.ptr(key_pages[s:e]), _lib.ptr(value_pages[s:e]), _lib.src_dtype_code(key_pages.dtype),
+            _lib.ptr(page_ids[s:e]), _lib.ptr(n_valid[s:e]), e - s, _lib.ptr(kv_pool), _lib.ptr(kv_scales), code,
+            KH, D, PS, L, P, int(layer_idx), _lib.stream_of(kv_pool),
+        )
+        _lib.check(rc, "quantize_pages")
+
+
+def dequantize_pages(kv_pool: Any, kv_scales: Any, layer_idx: int, page_ids: Any) -> Any:
+    """Returns float32 [NP, 2, KH, PS, D] = codes * scale of the given pages."""
+    import torch
+
+    _lib.require_cuda(kv_pool, kv_scales, page_ids)
+    code, P, L, KH, PS, D = _check_pool(kv_pool, kv_scales)
+    page_ids = page_ids.to(torch.int32).contiguous()
+    NP = page_ids.shape[0]
+    out = torch.empty((NP, 2, KH, PS, D), dtype=torch.float32, device=kv_pool.device)
+    lib = _lib.load()
+    step = 65535
+    for s in range(0, NP, step):
+        e = min(NP, s + step)
+        rc = lib.vrm_kv_dequant_pages(
+            _lib.ptr(kv_pool), _lib.ptr(kv_scales), code, _lib.ptr(page_ids[s:e]), e - s, _lib.ptr(out[s:e]),
+            KH, D, PS, L, P, int(layer_idx), _lib.stream_of(kv_pool),
+        )
+        _lib.check(rc, "dequantize_pages")
+    return out

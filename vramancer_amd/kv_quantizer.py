@@ -1,0 +1,264 @@
+"""TurboQuant KV compressor (randomized Hadamard + PolarQuant + QJL) on
+MI355X — drop-in for VRAMancer's ``core/kv_quantizer.py``.
+
+``KVCacheCompressor`` keeps the reference's constructor, buffers and public
+methods (core/kv_quantizer.py:207-576): the rotation signs and the JL matrix
+are drawn from torch's global RNG in the same order (``randint`` then
+``randn``), so a compressor built after ``torch.manual_seed(s)`` holds the
+same buffers as the reference's.  Compression, decompression and the
+rotated-space key reconstruction run in gfx950 kernels; the packed format
+(MSB-first bit packing of angles and QJL signs, core/kv_quantizer.py:46-105)
+is produced with tensor ops on the same device.
+
+There is no CPU path: CPU tensors raise ``RuntimeError`` and ``force_cpu``
+is rejected (the reference's CPU path is the oracle these kernels are tested
+against, not a fallback).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .turboquant_cuda import CUDATurboQuantOps
+
+__all__ = ["KVCacheCompressor", "TurboQuantCompressor", "BatchedCompressedRef"]
+
+
+# ---------------------------------------------------------------------------
+# Bit packing (MSB first) — same byte layout as core/kv_quantizer.py:46-105
+# ---------------------------------------------------------------------------
+
+def _pack_bits(signs):
+    """[..., M] 0/1 uint8 -> [..., ceil(M/8)] bytes, first element in the MSB."""
+    *batch, M = signs.shape
+    pad = (8 - M % 8) % 8
+    if pad:
+        signs = F.pad(signs, (0, pad))
+    weights = torch.tensor([128, 64, 32, 16, 8, 4, 2, 1], dtype=torch.uint8, device=signs.device)
+    grouped = signs.reshape(*batch, signs.shape[-1] // 8, 8)
+    return (grouped * weights).sum(dim=-1).to(torch.uint8)
+
+
+def _unpack_bits(packed, M):
+    """Inverse of _pack_bits: [..., ceil(M/8)] -> [..., M] uint8 of 0/1."""
+    *batch, nbytes = packed.shape
+    shifts = torch.tensor([7, 6, 5, 4, 3, 2, 1, 0], dtype=torch.uint8, device=packed.device)
+    bits = (packed.unsqueeze(-1) >> shifts) & 1
+    return bits.reshape(*batch, nbytes * 8)[..., :M]
+
+
+def _pack_angles(angles_list, bits_per_angle):
+    """Concatenates per-level [N, cols] angle bins and packs bits_per_angle bits
+    per value, most significant bit first."""
+    if not angles_list:
+        return torch.tensor([], dtype=torch.uint8)
+    flat = torch.cat(angles_list, dim=-1)
+    N = flat.shape[0]
+    shifts = torch.arange(bits_per_angle - 1, -1, -1, device=flat.device, dtype=torch.uint8)
+    bits = ((flat.unsqueeze(-1) >> shifts) & 1).reshape(N, -1)
+    return _pack_bits(bits)
+
+
+def _unpack_angles(packed, N, level_dims, bits_per_angle):
+    total = sum(level_dims)
+    bits = _unpack_bits(packed, total * bits_per_angle).reshape(N, total, bits_per_angle)
+    shifts = torch.arange(bits_per_angle - 1, -1, -1, device=packed.device, dtype=torch.uint8)
+    flat = (bits * (1 << shifts)).sum(dim=-1).to(torch.uint8)
+    out = []
+    offset = 0
+    for d in level_dims:
+        out.append(flat[:, offset:offset + d])
+        offset += d
+    return out
+
+
+class BatchedCompressedRef(dict):
+    """Lazy view of rows [offset, offset + n) of a batched compress result
+    (core/kv_quantizer.py:115-177): slicing is deferred until first access."""
+
+    __slots__ = ("_backing", "_off", "_n", "_shape", "_resolved")
+    _KEYS = ("radius", "angles", "qjl_signs", "qjl_norms", "shape")
+
+    def __init__(self, backing: dict, offset: int, n_rows: int, shape: tuple):
+        super().__init__()
+        self._backing = backing
+        self._off = offset
+        self._n = n_rows
+        self._shape = shape
+        self._resolved = False
+
+    def _resolve(self):
+        if self._resolved:
+            return
+        o, n, b = self._off, self._n, self._backing
+        super().__setitem__("radius", b["radius"][o:o + n])
+        super().__setitem__("angles", [a[o:o + n] for a in b["angles"]])
+        super().__setitem__("qjl_signs", b["qjl_signs"][o:o + n])
+        super().__setitem__("qjl_norms", b["qjl_norms"][o:o + n])
+        super().__setitem__("shape", self._shape)
+        self._backing = None
+        self._resolved = True
+
+    def __getitem__(self, key):
+        self._resolve()
+        return super().__getitem__(key)
+
+    def __contains__(self, key):
+        if not self._resolved:
+            return key in self._KEYS
+        return super().__contains__(key)
+
+    def get(self, key, default=None):
+        if not self._resolved:
+            if key in self._KEYS:
+                self._resolve()
+                return super().__getitem__(key)
+            return default
+        return super().get(key, default)
+
+    def keys(self):
+        self._resolve()
+        return super().keys()
+
+    def values(self):
+        self._resolve()
+        return super().values()
+
+    def items(self):
+        self._resolve()
+        return super().items()
+
+
+class KVCacheCompressor(nn.Module):
+    """TurboQuant KV compressor.
+
+    Args:
+        head_dim: attention head dimension (padded internally to a power of 2)
+        bits_per_angle: bits per quantized polar angle (default 3)
+        qjl_dim: JL projection rows (default padded_dim // 2)
+        force_cpu: accepted for signature compatibility; must be False
+    """
+
+    def __init__(self, head_dim: int, bits_per_angle: int = 3, qjl_dim: Optional[int] = None,
+                 force_cpu: bool = False):
+        super().__init__()
+        if force_cpu:
+            raise ValueError("force_cpu=True is not supported: this codec runs on the GPU only")
+        self.head_dim = head_dim
+        self.bits_per_angle = bits_per_angle
+        self._force_cpu = False
+        self._padded_dim = 1 << math.ceil(math.log2(max(head_dim, 2)))
+        self._n_levels = int(math.log2(self._padded_dim))
+        self.qjl_dim = qjl_dim or self._padded_dim // 2
+        # Same draws, in the same order, as core/kv_quantizer.py:231-236.
+        signs = torch.randint(0, 2, (self._padded_dim,)).float() * 2 - 1
+        self.register_buffer("_hadamard_signs", signs)
+        P = torch.randn(self.qjl_dim, self._padded_dim) / math.sqrt(self.qjl_dim)
+        self.register_buffer("jl_matrix", P)
+
+    # -- helpers --
+
+    def _ops_args(self):
+        return self.head_dim, self._padded_dim, self._n_levels, self.bits_per_angle
+
+    def _pack_compressed(self, d):
+        N = d["qjl_signs"].shape[0]
+        return {
+            "radius": d["radius"],
+            "angles_packed": _pack_angles(d["angles"], self.bits_per_angle),
+            "qjl_signs_packed": _pack_bits(d["qjl_signs"]),
+            "qjl_norms": d["qjl_norms"],
+            "shape": d["shape"],
+            "_N": N,
+            "_qjl_dim": d["qjl_signs"].shape[-1],
+            "_level_dims": [a.shape[-1] for a in d["angles"]],
+        }
+
+    def _unpack_compressed(self, d):
+        if "angles" in d:
+            return d
+        N = d["_N"]
+        return {
+            "radius": d["radius"],
+            "angles": _unpack_angles(d["angles_packed"], N, d["_level_dims"], self.bits_per_angle),
+            "qjl_signs": _unpack_bits(d["qjl_signs_packed"], d["_qjl_dim"]),
+            "qjl_norms": d["qjl_norms"],
+            "shape": d["shape"],
+        }
+
+    # -- public API (core/kv_quantizer.py:375-572) --
+
+    def compress(self, kv, pack: bool = True):
+        """Compresses [..., head_dim] vectors; returns the packed dict by default."""
+        result = CUDATurboQuantOps.compress_gpu(kv, *self._ops_args(), self._hadamard_signs, self.jl_matrix)
+        return self._pack_compressed(result) if pack else result
+
+    def compress_batch(self, kv_list: list, pack: bool = False) -> list:
+        """Compresses several tensors with one kernel launch; returns lazy raw
+        views (or packed dicts with pack=True).  A one-element list returns
+        ``[self.compress(kv)]`` (packed), as the reference does
+        (core/kv_quantizer.py:443-444)."""
+        if not kv_list:
+            return []
+        if len(kv_list) == 1:
+            return [self.compress(kv_list[0])]
+        shapes = [kv.shape for kv in kv_list]
+        rows = [kv.reshape(-1, self.head_dim).shape[0] for kv in kv_list]
+        flat = torch.cat([kv.reshape(-1, self.head_dim) for kv in kv_list], dim=0)
+        result = CUDATurboQuantOps.compress_gpu(flat, *self._ops_args(), self._hadamard_signs, self.jl_matrix)
+        out = []
+        offset = 0
+        for shape, n in zip(shapes, rows):
+            if pack:
+                sliced = {
+                    "radius": result["radius"][offset:offset + n],
+                    "angles": [a[offset:offset + n] for a in result["angles"]],
+                    "qjl_signs": result["qjl_signs"][offset:offset + n],
+                    "qjl_norms": result["qjl_norms"][offset:offset + n],
+                    "shape": shape,
+                }
+                out.append(self._pack_compressed(sliced))
+            else:
+                out.append(BatchedCompressedRef(result, offset, n, shape))
+            offset += n
+        return out
+
+    def decompress(self, compressed):
+        """Approximate K/V from polar codes only (no QJL), shaped like the input."""
+        compressed = self._unpack_compressed(compressed)
+        return CUDATurboQuantOps.decompress_gpu(compressed, *self._ops_args(), self._hadamard_signs)
+
+    def attention_score(self, q, compressed_k):
+        """[n_queries, seq_len] scores from compressed keys plus the QJL correction."""
+        compressed_k = self._unpack_compressed(compressed_k)
+        return CUDATurboQuantOps.attention_score_gpu(
+            q, compressed_k, *self._ops_args(), self._hadamard_signs, self.jl_matrix, self.qjl_dim)
+
+    def sparse_v_attend(self, q, compressed_k, compressed_v_list, scale=None, sparse_v_ratio=0.1):
+        """Scores from compressed keys, then values of the top ceil(ratio * seq)
+        tokens only (core/kv_quantizer.py:537-562)."""
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.head_dim)
+        weights = torch.softmax(self.attention_score(q, compressed_k) * scale, dim=-1)
+        seq_len = weights.shape[-1]
+        k = max(1, int(math.ceil(sparse_v_ratio * seq_len)))
+        if k >= seq_len:
+            v_mat = torch.cat([self.decompress(cv) for cv in compressed_v_list], dim=0)
+            return weights @ v_mat
+        topk_w, topk_idx = weights.topk(k, dim=-1)
+        topk_w = topk_w / topk_w.sum(dim=-1, keepdim=True)
+        v_mat = torch.cat([self.decompress(compressed_v_list[int(i)]) for i in topk_idx.squeeze(0).tolist()], dim=0)
+        return topk_w @ v_mat
+
+    def bits_per_dim(self):
+        """((padded_dim - 1) * bits + 16 + qjl_dim + 16) / head_dim."""
+        d = self._padded_dim
+        total = (d - 1) * self.bits_per_angle + 16 + self.qjl_dim + 16
+        return total / self.head_dim
+
+
+TurboQuantCompressor = KVCacheCompressor

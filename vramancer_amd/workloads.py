@@ -1,0 +1,202 @@
+"""Seeded synthetic decode workloads with the shapes of the benchmark
+configurations (inputs only; no model weights are involved).
+
+  fp32-plumbing  fp32 pool, B=4, H=KH=12, D=64, context 512, L=1
+  7b-bf16        bf16 pool, B=32, H=28, KH=4, D=128, context ~ U[1024, 8192],
+                 K/V ~ N(0, 0.5^2), pool with 10% spare pages, L=1
+  14b-int8       int8 pool (per-token scale), B=64, H=40, KH=8, D=128,
+                 context 4096, 16384 pages of the 48-layer page shape;
+                 K/V ~ N(0, 1) in bf16 with 2 of 128 channels per head x20
+  mixed-fp8      fp8-e4m3 pool (per-page scale), H=64, KH=8, D=128, 128
+                 sequences with lognormal context (median 2048, sigma 1,
+                 clipped to [16, 131072]) plus one of 131072, L=1
+
+Every page table is a seeded shuffle of the physical pages.  Tensors are
+generated on ``device`` with a seeded generator; the page table, context
+lengths and the pool contents are returned so a checker can copy them to the
+host.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+PAGE_SIZE = 16
+
+
+@dataclass
+class DecodeConfig:
+    name: str
+    batch: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    num_layers: int
+    codec: str                       # "f32" | "f16" | "bf16" | "int8" | "fp8"
+    context: str                     # "fixed" | "uniform" | "lognormal"
+    ctx_fixed: int = 0
+    ctx_low: int = 0
+    ctx_high: int = 0
+    ctx_median: float = 0.0
+    ctx_sigma: float = 0.0
+    ctx_clip: Sequence[int] = (16, 131072)
+    pinned_long: int = 0             # extra sequence of this length (0: none)
+    kv_std: float = 1.0
+    outlier_channels: int = 0
+    outlier_scale: float = 1.0
+    spare_pages: float = 0.0
+    page_size: int = PAGE_SIZE
+    meta: Dict[str, str] = field(default_factory=dict)
+
+
+CONFIGS: Dict[str, DecodeConfig] = {
+    "fp32-plumbing": DecodeConfig("fp32-plumbing", 4, 12, 12, 64, 1, "f32", "fixed", ctx_fixed=512),
+    "7b-bf16": DecodeConfig("7b-bf16", 32, 28, 4, 128, 1, "bf16", "uniform", ctx_low=1024, ctx_high=8192,
+                            kv_std=0.5, spare_pages=0.10),
+    "14b-int8": DecodeConfig("14b-int8", 64, 40, 8, 128, 48, "int8", "fixed", ctx_fixed=4096,
+                             outlier_channels=2, outlier_scale=20.0),
+    "mixed-fp8": DecodeConfig("mixed-fp8", 128, 64, 8, 128, 1, "fp8", "lognormal", ctx_median=2048.0,
+                              ctx_sigma=1.0, pinned_long=131072),
+}
+
+
+def scaled(cfg: DecodeConfig, batch: Optional[int] = None, ctx_div: int = 1, num_layers: Optional[int] = None,
+           pinned_long: Optional[int] = None) -> DecodeConfig:
+    """A smaller copy of a configuration with the same structure (for tests)."""
+    c = DecodeConfig(**{k: getattr(cfg, k) for k in cfg.__dataclass_fields__})
+    if batch is not None:
+        c.batch = batch
+    if num_layers is not None:
+        c.num_layers = num_layers
+    if ctx_div > 1:
+        c.ctx_fixed = max(1, c.ctx_fixed // ctx_div)
+        c.ctx_low = max(1, c.ctx_low // ctx_div)
+        c.ctx_high = max(c.ctx_low, c.ctx_high // ctx_div)
+        c.ctx_median = c.ctx_median / ctx_div
+        c.ctx_clip = (max(1, c.ctx_clip[0] // ctx_div), max(1, c.ctx_clip[1] // ctx_div))
+        c.pinned_long = c.pinned_long // ctx_div
+    if pinned_long is not None:
+        c.pinned_long = pinned_long
+    return c
+
+
+def context_lengths(cfg: DecodeConfig, seed: int) -> List[int]:
+    g = torch.Generator().manual_seed(seed)
+    if cfg.context == "fixed":
+        lens = [cfg.ctx_fixed] * cfg.batch
+    elif cfg.context == "uniform":
+        lens = torch.randint(cfg.ctx_low, cfg.ctx_high + 1, (cfg.batch,), generator=g).tolist()
+    else:
+        z = torch.randn(cfg.batch, generator=g, dtype=torch.float64)
+        vals = torch.exp(math.log(cfg.ctx_median) + cfg.ctx_sigma * z).round().long()
+        lens = vals.clamp(cfg.ctx_clip[0], cfg.ctx_clip[1]).tolist()
+    if cfg.pinned_long:
+        lens = lens + [cfg.pinned_long]
+    return [int(x) for x in lens]
+
+
+def _pool_dtype(codec: str):
+    return {
+        "f32": torch.float32,
+        "f16": torch.float16,
+        "bf16": torch.bfloat16,
+        "int8": torch.int8,
+        "fp8": torch.float8_e4m3fn,
+    }[codec]
+
+
+def _kv_pages(cfg: DecodeConfig, n: int, gen: torch.Generator, device, outlier_idx) -> torch.Tensor:
+    """[n, KH, PS, D] float32 K or V rows of the configured distribution."""
+    x = torch.randn((n, cfg.num_kv_heads, cfg.page_size, cfg.head_dim), generator=gen, device=device)
+    x = x * cfg.kv_std
+    if cfg.outlier_channels:
+        x[:, torch.arange(cfg.num_kv_heads, device=device)[:, None], :, outlier_idx] *= cfg.outlier_scale
+    return x
+
+
+def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: Sequence[int] = (0,),
+                       chunk_pages: int = 2048) -> dict:
+    """Builds (query, kv_pool, kv_scales, page_table, context_lens) on ``device``.
+
+    Only the layers in ``layers`` are filled; the others stay zero (they are
+    part of the page stride, not of the attended data).  Quantized pools are
+    filled through the library's page quantizer from bf16 rows.
+    """
+    from . import kv_quant
+
+    lens = context_lengths(cfg, seed)
+    B = len(lens)
+    PS = cfg.page_size
+    pages_per_seq = [(n + PS - 1) // PS for n in lens]
+    used = sum(pages_per_seq)
+    P = max(1, int(math.ceil(used * (1.0 + cfg.spare_pages))))
+    max_pp = max(1, max(pages_per_seq))
+    g_cpu = torch.Generator().manual_seed(seed + 1)
+    perm = torch.randperm(P, generator=g_cpu)
+    table = torch.full((B, max_pp), -1, dtype=torch.int32)
+    off = 0
+    for b, npg in enumerate(pages_per_seq):
+        table[b, :npg] = perm[off:off + npg].to(torch.int32)
+        off += npg
+    gen = torch.Generator(device=device).manual_seed(seed + 2)
+    H, KH, D, L = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.num_layers
+    query = torch.randn((B, H, D), generator=gen, device=device)
+    outlier_idx = None
+    if cfg.outlier_channels:
+        outlier_idx = torch.stack([
+            torch.randperm(D, generator=g_cpu)[:cfg.outlier_channels] for _ in range(KH)
+        ]).to(device)
+    dtype = _pool_dtype(cfg.codec)
+    kv_scales = None
+    if cfg.codec in ("int8", "fp8"):
+        kv_pool, kv_scales = kv_quant.allocate_pool(P, L, KH, D, cfg.codec, PS, device)
+    else:
+        kv_pool = torch.zeros((P, L, 2, KH, PS, D), dtype=dtype, device=device)
+    page_ids_all = torch.arange(P, dtype=torch.int32, device=device)
+    for layer in layers:
+        for s in range(0, P, chunk_pages):
+            e = min(P, s + chunk_pages)
+            k = _kv_pages(cfg, e - s, gen, device, outlier_idx)
+            v = _kv_pages(cfg, e - s, gen, device, outlier_idx)
+            if kv_scales is not None:
+                # the quantized pools start from bf16 activations
+                kv_quant.quantize_pages(kv_pool, kv_scales, layer, page_ids_all[s:e], k.to(torch.bfloat16),
+                                        v.to(torch.bfloat16))
+            else:
+                kv_pool[s:e, layer, 0] = k.to(dtype)
+                kv_pool[s:e, layer, 1] = v.to(dtype)
+    return {
+        "query": query,
+        "kv_pool": kv_pool,
+        "kv_scales": kv_scales,
+        "page_table": table.to(device),
+        "context_lens": torch.tensor(lens, dtype=torch.int32, device=device),
+        "layers": list(layers),
+        "num_pages": P,
+        "config": cfg,
+    }
+
+
+def algorithmic_bytes(cfg: DecodeConfig, lens: Sequence[int]) -> Dict[str, float]:
+    """Bytes one layer-step must move at minimum: valid-token K/V codes, their
+    scales at their granularity, Q and O in float32, and the page-table
+    entries read."""
+    PS = cfg.page_size
+    KH, D, H = cfg.num_kv_heads, cfg.head_dim, cfg.num_heads
+    tokens = sum(lens)
+    pages = sum((n + PS - 1) // PS for n in lens)
+    elem = {"f32": 4, "f16": 2, "bf16": 2, "int8": 1, "fp8": 1}[cfg.codec]
+    kv = tokens * KH * 2 * D * elem
+    if cfg.codec == "int8":
+        scales = tokens * KH * 2 * 4
+    elif cfg.codec == "fp8":
+        scales = pages * KH * 2 * 4
+    else:
+        scales = 0
+    qo = 2 * len(lens) * H * D * 4
+    table = pages * 4
+    return {"kv": kv, "scales": scales, "qo": qo, "table": table, "total": kv + scales + qo + table,
+            "tokens": tokens, "pages": pages}
