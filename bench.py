@@ -90,6 +90,8 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=4, help="sequences in the CPU-baseline sample")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -160,6 +162,15 @@ def main():
         append(i)
     us_append = time_events(append, 50)
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("copy calibration: 10 x 1 GiB device copies done")
+
     achieved = ab["total"] / (us_part * 1e-6) / 1e9
     overall = ab["total"] / (us_step * 1e-6) / 1e9
     traffic = None
@@ -210,7 +221,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "decode_split_kernel<K_I8,128,5>",
+            "kernel": "decode_mfma_kernel<K_I8,128> (G=5)",
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,

@@ -11,6 +11,9 @@ int8, per (token, kv-head) over head_dim:
 fp8-e4m3fn, per (page, layer, K/V, kv-head) over the page's valid tokens:
     scale = amax(|x|) / 448
     code  = (x / scale).to(float8_e4m3fn)         (round to nearest even)
+pool layout: each (page, layer, K/V, kv-head) slice holds PS x D codes; K is
+    token-major like the reference's pool, V is dim-major (code of token t,
+    dim d at d * PS + t).  ``v_token_major`` / ``v_dim_major`` convert.
 fp8 append of token x into slot s of a page with scale s_old (0 if s == 0):
     s_new = max(s_old, amax(|x|) / 448)
     if s_new > s_old: every code c in slots < s becomes e4m3((float(c) * s_old) / s_new)
@@ -75,3 +78,28 @@ def fp8_append(page_codes, old_scale, slot: int, x):
 
 def dequantize_fp8(codes_u8, scale):
     return e4m3_to_float(codes_u8) * scale
+
+
+def v_token_major(v_slices):
+    """Physical V slices [..., PS, D] (memory dim-major) -> logical [..., PS, D]."""
+    *lead, PS, D = v_slices.shape
+    return v_slices.reshape(*lead, D, PS).transpose(-1, -2)
+
+
+def v_dim_major(v_logical):
+    """Logical V [..., PS, D] -> the pool's physical [..., PS, D] view."""
+    *lead, PS, D = v_logical.shape
+    return v_logical.transpose(-1, -2).contiguous().reshape(*lead, PS, D)
+
+
+def pool_to_logical(pool):
+    """[P, L, 2, KH, PS, D] quantized pool -> same shape with V token-major."""
+    out = pool.clone()
+    out[:, :, 1] = v_token_major(pool[:, :, 1])
+    return out
+
+
+def pool_from_logical(pool_logical):
+    out = pool_logical.clone()
+    out[:, :, 1] = v_dim_major(pool_logical[:, :, 1])
+    return out

@@ -115,14 +115,23 @@ def unrotate(p: TQParams, x):
 
 # -- polar --
 
-def polar_encode(p: TQParams, x):
+def ieee_sqrt(t):
+    """Correctly rounded float32 square root (float64 sqrt rounded once).
+
+    PyTorch's CPU torch.sqrt goes through MKL's vector math library, which is
+    not correctly rounded for about 0.6% of float32 inputs; passing this
+    function as ``sqrt_fn`` evaluates the reference algorithm with IEEE sqrt."""
+    return torch.sqrt(t.double()).float()
+
+
+def polar_encode(p: TQParams, x, sqrt_fn=torch.sqrt):
     all_angles = []
     current = x
     for _ in range(p.n_levels):
         d_cur = current.shape[-1]
         pairs = current.view(*current.shape[:-1], d_cur // 2, 2)
         a, b = pairs[..., 0], pairs[..., 1]
-        radii = torch.sqrt(a * a + b * b + 1e-12)
+        radii = sqrt_fn(a * a + b * b + 1e-12)
         angles = torch.atan2(b, a)
         all_angles.append(angles)
         current = radii
@@ -200,13 +209,26 @@ def unpack_compressed(p: TQParams, d):
 
 # -- public operations --
 
-def compress(p: TQParams, kv, pack: bool = True, return_projection: bool = False):
+def angle_positions(p: TQParams, angles_list):
+    """Unclamped, untruncated bin coordinates ((angle - lo) / (hi - lo)) * 2^bits
+    of every level, for locating codes that sit on a bin edge."""
+    n_bins = 1 << p.bits_per_angle
+    out = []
+    for level, a in enumerate(angles_list):
+        lo, hi = _bounds(level)
+        out.append((a - lo) / (hi - lo) * n_bins)
+    return out
+
+
+def compress(p: TQParams, kv, pack: bool = True, return_projection: bool = False, sqrt_fn=torch.sqrt):
+    """core/kv_quantizer.py:391-417.  With return_projection, also returns the
+    float32 QJL projections, the residual and the bin coordinates."""
     orig_shape = kv.shape
     flat = kv.reshape(-1, p.head_dim)
     if p.padded_dim > p.head_dim:
         flat = F.pad(flat, (0, p.padded_dim - p.head_dim))
     rotated = rotate(p, flat)
-    radius, angles_list = polar_encode(p, rotated)
+    radius, angles_list = polar_encode(p, rotated, sqrt_fn=sqrt_fn)
     q_angles = [quantize_angle(p, a, level) for level, a in enumerate(angles_list)]
     reconstructed = polar_decode(p, radius, q_angles)
     residual = rotated - reconstructed
@@ -220,7 +242,7 @@ def compress(p: TQParams, kv, pack: bool = True, return_projection: bool = False
     }
     out = pack_compressed(p, raw) if pack else raw
     if return_projection:
-        return out, projected, residual
+        return out, projected, residual, angle_positions(p, angles_list)
     return out
 
 

@@ -68,12 +68,15 @@ def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pa
     base = torch.randn(P, L, 2, KH, PS, D, generator=g)
     scales = None
     if dtype == torch.int8:
-        from oracle.kv_codecs import quantize_int8
+        from oracle.kv_codecs import pool_from_logical, quantize_int8
         pool, scales = quantize_int8(base)
+        pool = pool_from_logical(pool)  # quantized pools keep V dim-major
     elif dtype == torch.float8_e4m3fn:
+        from oracle.kv_codecs import pool_from_logical
         amax = base.abs().amax(dim=(-2, -1))
         scales = amax / 448
         pool = (base / scales[..., None, None]).to(torch.float8_e4m3fn)
+        pool = pool_from_logical(pool.view(torch.uint8)).view(torch.float8_e4m3fn)
     else:
         pool = base.to(dtype)
     perm = torch.randperm(P, generator=g)

@@ -37,7 +37,7 @@ def test_int8_append_bit_exact(src_dtype, D):
     slots = torch.tensor([0, 15, 4, 2, 9, 1, 3, 0, 8], dtype=torch.int32)
     kv_quant.quantize_append(pool, scales, 2, page_ids.to(DEV), slots.to(DEV), k.to(DEV), v.to(DEV))
     torch.cuda.synchronize()
-    pool_c, sc_c = pool.cpu(), scales.cpu()
+    pool_c, sc_c = kv_quant.logical_view(pool).cpu(), scales.cpu()
     for n in range(N):
         for kv, src in ((0, k), (1, v)):
             codes, s = KC.quantize_int8(src[n])
@@ -60,7 +60,7 @@ def test_quantize_pages_bit_exact(codec):
     n_valid = torch.tensor([16, 16, 1, 9, 16, 0, 15], dtype=torch.int32)
     kv_quant.quantize_pages(pool, scales, 1, page_ids.to(DEV), kp.to(DEV), vp.to(DEV), n_valid.to(DEV))
     torch.cuda.synchronize()
-    pool_c = pool.cpu().view(torch.uint8)
+    pool_c = kv_quant.logical_view(pool).cpu().view(torch.uint8)
     sc_c = scales.cpu()
     for n in range(NP):
         pid, nv = int(page_ids[n]), int(n_valid[n])
@@ -106,7 +106,7 @@ def test_fp8_append_sequence_bit_exact():
                     ref_codes[pid, kv, h] = c
                     ref_scale[pid, kv, h] = s
     torch.cuda.synchronize()
-    assert torch.equal(pool.cpu().view(torch.uint8)[:, 0], ref_codes)
+    assert torch.equal(kv_quant.logical_view(pool).cpu().view(torch.uint8)[:, 0], ref_codes)
     assert torch.equal(scales.cpu()[:, 0], ref_scale)
 
 
@@ -120,7 +120,7 @@ def test_dequantize_pages_exact(codec):
     ids = torch.arange(P, dtype=torch.int32, device=DEV)
     kv_quant.quantize_pages(pool, scales, 1, ids, kp.to(DEV), vp.to(DEV))
     out = kv_quant.dequantize_pages(pool, scales, 1, torch.tensor([5, 0, 3], dtype=torch.int32, device=DEV)).cpu()
-    pc, sc = pool.cpu(), scales.cpu()
+    pc, sc = kv_quant.logical_view(pool).cpu(), scales.cpu()
     for i, pid in enumerate([5, 0, 3]):
         if codec == "int8":
             ref = KC.dequantize_int8(pc[pid, 1], sc[pid, 1])

@@ -1,11 +1,17 @@
 """GPU TurboQuant codec against the oracle (the reference's CPU path).
 
-Bit-exact: polar angle bins, fp16 radius, packed bytes, decompressed rows.
-QJL signs: bit-exact except where the reference's float32 BLAS projection is
-within its own rounding of zero (|p| <= 2^-18 * sum_i |r_i * jl_ji|); the GPU
-takes the sign of a float64 dot product.  QJL norms (fp16): bit-exact on the
-host where the eight-lane reduction order matches PyTorch's, otherwise within
-one fp16 ulp.  Scores: float32 tolerance.
+Two references are used:
+* the reference algorithm evaluated with IEEE arithmetic (oracle option
+  sqrt_fn=ieee_sqrt): polar bins, fp16 radius, fp16 QJL norm and the
+  decompressed rows must be bit-identical; QJL signs too, except where the
+  float32 BLAS projection of the oracle is within its own rounding of zero
+  (|p| <= 2^-18 * sum_i |r_i * jl_ji|), since the GPU takes the sign of a
+  float64 dot product;
+* the reference exactly as PyTorch evaluates it on this host (torch.sqrt is
+  MKL's vector sqrt, not correctly rounded for ~0.6% of inputs): codes may
+  differ only at such ties -- radius within one fp16 ulp, a bin off by one
+  only where the oracle's bin coordinate is within 1e-4 of a bin edge.
+Scores: float32 tolerance.
 """
 import math
 import os
@@ -34,27 +40,44 @@ def _student_t(rows, d, seed):
     return (z / torch.sqrt(chi2 / 3) / math.sqrt(3.0)).to(torch.bfloat16)
 
 
-def _compare(p, kv_cpu, gpu, tag):
-    ref, proj, residual = TQ.compress(p, kv_cpu, pack=False, return_projection=True)
-    assert torch.equal(gpu["radius"].cpu().view(torch.int16), ref["radius"].reshape(-1).view(torch.int16)), tag
-    ga = torch.cat([a.cpu() for a in gpu["angles"]], -1)
-    ra = torch.cat(ref["angles"], -1)
-    assert torch.equal(ga, ra), f"{tag}: {(ga != ra).sum().item()} angle bins differ"
-    gs = gpu["qjl_signs"].cpu()
-    diff = gs != ref["qjl_signs"]
+def _signs_ok(gpu_signs, ref_signs, proj, residual, p, tag):
+    diff = gpu_signs != ref_signs
     if diff.any():
         mag = residual.abs() @ p.jl_matrix.abs().t()
         ties = proj.abs() <= mag * 2.0 ** -18
         assert (ties | ~diff).all(), f"{tag}: {int((diff & ~ties).sum())} QJL signs differ outside ties"
-    print(f"[{tag}] qjl sign tie flips: {int(diff.sum())} of {diff.numel()}", flush=True)
-    gn = gpu["qjl_norms"].cpu().reshape(-1).float()
-    rn = ref["qjl_norms"].reshape(-1).float()
-    exact = torch.equal(gn, rn)
-    if not exact:
-        ulp = rn.abs() * 2.0 ** -10
-        assert ((gn - rn).abs() <= ulp).all(), tag
-    print(f"[{tag}] qjl norms bit-exact: {exact}", flush=True)
+    return int(diff.sum())
+
+
+def _compare_ieee(p, kv_cpu, gpu, tag):
+    """Bit-exact against the reference algorithm with IEEE sqrt."""
+    ref, proj, residual, _ = TQ.compress(p, kv_cpu, pack=False, return_projection=True, sqrt_fn=TQ.ieee_sqrt)
+    assert torch.equal(gpu["radius"].cpu().view(torch.int16), ref["radius"].reshape(-1).view(torch.int16)), tag
+    ga = torch.cat([a.cpu() for a in gpu["angles"]], -1)
+    ra = torch.cat(ref["angles"], -1)
+    assert torch.equal(ga, ra), f"{tag}: {(ga != ra).sum().item()} angle bins differ"
+    assert torch.equal(gpu["qjl_norms"].cpu().reshape(-1).view(torch.int16),
+                       ref["qjl_norms"].reshape(-1).view(torch.int16)), f"{tag}: qjl norms"
+    flips = _signs_ok(gpu["qjl_signs"].cpu(), ref["qjl_signs"], proj, residual, p, tag)
+    print(f"[{tag}] IEEE-exact; qjl sign tie flips: {flips} of {ref['qjl_signs'].numel()}", flush=True)
     return ref
+
+
+def _compare_host_torch(p, kv_cpu, gpu, tag):
+    """Against the reference as this host's PyTorch evaluates it."""
+    ref, proj, residual, pos = TQ.compress(p, kv_cpu, pack=False, return_projection=True)
+    gr = gpu["radius"].cpu().float()
+    rr = ref["radius"].reshape(-1).float()
+    assert ((gr - rr).abs() <= rr.abs() * 2.0 ** -10).all(), f"{tag}: radius beyond one fp16 ulp"
+    ga = torch.cat([a.cpu() for a in gpu["angles"]], -1).int()
+    ra = torch.cat(ref["angles"], -1).int()
+    x = torch.cat(pos, -1)
+    edge = (x - x.round()).abs() < 1e-4
+    bad = (ga != ra) & ~(edge & ((ga - ra).abs() == 1))
+    assert not bad.any(), f"{tag}: {int(bad.sum())} angle bins differ away from bin edges"
+    n_bins = int((ga != ra).sum())
+    n_rad = int((gr != rr).sum())
+    print(f"[{tag}] vs host torch: {n_rad} radius ulp ties, {n_bins} edge-bin ties of {ra.numel()}", flush=True)
 
 
 def test_compress_matches_reference_goldens():
@@ -77,7 +100,8 @@ def test_compress_matches_reference_goldens():
         dec = comp.decompress(raw).cpu().numpy()
         assert np.array_equal(dec, g[case + "/decompress"]), case
         p = TQ.make_params(hd, bits, seed=seed)
-        _compare(p, kv, raw, case)
+        _compare_ieee(p, kv, raw, case)
+        _compare_host_torch(p, kv, raw, case)
         score = comp.attention_score(torch.from_numpy(g[case + "/q"]).to(DEV), raw).cpu()
         torch.testing.assert_close(score, torch.from_numpy(g[case + "/score"]), atol=1e-4, rtol=1e-4)
 
@@ -89,7 +113,8 @@ def test_compress_large_student_t_bit_exact(bits):
     kv = _student_t(16384, 128, 77 + bits)
     gpu = CUDATurboQuantOps.compress_gpu(kv.to(DEV), 128, 128, 7, bits, p.signs.to(DEV), p.jl_matrix.to(DEV))
     torch.cuda.synchronize()
-    ref = _compare(p, kv, gpu, f"t3 b{bits}")
+    ref = _compare_ieee(p, kv, gpu, f"t3 b{bits}")
+    _compare_host_torch(p, kv, gpu, f"t3 b{bits}")
     dec = CUDATurboQuantOps.decompress_gpu(gpu, 128, 128, 7, bits, p.signs.to(DEV)).cpu()
     assert torch.equal(dec, TQ.decompress(p, ref))
 
@@ -101,7 +126,8 @@ def test_compress_other_shapes(head_dim, bits):
     kv = torch.randn(513, head_dim, generator=torch.Generator().manual_seed(1))
     gpu = CUDATurboQuantOps.compress_gpu(kv.to(DEV), head_dim, p.padded_dim, p.n_levels, bits, p.signs.to(DEV),
                                          p.jl_matrix.to(DEV))
-    ref = _compare(p, kv, gpu, f"d{head_dim} b{bits}")
+    ref = _compare_ieee(p, kv, gpu, f"d{head_dim} b{bits}")
+    _compare_host_torch(p, kv, gpu, f"d{head_dim} b{bits}")
     dec = CUDATurboQuantOps.decompress_gpu(gpu, head_dim, p.padded_dim, p.n_levels, bits, p.signs.to(DEV)).cpu()
     assert torch.equal(dec, TQ.decompress(p, ref))
 

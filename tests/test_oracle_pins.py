@@ -95,10 +95,23 @@ def test_decode_quantized_pools_dequantize_first():
     q = torch.randn(1, 4, D, generator=g)
     table = torch.tensor([[4, 1, 3]], dtype=torch.int32)
     lens = torch.tensor([40], dtype=torch.int32)
-    out = PD.paged_attention_decode(q, codes, table, lens, 0, 0.125, kv_scales=scales)
+    # the pool stores V dim-major; the closed form reads the logical codes
+    out = PD.paged_attention_decode(q, KC.pool_from_logical(codes), table, lens, 0, 0.125, kv_scales=scales)
     deq = KC.dequantize_int8(codes, scales)
     K, V = PD.gather_sequence(deq, table[0], 40, 0)
     torch.testing.assert_close(out[0].double(), PD.dense_attention(q[0], K, V, 0.125), atol=2e-5, rtol=1e-5)
+
+
+def test_quantized_pool_v_layout_by_hand():
+    # V of a page-head slice is stored dim-major: token t, dim d at d * PS + t
+    logical = torch.arange(2 * 16 * 4, dtype=torch.int32).reshape(1, 1, 2, 1, 16, 4).to(torch.int8)
+    phys = KC.pool_from_logical(logical)
+    assert torch.equal(phys[0, 0, 0], logical[0, 0, 0])          # K untouched
+    flat = phys[0, 0, 1, 0].reshape(-1)
+    for t in range(16):
+        for d in range(4):
+            assert flat[d * 16 + t] == logical[0, 0, 1, 0, t, d]
+    assert torch.equal(KC.pool_to_logical(phys), logical)
 
 
 def test_q4_dequant_by_hand():

@@ -8,6 +8,11 @@
 //   fp8 : per (page, head) scale = amax / 448, code = e4m3fn_rne(x / scale)
 // Divisions are IEEE round-to-nearest so codes are bit-identical to the same
 // formulas evaluated with PyTorch on the CPU.
+//
+// Layout of a quantized (page, layer, K/V, head) slice of PS x D codes: K is
+// token-major (code of token t, dim d at t * D + d, as the reference's pool);
+// V is dim-major (at d * PS + t), so that the decode kernel can feed 16
+// consecutive tokens of one dimension straight into an MFMA operand.
 #include "vrm_common.h"
 
 #include <math.h>
@@ -54,6 +59,9 @@ __device__ __forceinline__ size_t head_index(const QuantArgs& a, int pid, int kv
   return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h;
 }
 
+// Offset of (token t, dim d) inside a slice: K token-major, V dim-major.
+__device__ __forceinline__ int code_offset(int kv, int t, int d, int D) { return kv ? d * kPS + t : t * D + d; }
+
 // int8, one wavefront per (token row, K/V, head).  src rows: [N][KH][D]
 // (append) or [NP][KH][PS][D] (pages).
 template <int SRC, int D, bool PAGES>
@@ -78,9 +86,9 @@ __global__ void __launch_bounds__(64) quant_i8_kernel(QuantArgs a) {
   }
   amax = group_max<64>(amax);
   const float scale = __fdiv_rn(amax, 127.f);
-  int8_t* dst = reinterpret_cast<int8_t*>(a.pool) + (head_index(a, pid, kv, h) * kPS + slot) * D;
+  int8_t* dst = reinterpret_cast<int8_t*>(a.pool) + head_index(a, pid, kv, h) * kPS * D;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = int8_code(x[i], scale);
+  for (int i = 0; i < PER; ++i) dst[code_offset(kv, slot, i * 64 + lane, D)] = int8_code(x[i], scale);
   if (lane == 0) a.scales[head_index(a, pid, kv, h) * kPS + slot] = scale;
 }
 
@@ -115,7 +123,7 @@ __global__ void __launch_bounds__(256) quant_fp8_pages_kernel(QuantArgs a) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int idx = i * 256 + tid;
-    dst[idx] = (idx / D < n_valid) ? fp8_code(x[i], scale) : (uint8_t)0;
+    dst[code_offset(kv, idx / D, idx % D, D)] = (idx / D < n_valid) ? fp8_code(x[i], scale) : (uint8_t)0;
   }
   if (tid == 0) a.scales[head_index(a, pid, kv, h)] = scale;
 }
@@ -155,14 +163,15 @@ __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
   uint8_t* page = a.pool + hi * (size_t)(kPS * D);
   if (slot > 0 && scale > old_scale) {
     for (int idx = tid; idx < slot * D; idx += 256) {
-      const float y = e4m3fn_to_f32(page[idx]) * old_scale;
-      page[idx] = fp8_code(y, scale);
+      const int off = code_offset(kv, idx / D, idx % D, D);
+      const float y = e4m3fn_to_f32(page[off]) * old_scale;
+      page[off] = fp8_code(y, scale);
     }
   }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = i * 256 + tid;
-    if (d < D) page[(size_t)slot * D + d] = fp8_code(x[i], scale);
+    if (d < D) page[code_offset(kv, slot, d, D)] = fp8_code(x[i], scale);
   }
   if (tid == 0) a.scales[hi] = scale;
 }
@@ -182,10 +191,12 @@ __global__ void __launch_bounds__(256) dequant_pages_kernel(QuantArgs a, float* 
   const size_t hi = head_index(a, pid, kv, h);
   const uint8_t* codes = a.pool + hi * N;
   for (size_t i = threadIdx.x; i < N; i += 256) {
+    const int t = (int)(i / D), d = (int)(i % D);
+    const uint8_t c = codes[code_offset(kv, t, d, D)];
     if (FP8) {
-      o[i] = e4m3fn_to_f32(codes[i]) * a.scales[hi];
+      o[i] = e4m3fn_to_f32(c) * a.scales[hi];
     } else {
-      o[i] = (float)(int8_t)codes[i] * a.scales[hi * kPS + i / D];
+      o[i] = (float)(int8_t)c * a.scales[hi * kPS + t];
     }
   }
 }

@@ -20,26 +20,13 @@
 //    running rescale of the accumulators is needed;
 //  * partitions leave (max, sum, unnormalised acc) in the workspace and a
 //    second kernel merges them with log-sum-exp weights.
-#include "vrm_common.h"
+#include "vrm_decode.h"
 
 #include <math.h>
 
 namespace vrm {
+namespace dec {
 namespace {
-
-constexpr int kPS = 16;               // tokens per page (the reference's default)
-constexpr int kMaxPagesPerSplit = 64;  // one page id per lane
-constexpr float kLog2e = 1.4426950408889634f;
-
-enum KvKind { K_F32 = 0, K_F16 = 1, K_BF16 = 2, K_I8 = 3, K_FP8 = 4, K_Q4 = 5 };
-
-template <int KIND> struct Kv;
-template <> struct Kv<K_F32> { static constexpr int kElems = 4; };   // elements per 16 B
-template <> struct Kv<K_F16> { static constexpr int kElems = 8; };
-template <> struct Kv<K_BF16> { static constexpr int kElems = 8; };
-template <> struct Kv<K_I8> { static constexpr int kElems = 16; };
-template <> struct Kv<K_FP8> { static constexpr int kElems = 16; };
-template <> struct Kv<K_Q4> { static constexpr int kElems = 32; };
 
 template <int KIND>
 __device__ __forceinline__ void unpack16(const uint4 r, float* x) {
@@ -84,20 +71,7 @@ __device__ __forceinline__ void unpack16(const uint4 r, float* x) {
   }
 }
 
-struct DecodeArgs {
-  const float* query;
-  const uint8_t* pool;
-  const float* scales;        // int8 / fp8 scale arrays
-  const uint16_t* q4_scale;   // 4-bit pool group scales (fp16 bits)
-  const uint16_t* q4_zero;    // 4-bit pool group zeros (fp16 bits)
-  const int32_t* page_table;
-  const int32_t* ctx_lens;
-  float* part_acc;            // [B][H][nsplit][D]
-  float* part_ml;             // [B][H][nsplit][2]
-  int H, KH, L, P, max_pp, layer;
-  float qscale;               // scale * log2(e): scores live in the log2 domain
-  int pages_per_split, nsplit;
-};
+
 
 // Registers holding one page of K or V for this lane, plus its dequant factors.
 template <int KIND, int LPP>
@@ -371,13 +345,6 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restri
   for (int i = 0; i < PER; ++i) o[i * 64 + lane] = res[i] * inv;
 }
 
-// Largest divisor of the GQA group size that fits the register budget.
-int pick_group_tile(int group, int max_tile) {
-  for (int g = max_tile; g >= 1; --g)
-    if (group % g == 0) return g;
-  return 1;
-}
-
 template <int KIND, int D, int G>
 hipError_t launch_split(const DecodeArgs& a, int B, hipStream_t st) {
   const int chunks = (a.H / a.KH) / G;
@@ -438,14 +405,17 @@ hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStrea
   return hipGetLastError();
 }
 
-// Pages per partition: enough partitions to give the chip >= ~4 waves per
-// SIMD of work, each partition at most 64 pages (1024 tokens).
-int pages_per_split_for(int B, int H, int KH, int max_pp, int max_tile) {
-  const long units = (long)B * KH * ((H / KH) / pick_group_tile(H / KH, max_tile));
+// Pages per partition: enough (sequence, kv-head, partition) work items to
+// give the chip ~16 waves per CU, each partition a multiple of 4 pages (the
+// 64-token matrix-core chunk) and at most 32 pages (512 tokens, which bounds
+// the per-wave LDS score buffer).  Depends only on the shape, never on dtype.
+int pages_per_split_for(int B, int KH, int max_pp) {
+  const long units = (long)B * KH;
   const long target = 4096;
   long want_splits = (target + units - 1) / units;
   if (want_splits < 1) want_splits = 1;
   long pps = (max_pp + want_splits - 1) / want_splits;
+  pps = (pps + 3) / 4 * 4;
   if (pps < 4) pps = 4;
   if (pps > kMaxPagesPerSplit) pps = kMaxPagesPerSplit;
   return (int)pps;
@@ -494,9 +464,10 @@ enum Passes { kBoth = 3, kPartitionsOnly = 1, kMergeOnly = 2 };
 
 int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D,
                float scale, hipStream_t st, int passes) {
-  const int max_tile = kind == K_Q4 ? 4 : 8;
+  const bool mfma = (kind == K_I8 || kind == K_FP8);
+  const int max_tile = kind == K_Q4 ? 4 : mfma ? 16 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
-  a.pages_per_split = pages_per_split_for(B, a.H, a.KH, a.max_pp, max_tile);
+  a.pages_per_split = pages_per_split_for(B, a.KH, a.max_pp);
   a.nsplit = (a.max_pp + a.pages_per_split - 1) / a.pages_per_split;
   if (a.nsplit > 65535) {
     set_error("vrm_paged_decode: page table too wide (%d pages)", a.max_pp);
@@ -516,8 +487,8 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
       case K_F32: e = dispatch_d<K_F32>(a, B, D, G, st); break;
       case K_F16: e = dispatch_d<K_F16>(a, B, D, G, st); break;
       case K_BF16: e = dispatch_d<K_BF16>(a, B, D, G, st); break;
-      case K_I8: e = dispatch_d<K_I8>(a, B, D, G, st); break;
-      case K_FP8: e = dispatch_d<K_FP8>(a, B, D, G, st); break;
+      case K_I8:
+      case K_FP8: e = launch_quant_mfma(a, kind, B, D, G, st); break;
       default: e = dispatch_d<K_Q4>(a, B, D, G, st); break;
     }
     if (e != hipSuccess) {
@@ -584,14 +555,16 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
 }
 
 }  // namespace
+}  // namespace dec
 }  // namespace vrm
 
 using namespace vrm;
+using namespace vrm::dec;
 
 extern "C" int vrm_paged_decode_num_splits(int B, int H, int KH, int max_pp, int page_size) {
   (void)page_size;
   if (B <= 0 || H <= 0 || KH <= 0 || max_pp <= 0 || H % KH) return 0;
-  const int pps = pages_per_split_for(B, H, KH, max_pp, 8);
+  const int pps = pages_per_split_for(B, KH, max_pp);
   return (max_pp + pps - 1) / pps;
 }
 

@@ -28,6 +28,11 @@ namespace {
 
 #pragma clang fp contract(off)
 
+// IEEE square root.  HIP's __fsqrt_rn is the approximate native v_sqrt_f32 in
+// this toolchain; sqrtf lowers to the correctly rounded sequence (hipcc's
+// default -fhip-fp32-correctly-rounded-divide-sqrt), as does '/'.
+__device__ __forceinline__ float sqrt_rn(float x) { return sqrtf(x); }
+
 template <int SRC>
 __device__ __forceinline__ float load_row(const void* p, size_t i) {
   if constexpr (SRC == VRM_SRC_F32) {
@@ -163,7 +168,7 @@ __global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
     const int off = PD - (PD >> level);
     for (int i = lane; i < count; i += 64) {
       const float x0 = cur[2 * i], x1 = cur[2 * i + 1];
-      const float r = __fsqrt_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), 1e-12f));
+      const float r = sqrt_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), 1e-12f));
       const float th = vrm_fdlibm::atan2f(x1, x0);
       float nrm = level == 0 ? __fdiv_rn(__fsub_rn(th, lo0), range0) : __fdiv_rn(th, range1);
       int idx = (int)__fmul_rn(nrm, nbf);  // truncation toward zero, as .long()
@@ -206,7 +211,7 @@ __global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
     float s = norm_acc[0];
 #pragma unroll
     for (int k = 1; k < 8; ++k) s = __fadd_rn(s, norm_acc[k]);
-    a.qjl_norms[row] = f32_to_f16_bits(__fsqrt_rn(s));
+    a.qjl_norms[row] = f32_to_f16_bits(sqrt_rn(s));
   }
 }
 

@@ -14,6 +14,11 @@ defines them in the style of the reference's pool API:
   ``scale = amax / 448``, ``code = e4m3fn(x / scale)`` rounded to nearest even.
   On append the page scale only grows; when it grows, codes already in the
   page are re-encoded as ``e4m3fn(float(code) * old / new)``;
+* each (page, layer, K/V, kv-head) slice holds PS x D codes; K is
+  token-major as in the reference, V is dim-major (token t, dim d at
+  d * PS + t) so the decode kernel can feed 16 tokens of one dimension to a
+  matrix-core operand with one load; ``logical_view`` returns the pool with
+  V token-major for inspection;
 * the write itself replaces the raw index-put of
   ``PagedKVCacheManager.write_kv`` (core/paged_attention.py:611-612).
 """
@@ -24,6 +29,7 @@ from typing import Any, Optional, Tuple
 from . import _lib
 
 __all__ = [
+    "logical_view",
     "allocate_pool",
     "quantize_append",
     "quantize_pages",
@@ -56,6 +62,21 @@ def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, head_dim: 
     else:
         scales = torch.zeros((num_pages, num_layers, 2, num_kv_heads), dtype=torch.float32, device=device)
     return pool, scales
+
+
+def logical_view(kv_pool):
+    """Copy of a quantized pool with V token-major ([.., PS, D] as indexed)."""
+    P, L, two, KH, PS, D = kv_pool.shape
+    raw = kv_pool.view(torch_uint8())
+    out = raw.clone()
+    out[:, :, 1] = raw[:, :, 1].reshape(P, L, KH, D, PS).transpose(-1, -2)
+    return out.view(kv_pool.dtype)
+
+
+def torch_uint8():
+    import torch
+
+    return torch.uint8
 
 
 def _check_pool(kv_pool, kv_scales):
