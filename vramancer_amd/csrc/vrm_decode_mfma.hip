@@ -293,22 +293,25 @@ __global__ void __launch_bounds__(64) decode_mfma_kernel(DecodeArgs a, int G) {
   }
 
   // The first V loads of phase 3 go out before the softmax phase, which does no
-  // global memory traffic of its own.  Phase 3 step (blk, ch) reads chunk ch of
-  // column block blk; slot ch of the ring holds that row and is refilled with
-  // chunk ch of the next block, one block (8 chunks) ahead.
+  // global memory traffic of its own.  Phase 3 walks steps s = blk * NCH + ch
+  // (column block blk, chunk ch of 4 pages) through a ring of VR slots: slot
+  // s % VR holds step s and is refilled with step s + VR.
   constexpr int NCH = kMaxPagesPerSplit / 4;  // chunks of 4 pages per partition, at most
+  constexpr int NSTEP = NB * NCH;
+  constexpr int VR = 8;                       // 16-byte V rows in flight per lane
   const int nchunks = (n_pages + 3) / 4;
-  auto load_v = [&](int blk, int ch) -> uint4 {
-    blk = min(blk, NB - 1);                 // past the last block: reload (never used)
-    const int pg = min(ch, nchunks - 1) * 4 + grp;
+  auto load_v = [&](int step) -> uint4 {
+    step = min(step, NSTEP - 1);            // past the end: reload the last row (never used)
+    const int blk = step / NCH;
+    const int pg = min(step % NCH, nchunks - 1) * 4 + grp;
     const int pid = pg < n_pages ? pid_lds[pg] : -1;
     const bool ok = page_ok(pid);
     const uint4 v = ld16(layer_base + (size_t)(ok ? pid : 0) * page_stride + kv_stride + (size_t)(blk * 16 + col) * kPS);
     return ok ? v : make_uint4(0, 0, 0, 0);
   };
-  uint4 vring[NCH];
+  uint4 vring[VR];
 #pragma unroll
-  for (int ch = 0; ch < NCH; ++ch) vring[ch] = load_v(0, ch);
+  for (int u = 0; u < VR; ++u) vring[u] = load_v(u);
   wave_sync();
 
   // ---------------- phase 2: softmax statistics and PV operands ----------------
@@ -386,8 +389,9 @@ __global__ void __launch_bounds__(64) decode_mfma_kernel(DecodeArgs a, int G) {
   for (int blk = 0; blk < NB; ++blk) {
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
-      const uint4 vc = vring[ch];
-      vring[ch] = load_v(blk + 1, ch);
+      const int step = blk * NCH + ch;
+      const uint4 vc = vring[step % VR];
+      vring[step % VR] = load_v(step + VR);
       if (ch < nchunks) {
         if constexpr (KIND == K_I8) {
           const int8_t* dig = reinterpret_cast<const int8_t*>(s_lds + hr * TS) + ch * 64 + grp * 16;

@@ -309,7 +309,9 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
 }
 
 // Merges the partitions of one (sequence, head): out = sum_s w_s acc_s / sum_s w_s l_s
-// with w_s = 2^(m_s - max_s m_s).
+// with w_s = 2^(m_s - max_s m_s).  Partitions are read 16 at a time with all
+// their loads issued together (clamped, unconditional), folding each batch
+// into a running maximum.
 template <int D>
 __global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restrict__ part_acc,
                                                            const float* __restrict__ part_ml,
@@ -317,6 +319,7 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restri
                                                            float* __restrict__ out, int H, int nsplit,
                                                            int pages_per_split, int max_pp) {
   constexpr int PER = D / 64;
+  constexpr int BATCH = 16;
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int ctx = ctx_lens[b];
   float* o = out + ((size_t)b * H + h) * D;
@@ -324,21 +327,37 @@ __global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restri
   const int nact = min(nsplit, (num_pages + pages_per_split - 1) / pages_per_split);
   const float* ml = part_ml + ((size_t)b * H + h) * nsplit * 2;
   const float* acc = part_acc + ((size_t)b * H + h) * nsplit * D;
-  float M = -INFINITY;
-  for (int s = 0; s < nact; ++s) M = fmaxf(M, ml[2 * s]);
+  float M = -INFINITY, Lsum = 0.f;
   float res[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) res[i] = 0.f;
-  float Lsum = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < nact; ++s) {
-      const float m = ml[2 * s];
-      if (m == -INFINITY) continue;
-      const float w = exp2f(m - M);
-      Lsum = fmaf(w, ml[2 * s + 1], Lsum);
+  for (int s0 = 0; s0 < nact; s0 += BATCH) {
+    float m[BATCH], l[BATCH], x[BATCH][PER];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, acc[(size_t)s * D + i * 64 + lane], res[i]);
+    for (int k = 0; k < BATCH; ++k) {
+      const int s = min(s0 + k, nact - 1);
+      m[k] = ml[2 * s];
+      l[k] = ml[2 * s + 1];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) x[k][i] = acc[(size_t)s * D + i * 64 + lane];
+      if (s0 + k >= nact) m[k] = -INFINITY;
     }
+    float cm = M;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) cm = fmaxf(cm, m[k]);
+    if (cm == -INFINITY) continue;
+    const float keep = (M == -INFINITY) ? 0.f : exp2f(M - cm);
+    Lsum *= keep;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) res[i] *= keep;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const float w = (m[k] == -INFINITY) ? 0.f : exp2f(m[k] - cm);
+      Lsum = fmaf(w, l[k], Lsum);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, x[k][i], res[i]);
+    }
+    M = cm;
   }
   const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
 #pragma unroll
