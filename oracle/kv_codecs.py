@@ -11,9 +11,13 @@ int8, per (token, kv-head) over head_dim:
 fp8-e4m3fn, per (page, layer, K/V, kv-head) over the page's valid tokens:
     scale = amax(|x|) / 448
     code  = (x / scale).to(float8_e4m3fn)         (round to nearest even)
-pool layout: each (page, layer, K/V, kv-head) slice holds PS x D codes; K is
-    token-major like the reference's pool, V is dim-major (code of token t,
-    dim d at d * PS + t).  ``v_token_major`` / ``v_dim_major`` convert.
+pool layout: each (page, layer, K/V, kv-head) slice holds PS x D codes
+    (PS = 16, D a multiple of 16); K is token-major like the reference's pool,
+    V is tiled: the code of token t, dim d sits at byte
+        ((t // 4 * 16 + d % 16) * (D // 16) + d // 16) * 4 + t % 4
+    (four consecutive tokens of one dim share a dword; the 16 dims d % 16 of a
+    token quad are D / 4 bytes apart).  ``v_token_major`` / ``v_pool_order``
+    convert.
 fp8 append of token x into slot s of a page with scale s_old (0 if s == 0):
     s_new = max(s_old, amax(|x|) / 448)
     if s_new > s_old: every code c in slots < s becomes e4m3((float(c) * s_old) / s_new)
@@ -81,15 +85,21 @@ def dequantize_fp8(codes_u8, scale):
 
 
 def v_token_major(v_slices):
-    """Physical V slices [..., PS, D] (memory dim-major) -> logical [..., PS, D]."""
+    """Physical V slices [..., 16, D] (tiled as the pool stores them) ->
+    logical [..., 16, D] (token t, dim d at [t, d])."""
     *lead, PS, D = v_slices.shape
-    return v_slices.reshape(*lead, D, PS).transpose(-1, -2)
+    assert PS == 16 and D % 16 == 0, (PS, D)
+    # physical axes (t // 4, d % 16, d // 16, t % 4) -> logical (t // 4, t % 4, d // 16, d % 16)
+    tiles = v_slices.reshape(*lead, 4, 16, D // 16, 4)
+    return tiles.transpose(-1, -3).reshape(*lead, PS, D)
 
 
-def v_dim_major(v_logical):
-    """Logical V [..., PS, D] -> the pool's physical [..., PS, D] view."""
+def v_pool_order(v_logical):
+    """Logical V [..., 16, D] -> the pool's tiled physical [..., 16, D]."""
     *lead, PS, D = v_logical.shape
-    return v_logical.transpose(-1, -2).contiguous().reshape(*lead, PS, D)
+    assert PS == 16 and D % 16 == 0, (PS, D)
+    tiles = v_logical.reshape(*lead, 4, 4, D // 16, 16)
+    return tiles.transpose(-1, -3).contiguous().reshape(*lead, PS, D)
 
 
 def pool_to_logical(pool):
@@ -101,5 +111,5 @@ def pool_to_logical(pool):
 
 def pool_from_logical(pool_logical):
     out = pool_logical.clone()
-    out[:, :, 1] = v_dim_major(pool_logical[:, :, 1])
+    out[:, :, 1] = v_pool_order(pool_logical[:, :, 1])
     return out

@@ -5,7 +5,7 @@
 gather -> [KH, ctx, D] float32, repeat_interleave for GQA (head h reads kv-head
 h // (H / KH)), bmm -> softmax -> bmm.  Quantized pools are dequantized first
 (int8: code * per-token scale; fp8: float(code) * per-page scale, with V
-read dim-major as those pools store it), as the reference's fused-dequant
+read in the tiled order those pools store it), as the reference's fused-dequant
 contract implies.  ``paged_attention_decode_q4``
 follows core/paged_attention_cuda.py:291-348.  ``dense_attention`` is an
 independent fp64 closed form used to pin the restatement.
@@ -21,7 +21,7 @@ import torch
 def _dequant_pages(kv_pool, kv_scales, page_ids, layer_idx, kv):
     pages = kv_pool[page_ids, layer_idx, kv]  # [n, KH, PS, D]
     if kv == 1 and kv_pool.dtype in (torch.int8, torch.float8_e4m3fn):
-        # quantized pools keep V dim-major inside each page-head slice
+        # quantized pools keep V tiled inside each page-head slice
         from .kv_codecs import v_token_major
         pages = v_token_major(pages)
     if kv_pool.dtype == torch.int8:

@@ -70,7 +70,7 @@ def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pa
     if dtype == torch.int8:
         from oracle.kv_codecs import pool_from_logical, quantize_int8
         pool, scales = quantize_int8(base)
-        pool = pool_from_logical(pool)  # quantized pools keep V dim-major
+        pool = pool_from_logical(pool)  # quantized pools keep V tiled
     elif dtype == torch.float8_e4m3fn:
         from oracle.kv_codecs import pool_from_logical
         amax = base.abs().amax(dim=(-2, -1))

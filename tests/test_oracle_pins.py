@@ -95,7 +95,7 @@ def test_decode_quantized_pools_dequantize_first():
     q = torch.randn(1, 4, D, generator=g)
     table = torch.tensor([[4, 1, 3]], dtype=torch.int32)
     lens = torch.tensor([40], dtype=torch.int32)
-    # the pool stores V dim-major; the closed form reads the logical codes
+    # the pool stores V tiled; the closed form reads the logical codes
     out = PD.paged_attention_decode(q, KC.pool_from_logical(codes), table, lens, 0, 0.125, kv_scales=scales)
     deq = KC.dequantize_int8(codes, scales)
     K, V = PD.gather_sequence(deq, table[0], 40, 0)
@@ -103,14 +103,26 @@ def test_decode_quantized_pools_dequantize_first():
 
 
 def test_quantized_pool_v_layout_by_hand():
-    # V of a page-head slice is stored dim-major: token t, dim d at d * PS + t
-    logical = torch.arange(2 * 16 * 4, dtype=torch.int32).reshape(1, 1, 2, 1, 16, 4).to(torch.int8)
+    # V of a page-head slice is tiled: token t, dim d at
+    # ((t // 4 * 16 + d % 16) * (D // 16) + d // 16) * 4 + t % 4
+    D = 32
+    logical = torch.arange(2 * 16 * D, dtype=torch.int32).reshape(1, 1, 2, 1, 16, D)
     phys = KC.pool_from_logical(logical)
     assert torch.equal(phys[0, 0, 0], logical[0, 0, 0])          # K untouched
     flat = phys[0, 0, 1, 0].reshape(-1)
+    seen = set()
     for t in range(16):
-        for d in range(4):
-            assert flat[d * 16 + t] == logical[0, 0, 1, 0, t, d]
+        for d in range(D):
+            off = ((t // 4 * 16 + d % 16) * (D // 16) + d // 16) * 4 + t % 4
+            assert flat[off] == logical[0, 0, 1, 0, t, d]
+            seen.add(off)
+    assert len(seen) == 16 * D
+    # lane (col, grp) of the decode reads tokens 4 grp .. 4 grp + 3 of dims
+    # col, col + 16, ... as D / 4 consecutive bytes
+    col, grp = 5, 2
+    run = flat[(grp * 16 + col) * (D // 4):(grp * 16 + col + 1) * (D // 4)].reshape(D // 16, 4)
+    for blk in range(D // 16):
+        assert torch.equal(run[blk], logical[0, 0, 1, 0, 4 * grp:4 * grp + 4, 16 * blk + col])
     assert torch.equal(KC.pool_to_logical(phys), logical)
 
 

@@ -29,6 +29,8 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in VGPRs: the decode rescales them with VALU ops
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE_DIR}",
 ]
 

@@ -6,7 +6,7 @@ namespace vrm {
 namespace dec {
 
 constexpr int kPS = 16;               // tokens per page (the reference's default)
-constexpr int kMaxPagesPerSplit = 16;  // <= 64 so one page id fits per lane
+constexpr int kMaxPagesPerSplit = 64;  // one page id per lane of a wavefront
 constexpr float kLog2e = 1.4426950408889634f;
 
 enum KvKind { K_F32 = 0, K_F16 = 1, K_BF16 = 2, K_I8 = 3, K_FP8 = 4, K_Q4 = 5 };

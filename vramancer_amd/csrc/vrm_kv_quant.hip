@@ -11,8 +11,10 @@
 //
 // Layout of a quantized (page, layer, K/V, head) slice of PS x D codes: K is
 // token-major (code of token t, dim d at t * D + d, as the reference's pool);
-// V is dim-major (at d * PS + t), so that the decode kernel can feed 16
-// consecutive tokens of one dimension straight into an MFMA operand.
+// V is tiled, code of token t, dim d at
+//   ((t / 4 * 16 + d % 16) * (D / 16) + d / 16) * 4 + t % 4,
+// so that a decode lane finds the 4 tokens of its MFMA k-slice for the dims
+// col, col + 16, ... of its operand row in D / 4 consecutive bytes.
 #include "vrm_common.h"
 
 #include <math.h>
@@ -59,8 +61,10 @@ __device__ __forceinline__ size_t head_index(const QuantArgs& a, int pid, int kv
   return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h;
 }
 
-// Offset of (token t, dim d) inside a slice: K token-major, V dim-major.
-__device__ __forceinline__ int code_offset(int kv, int t, int d, int D) { return kv ? d * kPS + t : t * D + d; }
+// Offset of (token t, dim d) inside a slice: K token-major, V tiled.
+__device__ __forceinline__ int code_offset(int kv, int t, int d, int D) {
+  return kv ? (((t >> 2) * 16 + (d & 15)) * (D >> 4) + (d >> 4)) * 4 + (t & 3) : t * D + d;
+}
 
 // int8, one wavefront per (token row, K/V, head).  src rows: [N][KH][D]
 // (append) or [NP][KH][PS][D] (pages).

@@ -13,8 +13,9 @@
 //  * each lane issues 16-byte loads of the contiguous [PS][D] page slice; the
 //    page ids of a partition are fetched with one vector load up front and the
 //    next page is loaded while the current one is consumed;
-//  * dequantization happens in registers (int8 * per-token scale, e4m3 *
-//    per-page scale, (nibble - zero) * scale for the 4-bit pool);
+//  * this VALU kernel serves the float pools and the 4-bit pool (dequantized
+//    in registers as (nibble - zero) * scale); the int8 and fp8 pools go to
+//    the single-pass matrix-core kernel of vrm_decode_mfma.hip;
 //  * phase 1 writes all scores of the partition to LDS, phase 2 takes the
 //    exact partition maximum, phase 3 streams V once with fixed weights, so no
 //    running rescale of the accumulators is needed;
@@ -46,18 +47,6 @@ __device__ __forceinline__ void unpack16(const uint4 r, float* x) {
       x[2 * i] = __uint_as_float(w[i] << 16);
       x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
-  } else if constexpr (KIND == K_I8) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[4 * i + j] = (float)(int8_t)(w[i] >> (8 * j));
-    }
-  } else if constexpr (KIND == K_FP8) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[4 * i + j] = e4m3fn_to_f32((w[i] >> (8 * j)) & 0xffu);
-    }
   } else {  // K_Q4: raw nibbles; byte j holds d = 2j (low) and 2j + 1 (high)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -77,8 +66,8 @@ __device__ __forceinline__ void unpack16(const uint4 r, float* x) {
 template <int KIND, int LPP>
 struct PageRegs {
   uint4 data[LPP];
-  float s0[LPP];  // K: key scale of the lane's token / V: value scale (int8, q4)
-  float s1[LPP];  // K: value scale of the lane's token (int8) / V, q4: zero point
+  float s0[LPP];  // q4: group scale of the lane's chunk
+  float s1[LPP];  // q4: group zero point
 };
 
 // One wavefront per (split, kv head x head chunk, sequence).
@@ -97,8 +86,7 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
 
   extern __shared__ float lds[];
   const int TS = a.pages_per_split * kPS;
-  float* s_lds = lds;                 // [G][TS] scores, then weights * V scale
-  float* v_scale_lds = lds + G * TS;  // [TS] per-token V dequant factor (int8)
+  float* s_lds = lds;  // [G][TS] scores, then softmax weights
 
   const int lane = threadIdx.x;
   const int split = blockIdx.x;
@@ -151,18 +139,7 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
                        : make_uint4(0, 0, 0, 0);
       r.s0[j] = 1.f;
       r.s1[j] = 0.f;
-      if constexpr (KIND == K_I8) {
-        if (live) {
-          const size_t ts = head_index(pid, kv) * kPS + tp;
-          r.s0[j] = a.scales[ts];
-          if (kv == 0) r.s1[j] = a.scales[ts + (size_t)a.KH * kPS];  // V scale of the same token
-        }
-      } else if constexpr (KIND == K_FP8) {
-        if (live) {
-          r.s0[j] = a.scales[head_index(pid, kv)];
-          if (kv == 0) r.s1[j] = a.scales[head_index(pid, 1)];
-        }
-      } else if constexpr (KIND == K_Q4) {
+      if constexpr (KIND == K_Q4) {
         if (live) {
           const size_t rs = (head_index(pid, kv) * kPS + tp) * Q4G + c;  // lane chunk c == group c
           r.s0[j] = f16_bits_to_f32(a.q4_scale[rs]);
@@ -212,12 +189,7 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
         }
         if (c == 0 && lane_live && tp < kPS && t < TS) {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float sc = part[g];
-            if constexpr (KIND == K_I8 || KIND == K_FP8) sc *= cur.s0[j];
-            s_lds[g * TS + t] = valid ? sc : -INFINITY;
-          }
-          v_scale_lds[t] = (KIND == K_I8 || KIND == K_FP8) ? cur.s1[j] : 1.f;
+          for (int g = 0; g < G; ++g) s_lds[g * TS + t] = valid ? part[g] : -INFINITY;
         }
       }
       cur = nxt;
@@ -238,7 +210,7 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
       const float s = s_lds[g * TS + t];
       const float p = (s == -INFINITY) ? 0.f : exp2f(s - mx);
       sum += p;
-      s_lds[g * TS + t] = p * v_scale_lds[t];
+      s_lds[g * TS + t] = p;
     }
     m_g[g] = mx;
     l_g[g] = group_sum<64>(sum);
@@ -368,7 +340,7 @@ template <int KIND, int D, int G>
 hipError_t launch_split(const DecodeArgs& a, int B, hipStream_t st) {
   const int chunks = (a.H / a.KH) / G;
   dim3 grid(a.nsplit, a.KH * chunks, B);
-  const size_t lds = (size_t)(G + 1) * a.pages_per_split * kPS * sizeof(float);
+  const size_t lds = (size_t)G * a.pages_per_split * kPS * sizeof(float);
   hipLaunchKernelGGL((decode_split_kernel<KIND, D, G>), grid, dim3(64), lds, st, a);
   return hipGetLastError();
 }
@@ -424,13 +396,15 @@ hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStrea
   return hipGetLastError();
 }
 
-// Pages per partition: enough (sequence, kv-head, partition) work items to
-// give the chip ~16 waves per CU, each partition a multiple of 4 pages (the
-// 64-token matrix-core chunk) and at most 32 pages (512 tokens, which bounds
-// the per-wave LDS score buffer).  Depends only on the shape, never on dtype.
+// Pages per partition: enough (sequence, kv-head, partition) work items for
+// about 8 wavefronts per CU of the 256-CU chip, so that each wavefront streams
+// one long partition (its page-table fetch and query set-up paid once) and
+// the merge has few partials to combine; a multiple of 4 pages, at most 64
+// (one page id per lane).  Depends only on the shape, never on the dtype, so
+// the partition and merge passes can be enqueued separately.
 int pages_per_split_for(int B, int KH, int max_pp) {
   const long units = (long)B * KH;
-  const long target = 4096;
+  const long target = 2048;
   long want_splits = (target + units - 1) / units;
   if (want_splits < 1) want_splits = 1;
   long pps = (max_pp + want_splits - 1) / want_splits;
@@ -471,7 +445,7 @@ int check_common(const float* query, const void* pool, const int32_t* page_table
     set_error("vrm_paged_decode: head_dim %d unsupported (64, 128, 256)", D);
     return VRM_ERR_UNSUPPORTED;
   }
-  if ((long)B * H > 65535L * 65535L) {
+  if (B > 65535 || (long)B * H > 65535L * 65535L) {
     set_error("vrm_paged_decode: batch too large");
     return VRM_ERR_UNSUPPORTED;
   }

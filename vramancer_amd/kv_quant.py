@@ -15,10 +15,11 @@ defines them in the style of the reference's pool API:
   On append the page scale only grows; when it grows, codes already in the
   page are re-encoded as ``e4m3fn(float(code) * old / new)``;
 * each (page, layer, K/V, kv-head) slice holds PS x D codes; K is
-  token-major as in the reference, V is dim-major (token t, dim d at
-  d * PS + t) so the decode kernel can feed 16 tokens of one dimension to a
-  matrix-core operand with one load; ``logical_view`` returns the pool with
-  V token-major for inspection;
+  token-major as in the reference, V is tiled (token t, dim d at byte
+  ``((t // 4 * 16 + d % 16) * (D // 16) + d // 16) * 4 + t % 4``) so that
+  each lane of the decode kernel loads its matrix-core operand for one page
+  as D / 4 consecutive bytes; ``logical_view`` returns the pool with V
+  token-major for inspection;
 * the write itself replaces the raw index-put of
   ``PagedKVCacheManager.write_kv`` (core/paged_attention.py:611-612).
 """
@@ -69,7 +70,9 @@ def logical_view(kv_pool):
     P, L, two, KH, PS, D = kv_pool.shape
     raw = kv_pool.view(torch_uint8())
     out = raw.clone()
-    out[:, :, 1] = raw[:, :, 1].reshape(P, L, KH, D, PS).transpose(-1, -2)
+    # physical axes (t // 4, d % 16, d // 16, t % 4) -> (t // 4, t % 4, d // 16, d % 16)
+    tiles = raw[:, :, 1].reshape(P, L, KH, PS // 4, 16, D // 16, 4)
+    out[:, :, 1] = tiles.transpose(-1, -3).reshape(P, L, KH, PS, D)
     return out.view(kv_pool.dtype)
 
 
