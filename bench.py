@@ -87,8 +87,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seqs", type=int, default=4, help="sequences in the CPU-baseline sample")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
@@ -221,7 +221,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "decode_mfma_kernel<K_I8,128> (G=5)",
+            "kernel": "decode_stream_kernel<K_I8,128> (G=5, 8 wavefronts per workgroup)",
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,
