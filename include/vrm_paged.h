@@ -15,6 +15,13 @@
  *      kv_pool[P][L][2][KH][PS][D]    (index 2 selects K=0 / V=1)
  * with PS = 16 tokens per page.  A sequence's logical page i lives in physical
  * page page_table[b][i]; tokens t < context_lens[b] are attended.
+ * Float pools (f32, f16, bf16) keep each [PS][D] slice token-major, exactly as
+ * the reference writes it.  The int8 and fp8 pools (this library's codecs,
+ * written only by vrm_kv_quant_*) keep K token-major and store the V slice
+ * tiled: the code of token t, dim d sits at byte
+ *      ((t / 4 * 16 + d % 16) * (D / 16) + d / 16) * 4 + t % 4
+ * of the slice, so that one decode lane loads its matrix-core operand for a
+ * page as D / 4 consecutive bytes.
  */
 #ifndef VRM_PAGED_H
 #define VRM_PAGED_H
