@@ -14,6 +14,11 @@ the line also carries the achieved HBM bandwidth on algorithmic bytes, the
 tokens/s this implies for a 48-layer model, the roofline of the dominant
 kernel (the split-K partition pass, timed alone with events on its stream)
 and the reference's CPU path (the oracle restatement) timed on a sample.
+
+``--workload`` measures one of the other decode shapes the same way (7b-bf16:
+B=32, 28/4 heads, bf16 pool, context ~U[1024, 8192]; mixed-fp8: 129
+sequences, 64/8 heads, fp8 pool, lognormal contexts plus one of 131072;
+fp32-plumbing); the default line is 14b-int8.
 """
 from __future__ import annotations
 
@@ -36,6 +41,11 @@ METRIC = "paged-attn decode µs/layer-step + HBM GB/s (% of peak), 14B-shape qua
 PEAK_HBM_GBPS = 8000.0
 LAYERS_FILLED = (0, 12, 24, 36)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_14b_int8.json")
+KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_BF16, "int8": _lib.VRM_KV_I8,
+           "fp8": _lib.VRM_KV_FP8E4M3}
+KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
+          "bf16": "decode_stream_float_kernel<K_BF16,{D}>", "f16": "decode_stream_float_kernel<K_F16,{D}>",
+          "f32": "decode_split_kernel<K_F32,{D},G>"}
 
 
 def log(msg):
@@ -56,7 +66,8 @@ def time_events(fn, steps):
 
 def cpu_baseline(inp, layer, n_seq, reps):
     """The reference's PyTorch decode path (restated in oracle/) on the host
-    cores, over the first n_seq sequences of the same workload."""
+    cores, over the first n_seq sequences of the same workload.  Returns
+    microseconds per context token and the thread count."""
     from oracle import paged_decode as PD
 
     torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
@@ -67,7 +78,9 @@ def cpu_baseline(inp, layer, n_seq, reps):
     remap = torch.full((inp["num_pages"],), -1, dtype=torch.long, device=pages.device)
     remap[pages] = torch.arange(pages.numel(), device=pages.device)
     pool = inp["kv_pool"][pages][:, layer:layer + 1].cpu()
-    scales = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
+    scales = None
+    if inp["kv_scales"] is not None:
+        scales = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
     tbl = remap[table.long()].to(torch.int32).cpu()
     q = inp["query"][:n_seq].cpu()
     lens = inp["context_lens"][:n_seq].cpu()
@@ -78,8 +91,8 @@ def cpu_baseline(inp, layer, n_seq, reps):
         PD.paged_attention_decode(q, pool, tbl, lens, 0, kv_scales=scales)
         times.append(time.perf_counter() - t0)
     times.sort()
-    per_seq_us = times[len(times) // 2] / n_seq * 1e6
-    return per_seq_us, threads
+    per_token_us = times[len(times) // 2] / max(1, int(lens.sum())) * 1e6
+    return per_token_us, threads
 
 
 def main():
@@ -90,6 +103,8 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU-baseline sample")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default="14b-int8", choices=sorted(workloads.CONFIGS),
+                    help="decode shape to measure (the headline line is 14b-int8)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -102,9 +117,13 @@ def main():
         sys.exit(2)
     lib = _lib.load()
     dev = torch.device("cuda:0")
-    cfg = workloads.CONFIGS["14b-int8"]
-    log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {LAYERS_FILLED})")
-    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=LAYERS_FILLED)
+    cfg = workloads.CONFIGS[args.workload]
+    if cfg.num_layers < 4:
+        # steps rotate over 4 layers so that consecutive steps never hit in the Infinity Cache
+        cfg = workloads.scaled(cfg, num_layers=4)
+    layers = LAYERS_FILLED if cfg.num_layers > max(LAYERS_FILLED) else tuple(range(4))
+    log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {layers})")
+    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=layers)
     torch.cuda.synchronize()
     q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
     B, H, D = q.shape
@@ -115,22 +134,23 @@ def main():
     ws = decode_workspace(B, H, KH, D, max_pp, dev, PS)
     nsplit = lib.vrm_paged_decode_num_splits(B, H, KH, max_pp, PS)
     stream = _lib.stream_of(q)
-    code = _lib.VRM_KV_I8
+    code = KV_CODE[cfg.codec]
+    sc_ptr = sc.data_ptr() if sc is not None else None
     lens_list = lens.tolist()
     ab = workloads.algorithmic_bytes(cfg, lens_list)
     log(f"pool {P} pages, {nsplit} partitions/sequence, algorithmic bytes/layer-step {ab['total'] / 1e6:.2f} MB")
 
     def full(i):
-        layer = LAYERS_FILLED[i % len(LAYERS_FILLED)]
-        rc = lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(), lens.data_ptr(),
+        layer = layers[i % len(layers)]
+        rc = lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(), lens.data_ptr(),
                                   out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp, layer,
                                   scale, code, stream)
         if rc:
             _lib.check(rc, "decode")
 
     def partitions(i):
-        layer = LAYERS_FILLED[i % len(LAYERS_FILLED)]
-        rc = lib.vrm_paged_decode_partitions(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(),
+        layer = layers[i % len(layers)]
+        rc = lib.vrm_paged_decode_partitions(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(),
                                              lens.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P,
                                              max_pp, layer, scale, code, stream)
         if rc:
@@ -139,28 +159,31 @@ def main():
     for i in range(args.warmup):
         full(i)
     torch.cuda.synchronize()
+    pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
     log(f"timing {args.steps} layer-steps")
     us_step = time_events(full, args.steps)
     us_part = time_events(partitions, args.steps)
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
-    # append one token per sequence (quantize-on-append), timed separately
-    kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
-    vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
-    last = (lens - 1).clamp(min=0)
-    pid = table.gather(1, (last // PS).long()[:, None]).squeeze(1).contiguous()
-    slot = (last % PS).to(torch.int32).contiguous()
+    us_append = None
+    if sc is not None:
+        # append one token per sequence (quantize-on-append), timed separately
+        kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+        vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+        last = (lens - 1).clamp(min=0)
+        pid = table.gather(1, (last // PS).long()[:, None]).squeeze(1).contiguous()
+        slot = (last % PS).to(torch.int32).contiguous()
 
-    def append(i):
-        rc = lib.vrm_kv_quant_append(kn.data_ptr(), vn.data_ptr(), _lib.VRM_SRC_BF16, pid.data_ptr(),
-                                     slot.data_ptr(), B, pool.data_ptr(), sc.data_ptr(), code, KH, D, PS, L, P,
-                                     LAYERS_FILLED[0], stream)
-        if rc:
-            _lib.check(rc, "append")
+        def append(i):
+            rc = lib.vrm_kv_quant_append(kn.data_ptr(), vn.data_ptr(), _lib.VRM_SRC_BF16, pid.data_ptr(),
+                                         slot.data_ptr(), B, pool.data_ptr(), sc.data_ptr(), code, KH, D, PS, L, P,
+                                         layers[0], stream)
+            if rc:
+                _lib.check(rc, "append")
 
-    for i in range(5):
-        append(i)
-    us_append = time_events(append, 50)
+        for i in range(5):
+            append(i)
+        us_append = time_events(append, 50)
 
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
@@ -174,22 +197,32 @@ def main():
     achieved = ab["total"] / (us_part * 1e-6) / 1e9
     overall = ab["total"] / (us_step * 1e-6) / 1e9
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    if cfg.name == "14b-int8" and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     cpu = None
     if not args.no_cpu:
         log(f"CPU baseline on {args.cpu_seqs} sequences")
-        per_seq_us, threads = cpu_baseline(inp, LAYERS_FILLED[0], args.cpu_seqs, args.cpu_reps)
+        per_token_us, threads = cpu_baseline(inp, layers[0], min(args.cpu_seqs, B), args.cpu_reps)
         cpu = {
-            "value": round(per_seq_us * B, 1),
+            "value": round(per_token_us * sum(lens_list), 1),
             "unit": "us/layer-step",
             "cores": threads,
             "kind": "port",
-            "sample": (f"oracle restatement of the reference's PyTorch decode (int8 dequant + gather + "
-                       f"repeat_interleave + bmm/softmax/bmm, fp32) over {args.cpu_seqs} of the {B} sequences, "
-                       f"median of {args.cpu_reps}, scaled to the full batch"),
+            "sample": (f"oracle restatement of the reference's PyTorch decode ({cfg.codec} dequant + gather + "
+                       f"repeat_interleave + bmm/softmax/bmm, fp32) over the first {min(args.cpu_seqs, B)} of the "
+                       f"{B} sequences, median of {args.cpu_reps}, scaled by the batch's total context"),
         }
+    elem = {"f32": "f32", "f16": "f16", "bf16": "bf16", "int8": "int8", "fp8": "fp8e4m3"}[cfg.codec]
+    desc = {
+        "14b-int8": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
+                     "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
+        "7b-bf16": "7b-bf16 paged decode: B=32, H=28, KH=4, D=128, context ~U[1024, 8192], page 16, bf16 pool",
+        "mixed-fp8": ("mixed-fp8 paged decode: 128 sequences lognormal(median 2048, sigma 1) + one of 131072, "
+                      "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales"),
+        "fp32-plumbing": "fp32-plumbing paged decode: B=4, H=KH=12, D=64, context 512, page 16, fp32 pool",
+    }[cfg.name]
+    G = next(g for g in range(16, 0, -1) if (H // KH) % g == 0)
     result = {
         "metric": METRIC,
         "value": round(us_step, 3),
@@ -201,18 +234,18 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": elem,
         "data": "synthetic",
         "config": {
-            "workload": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
-                         "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
-            "batch": B, "num_heads": H, "num_kv_heads": KH, "head_dim": D, "context": 4096, "page_size": PS,
-            "num_layers": L, "num_pages": P, "partitions": nsplit, "layers_rotated": list(LAYERS_FILLED),
+            "workload": desc,
+            "batch": B, "num_heads": H, "num_kv_heads": KH, "head_dim": D, "context_tokens": int(sum(lens_list)),
+            "page_size": PS, "num_layers": L, "num_pages": P, "pages_per_partition": pps, "work_items": n_items,
+            "layers_rotated": list(layers),
         },
         "hbm_gbps": round(overall, 1),
         "pct_of_peak": round(100 * overall / PEAK_HBM_GBPS, 2),
-        "tokens_per_s": round(B / (us_step * 1e-6 * L), 1),
-        "append_us": round(us_append, 2),
+        "tokens_per_s": round(B / (us_step * 1e-6 * L), 1) if L > 1 else None,
+        "append_us": round(us_append, 2) if us_append is not None else None,
         "algorithmic_bytes": int(ab["total"]),
         "roofline": {
             "bound": "hbm",
@@ -221,7 +254,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": "decode_stream_kernel<K_I8,128> (G=5, 8 wavefronts per workgroup)",
+            "kernel": KERNEL[cfg.codec].format(D=D) + f" (G={G}, partition pass)",
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,

@@ -36,11 +36,20 @@ def test_abi_version(lib):
     assert lib.vrm_abi_version() == _lib.VRM_ABI_VERSION == 1
 
 
+def _header_bytes(B):
+    return ((16 + 2 * B + 1) * 4 + 255) // 256 * 256
+
+
 def test_split_geometry_is_host_only(lib):
-    # 14B int8 shape: 64 sequences x 8 kv heads, 256 pages each
+    # 14B int8 shape: 64 sequences x 8 kv heads; the workspace holds a header
+    # (partition size, first work item of each sequence) and the partials of
+    # at most B + ceil(2048 / KH) work items
     ns = lib.vrm_paged_decode_num_splits(64, 40, 8, 256, 16)
-    assert ns >= 1
-    assert lib.vrm_paged_decode_workspace_bytes(64, 40, 128, ns) == 64 * 40 * ns * 130 * 4
+    assert 64 * ns >= 64 + 2048 // 8
+    assert lib.vrm_paged_decode_workspace_bytes(64, 40, 128, ns) == _header_bytes(64) + 64 * 40 * ns * 130 * 4
+    # the capacity does not depend on the page-table width (long contexts get longer partitions)
+    assert lib.vrm_paged_decode_num_splits(64, 40, 8, 8192, 16) == ns
+    assert lib.vrm_paged_decode_num_splits(129, 64, 8, 8192, 16) * 129 >= 129 + 256
     assert lib.vrm_paged_decode_num_splits(1, 3, 2, 4, 16) == 0  # H % KH != 0
 
 

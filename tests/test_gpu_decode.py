@@ -227,3 +227,43 @@ def test_decode_full_size_int8_sampled_parity_and_relabel_invariance():
     out2 = paged_attention_decode(q, pool2, table2, lens, 1, kv_scales=sc2)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_decode_float_pool_ignores_garbage_past_context(dtype):
+    """Slots past the context in the last page, and pages the table marks
+    absent, may hold anything (here NaN and inf); the output must equal the
+    oracle's, which never reads them."""
+    _say(f"garbage past context {dtype}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, 128, [37, 160, 5], seed=31)
+    for b, c in enumerate(lens.tolist()):
+        last = int(table[b, (c - 1) // 16])
+        pool[last, 1, :, :, c % 16 or 16:, :] = float("nan")
+    spare = sorted(set(range(pool.shape[0])) - set(table[table >= 0].tolist()))[0]
+    pool[spare, 1] = float("inf")  # a page the table never references
+    table[1, 3] = -1  # an absent page in the middle of sequence 1
+    out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), 1)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    for b in range(3):
+        K, V = PD.gather_sequence(pool, table[b], int(lens[b]), 1, skip_invalid=True)
+        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(128))
+        _assert_close(out[b].cpu(), ref, f"seq {b}")
+
+
+def test_decode_full_size_bf16_sampled_parity():
+    """7B bf16 at its full size (B=32, 28/4 heads, context ~U[1024, 8192]):
+    a sample of sequences matches the oracle."""
+    cfg = workloads.CONFIGS["7b-bf16"]
+    _say("7b-bf16 full size")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=5, layers=(0,))
+    q, pool, table, lens = inp["query"], inp["kv_pool"], inp["page_table"], inp["context_lens"]
+    out = paged_attention_decode(q, pool, table, lens, 0)
+    torch.cuda.synchronize()
+    for b in (0, 13, 31):
+        n = (int(lens[b]) + 15) // 16
+        pages = table[b, :n].long()
+        sub_pool = pool[pages].cpu()
+        sub_table = torch.arange(n, dtype=torch.int32)[None]
+        ref = PD.paged_attention_decode(q[b:b + 1].cpu(), sub_pool, sub_table, lens[b:b + 1].cpu(), 0)
+        _assert_close(out[b:b + 1], ref, f"7b seq {b} ctx {int(lens[b])}")

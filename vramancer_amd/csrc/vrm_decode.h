@@ -6,7 +6,6 @@ namespace vrm {
 namespace dec {
 
 constexpr int kPS = 16;               // tokens per page (the reference's default)
-constexpr int kMaxPagesPerSplit = 64;  // one page id per lane of a wavefront
 constexpr float kLog2e = 1.4426950408889634f;
 
 enum KvKind { K_F32 = 0, K_F16 = 1, K_BF16 = 2, K_I8 = 3, K_FP8 = 4, K_Q4 = 5 };
@@ -28,16 +27,146 @@ struct DecodeArgs {
   const uint16_t* q4_zero;    // 4-bit pool group zeros (fp16 bits)
   const int32_t* page_table;
   const int32_t* ctx_lens;
-  float* part_acc;            // [B][H][nsplit][D]
-  float* part_ml;             // [B][H][nsplit][2]
-  int H, KH, L, P, max_pp, layer;
+  int32_t* header;            // workspace header (see work items below)
+  float* part_acc;            // [items][H][D]
+  float* part_ml;             // [items][H][2]
+  int B, H, KH, L, P, max_pp, layer;
   float qscale;               // scale * log2(e): scores live in the log2 domain
-  int pages_per_split, nsplit;
+  int target;                 // work items the partition size aims for
 };
 
-// Matrix-core (MFMA) split pass for the quantized pools; KIND is K_I8 or
-// K_FP8, D the head dimension, G the query heads per wavefront (<= 16).
-hipError_t launch_quant_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
+// ---------------------------------------------------------------------------
+// Work items (length-aware split-K).
+//
+// All sequences' pages are cut into partitions of pps pages.  The host passes
+// `target`, the work items the chip holds at once (resident wavefronts of the
+// kernel / wavefronts per item).  On the device, from the batch's total page
+// count S: pps = max(4, roundup4(ceil(S / target))), so one resident round of
+// equal partitions covers the batch; when the shorter tail partitions this
+// leaves (one per sequence whose page count pps does not divide) exceed an
+// eighth of the round, pps is halved (from S / (2 target)) so that the
+// remainders spread over more, smaller items.  Sequence b has
+// nf_b = floor(pages_b / pps) full partitions and at most one tail.  Work
+// items enumerate every full partition first (sequence-major; they all cost
+// the same), then the tails, so the dispatcher starts the equal-sized work
+// before the small remainders.  Since S / pps <= 2 target, a batch has at
+// most B + 2 target items, a bound the host knows without reading the
+// context lengths.
+//
+// Workspace header (int32), written by the partition pass for the merge:
+//   [0] pps   [1] number of items   [2] number of full items
+//   [kHeaderInts + b],         b = 0 .. B : first full item of sequence b
+//                                           (entry B = number of full items)
+//   [kHeaderInts + B + 1 + b], b < B      : tail item of sequence b, or -1
+// ---------------------------------------------------------------------------
+constexpr int kMaxTargetWaves = 4096;  // cap on the resident wavefronts a target counts
+constexpr int kHeaderInts = 16;
+
+inline size_t header_bytes(int B) { return ((size_t)(kHeaderInts + 2 * B + 1) * 4 + 255) / 256 * 256; }
+
+struct WorkItem {
+  int b;        // sequence
+  int p_begin;  // first logical page of the partition
+  int n_pages;  // pages in the partition (>= 1)
+  int ctx;      // context length of the sequence
+};
+
+__device__ __forceinline__ int seq_pages(int ctx, int max_pp) {
+  return ctx > 0 ? min((ctx + kPS - 1) / kPS, max_pp) : 0;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __builtin_amdgcn_ds_bpermute((__lane_id() ^ m) << 2, v);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __builtin_amdgcn_ds_bpermute(max(lane - d, 0) << 2, v);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Finds work item `item` of the batch.  Every wave of a launch derives the
+// same geometry from the context lengths; when `writer` is set the wave also
+// stores it in the header.  Returns false when `item` lies past the last item.
+__device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, int B, int max_pp, int target,
+                                          int item, bool writer, int32_t* __restrict__ header, WorkItem& w) {
+  const int lane = __lane_id();
+  int S = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    S += b < B ? seq_pages(ctx_lens[b], max_pp) : 0;
+  }
+  S = wave_sum_int(S);
+  auto roundup4 = [](int v) { return max(4, (v + 3) / 4 * 4); };
+  int pps = roundup4((S + target - 1) / target);
+  int tails = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    const int pages = b < B ? seq_pages(ctx_lens[b], max_pp) : 0;
+    tails += (pages % pps) != 0 ? 1 : 0;
+  }
+  if (wave_sum_int(tails) * 8 > target) pps = roundup4((S + 2 * target - 1) / (2 * target));
+  int n_full = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    n_full += b < B ? seq_pages(ctx_lens[b], max_pp) / pps : 0;
+  }
+  n_full = wave_sum_int(n_full);
+  bool found = false;
+  int carry_f = 0, carry_t = n_full;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    const int ctx = b < B ? ctx_lens[b] : 0;
+    const int pages = seq_pages(ctx, max_pp);
+    const int nf = pages / pps;
+    const int nt = pages - nf * pps > 0 ? 1 : 0;
+    const int incl_f = wave_inclusive_scan(nf) + carry_f;
+    const int incl_t = wave_inclusive_scan(nt) + carry_t;
+    const int excl_f = incl_f - nf;
+    const int excl_t = incl_t - nt;
+    if (writer && b < B) {
+      header[kHeaderInts + b] = excl_f;
+      header[kHeaderInts + B + 1 + b] = nt ? excl_t : -1;
+    }
+    if (!found) {
+      const bool in_full = item >= excl_f && item < incl_f;
+      const bool in_tail = nt && item == excl_t;
+      const unsigned long long hit = __ballot(in_full || in_tail);
+      if (hit) {
+        const int l = __builtin_ffsll(hit) - 1;
+        const bool full = __builtin_amdgcn_readlane(in_full ? 1 : 0, l);
+        const int pg = __builtin_amdgcn_readlane(pages, l);
+        w.b = c + l;
+        w.p_begin = full ? (item - __builtin_amdgcn_readlane(excl_f, l)) * pps : (pg / pps) * pps;
+        w.n_pages = full ? pps : pg - w.p_begin;
+        w.ctx = __builtin_amdgcn_readlane(ctx, l);
+        found = true;
+      }
+    }
+    carry_f = __builtin_amdgcn_readlane(incl_f, 63);
+    carry_t = __builtin_amdgcn_readlane(incl_t, 63);
+  }
+  if (writer && lane == 0) {
+    header[0] = pps;
+    header[1] = carry_t;
+    header[2] = n_full;
+    header[kHeaderInts + B] = n_full;
+  }
+  return found;
+}
+
+// Work items one resident round of `kernel` holds (see work items above).
+int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int units);
+
+// Single-pass matrix-core (MFMA) split pass; kind is K_I8, K_FP8, K_BF16 or
+// K_F16, D the head dimension, G the query heads per wavefront (<= 16).
+hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
 // Largest divisor of the GQA group size that is <= max_tile.
 inline int pick_group_tile(int group, int max_tile) {

@@ -43,6 +43,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr float kInv254 = 1.0f / 254.0f;
 // The running maximum is raised only when a new score exceeds it by more than
@@ -128,14 +129,15 @@ struct PageSlot {
   uint4 v[NJ];  // tokens 4 grp .. + 3 of dims col + 16 blk, blk = 4 j .. 4 j + 3
   float4 ks;    // int8: K scales of tokens 4 grp .. + 3; fp8: .x = the page's K scale
   float4 vs;    // int8: V scales of the same tokens;      fp8: .x = the page's V scale
+  bool ok;      // page id inside the pool (wave-uniform)
 };
 
 // Workgroup: W wavefronts for W consecutive (kv-head, head chunk) units of
-// one sequence and one partition; they stream the neighbouring head slices of
+// one work item (sequence, partition); they stream the neighbouring head slices of
 // the same pages (W * 4 KB of K and V per page for int8 D = 128, in one
 // contiguous run for a whole page-layer), which keeps DRAM accesses local.
 // The wavefronts share nothing and never synchronise.
-constexpr int kMaxWaves = 8;
+constexpr int kMaxWaves = 4;
 
 template <int KIND, int D>
 __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArgs a, int G) {
@@ -149,35 +151,26 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int split = blockIdx.x;
-  const int b = blockIdx.z;
   const int group = a.H / a.KH;
   const int chunks = group / G;
   const int unit = blockIdx.y * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kvh = unit / chunks;
   const int h0 = kvh * group + (unit % chunks) * G;
 
-  // page ids of this partition: lane i holds logical page p_begin + i (fetched
-  // without waiting for the context length)
-  const int p_begin = split * a.pages_per_split;
-  int my_pid = -1;
-  if (p_begin + lane < a.max_pp && lane < a.pages_per_split)
-    my_pid = a.page_table[(size_t)b * a.max_pp + p_begin + lane];
-
-  const int ctx = a.ctx_lens[b];
-  const int num_pages = ctx > 0 ? min((ctx + kPS - 1) / kPS, a.max_pp) : 0;
-  const int p_end = min(p_begin + a.pages_per_split, num_pages);
-  float* ml_base = a.part_ml + (((size_t)b * a.H + h0) * a.nsplit + split) * 2;
-  if (p_begin >= p_end) {  // wave-uniform: the whole partition lies past the context
-    if (lane < G) {
-      ml_base[(size_t)lane * a.nsplit * 2] = -INFINITY;
-      ml_base[(size_t)lane * a.nsplit * 2 + 1] = 0.f;
-    }
-    return;
-  }
-  const int n_pages = p_end - p_begin;
+  // work item (sequence, partition) of this workgroup; the first wave of the
+  // launch also records the partition geometry for the merge pass
+  const int item = blockIdx.x;
+  WorkItem wi;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  const int b = wi.b;
+  const int n_pages = wi.n_pages;
   const int last = n_pages - 1;
-  const int tok_end = min(p_end * kPS, ctx) - p_begin * kPS;
+  const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);  // valid tokens of the partition
+  // page ids, fetched RING pages ahead of the data: lane u < RING reads the id
+  // of page first + u (clamped to the last page)
+  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
+  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
 
   const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
   const size_t page_stride = kv_stride * 2 * a.L;
@@ -249,9 +242,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   // Loads are issued unconditionally from a clamped, always valid address and
   // zeroed afterwards for an absent page, so every slot keeps the same loads
   // in flight (a branch around a load makes the compiler wait for all of them).
-  auto load_page = [&](PageSlot<D>& s, int pi) {
-    const int pid = __builtin_amdgcn_readlane(my_pid, pi);
+  auto load_page = [&](PageSlot<D>& s, int pid) {
     const bool ok = page_ok(pid);
+    s.ok = ok;
     const int pc = ok ? pid : 0;
     const uint8_t* pb = layer_base + (size_t)pc * page_stride;
     const uint8_t* kb = pb + col * D + grp * 16;
@@ -305,10 +298,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[r] = c[r] * s.ks.x;
     }
-    const bool ok = page_ok(__builtin_amdgcn_readlane(my_pid, pi));
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      if (!(ok && pi * kPS + grp * 4 + r < tok_end)) sc[r] = -INFINITY;
+      if (!(s.ok && pi * kPS + grp * 4 + r < tok_end)) sc[r] = -INFINITY;
   };
 
   // Pages pi and pi + 1 (the second may lie past the partition).
@@ -377,15 +369,19 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   // pair covers only the slots that pair consumes.
   {
     PageSlot<D> ring[RING];
+    const int ids0 = ids_at(0);
+    int ids_next = ids_at(RING);
 #pragma unroll
-    for (int u = 0; u < RING; ++u) load_page(ring[u], min(u, last));
+    for (int u = 0; u < RING; ++u) load_page(ring[u], __builtin_amdgcn_readlane(ids0, u));
     for (int base = 0; base < n_pages; base += RING) {
+      const int ids_ahead = ids_at(base + 2 * RING);
 #pragma unroll
       for (int u = 0; u < RING; u += 2) {
         if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
-        load_page(ring[u], min(base + u + RING, last));
-        load_page(ring[u + 1], min(base + u + 1 + RING, last));
+        load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
+        load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
       }
+      ids_next = ids_ahead;
     }
   }
 
@@ -393,16 +389,255 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   if (col < G) {
-    float* out = a.part_acc + ((((size_t)b * a.H + h0 + col) * a.nsplit + split) * D);
+    float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk)
       *reinterpret_cast<float4*>(out + blk * 16 + grp * 4) =
           make_float4(acc[blk][0], acc[blk][1], acc[blk][2], acc[blk][3]);
     if (grp == 0) {
-      ml_base[(size_t)col * a.nsplit * 2] = l_tot > 0.f ? m_run : -INFINITY;
-      ml_base[(size_t)col * a.nsplit * 2 + 1] = l_tot;
+      ml_base[col * 2] = l_tot > 0.f ? m_run : -INFINITY;
+      ml_base[col * 2 + 1] = l_tot;
     }
   }
+}
+
+
+// ---------------------------------------------------------------------------
+// Float pools (bf16, f16): the same single-pass stream over the reference's
+// token-major pages.
+//   S^T = K Q^T     v_mfma_f32_16x16x32_{bf16,f16}: K rows as stored (lane
+//                   (t, g) loads dims 32 c + 8 g .. + 7 of token t), the fp32
+//                   query as a hi + lo pair of the pool's type.
+//   V transpose     the PV product needs each lane to hold tokens, not dims.
+//                   One MFMA against a one-hot operand, T = V E_h with
+//                   E_h[k][col] = (k == 16 h + col), moves dims 32 c + 16 h +
+//                   col of 16 tokens into lane (col, g) as 4 token rows; the
+//                   values are copied exactly (one product by 1.0 per output).
+//   O^T += V^T P^T  as in the quantized kernel, two pages per step, P as a hi +
+//                   lo pair of the pool's type.
+// ---------------------------------------------------------------------------
+template <int KIND> struct FloatOps;
+template <> struct FloatOps<K_BF16> {
+  using vec = v8bf;
+  using el = __bf16;
+  static __device__ __forceinline__ v4f mma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static constexpr uint16_t kOne = 0x3f80;
+};
+template <> struct FloatOps<K_F16> {
+  using vec = v8h;
+  using el = _Float16;
+  static __device__ __forceinline__ v4f mma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static constexpr uint16_t kOne = 0x3c00;
+};
+
+template <int D>
+struct FloatSlot {
+  static constexpr int NC = D / 32;
+  uint4 k[NC];  // token col, dims 32 c + 8 grp .. + 7
+  uint4 v[NC];  // same positions of V
+  bool ok;      // page id inside the pool (wave-uniform)
+};
+
+template <int KIND, int D>
+__global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(DecodeArgs a, int G) {
+  using Ops = FloatOps<KIND>;
+  using vec = typename Ops::vec;
+  using el = typename Ops::el;
+  constexpr int RING = D <= 128 ? 4 : 2;
+  constexpr int ROW = D * 2;              // bytes per token row
+  constexpr int HEAD_BYTES = kPS * ROW;   // one (page, layer, K/V, head) slice
+  constexpr int NC = D / 32;              // 32-dim chunks: one 16-byte load per lane each
+  constexpr int NB = D / 16;              // 16-dim blocks of the output column
+  static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int group = a.H / a.KH;
+  const int chunks = group / G;
+  const int unit = blockIdx.y * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kvh = unit / chunks;
+  const int h0 = kvh * group + (unit % chunks) * G;
+
+  // work item (sequence, partition) of this workgroup; the first wave of the
+  // launch also records the partition geometry for the merge pass
+  const int item = blockIdx.x;
+  WorkItem wi;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  const int b = wi.b;
+  const int n_pages = wi.n_pages;
+  const int last = n_pages - 1;
+  const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);  // valid tokens of the partition
+  // page ids, fetched RING pages ahead of the data: lane u < RING reads the id
+  // of page first + u (clamped to the last page)
+  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
+  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
+
+  const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
+  const size_t page_stride = kv_stride * 2 * a.L;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
+  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+
+  // query operand (B of S^T): lane (col, grp) holds q[32 c + 8 grp + e] * qscale, hi + lo
+  const float* qrow = a.query + ((size_t)b * a.H + h0 + min(col, G - 1)) * D;
+  vec QH[NC][2];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float4 f0 = ldf4(qrow + 32 * c + 8 * grp);
+    const float4 f1 = ldf4(qrow + 32 * c + 8 * grp + 4);
+    const float x[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = x[e] * a.qscale;
+      const el hi = (el)v;
+      QH[c][0][e] = hi;
+      QH[c][1][e] = (el)(v - (float)hi);
+    }
+  }
+  // one-hot operands of the V transpose: lane (col, grp), element e is
+  // E_h[8 grp + e][col] = (8 grp + e == 16 h + col)
+  vec onehot[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      onehot[h][e] = __builtin_bit_cast(el, (uint16_t)((grp == 2 * h + (col >> 3) && e == (col & 7)) ? Ops::kOne : 0));
+
+  float m_run = kNoMax;
+  float l_run = 0.f;
+  v4f acc[NB];
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) acc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto load_page = [&](FloatSlot<D>& s, int pid) {
+    s.ok = page_ok(pid);
+    const int pc = s.ok ? pid : 0;
+    const uint8_t* kb = layer_base + (size_t)pc * page_stride + col * ROW + grp * 16;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      s.k[c] = ld16(kb + c * 64);
+      s.v[c] = ld16(kb + kv_stride + c * 64);
+    }
+  };
+
+  auto page_scores = [&](const FloatSlot<D>& s, int pi, float* sc) {
+    v4f c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const vec kop = __builtin_bit_cast(vec, s.k[c]);
+      c4 = Ops::mma(kop, QH[c][0], c4);
+      c4 = Ops::mma(kop, QH[c][1], c4);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = (s.ok && pi * kPS + grp * 4 + r < tok_end) ? c4[r] : -INFINITY;
+  };
+
+  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page; tokens
+  // that are absent or past the context read as 0 (whatever the page holds).
+  auto v_block = [&](const FloatSlot<D>& s, int pi, int blk, bool valid_page, float* out4) {
+    const v4f t = Ops::mma(__builtin_bit_cast(vec, s.v[blk >> 1]), onehot[blk & 1], v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out4[r] = (valid_page && pi * kPS + grp * 4 + r < tok_end) ? t[r] : 0.f;
+  };
+
+  auto process_pair = [&](const FloatSlot<D>& s0, const FloatSlot<D>& s1, int pi, bool has1) {
+    float sc[8];
+    page_scores(s0, pi, sc);
+    if (has1) {
+      page_scores(s1, pi + 1, sc + 4);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
+    }
+    float pm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
+    pm = fmaxf(pm, xor_shfl<16>(pm));
+    pm = fmaxf(pm, xor_shfl<32>(pm));
+    if (pm > m_run + kLazyRescale) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
+      l_run *= alpha;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) acc[blk] *= alpha;
+      m_run = pm;
+    }
+    vec Bh, Bl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sc[e] - m_run);
+      l_run += p;
+      const el hi = (el)p;
+      Bh[e] = hi;
+      Bl[e] = (el)(p - (float)hi);
+    }
+    const bool ok0 = s0.ok;
+    const bool ok1 = has1 && s1.ok;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      float t[8];
+      v_block(s0, pi, blk, ok0, t);
+      v_block(s1, pi + 1, blk, ok1, t + 4);
+      vec A;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] = (el)t[e];  // exact: the values came from the pool
+      acc[blk] = Ops::mma(A, Bh, acc[blk]);
+      acc[blk] = Ops::mma(A, Bl, acc[blk]);
+    }
+  };
+
+  {
+    FloatSlot<D> ring[RING];
+    const int ids0 = ids_at(0);
+    int ids_next = ids_at(RING);
+#pragma unroll
+    for (int u = 0; u < RING; ++u) load_page(ring[u], __builtin_amdgcn_readlane(ids0, u));
+    for (int base = 0; base < n_pages; base += RING) {
+      const int ids_ahead = ids_at(base + 2 * RING);
+#pragma unroll
+      for (int u = 0; u < RING; u += 2) {
+        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
+        load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
+        load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
+      }
+      ids_next = ids_ahead;
+    }
+  }
+
+  float l_tot = l_run + xor_shfl<16>(l_run);
+  l_tot += xor_shfl<32>(l_tot);
+  if (col < G) {
+    float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk)
+      *reinterpret_cast<float4*>(out + blk * 16 + grp * 4) =
+          make_float4(acc[blk][0], acc[blk][1], acc[blk][2], acc[blk][3]);
+    if (grp == 0) {
+      ml_base[col * 2] = l_tot > 0.f ? m_run : -INFINITY;
+      ml_base[col * 2 + 1] = l_tot;
+    }
+  }
+}
+
+template <int KIND, int D>
+void launch_kernel(const DecodeArgs& a0, int B, int units, int W, int G, hipStream_t st) {
+  const void* fn;
+  if constexpr (KIND == K_I8 || KIND == K_FP8)
+    fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D>);
+  else
+    fn = reinterpret_cast<const void*>(&decode_stream_float_kernel<KIND, D <= 128 ? D : 128>);
+  DecodeArgs a = a0;
+  a.target = items_target(fn, W, 0, units);
+  dim3 grid(B + 2 * a.target, units / W, 1);  // at most B + 2 target work items
+  dim3 block(64 * W);
+  if constexpr (KIND == K_I8 || KIND == K_FP8)
+    hipLaunchKernelGGL((decode_stream_kernel<KIND, D>), grid, block, 0, st, a, G);
+  else if constexpr (D <= 128)
+    hipLaunchKernelGGL((decode_stream_float_kernel<KIND, D>), grid, block, 0, st, a, G);
 }
 
 template <int KIND>
@@ -410,21 +645,25 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   const int units = a.KH * ((a.H / a.KH) / G);  // (kv-head, head chunk) units per sequence
   int W = kMaxWaves;
   while (units % W) --W;
-  dim3 grid(a.nsplit, units / W, B);
-  dim3 block(64 * W);
   switch (D) {
-    case 64: hipLaunchKernelGGL((decode_stream_kernel<KIND, 64>), grid, block, 0, st, a, G); break;
-    case 128: hipLaunchKernelGGL((decode_stream_kernel<KIND, 128>), grid, block, 0, st, a, G); break;
-    default: hipLaunchKernelGGL((decode_stream_kernel<KIND, 256>), grid, block, 0, st, a, G); break;
+    case 64: launch_kernel<KIND, 64>(a, B, units, W, G, st); break;
+    case 128: launch_kernel<KIND, 128>(a, B, units, W, G, st); break;
+    default: launch_kernel<KIND, 256>(a, B, units, W, G, st); break;
   }
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_quant_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
-  if (G < 1 || G > 16 || a.pages_per_split > kMaxPagesPerSplit) return hipErrorInvalidValue;
-  return kind == K_I8 ? launch_d<K_I8>(a, B, D, G, st) : launch_d<K_FP8>(a, B, D, G, st);
+hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
+  if (G < 1 || G > 16) return hipErrorInvalidValue;
+  switch (kind) {
+    case K_I8: return launch_d<K_I8>(a, B, D, G, st);
+    case K_FP8: return launch_d<K_FP8>(a, B, D, G, st);
+    case K_BF16: return D <= 128 ? launch_d<K_BF16>(a, B, D, G, st) : hipErrorInvalidValue;
+    case K_F16: return D <= 128 ? launch_d<K_F16>(a, B, D, G, st) : hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace dec

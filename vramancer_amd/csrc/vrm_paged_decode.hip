@@ -13,9 +13,9 @@
 //  * each lane issues 16-byte loads of the contiguous [PS][D] page slice; the
 //    page ids of a partition are fetched with one vector load up front and the
 //    next page is loaded while the current one is consumed;
-//  * this VALU kernel serves the float pools and the 4-bit pool (dequantized
-//    in registers as (nibble - zero) * scale); the int8 and fp8 pools go to
-//    the single-pass matrix-core kernel of vrm_decode_mfma.hip;
+//  * this VALU kernel serves the float32 pool and the 4-bit pool (dequantized
+//    in registers as (nibble - zero) * scale); the bf16, f16, int8 and fp8
+//    pools go to the single-pass matrix-core kernels of vrm_decode_mfma.hip;
 //  * phase 1 writes all scores of the partition to LDS, phase 2 takes the
 //    exact partition maximum, phase 3 streams V once with fixed weights, so no
 //    running rescale of the accumulators is needed;
@@ -25,8 +25,40 @@
 
 #include <math.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace vrm {
 namespace dec {
+
+// Work items one resident round of `kernel` holds: resident wavefronts (CU
+// count x workgroups per CU from the occupancy query, capped at
+// kMaxTargetWaves) over the wavefronts of one item.  Cached per kernel.
+int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int units) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int waves = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({kernel, waves_per_block});
+    if (it != cache.end()) waves = it->second;
+  }
+  if (waves == 0) {
+    int dev = 0, cus = 0, blocks = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64 * waves_per_block, lds_bytes) != hipSuccess ||
+        blocks <= 0)
+      blocks = 1;
+    waves = cus * blocks * waves_per_block;
+    std::lock_guard<std::mutex> lock(mu);
+    cache[{kernel, waves_per_block}] = waves;
+  }
+  return std::max(1, std::min(waves, kMaxTargetWaves) / units);
+}
+
 namespace {
 
 template <int KIND>
@@ -70,7 +102,12 @@ struct PageRegs {
   float s1[LPP];  // q4: group zero point
 };
 
-// One wavefront per (split, kv head x head chunk, sequence).
+// One wavefront per (work item, kv head x head chunk).  A partition longer
+// than kChunkPages pages is walked in chunks; each chunk runs the three
+// phases below with its own exact maximum and is folded into the running
+// (max, sum, acc) of the partition.
+constexpr int kChunkPages = 64;
+
 template <int KIND, int D, int G>
 __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
   constexpr int E = Kv<KIND>::kElems;         // elements per 16-byte lane chunk
@@ -80,40 +117,24 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
   constexpr int LPP = (kPS + TPL - 1) / TPL;  // wave loads per page
   constexpr int HEAD_BYTES = kPS * RB;        // one (page, layer, kv, head) slice
   constexpr int Q4G = D / 32;                 // 4-bit groups per row
+  constexpr int TS = kChunkPages * kPS;       // tokens per chunk
   static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "lane mapping");
   static_assert(TPL <= kPS || (TPL % kPS) == 0, "page mapping");
   static_assert(LPP * TPL * RB == (TPL <= kPS ? HEAD_BYTES : TPL * RB), "load coverage");
 
   extern __shared__ float lds[];
-  const int TS = a.pages_per_split * kPS;
   float* s_lds = lds;  // [G][TS] scores, then softmax weights
 
   const int lane = threadIdx.x;
-  const int split = blockIdx.x;
-  const int b = blockIdx.z;
   const int group = a.H / a.KH;
   const int chunks = group / G;
-  const int kvh = blockIdx.y / chunks;
-  const int h0 = kvh * group + (blockIdx.y % chunks) * G;
-
-  const int ctx = a.ctx_lens[b];
-  const int num_pages = ctx > 0 ? min((ctx + kPS - 1) / kPS, a.max_pp) : 0;
-  const int p_begin = split * a.pages_per_split;
-  const int p_end = min(p_begin + a.pages_per_split, num_pages);
-  float* ml_base = a.part_ml + (((size_t)b * a.H + h0) * a.nsplit + split) * 2;
-  if (p_begin >= p_end) {
-    if (lane < G) {
-      ml_base[(size_t)lane * a.nsplit * 2] = -INFINITY;
-      ml_base[(size_t)lane * a.nsplit * 2 + 1] = 0.f;
-    }
-    return;
-  }
-  const int n_pages = p_end - p_begin;
-  const int tok_end = min(p_end * kPS, ctx) - p_begin * kPS;  // valid tokens in split
-
-  // Page ids of this split: lane i holds logical page p_begin + i.
-  int my_pid = -1;
-  if (lane < n_pages) my_pid = a.page_table[(size_t)b * a.max_pp + p_begin + lane];
+  const int unit = blockIdx.y;
+  const int kvh = unit / chunks;
+  const int h0 = kvh * group + (unit % chunks) * G;
+  const int item = blockIdx.x;
+  WorkItem wi;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  const int b = wi.b;
 
   const int c = lane % LPT;   // which 16-byte chunk of a token row
   const int tl = lane / LPT;  // which token of a wave load
@@ -158,6 +179,22 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
     for (int e = 0; e < E; ++e) qr[g][e] = qh[c * E + e] * a.qscale;
   }
 
+  float m_run[G], l_run[G], acc[G][E];  // running softmax state of the partition
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+  }
+
+  for (int c0 = 0; c0 < wi.n_pages; c0 += kChunkPages) {
+  const int n_pages = min(kChunkPages, wi.n_pages - c0);
+  const int tok_end = min(n_pages * kPS, wi.ctx - (wi.p_begin + c0) * kPS);  // valid tokens in the chunk
+  // Page ids of this chunk: lane i holds logical page p_begin + c0 + i.
+  int my_pid = -1;
+  if (lane < n_pages) my_pid = a.page_table[(size_t)b * a.max_pp + wi.p_begin + c0 + lane];
+
   // ---------------- phase 1: scores ----------------
   {
     PageRegs<KIND, LPP> cur;
@@ -198,31 +235,29 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  // ---------------- phase 2: exact softmax statistics ----------------
-  float m_g[G], l_g[G];
+  // ---------------- phase 2: exact chunk maximum, folded into the running state ----------------
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mx = -INFINITY;
     for (int t = lane; t < tok_end; t += 64) mx = fmaxf(mx, s_lds[g * TS + t]);
     mx = group_max<64>(mx);
+    const float m_new = fmaxf(m_run[g], mx);
+    const float keep = (m_run[g] == -INFINITY) ? 0.f : exp2f(m_run[g] - m_new);
     float sum = 0.f;
     for (int t = lane; t < tok_end; t += 64) {
       const float s = s_lds[g * TS + t];
-      const float p = (s == -INFINITY) ? 0.f : exp2f(s - mx);
+      const float p = (s == -INFINITY) ? 0.f : exp2f(s - m_new);
       sum += p;
       s_lds[g * TS + t] = p;
     }
-    m_g[g] = mx;
-    l_g[g] = group_sum<64>(sum);
+    l_run[g] = l_run[g] * keep + group_sum<64>(sum);
+    m_run[g] = m_new;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] *= keep;
   }
   __syncthreads();
 
   // ---------------- phase 3: weighted V ----------------
-  float acc[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
   {
     PageRegs<KIND, LPP> cur;
     int pid_cur = __builtin_amdgcn_readlane(my_pid, 0);
@@ -257,6 +292,9 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
     }
   }
 
+  __syncthreads();  // the next chunk overwrites the scores
+  }  // chunk loop
+
   // Lanes that hold the same chunk c (different tokens) sum their partials.
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -266,7 +304,7 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
   if (tl == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float* dst = a.part_acc + ((((size_t)b * a.H + h0 + g) * a.nsplit + split) * D) + c * E;
+      float* dst = a.part_acc + ((size_t)item * a.H + h0 + g) * D + c * E;
 #pragma unroll
       for (int e = 0; e < E; ++e) dst[e] = acc[g][e];
     }
@@ -274,73 +312,122 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      ml_base[(size_t)g * a.nsplit * 2] = m_g[g];
-      ml_base[(size_t)g * a.nsplit * 2 + 1] = l_g[g];
+      a.part_ml[((size_t)item * a.H + h0 + g) * 2] = m_run[g];
+      a.part_ml[((size_t)item * a.H + h0 + g) * 2 + 1] = l_run[g];
     }
   }
 }
 
 // Merges the partitions of one (sequence, head): out = sum_s w_s acc_s / sum_s w_s l_s
-// with w_s = 2^(m_s - max_s m_s).  Partitions are read 16 at a time with all
-// their loads issued together (clamped, unconditional), folding each batch
-// into a running maximum.
+// with w_s = 2^(m_s - max_s m_s).  The items of sequence b are its full
+// partitions first_b .. first_{b+1} - 1 and its tail item, as recorded in the
+// header by the partition pass.  Four wavefronts each fold every fourth
+// partial, BATCH at a time with all loads issued together (clamped,
+// unconditional), and the four results are combined through LDS.
 template <int D>
-__global__ void __launch_bounds__(64) decode_reduce_kernel(const float* __restrict__ part_acc,
-                                                           const float* __restrict__ part_ml,
-                                                           const int32_t* __restrict__ ctx_lens,
-                                                           float* __restrict__ out, int H, int nsplit,
-                                                           int pages_per_split, int max_pp) {
+__global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restrict__ part_acc,
+                                                            const float* __restrict__ part_ml,
+                                                            const int32_t* __restrict__ header,
+                                                            float* __restrict__ out, int H, int B) {
   constexpr int PER = D / 64;
-  constexpr int BATCH = 16;
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int ctx = ctx_lens[b];
-  float* o = out + ((size_t)b * H + h) * D;
-  const int num_pages = ctx > 0 ? min((ctx + kPS - 1) / kPS, max_pp) : 0;
-  const int nact = min(nsplit, (num_pages + pages_per_split - 1) / pages_per_split);
-  const float* ml = part_ml + ((size_t)b * H + h) * nsplit * 2;
-  const float* acc = part_acc + ((size_t)b * H + h) * nsplit * D;
+  constexpr int BATCH = 4;
+  constexpr int WAVES = 4;
+  __shared__ float sh_m[WAVES], sh_l[WAVES];
+  __shared__ float sh_res[WAVES][D];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int first = header[kHeaderInts + b];
+  const int nf = header[kHeaderInts + b + 1] - first;
+  const int tail = header[kHeaderInts + B + 1 + b];
+  const int nact = nf + (tail >= 0 ? 1 : 0);
+  auto item_of = [&](int s) { return s < nf ? first + s : tail; };
   float M = -INFINITY, Lsum = 0.f;
   float res[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) res[i] = 0.f;
-  for (int s0 = 0; s0 < nact; s0 += BATCH) {
-    float m[BATCH], l[BATCH], x[BATCH][PER];
+  // Two register batches: the loads of batch k + 1 are in flight while batch k
+  // is folded, so a long sequence costs one memory latency, not one per batch.
+  float m[2][BATCH], l[2][BATCH], x[2][BATCH][PER];
+  auto load_batch = [&](int buf, int s0) {
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) {
-      const int s = min(s0 + k, nact - 1);
-      m[k] = ml[2 * s];
-      l[k] = ml[2 * s + 1];
+      const int s = s0 + k * WAVES;
+      const size_t it = (size_t)item_of(min(s, nact - 1)) * H + h;
+      m[buf][k] = part_ml[it * 2];
+      l[buf][k] = part_ml[it * 2 + 1];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) x[k][i] = acc[(size_t)s * D + i * 64 + lane];
-      if (s0 + k >= nact) m[k] = -INFINITY;
+      for (int i = 0; i < PER; ++i) x[buf][k][i] = part_acc[it * D + i * 64 + lane];
     }
+  };
+  auto fold_batch = [&](int buf, int s0) {
     float cm = M;
 #pragma unroll
-    for (int k = 0; k < BATCH; ++k) cm = fmaxf(cm, m[k]);
-    if (cm == -INFINITY) continue;
+    for (int k = 0; k < BATCH; ++k)
+      if (s0 + k * WAVES < nact) cm = fmaxf(cm, m[buf][k]);
+    if (cm == -INFINITY) return;
     const float keep = (M == -INFINITY) ? 0.f : exp2f(M - cm);
     Lsum *= keep;
 #pragma unroll
     for (int i = 0; i < PER; ++i) res[i] *= keep;
 #pragma unroll
     for (int k = 0; k < BATCH; ++k) {
-      const float w = (m[k] == -INFINITY) ? 0.f : exp2f(m[k] - cm);
-      Lsum = fmaf(w, l[k], Lsum);
+      const bool live = s0 + k * WAVES < nact && m[buf][k] != -INFINITY;
+      const float w = live ? exp2f(m[buf][k] - cm) : 0.f;
+      Lsum = fmaf(w, l[buf][k], Lsum);
 #pragma unroll
-      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, x[k][i], res[i]);
+      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, x[buf][k][i], res[i]);
     }
     M = cm;
+  };
+  constexpr int STEP = WAVES * BATCH;
+  if (wave < nact) {
+    load_batch(0, wave);
+    int s0 = wave;
+    for (; s0 + STEP < nact; s0 += 2 * STEP) {
+      load_batch(1, s0 + STEP);
+      fold_batch(0, s0);
+      load_batch(0, s0 + 2 * STEP);  // unconditional (clamped): a branch would make the compiler wait for all loads
+      fold_batch(1, s0 + STEP);
+    }
+    if (s0 < nact) fold_batch(0, s0);
   }
-  const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
+  if (lane == 0) {
+    sh_m[wave] = M;
+    sh_l[wave] = Lsum;
+  }
 #pragma unroll
-  for (int i = 0; i < PER; ++i) o[i * 64 + lane] = res[i] * inv;
+  for (int i = 0; i < PER; ++i) sh_res[wave][i * 64 + lane] = res[i];
+  __syncthreads();
+  if (wave == 0) {
+    float gm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) gm = fmaxf(gm, sh_m[w]);
+    float L = 0.f, o[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[i] = 0.f;
+    if (gm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float f = sh_m[w] == -INFINITY ? 0.f : exp2f(sh_m[w] - gm);
+        L = fmaf(f, sh_l[w], L);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) o[i] = fmaf(f, sh_res[w][i * 64 + lane], o[i]);
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float* dst = out + ((size_t)b * H + h) * D;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = o[i] * inv;
+  }
 }
 
 template <int KIND, int D, int G>
-hipError_t launch_split(const DecodeArgs& a, int B, hipStream_t st) {
-  const int chunks = (a.H / a.KH) / G;
-  dim3 grid(a.nsplit, a.KH * chunks, B);
-  const size_t lds = (size_t)G * a.pages_per_split * kPS * sizeof(float);
+hipError_t launch_split(const DecodeArgs& a0, int B, hipStream_t st) {
+  const int units = a0.KH * ((a0.H / a0.KH) / G);
+  const size_t lds = (size_t)G * kChunkPages * kPS * sizeof(float);
+  DecodeArgs a = a0;
+  a.target = items_target(reinterpret_cast<const void*>(&decode_split_kernel<KIND, D, G>), 1, lds, units);
+  dim3 grid(B + 2 * a.target, units, 1);  // at most B + 2 target work items
   hipLaunchKernelGGL((decode_split_kernel<KIND, D, G>), grid, dim3(64), lds, st, a);
   return hipGetLastError();
 }
@@ -379,40 +466,27 @@ hipError_t dispatch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) 
 
 hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStream_t st) {
   dim3 grid(a.H, B);
+  const dim3 block(256);
   switch (D) {
     case 64:
-      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
-                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.H, B);
       break;
     case 128:
-      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
-                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.H, B);
       break;
     default:
-      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, dim3(64), 0, st, a.part_acc, a.part_ml, a.ctx_lens, out,
-                         a.H, a.nsplit, a.pages_per_split, a.max_pp);
+      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.H, B);
       break;
   }
   return hipGetLastError();
 }
 
-// Pages per partition: enough (sequence, kv-head, partition) work items for
-// about 8 wavefronts per CU of the 256-CU chip, so that each wavefront streams
-// one long partition (its page-table fetch and query set-up paid once) and
-// the merge has few partials to combine; a multiple of 4 pages, at most 64
-// (one page id per lane).  Depends only on the shape, never on the dtype, so
-// the partition and merge passes can be enqueued separately.
-int pages_per_split_for(int B, int KH, int max_pp) {
-  const long units = (long)B * KH;
-  const long target = 2048;
-  long want_splits = (target + units - 1) / units;
-  if (want_splits < 1) want_splits = 1;
-  long pps = (max_pp + want_splits - 1) / want_splits;
-  pps = (pps + 3) / 4 * 4;
-  if (pps < 4) pps = 4;
-  if (pps > kMaxPagesPerSplit) pps = kMaxPagesPerSplit;
-  return (int)pps;
-}
+// Work-item capacity of the workspace: a call has at most B + 2 target items
+// and target <= kMaxTargetWaves / units with units >= KH wavefronts per item.
+long items_capacity(int B, int KH) { return (long)B + 2L * ((kMaxTargetWaves + KH - 1) / KH); }
 
 int check_common(const float* query, const void* pool, const int32_t* page_table, const int32_t* ctx, float* out,
                  int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx, float scale) {
@@ -457,31 +531,33 @@ enum Passes { kBoth = 3, kPartitionsOnly = 1, kMergeOnly = 2 };
 
 int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D,
                float scale, hipStream_t st, int passes) {
-  const bool mfma = (kind == K_I8 || kind == K_FP8);
+  // The matrix-core stream kernels take the quantized pools at every head_dim
+  // and the 16-bit float pools at D <= 128 (at D = 256 their registers
+  // spill); the rest runs on the VALU kernel.
+  const bool mfma = kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128);
   const int max_tile = kind == K_Q4 ? 4 : mfma ? 16 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
-  a.pages_per_split = pages_per_split_for(B, a.KH, a.max_pp);
-  a.nsplit = (a.max_pp + a.pages_per_split - 1) / a.pages_per_split;
-  if (a.nsplit > 65535) {
-    set_error("vrm_paged_decode: page table too wide (%d pages)", a.max_pp);
-    return VRM_ERR_UNSUPPORTED;
-  }
-  const size_t need = vrm_paged_decode_workspace_bytes(B, a.H, D, a.nsplit);
+  const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
+  (void)units;
+  a.B = B;
+  const long cap = items_capacity(B, a.KH);
+  const size_t need = header_bytes(B) + (size_t)cap * a.H * (D + 2) * sizeof(float);
   if (!workspace || workspace_bytes < need) {
     set_error("vrm_paged_decode: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
     return VRM_ERR_WORKSPACE;
   }
-  a.part_acc = reinterpret_cast<float*>(workspace);
-  a.part_ml = a.part_acc + (size_t)B * a.H * a.nsplit * D;
+  a.header = reinterpret_cast<int32_t*>(workspace);
+  a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
+  a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
   hipError_t e = hipSuccess;
   if (passes & kPartitionsOnly) {
     switch (kind) {
       case K_F32: e = dispatch_d<K_F32>(a, B, D, G, st); break;
-      case K_F16: e = dispatch_d<K_F16>(a, B, D, G, st); break;
-      case K_BF16: e = dispatch_d<K_BF16>(a, B, D, G, st); break;
+      case K_F16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_F16>(a, B, D, G, st); break;
+      case K_BF16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_BF16>(a, B, D, G, st); break;
       case K_I8:
-      case K_FP8: e = launch_quant_mfma(a, kind, B, D, G, st); break;
+      case K_FP8: e = launch_stream_mfma(a, kind, B, D, G, st); break;
       default: e = dispatch_d<K_Q4>(a, B, D, G, st); break;
     }
     if (e != hipSuccess) {
@@ -557,13 +633,13 @@ using namespace vrm::dec;
 extern "C" int vrm_paged_decode_num_splits(int B, int H, int KH, int max_pp, int page_size) {
   (void)page_size;
   if (B <= 0 || H <= 0 || KH <= 0 || max_pp <= 0 || H % KH) return 0;
-  const int pps = pages_per_split_for(B, KH, max_pp);
-  return (max_pp + pps - 1) / pps;
+  // partition slots per sequence: B * nsplit >= the work-item capacity
+  return (int)((items_capacity(B, KH) + B - 1) / B);
 }
 
 extern "C" size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit) {
   if (B <= 0 || H <= 0 || D <= 0 || nsplit <= 0) return 0;
-  return (size_t)B * H * nsplit * (D + 2) * sizeof(float);
+  return header_bytes(B) + (size_t)B * H * nsplit * (D + 2) * sizeof(float);
 }
 
 extern "C" int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_scales,
@@ -607,8 +683,9 @@ extern "C" int vrm_paged_decode_merge(const int32_t* context_lens, float* out, c
   a.max_pp = max_pp;
   a.L = 1;
   a.P = 1;
-  // The merge only depends on the partition geometry, which is the same for every dtype except
-  // the 4-bit pool; callers of the 4-bit pool use vrm_paged_decode_q4.
+  // The merge reads the partition geometry the partition pass left in the
+  // workspace header; the dtype below only selects the workspace layout,
+  // which is the same for every pool.
   return run_decode(a, K_I8, out, const_cast<void*>(workspace), workspace_bytes, B, D, 1.f,
                     reinterpret_cast<hipStream_t>(stream), kMergeOnly);
 }
