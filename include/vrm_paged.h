@@ -227,6 +227,73 @@ int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* angles, int
                               const float* signs, const float* angle_lut, float* out,
                               int rotated, vrm_stream_t stream);
 
+/* --------------------------------------------------------------------------
+ * TurboQuant pages.  The reference keeps TurboQuant-compressed K/V in Python
+ * dicts per (page, layer, slot) (core/paged_attention.py:568-675, 1420-1496)
+ * and attends them with compute_attention_turbo (:1259-1418).  Here the same
+ * codes live in a device pool tq_pool[P][L][2][KH][slice] (bytes), one slice
+ * of vrm_tq_slice_bytes() per (page, layer, K/V, kv-head) holding the page's
+ * 16 tokens: angle bins (in a lane-friendly order of the reference's 127
+ * bins), fp16 radius and, for K, the 64 QJL sign bits and the fp16 residual
+ * norm.  Built for head_dim 128 (padded_dim 128), qjl_dim 64 and 2..4 bits
+ * per angle; signs / jl / angle_lut are the compressor's buffers and the
+ * {cos, sin} table of vrm_turboquant_compress.
+ * -------------------------------------------------------------------------- */
+
+/* Bytes of one (page, layer, K/V, kv-head) slice; 0 for an unsupported shape. */
+size_t vrm_tq_slice_bytes(int head_dim, int bits, int qjl_dim);
+
+/*
+ * Compresses N new tokens (key/value [N][KH][D] of src_dtype) into slot
+ * slots[n] of page page_ids[n], layer layer_idx.  Codes are those of
+ * vrm_turboquant_compress (the reference's KVCacheCompressor.compress CPU
+ * path); V rows store angles and radius only (the attention never reads a
+ * value's QJL fields).  Replaces write_kv's enqueue + flush_compression
+ * (core/paged_attention.py:615-675).  Rows aimed at pages outside [0, P) or
+ * slots outside [0, 16) are dropped.
+ */
+int vrm_tq_quant_append(const void* key, const void* value, int src_dtype,
+                        const int32_t* page_ids, const int32_t* slots, int N,
+                        uint8_t* tq_pool, int KH, int D, int PS, int L, int P, int layer_idx,
+                        int bits, int qjl_dim, const float* signs, const float* jl,
+                        const float* angle_lut, vrm_stream_t stream);
+
+/*
+ * Bulk write of whole pages (key/value [NP][KH][16][D]); page n holds
+ * n_valid[n] tokens, later slots get zero codes.  Replaces compress_page_bulk
+ * (core/paged_attention.py:1420-1496).
+ */
+int vrm_tq_quant_pages(const void* key, const void* value, int src_dtype,
+                       const int32_t* page_ids, const int32_t* n_valid, int NP,
+                       uint8_t* tq_pool, int KH, int D, int PS, int L, int P, int layer_idx,
+                       int bits, int qjl_dim, const float* signs, const float* jl,
+                       const float* angle_lut, vrm_stream_t stream);
+
+/*
+ * Reads pages back in the reference's raw code format: row
+ * ((n * 2 + kv) * KH + h) * 16 + t gets radius (fp16 bits), the 127
+ * level-major bins, 64 sign bytes and the norm (V rows: zero signs / norm).
+ * Inspection and offload helper.
+ */
+int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids, int NP,
+                      int KH, int D, int PS, int L, int P, int layer_idx, int bits, int qjl_dim,
+                      uint16_t* radius, uint8_t* angles, uint8_t* qjl_signs, uint16_t* qjl_norms,
+                      vrm_stream_t stream);
+
+/*
+ * Paged decode over TurboQuant pages: for query head h (kv-head h / (H / KH)),
+ * out = softmax(scale * score) V with score_t = q_rot . k_polar_t + the QJL
+ * correction, and V the decompressed values, as
+ * PagedKVCacheManager.compute_attention_turbo (core/paged_attention.py:
+ * 1259-1418) with dense values (sparse_v_ratio 1.0).  Workspace and split
+ * contract as vrm_paged_decode.
+ */
+int vrm_paged_decode_tq(const float* query, const uint8_t* tq_pool, const int32_t* page_table,
+                        const int32_t* context_lens, float* out, void* workspace, size_t workspace_bytes,
+                        int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx,
+                        float scale, int bits, int qjl_dim, const float* signs, const float* jl,
+                        const float* angle_lut, vrm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -139,3 +139,58 @@ def dense_attention(q, K, V, scale):
         w = torch.exp(s)
         out[h] = (w[:, None] * V[kh]).sum(0) / w.sum()
     return out
+
+
+def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scale=None):
+    """[B, H, D] float32 attention over TurboQuant pages, as
+    PagedKVCacheManager.compute_attention_turbo (core/paged_attention.py:
+    1259-1418) evaluates it with dense values (sparse_v_ratio 1.0): per kv-head,
+    scores = attention_score(q_group, merged compressed keys) * scale (QJL-
+    corrected, on the rotated query; core/kv_quantizer.py:502-535), softmax,
+    then weights @ decompress(values) (core/kv_quantizer.py:481-500).  Query
+    head h reads kv-head h // (H / KH), the paged decode's mapping (the
+    reference's turbo path uses h % KH, an inconsistency of the reference).
+
+    ``p`` are the compressor's parameters (oracle.turboquant.make_params);
+    ``codes`` holds one layer's raw codes indexed [page, K/V, kv-head, token]:
+    radius fp16, angles uint8 [.., 127] level-major, qjl_signs uint8 [.., 64],
+    qjl_norms fp16.  Pages whose id is < 0 or >= P are skipped.
+    """
+    from . import turboquant as TQ
+
+    B, H, D = query.shape
+    P, _, KH, PS = codes["radius"].shape
+    ratio = H // KH
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    level_dims = [p.padded_dim >> (l + 1) for l in range(p.n_levels)]
+    out = torch.zeros(B, H, D)
+    for b in range(B):
+        ctx = int(context_lens[b])
+        if ctx <= 0:
+            continue
+        n = (ctx + PS - 1) // PS
+        tokens = [(int(page_table[b, t // PS]), t % PS) for t in range(ctx)]
+        tokens = [(pid, s) for pid, s in tokens if 0 <= pid < P]
+        if not tokens:
+            continue
+        pids = torch.tensor([pid for pid, _ in tokens])
+        slots = torch.tensor([s for _, s in tokens])
+
+        def gather(kv, kvh):
+            ang = codes["angles"][pids, kv, kvh, slots]
+            return {
+                "radius": codes["radius"][pids, kv, kvh, slots].reshape(-1, 1),
+                "angles": list(torch.split(ang, level_dims, dim=-1)),
+                "qjl_signs": codes["qjl_signs"][pids, kv, kvh, slots],
+                "qjl_norms": codes["qjl_norms"][pids, kv, kvh, slots].reshape(-1, 1),
+                "shape": (len(tokens), D),
+            }
+
+        for kvh in range(KH):
+            ck, cv = gather(0, kvh), gather(1, kvh)
+            q_group = query[b, kvh * ratio:(kvh + 1) * ratio].float()
+            scores = TQ.attention_score(p, q_group, ck) * scale
+            weights = torch.softmax(scores, dim=-1)
+            out[b, kvh * ratio:(kvh + 1) * ratio] = weights @ TQ.decompress(p, cv)
+    return out

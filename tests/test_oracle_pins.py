@@ -329,3 +329,65 @@ def test_qjl_estimator_correlates():
     est = TQ.qjl_score_correction(p, queries, signs, norms)
     corr = torch.corrcoef(torch.stack([(queries @ keys.t()).flatten(), est.flatten()]))[0, 1]
     assert corr > 0.3
+
+
+def _turbo_codes(p, P, KH, seed):
+    """Raw codes of random K/V pages, indexed [page, K/V, kv-head, token]."""
+    g = torch.Generator().manual_seed(seed)
+    codes = {}
+    parts = []
+    for kv in range(2):
+        x = torch.randn(P * KH * 16, 128, generator=g)
+        parts.append(TQ.compress(p, x, pack=False))
+    codes["radius"] = torch.stack([c["radius"].reshape(P, KH, 16) for c in parts], 1)
+    codes["angles"] = torch.stack([torch.cat(c["angles"], -1).reshape(P, KH, 16, 127) for c in parts], 1)
+    codes["qjl_signs"] = torch.stack([c["qjl_signs"].reshape(P, KH, 16, 64) for c in parts], 1)
+    codes["qjl_norms"] = torch.stack([c["qjl_norms"].reshape(P, KH, 16) for c in parts], 1)
+    return codes
+
+
+def test_turbo_paged_oracle_without_qjl_is_dense_attention_over_decompressed_kv():
+    # with zero residual norms the score is q_rot . k_polar = q . decompress(k)
+    # (the rotation is orthonormal), so the paged turbo attention reduces to
+    # the fp64 closed form over the decompressed keys and values
+    p = TQ.make_params(128, 3, seed=5)
+    P, KH, H = 6, 2, 6
+    codes = _turbo_codes(p, P, KH, 1)
+    codes["qjl_norms"].zero_()
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(2, H, 128, generator=g)
+    table = torch.tensor([[4, 1, 3], [0, 5, -1]], dtype=torch.int32)
+    lens = torch.tensor([40, 20], dtype=torch.int32)
+    out = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.09)
+    for b in range(2):
+        ks, vs = [], []
+        for t in range(int(lens[b])):
+            pid, s = int(table[b, t // 16]), t % 16
+            rows = []
+            for kv in range(2):
+                c = {"radius": codes["radius"][pid, kv, :, s].reshape(-1, 1),
+                     "angles": list(torch.split(codes["angles"][pid, kv, :, s], [64, 32, 16, 8, 4, 2, 1], -1)),
+                     "shape": (KH, 128)}
+                rows.append(TQ.decompress(p, c))
+            ks.append(rows[0])
+            vs.append(rows[1])
+        K = torch.stack(ks, 1).double()
+        V = torch.stack(vs, 1).double()
+        ref = PD.dense_attention(q[b], K, V, 0.09)
+        torch.testing.assert_close(out[b].double(), ref, atol=2e-5, rtol=1e-5)
+
+
+def test_turbo_paged_oracle_relabel_invariance():
+    p = TQ.make_params(128, 4, seed=6)
+    P, KH, H = 5, 1, 3
+    codes = _turbo_codes(p, P, KH, 3)
+    q = torch.randn(1, H, 128, generator=torch.Generator().manual_seed(4))
+    table = torch.tensor([[2, 0, 4]], dtype=torch.int32)
+    lens = torch.tensor([45], dtype=torch.int32)
+    out = PD.paged_attention_decode_turbo(p, q, codes, table, lens)
+    perm = torch.tensor([3, 4, 0, 1, 2])  # new page i holds old page perm[i]
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(P)
+    codes2 = {k: v[perm] for k, v in codes.items()}
+    out2 = PD.paged_attention_decode_turbo(p, q, codes2, inv[table.long()].to(torch.int32), lens)
+    assert torch.equal(out, out2)

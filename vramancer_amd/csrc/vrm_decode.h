@@ -168,6 +168,15 @@ int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int 
 // K_F16, D the head dimension, G the query heads per wavefront (<= 16).
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
+// Paged decode over TurboQuant pages (vrm_decode_tq.hip).
+struct TqDecodeArgs {
+  const float* signs;  // [128] Hadamard signs
+  const float* jl;     // [64][128] JL matrix
+  const float* lut;    // [cos level 0, sin level 0, cos levels >= 1, sin levels >= 1][2^bits]
+  float qjl_coef;      // sqrt(pi / 2) / 64
+};
+hipError_t launch_tq_decode(const DecodeArgs& a, const TqDecodeArgs& tq, int bits, int B, int G, hipStream_t st);
+
 // Largest divisor of the GQA group size that is <= max_tile.
 inline int pick_group_tile(int group, int max_tile) {
   for (int g = max_tile; g >= 1; --g)

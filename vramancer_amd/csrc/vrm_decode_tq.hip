@@ -1,0 +1,441 @@
+// Paged decode over TurboQuant pages (gfx950): the attention of the
+// reference's compute_attention_turbo (core/paged_attention.py:1259-1418,
+// dense values, head h reading kv-head h / (H / KH)) without decompressing
+// anything to memory.
+//
+// For each (sequence, query head), over the tokens of its pages:
+//   score_t = q_rot . k_polar_t + sqrt(pi / 2) / 64 * norm_t * (q_rot JL^T) . (2 s_t - 1)
+//   out     = unrotate( sum_t softmax(scale * score)_t v_polar_t )
+// with q_rot = H(q * signs) / sqrt(128) and k_polar / v_polar the polar
+// reconstructions (rotated domain, from the fp16 radius) of
+// KVCacheCompressor.attention_score / decompress (core/kv_quantizer.py:
+// 481-535).  The inverse rotation is linear, so it is applied once to the
+// weighted sum instead of to every value.
+//
+// Work split as in the other stream kernels (work items of find_item, one
+// wavefront per (kv-head, head chunk), up to 16 query heads in the columns of
+// 16x16 MFMA tiles).  Lane (t, g) = (lane % 16, lane / 16) rebuilds dims
+// 32 g .. 32 g + 31 of token t of a page from quarter g of the token's angle
+// record (vrm_tq_layout.h), multiplying the radius by the {cos, sin} of the
+// bin centres level by level (6 down to 0) as the reference does, so the
+// reconstruction equals the reference's polar decode bit for bit.
+//   S^T   = K Q^T on v_mfma_f32_16x16x32_f16, K and q_rot as hi + lo fp16
+//           (k index (chunk c, group g, element e) <-> dim 32 g + 8 c + e);
+//   QJL   = S P^T: the sign bits as exact +-1 fp16 against q_rot JL^T
+//           (computed on the matrix cores at set-up, hi + lo);
+//   V     rounded to fp16, moved to token-per-lane order by an exact one-hot
+//         MFMA transpose, then O^T += V^T P^T with P as hi + lo.
+#include "vrm_decode.h"
+#include "vrm_tq_layout.h"
+
+#include <math.h>
+
+namespace vrm {
+namespace dec {
+namespace {
+
+namespace T = vrm::tq;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kWaves = 4;             // wavefronts per workgroup (at most)
+constexpr float kLazyRescale = 3.0f;  // as in vrm_decode_mfma.hip
+constexpr float kNoMax = -1.0e30f;
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits); }
+
+// Bin of slot s of a quarter held in w[0 .. BITS - 1] (little-endian bit
+// stream); s is a constant after unrolling, so the indexing folds away.
+template <int BITS>
+__device__ __forceinline__ int slot_bin(const uint32_t* w, int s) {
+  const int bit = s * BITS, dw = bit / 32, sh = bit % 32;
+  const uint32_t mask = (1u << BITS) - 1;
+  if (sh + BITS <= 32) return (int)((w[dw] >> sh) & mask);
+  return (int)(((w[dw] >> sh) | (w[dw + 1] << (32 - sh))) & mask);
+}
+
+// In-register Walsh-Hadamard transform of 128 values, element e in lane e % 64,
+// register e / 64, in the reference's butterfly order.
+__device__ __forceinline__ void fwht128(float (&v)[2], int lane) {
+#pragma unroll
+  for (int h = 1; h < 64; h <<= 1) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float other;
+      switch (h) {
+        case 1: other = xor_shfl<1>(v[k]); break;
+        case 2: other = xor_shfl<2>(v[k]); break;
+        case 4: other = xor_shfl<4>(v[k]); break;
+        case 8: other = xor_shfl<8>(v[k]); break;
+        case 16: other = xor_shfl<16>(v[k]); break;
+        default: other = xor_shfl<32>(v[k]); break;
+      }
+      v[k] = (lane & h) ? other - v[k] : v[k] + other;
+    }
+  }
+  const float a = v[0], b = v[1];
+  v[0] = a + b;
+  v[1] = a - b;
+}
+
+template <int BITS>
+struct TqSlot {
+  uint32_t kq[BITS];  // K angle quarter grp of token col
+  uint32_t vq[BITS];  // V angle quarter grp of token col
+  uint32_t ktop[2];   // last dword of K quarters 0 and 1 + grp / 2 (level 6 / level 5 spares)
+  uint32_t vtop[2];
+  uint32_t krad, vrad, knorm;  // fp16 bits
+  uint2 ksign;                 // 64 QJL sign bits of token col
+  bool ok;                     // page id inside the pool (wave-uniform)
+};
+
+template <int BITS>
+__global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G) {
+  constexpr int NB = 1 << BITS;
+  constexpr int RING = 4;
+  constexpr int SLICE = T::slice_bytes(BITS);
+  constexpr int ABYTES = T::angle_bytes(BITS);
+  constexpr int D = T::kPD;
+
+  __shared__ float2 lut[2][NB];             // {cos, sin} of bin centres: level 0, levels >= 1
+  __shared__ float qbuf[kWaves][16][D + 4];  // per wave: q_rot rows, later the output columns
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int group = a.H / a.KH;
+  const int chunks = group / G;
+  const int unit = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int kvh = unit / chunks;
+  const int h0 = kvh * group + (unit % chunks) * G;
+
+  for (int i = threadIdx.x; i < 2 * NB; i += blockDim.x) {
+    const int tab = i / NB, bin = i % NB;
+    lut[tab][bin] = make_float2(tq.lut[(2 * tab) * NB + bin], tq.lut[(2 * tab + 1) * NB + bin]);
+  }
+  __syncthreads();
+
+  const int item = blockIdx.x;
+  WorkItem wi;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  const int b = wi.b;
+  const int n_pages = wi.n_pages;
+  const int last = n_pages - 1;
+  const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);
+  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
+  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  float(*qb)[D + 4] = qbuf[wave];
+
+  // ---------------- q_rot of this wave's heads (row r: head min(r, G - 1)) ----------------
+  const float root = (float)sqrt(128.0);
+#pragma unroll 1
+  for (int r = 0; r < 16; ++r) {
+    const float* qrow = a.query + ((size_t)b * a.H + h0 + min(r, G - 1)) * D;
+    float v[2] = {qrow[lane] * tq.signs[lane], qrow[lane + 64] * tq.signs[lane + 64]};
+    fwht128(v, lane);
+    qb[r][lane] = v[0] / root;
+    qb[r][lane + 64] = v[1] / root;
+  }
+  wave_sync();
+  // B operand of S^T: lane (col, grp) holds q_rot[col][32 grp + 8 c + e] * qscale
+  v8h QH[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = qb[col][32 * grp + 8 * c + e] * a.qscale;
+      const _Float16 hi = (_Float16)x;
+      QH[c][0][e] = hi;
+      QH[c][1][e] = (_Float16)(x - (float)hi);
+    }
+  // q_proj^T = JL q_rot^T on the matrix cores: tile j (JL rows 16 j ..), result
+  // in lane (col, grp) for rows 16 j + 4 grp + r.  The QJL product uses the
+  // matching k order: chunk c, element e <-> JL row 16 (2 c + e / 4) + 4 grp + e % 4.
+  v8h PJ[2][2];
+  {
+    float pj[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v8h ah, al, bh, bl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = tq.jl[(size_t)(16 * j + col) * D + 32 * c + 8 * grp + e];
+          ah[e] = (_Float16)x;
+          al[e] = (_Float16)(x - (float)ah[e]);
+          const float y = qb[col][32 * c + 8 * grp + e];
+          bh[e] = (_Float16)y;
+          bl[e] = (_Float16)(y - (float)bh[e]);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pj[j][r] = acc[r];
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = pj[2 * c + e / 4][e % 4];
+        const _Float16 hi = (_Float16)x;
+        PJ[c][0][e] = hi;
+        PJ[c][1][e] = (_Float16)(x - (float)hi);
+      }
+  }
+  // one-hot operands of the V transpose: E_h[8 grp + e][col] = (8 grp + e == 16 h + col)
+  v8h onehot[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      onehot[h][e] = (grp == 2 * h + (col >> 3) && e == (col & 7)) ? (_Float16)1.f : (_Float16)0.f;
+  const float qjl_scale = a.qscale * tq.qjl_coef;
+
+  // ---------------- streaming state ----------------
+  float m_run = kNoMax, l_run = 0.f;
+  // O^T block 2 c + h: row 4 grp + r <-> dim 32 (2 h + (4 grp + r) / 8) + 8 c + (4 grp + r) % 8
+  v4f acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const size_t kv_stride = (size_t)a.KH * SLICE;
+  const size_t page_stride = kv_stride * 2 * a.L;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * SLICE;
+  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+  const int top1 = (1 + (grp >> 1)) * BITS + BITS - 1;  // dword of slot 31 of quarter 1 + grp / 2
+
+  auto load_page = [&](TqSlot<BITS>& s, int pid) {
+    s.ok = page_ok(pid);
+    const uint8_t* ks = layer_base + (size_t)(s.ok ? pid : 0) * page_stride;
+    const uint8_t* vs = ks + kv_stride;
+    const uint32_t* krec = reinterpret_cast<const uint32_t*>(ks + col * ABYTES);
+    const uint32_t* vrec = reinterpret_cast<const uint32_t*>(vs + col * ABYTES);
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) {
+      s.kq[i] = krec[grp * BITS + i];
+      s.vq[i] = vrec[grp * BITS + i];
+    }
+    s.ktop[0] = krec[BITS - 1];
+    s.ktop[1] = krec[top1];
+    s.vtop[0] = vrec[BITS - 1];
+    s.vtop[1] = vrec[top1];
+    s.krad = reinterpret_cast<const uint16_t*>(ks + T::radius_offset(BITS))[col];
+    s.vrad = reinterpret_cast<const uint16_t*>(vs + T::radius_offset(BITS))[col];
+    s.knorm = reinterpret_cast<const uint16_t*>(ks + T::norms_offset(BITS))[col];
+    s.ksign = reinterpret_cast<const uint2*>(ks + T::signs_offset(BITS))[col];
+  };
+
+  // dims 32 grp .. 32 grp + 31 of one token, in the reference's order of products
+  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, uint32_t rad_bits, float (&cur)[32]) {
+    constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
+    const float2 t6 = lut[1][(top0 >> sh31) & (NB - 1)];
+    const float2 t5 = lut[1][(topq >> sh31) & (NB - 1)];
+    float p = f16_to_f32(rad_bits);
+    p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
+    p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
+    cur[0] = p;
+#pragma unroll
+    for (int lev = 4; lev >= 0; --lev) {
+      const int n = 1 << (4 - lev);  // nodes of this level in the quarter; slots n - 1 ..
+#pragma unroll
+      for (int i = n - 1; i >= 0; --i) {  // descending: each source is read before it is overwritten
+        const float2 cs = lut[lev == 0 ? 0 : 1][slot_bin<BITS>(q, n - 1 + i)];
+        const float x = cur[i];
+        cur[2 * i] = x * cs.x;
+        cur[2 * i + 1] = x * cs.y;
+      }
+    }
+  };
+
+  // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi.
+  auto page_scores = [&](const TqSlot<BITS>& s, int pi, float* sc) {
+    float kv[32];
+    rebuild(s.kq, s.ktop[0], s.ktop[1], s.krad, kv);
+    v4f c4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      v8h kh, kl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = kv[8 * c + e];
+        kh[e] = (_Float16)x;
+        kl[e] = (_Float16)(x - (float)kh[e]);
+      }
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][0], c4, 0, 0, 0);
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][1], c4, 0, 0, 0);
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, QH[c][0], c4, 0, 0, 0);
+    }
+    v4f cq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      v8h sg;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = 16 * (2 * c + e / 4) + 4 * grp + (e % 4);
+        const uint32_t bit = (j < 32 ? s.ksign.x >> j : s.ksign.y >> (j - 32)) & 1u;
+        sg[e] = bit ? (_Float16)1.f : (_Float16)-1.f;
+      }
+      cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][0], cq, 0, 0, 0);
+      cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][1], cq, 0, 0, 0);
+    }
+    const float nrm = f16_to_f32(s.knorm);  // norm of token col; row r needs token 4 grp + r
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * grp + r;
+      const float nt = __int_as_float(__builtin_amdgcn_ds_bpermute(t << 2, __float_as_int(nrm)));  // lane t holds token t
+      sc[r] = (s.ok && pi * kPS + t < tok_end) ? c4[r] + qjl_scale * nt * cq[r] : -INFINITY;
+    }
+  };
+
+  // V of 16 dims (block 2 c + h) for this lane's 4 tokens of one page, exact
+  // fp16 values in token-per-lane order; absent pages and tokens past the
+  // context read as 0 whatever the page holds.
+  auto v_block = [&](const v8h& vop, int h, int pi, bool ok, float* out4) {
+    const v4f t = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, onehot[h], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out4[r] = (ok && pi * kPS + grp * 4 + r < tok_end) ? t[r] : 0.f;
+  };
+  auto v_operand = [&](const TqSlot<BITS>& s, v8h (&vop)[4]) {
+    float vv[32];
+    rebuild(s.vq, s.vtop[0], s.vtop[1], s.vrad, vv);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vop[c][e] = (_Float16)vv[8 * c + e];
+  };
+
+  auto process_pair = [&](const TqSlot<BITS>& s0, const TqSlot<BITS>& s1, int pi, bool has1) {
+    float sc[8];
+    page_scores(s0, pi, sc);
+    if (has1) {
+      page_scores(s1, pi + 1, sc + 4);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
+    }
+    float pm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
+    pm = fmaxf(pm, xor_shfl<16>(pm));
+    pm = fmaxf(pm, xor_shfl<32>(pm));
+    if (pm > m_run + kLazyRescale) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      m_run = pm;
+    }
+    v8h Bh, Bl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sc[e] - m_run);
+      l_run += p;
+      const _Float16 hi = (_Float16)p;
+      Bh[e] = hi;
+      Bl[e] = (_Float16)(p - (float)hi);
+    }
+    v8h vop0[4], vop1[4];
+    v_operand(s0, vop0);
+    if (has1) v_operand(s1, vop1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float t[8];
+        v_block(vop0[c], h, pi, s0.ok, t);
+        if (has1) {
+          v_block(vop1[c], h, pi + 1, s1.ok, t + 4);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t[4 + r] = 0.f;
+        }
+        v8h A;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) A[e] = (_Float16)t[e];  // exact: fp16 values
+        acc[2 * c + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bh, acc[2 * c + h], 0, 0, 0);
+        acc[2 * c + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bl, acc[2 * c + h], 0, 0, 0);
+      }
+  };
+
+  // ---------------- stream the partition ----------------
+  {
+    TqSlot<BITS> ring[RING];
+    const int ids0 = ids_at(0);
+    int ids_next = ids_at(RING);
+#pragma unroll
+    for (int u = 0; u < RING; ++u) load_page(ring[u], __builtin_amdgcn_readlane(ids0, u));
+    for (int base = 0; base < n_pages; base += RING) {
+      const int ids_ahead = ids_at(base + 2 * RING);
+#pragma unroll
+      for (int u = 0; u < RING; u += 2) {
+        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
+        load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
+        load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
+      }
+      ids_next = ids_ahead;
+    }
+  }
+
+  // ---------------- partition result: columns to natural dims, unrotate ----------------
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * grp + r;
+        qb[col][32 * (2 * h + (row >> 3)) + 8 * c + (row & 7)] = acc[2 * c + h][r];
+      }
+  float l_tot = l_run + xor_shfl<16>(l_run);
+  l_tot += xor_shfl<32>(l_tot);
+  wave_sync();
+  const float s_lo = tq.signs[lane], s_hi = tq.signs[lane + 64];
+  for (int hh = 0; hh < G; ++hh) {
+    float v[2] = {qb[hh][lane], qb[hh][lane + 64]};
+    fwht128(v, lane);
+    float* out = a.part_acc + ((size_t)item * a.H + h0 + hh) * D;
+    out[lane] = v[0] / root * s_lo;
+    out[lane + 64] = v[1] / root * s_hi;
+  }
+  if (col < G && grp == 0) {
+    float* ml = a.part_ml + ((size_t)item * a.H + h0 + col) * 2;
+    ml[0] = l_tot > 0.f ? m_run : -INFINITY;
+    ml[1] = l_tot;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int G, hipStream_t st) {
+  const int units = a0.KH * ((a0.H / a0.KH) / G);
+  int W = kWaves;
+  while (units % W) --W;
+  DecodeArgs a = a0;
+  const void* fn = bits == 2   ? reinterpret_cast<const void*>(&decode_tq_kernel<2>)
+                   : bits == 3 ? reinterpret_cast<const void*>(&decode_tq_kernel<3>)
+                               : reinterpret_cast<const void*>(&decode_tq_kernel<4>);
+  a.target = items_target(fn, W, 0, units);
+  dim3 grid(B + 2 * a.target, units / W, 1);
+  dim3 block(64 * W);
+  switch (bits) {
+    case 2: hipLaunchKernelGGL(decode_tq_kernel<2>, grid, block, 0, st, a, tq, G); break;
+    case 3: hipLaunchKernelGGL(decode_tq_kernel<3>, grid, block, 0, st, a, tq, G); break;
+    default: hipLaunchKernelGGL(decode_tq_kernel<4>, grid, block, 0, st, a, tq, G); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace dec
+}  // namespace vrm

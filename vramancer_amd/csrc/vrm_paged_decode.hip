@@ -576,6 +576,35 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   return VRM_OK;
 }
 
+// Partition pass over TurboQuant pages, then the shared merge.
+int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, float* out, void* workspace, size_t workspace_bytes,
+                  int B, int D, float scale, hipStream_t st) {
+  const int G = pick_group_tile(a.H / a.KH, 16);
+  a.B = B;
+  const long cap = items_capacity(B, a.KH);
+  const size_t need = header_bytes(B) + (size_t)cap * a.H * (D + 2) * sizeof(float);
+  if (!workspace || workspace_bytes < need) {
+    set_error("vrm_paged_decode_tq: workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+    return VRM_ERR_WORKSPACE;
+  }
+  a.header = reinterpret_cast<int32_t*>(workspace);
+  a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
+  a.part_ml = a.part_acc + (size_t)cap * a.H * D;
+  a.qscale = scale * kLog2e;
+  hipError_t e = launch_tq_decode(a, tq, bits, B, G, st);
+  if (e != hipSuccess) {
+    set_error("vrm_paged_decode_tq: partition kernel launch failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  e = launch_reduce(a, out, B, D, st);
+  if (e != hipSuccess) {
+    set_error("vrm_paged_decode_tq: merge kernel launch failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  clear_error();
+  return VRM_OK;
+}
+
 int kind_of(int kv_dtype) {
   switch (kv_dtype) {
     case VRM_KV_F32: return K_F32;
@@ -721,4 +750,41 @@ extern "C" int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4
   a.layer = layer_idx;
   return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
                     kBoth);
+}
+
+extern "C" int vrm_paged_decode_tq(const float* query, const uint8_t* tq_pool, const int32_t* page_table,
+                                   const int32_t* context_lens, float* out, void* workspace, size_t workspace_bytes,
+                                   int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx,
+                                   float scale, int bits, int qjl_dim, const float* signs, const float* jl,
+                                   const float* angle_lut, vrm_stream_t stream) {
+  int rc = check_common(query, tq_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  if (D != 128 || qjl_dim != 64) {
+    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128 and qjl_dim 64 (got %d, %d)", D,
+              qjl_dim);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (bits < 2 || bits > 4) {
+    set_error("vrm_paged_decode_tq: bits_per_angle %d unsupported (2, 3, 4)", bits);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (!signs || !jl || !angle_lut) {
+    set_error("vrm_paged_decode_tq: null compressor buffer");
+    return VRM_ERR_ARG;
+  }
+  DecodeArgs a{};
+  a.query = query;
+  a.pool = tq_pool;
+  a.page_table = page_table;
+  a.ctx_lens = context_lens;
+  a.H = H;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.max_pp = max_pp;
+  a.layer = layer_idx;
+  TqDecodeArgs tq{signs, jl, angle_lut, (float)(1.2533141373155003 / 64.0)};
+  return run_tq_decode(a, tq, bits, out, workspace, workspace_bytes, B, D, scale,
+                       reinterpret_cast<hipStream_t>(stream));
 }

@@ -1,0 +1,80 @@
+// Layout of a TurboQuant KV page of this library (head_dim 128: padded_dim
+// 128, 7 polar levels, 127 angles, 64 QJL signs).
+//
+// The pool keeps the reference's addressing, tq_pool[P][L][2][KH][slice],
+// one slice of kTqSliceBytes(bits) bytes per (page, layer, K/V, kv-head) with
+// the 16 tokens of the page:
+//   angles  [16][16 * bits]   bytes 0 ..            (token t at t * 16 * bits)
+//   signs   [16][8]           QJL sign bits (K only; bit j = residual . jl_j > 0)
+//   radius  [16]              fp16 final polar radius
+//   norms   [16]              fp16 residual norm (K only)
+// V slices use the angles and radius fields only (same offsets).
+//
+// Angle record of one token: four quarters of 4 * bits bytes.  Quarter g holds
+// the 31 angles of the subtree over dims 32 g .. 32 g + 31 plus one spare slot
+// that carries a top-level angle, so that a decode lane owning those dims
+// reads one aligned 4 * bits-byte word:
+//   slot 0            level 4, angle g
+//   slots 1 .. 2      level 3, angles 2 g .. 2 g + 1
+//   slots 3 .. 6      level 2, angles 4 g .. 4 g + 3
+//   slots 7 .. 14     level 1, angles 8 g .. 8 g + 7
+//   slots 15 .. 30    level 0, angles 16 g .. 16 g + 15
+//   slot 31           quarter 0: level 6 angle; quarter 1: level 5 angle 0;
+//                     quarter 2: level 5 angle 1; quarter 3: 0
+// Slot s occupies bits [s * bits, (s + 1) * bits) of its quarter, bit i of a
+// quarter being bit i % 8 of its byte i / 8 (little-endian).  The record has
+// exactly the 127 * bits bits of the reference's packed angles (plus bits
+// padding bits).  Angle levels and indices are those of the reference's
+// level-major bins (core/kv_quantizer.py:262-287): level l holds 64 >> l
+// angles and angle i of level l pairs elements 2 i, 2 i + 1 of level l - 1.
+#pragma once
+#include <stdint.h>
+
+namespace vrm {
+namespace tq {
+
+constexpr int kPD = 128;      // padded head dimension
+constexpr int kLevels = 7;    // log2(kPD)
+constexpr int kAngles = 127;  // kPD - 1
+constexpr int kQjl = 64;      // QJL projection rows
+constexpr int kTokens = 16;   // tokens per page
+
+__host__ __device__ constexpr int angle_bytes(int bits) { return 16 * bits; }        // per token
+__host__ __device__ constexpr int signs_offset(int bits) { return kTokens * angle_bytes(bits); }
+__host__ __device__ constexpr int radius_offset(int bits) { return signs_offset(bits) + kTokens * 8; }
+__host__ __device__ constexpr int norms_offset(int bits) { return radius_offset(bits) + kTokens * 2; }
+__host__ __device__ constexpr int slice_bytes(int bits) { return norms_offset(bits) + kTokens * 2; }
+
+// Offset of level l in the reference's level-major bin array: sum_{i<l} 64 >> i.
+__host__ __device__ constexpr int level_offset(int l) { return kPD - (kPD >> l); }
+
+// (quarter, slot) of angle i of level l.
+__host__ __device__ inline void slot_of(int l, int i, int& quarter, int& slot) {
+  if (l <= 4) {
+    const int per = 1 << (4 - l);  // angles of level l per quarter
+    quarter = i / per;
+    slot = (per - 1) + (i % per);
+  } else if (l == 5) {
+    quarter = 1 + i;
+    slot = 31;
+  } else {
+    quarter = 0;
+    slot = 31;
+  }
+}
+
+// Level-major bin index (reference order) of slot s of quarter g, or -1 for
+// the unused spare of quarter 3.
+__host__ __device__ inline int bin_index_of(int g, int s) {
+  if (s == 31) return g == 0 ? level_offset(6) : (g <= 2 ? level_offset(5) + (g - 1) : -1);
+  int l = 4, first = 0;
+  while (s >= first + (1 << (4 - l))) {
+    first += 1 << (4 - l);
+    --l;
+  }
+  const int per = 1 << (4 - l);
+  return level_offset(l) + g * per + (s - first);
+}
+
+}  // namespace tq
+}  // namespace vrm

@@ -20,6 +20,7 @@
 // One 64-lane wavefront per row; the row lives in LDS between stages.
 #include "vrm_common.h"
 #include "vrm_fdlibm_atan2f.h"
+#include "vrm_tq_layout.h"
 
 #include <math.h>
 
@@ -125,44 +126,47 @@ __device__ __forceinline__ void polar_decode(float radius, const uint8_t* bins, 
   }
 }
 
+// LDS working set of one row.
+template <int PD>
+struct RowLds {
+  float rot[PD];  // rotated row, then the residual
+  float bufA[PD / 2];
+  float bufB[PD / 2];
+  float recon[PD];
+  uint8_t bins[PD];
+  float norm_acc[8];
+};
+
+// Rotation and polar encoding of one row (source element e at src[e] for
+// e < head_dim, zero padding above): leaves the level-major bins in w.bins,
+// the rotated row in v (element e in lane e % 64, register e / 64) and in
+// w.rot, and returns the fp32 final radius.
 template <int SRC, int PD>
-__global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
+__device__ __forceinline__ float encode_row(const void* src, size_t first, int head_dim, const float* signs, int bits,
+                                            float (&v)[PD / 64], RowLds<PD>& w, int lane) {
   constexpr int PER = PD / 64;
   constexpr int NL = __builtin_ctz(PD);
-  __shared__ float rot[PD];
-  __shared__ float bufA[PD / 2];
-  __shared__ float bufB[PD / 2];
-  __shared__ float recon[PD];
-  __shared__ uint8_t bins[PD];
-  __shared__ float norm_acc[8];
-
-  const int lane = threadIdx.x;
-  const int row = blockIdx.x;
-  const int nb = 1 << a.bits;
-
-  // ---- rotate ----
-  float v[PER];
+  const int nb = 1 << bits;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = k * 64 + lane;
-    const float x = e < a.head_dim ? load_row<SRC>(a.kv, (size_t)row * a.head_dim + e) : 0.f;
-    v[k] = __fmul_rn(x, a.signs[e]);
+    const float x = e < head_dim ? load_row<SRC>(src, first + e) : 0.f;
+    v[k] = __fmul_rn(x, signs[e]);
   }
   fwht<PD>(v, lane);
   const float root = (float)sqrt((double)PD);
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     v[k] = __fdiv_rn(v[k], root);
-    rot[k * 64 + lane] = v[k];
+    w.rot[k * 64 + lane] = v[k];
   }
   __syncthreads();
 
-  // ---- polar encode + bin ----
   const float lo0 = (float)-3.141592653589793, range0 = (float)6.283185307179586;
   const float range1 = (float)1.5707963267948966;
   const float nbf = (float)nb;
-  const float* cur = rot;
-  float* nxt = bufA;
+  const float* cur = w.rot;
+  float* nxt = w.bufA;
   for (int level = 0; level < NL; ++level) {
     const int count = PD >> (level + 1);
     const int off = PD - (PD >> level);
@@ -173,46 +177,190 @@ __global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
       float nrm = level == 0 ? __fdiv_rn(__fsub_rn(th, lo0), range0) : __fdiv_rn(th, range1);
       int idx = (int)__fmul_rn(nrm, nbf);  // truncation toward zero, as .long()
       idx = min(max(idx, 0), nb - 1);
-      bins[off + i] = (uint8_t)idx;
-      a.angles[(size_t)row * (PD - 1) + off + i] = (uint8_t)idx;
+      w.bins[off + i] = (uint8_t)idx;
       nxt[i] = r;
     }
     __syncthreads();
     cur = nxt;
-    nxt = (nxt == bufA) ? bufB : bufA;
+    nxt = (nxt == w.bufA) ? w.bufB : w.bufA;
   }
-  const float radius = cur[0];
-  if (lane == 0) a.radius[row] = f32_to_f16_bits(radius);
+  return cur[0];
+}
 
-  // ---- reconstruct from the fp32 radius, residual ----
-  polar_decode<PD>(radius, bins, a.lut, nb, bufA, bufB, recon, lane);
+// Residual against the reconstruction from the fp32 radius, its QJL signs
+// (float64 dot products; sign(j) is handed to put_sign) and the residual norm
+// (eight interleaved fused accumulators summed in order, as PyTorch's CPU
+// 2-norm reduces a 128-float row).  Returns the norm.
+template <int PD, typename PutSign>
+__device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius, const float* lut, int bits,
+                                         const float* jl, int qjl_dim, RowLds<PD>& w, int lane, PutSign put_sign) {
+  constexpr int PER = PD / 64;
+  polar_decode<PD>(radius, w.bins, lut, 1 << bits, w.bufA, w.bufB, w.recon, lane);
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = k * 64 + lane;
-    rot[e] = __fsub_rn(v[k], recon[e]);  // rot now holds the residual
+    w.rot[e] = __fsub_rn(v[k], w.recon[e]);  // rot now holds the residual
   }
   __syncthreads();
-
-  // ---- QJL signs (float64 dot) ----
-  for (int j = lane; j < a.qjl_dim; j += 64) {
-    const float* jr = a.jl + (size_t)j * PD;
+  for (int j = lane; j < qjl_dim; j += 64) {
+    const float* jr = jl + (size_t)j * PD;
     double s = 0.0;
-    for (int e = 0; e < PD; ++e) s = fma((double)rot[e], (double)jr[e], s);
-    a.qjl_signs[(size_t)row * a.qjl_dim + j] = s > 0.0 ? 1 : 0;
+    for (int e = 0; e < PD; ++e) s = fma((double)w.rot[e], (double)jr[e], s);
+    put_sign(j, s > 0.0);
   }
-  // ---- residual norm: 8 interleaved fused accumulators, summed in order ----
   if (lane < 8) {
     float acc = 0.f;
-    for (int e = lane; e < PD; e += 8) acc = fmaf(rot[e], rot[e], acc);
-    norm_acc[lane] = acc;
+    for (int e = lane; e < PD; e += 8) acc = fmaf(w.rot[e], w.rot[e], acc);
+    w.norm_acc[lane] = acc;
   }
   __syncthreads();
-  if (lane == 0) {
-    float s = norm_acc[0];
+  float s = w.norm_acc[0];
 #pragma unroll
-    for (int k = 1; k < 8; ++k) s = __fadd_rn(s, norm_acc[k]);
-    a.qjl_norms[row] = f32_to_f16_bits(sqrt_rn(s));
+  for (int k = 1; k < 8; ++k) s = __fadd_rn(s, w.norm_acc[k]);
+  return sqrt_rn(s);
+}
+
+template <int SRC, int PD>
+__global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
+  __shared__ RowLds<PD> w;
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
+  float v[PD / 64];
+  const float radius = encode_row<SRC, PD>(a.kv, (size_t)row * a.head_dim, a.head_dim, a.signs, a.bits, v, w, lane);
+  for (int i = lane; i < PD - 1; i += 64) a.angles[(size_t)row * (PD - 1) + i] = w.bins[i];
+  if (lane == 0) a.radius[row] = f32_to_f16_bits(radius);
+  const float norm = qjl_row<PD>(v, radius, a.lut, a.bits, a.jl, a.qjl_dim, w, lane, [&](int j, bool pos) {
+    a.qjl_signs[(size_t)row * a.qjl_dim + j] = pos ? 1 : 0;
+  });
+  if (lane == 0) a.qjl_norms[row] = f32_to_f16_bits(norm);
+}
+
+// ---------------------------------------------------------------------------
+// Writes TurboQuant codes straight into the pages of a TurboQuant pool
+// (layout in vrm_tq_layout.h).  One wavefront per (row, K/V): the codes are
+// those of tq_compress_kernel; V rows skip the QJL stage, whose output the
+// attention never reads for values.
+// ---------------------------------------------------------------------------
+struct TqPoolArgs {
+  const void* key;
+  const void* value;
+  const int32_t* page_ids;
+  const int32_t* slots;    // append: slot of each token; pages: nullptr
+  const int32_t* n_valid;  // pages: valid tokens of each page; append: nullptr
+  uint8_t* pool;
+  int KH, L, P, layer, bits, head_dim;
+  const float* signs;
+  const float* jl;
+  const float* lut;
+};
+
+template <int SRC>
+__global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
+  namespace L = vrm::tq;
+  constexpr int PD = L::kPD;
+  __shared__ RowLds<PD> w;
+  __shared__ uint32_t sign_bits[L::kQjl / 32];
+  const int lane = threadIdx.x;
+  const int kv = blockIdx.y;
+  // append: x = n * KH + h (token n); pages: x = (np * KH + h) * 16 + t
+  int n, h, t;
+  size_t src_first;
+  bool live = true;
+  if (a.slots) {
+    n = blockIdx.x / a.KH;
+    h = blockIdx.x % a.KH;
+    t = a.slots[n];
+    src_first = (size_t)blockIdx.x * a.head_dim;
+  } else {
+    t = blockIdx.x % L::kTokens;
+    h = (blockIdx.x / L::kTokens) % a.KH;
+    n = blockIdx.x / (L::kTokens * a.KH);
+    live = t < a.n_valid[n];
+    src_first = (size_t)blockIdx.x * a.head_dim;
   }
+  const int pid = a.page_ids[n];
+  if (pid < 0 || pid >= a.P || t < 0 || t >= L::kTokens) return;  // rows aimed outside the pool are dropped
+  uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::slice_bytes(a.bits);
+  const int abytes = L::angle_bytes(a.bits);
+  uint8_t* rec = slice + (size_t)t * abytes;
+  uint16_t* radius_out = reinterpret_cast<uint16_t*>(slice + L::radius_offset(a.bits)) + t;
+  if (!live) {  // slots past the page's valid tokens hold zero records
+    for (int i = lane; i < abytes; i += 64) rec[i] = 0;
+    if (lane == 0) *radius_out = 0;
+    if (kv == 0) {
+      if (lane < 8) slice[L::signs_offset(a.bits) + t * 8 + lane] = 0;
+      if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(a.bits))[t] = 0;
+    }
+    return;
+  }
+  float v[PD / 64];
+  const void* src = kv ? a.value : a.key;
+  const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, a.bits, v, w, lane);
+  // angle record: dword k of quarter g covers quarter bits [32 k, 32 k + 32)
+  const int qdw = a.bits;  // dwords per quarter (4 * bits bytes)
+  if (lane < 4 * qdw) {
+    const int g = lane / qdw, k = lane % qdw;
+    uint32_t word = 0;
+    for (int slot = (32 * k) / a.bits; slot < 32 && slot * a.bits < 32 * k + 32; ++slot) {
+      const int bi = L::bin_index_of(g, slot);
+      if (bi < 0) continue;
+      const int shift = slot * a.bits - 32 * k;  // may be negative for a slot straddling the dword start
+      const uint32_t val = w.bins[bi];
+      word |= shift >= 0 ? (val << shift) : (val >> -shift);
+    }
+    reinterpret_cast<uint32_t*>(rec)[lane] = word;
+  }
+  if (lane == 0) *radius_out = f32_to_f16_bits(radius);
+  if (kv == 1) return;
+  if (lane < L::kQjl / 32) sign_bits[lane] = 0;
+  __syncthreads();
+  const float norm = qjl_row<PD>(v, radius, a.lut, a.bits, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
+    if (pos) atomicOr(&sign_bits[j >> 5], 1u << (j & 31));
+  });
+  __syncthreads();
+  if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(a.bits) + t * 8)[lane] = sign_bits[lane];
+  if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(a.bits))[t] = f32_to_f16_bits(norm);
+}
+
+// Reads a TurboQuant pool back into the reference's raw code format, for
+// inspection and for the codec tests: for page n, kv, head h, token t (row
+// ((n * 2 + kv) * KH + h) * 16 + t), radius, level-major bins, sign bytes and
+// norm.  V rows get zero signs and norms.
+__global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, const int32_t* page_ids, int KH,
+                                                          int L_, int P, int layer, int bits, uint16_t* radius,
+                                                          uint8_t* angles, uint8_t* qjl_signs, uint16_t* norms) {
+  namespace L = vrm::tq;
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
+  const int t = row % L::kTokens;
+  const int h = (row / L::kTokens) % KH;
+  const int kv = (row / (L::kTokens * KH)) % 2;
+  const int n = row / (L::kTokens * KH * 2);
+  const int pid = page_ids[n];
+  if (pid < 0 || pid >= P) {  // absent page: zero codes
+    for (int i = lane; i < L::kAngles; i += 64) angles[(size_t)row * L::kAngles + i] = 0;
+    if (lane < L::kQjl) qjl_signs[(size_t)row * L::kQjl + lane] = 0;
+    if (lane == 0) radius[row] = norms[row] = 0;
+    return;
+  }
+  const uint8_t* slice = pool + ((((size_t)pid * L_ + layer) * 2 + kv) * KH + h) * L::slice_bytes(bits);
+  const uint8_t* rec = slice + (size_t)t * L::angle_bytes(bits);
+  for (int i = lane; i < L::kAngles; i += 64) {
+    // find (quarter, slot) of level-major bin i
+    int l = 0;
+    while (i >= L::level_offset(l + 1)) ++l;
+    int g, s;
+    L::slot_of(l, i - L::level_offset(l), g, s);
+    const int bit = g * 32 * bits + s * bits;
+    uint32_t x = rec[bit / 8] | ((bit / 8 + 1 < L::angle_bytes(bits)) ? (uint32_t)rec[bit / 8 + 1] << 8 : 0u);
+    angles[(size_t)row * L::kAngles + i] = (uint8_t)((x >> (bit % 8)) & ((1u << bits) - 1));
+  }
+  if (lane == 0) radius[row] = reinterpret_cast<const uint16_t*>(slice + L::radius_offset(bits))[t];
+  if (lane < L::kQjl) {
+    const uint8_t byte = kv == 0 ? slice[L::signs_offset(bits) + t * 8 + lane / 8] : 0;
+    qjl_signs[(size_t)row * L::kQjl + lane] = (byte >> (lane % 8)) & 1;
+  }
+  if (lane == 0) norms[row] = kv == 0 ? reinterpret_cast<const uint16_t*>(slice + L::norms_offset(bits))[t] : 0;
 }
 
 template <int PD>
@@ -350,5 +498,133 @@ extern "C" int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* 
     case 128: hipLaunchKernelGGL(tq_decompress_kernel<128>, dim3(N), dim3(64), 0, st, a, rotated); break;
     default: hipLaunchKernelGGL(tq_decompress_kernel<256>, dim3(N), dim3(64), 0, st, a, rotated); break;
   }
+  return launch_status(who);
+}
+
+namespace {
+int check_tq_pool(int KH, int D, int PS, int L, int P, int layer_idx, int bits, int qjl_dim, const char* who) {
+  if (KH <= 0 || L <= 0 || P <= 0 || layer_idx < 0 || layer_idx >= L) {
+    set_error("%s: bad sizes (KH=%d L=%d P=%d layer=%d)", who, KH, L, P, layer_idx);
+    return VRM_ERR_ARG;
+  }
+  if (D != tq::kPD || PS != tq::kTokens || qjl_dim != tq::kQjl) {
+    set_error("%s: TurboQuant pages are built for head_dim 128, page 16, qjl_dim 64 (got %d, %d, %d)", who, D, PS,
+              qjl_dim);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (bits < 2 || bits > 4) {
+    set_error("%s: bits_per_angle %d unsupported (2, 3, 4)", who, bits);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  return VRM_OK;
+}
+
+int tq_pool_write(const void* key, const void* value, int src_dtype, const int32_t* page_ids, const int32_t* slots,
+                  const int32_t* n_valid, int rows, uint8_t* tq_pool, int KH, int D, int PS, int L, int P,
+                  int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl, const float* angle_lut,
+                  vrm_stream_t stream, const char* who) {
+  int rc = check_tq_pool(KH, D, PS, L, P, layer_idx, bits, qjl_dim, who);
+  if (rc) return rc;
+  if (rows < 0) {
+    set_error("%s: negative count", who);
+    return VRM_ERR_ARG;
+  }
+  if (src_dtype != VRM_SRC_F32 && src_dtype != VRM_SRC_F16 && src_dtype != VRM_SRC_BF16) {
+    set_error("%s: unknown source dtype %d", who, src_dtype);
+    return VRM_ERR_ARG;
+  }
+  if (rows == 0) return VRM_OK;
+  if (!key || !value || !page_ids || !tq_pool || !signs || !jl || !angle_lut || (!slots && !n_valid)) {
+    set_error("%s: null pointer argument", who);
+    return VRM_ERR_ARG;
+  }
+  if (rows > 0x7fffffff / 2) {
+    set_error("%s: too many rows", who);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  TqPoolArgs a{};
+  a.key = key;
+  a.value = value;
+  a.page_ids = page_ids;
+  a.slots = slots;
+  a.n_valid = n_valid;
+  a.pool = tq_pool;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.layer = layer_idx;
+  a.bits = bits;
+  a.head_dim = D;
+  a.signs = signs;
+  a.jl = jl;
+  a.lut = angle_lut;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(rows, 2);
+  switch (src_dtype) {
+    case VRM_SRC_F32: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_F32>, grid, dim3(64), 0, st, a); break;
+    case VRM_SRC_F16: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_F16>, grid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_BF16>, grid, dim3(64), 0, st, a); break;
+  }
+  return launch_status(who);
+}
+}  // namespace
+
+extern "C" size_t vrm_tq_slice_bytes(int head_dim, int bits, int qjl_dim) {
+  if (head_dim != tq::kPD || qjl_dim != tq::kQjl || bits < 2 || bits > 4) return 0;
+  return (size_t)tq::slice_bytes(bits);
+}
+
+extern "C" int vrm_tq_quant_append(const void* key, const void* value, int src_dtype, const int32_t* page_ids,
+                                   const int32_t* slots, int N, uint8_t* tq_pool, int KH, int D, int PS, int L,
+                                   int P, int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl,
+                                   const float* angle_lut, vrm_stream_t stream) {
+  const char* who = "vrm_tq_quant_append";
+  if (N < 0 || KH <= 0 || (long)N * KH > 0x3fffffff) {
+    set_error("%s: bad sizes (N=%d KH=%d)", who, N, KH);
+    return VRM_ERR_ARG;
+  }
+  if (N > 0 && !slots) {
+    set_error("%s: null slots", who);
+    return VRM_ERR_ARG;
+  }
+  return tq_pool_write(key, value, src_dtype, page_ids, slots, nullptr, N * KH, tq_pool, KH, D, PS, L, P, layer_idx,
+                       bits, qjl_dim, signs, jl, angle_lut, stream, who);
+}
+
+extern "C" int vrm_tq_quant_pages(const void* key, const void* value, int src_dtype, const int32_t* page_ids,
+                                  const int32_t* n_valid, int NP, uint8_t* tq_pool, int KH, int D, int PS, int L,
+                                  int P, int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl,
+                                  const float* angle_lut, vrm_stream_t stream) {
+  const char* who = "vrm_tq_quant_pages";
+  if (NP < 0 || KH <= 0 || (long)NP * KH * tq::kTokens > 0x3fffffff) {
+    set_error("%s: bad sizes (NP=%d KH=%d)", who, NP, KH);
+    return VRM_ERR_ARG;
+  }
+  if (NP > 0 && !n_valid) {
+    set_error("%s: null n_valid", who);
+    return VRM_ERR_ARG;
+  }
+  return tq_pool_write(key, value, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D, PS,
+                       L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who);
+}
+
+extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids, int NP, int KH, int D, int PS,
+                                 int L, int P, int layer_idx, int bits, int qjl_dim, uint16_t* radius,
+                                 uint8_t* angles, uint8_t* qjl_signs, uint16_t* qjl_norms, vrm_stream_t stream) {
+  const char* who = "vrm_tq_read_pages";
+  int rc = check_tq_pool(KH, D, PS, L, P, layer_idx, bits, qjl_dim, who);
+  if (rc) return rc;
+  if (NP < 0 || (long)NP * 2 * KH * tq::kTokens > 0x7fffffff) {
+    set_error("%s: bad count %d", who, NP);
+    return VRM_ERR_ARG;
+  }
+  if (NP == 0) return VRM_OK;
+  if (!tq_pool || !page_ids || !radius || !angles || !qjl_signs || !qjl_norms) {
+    set_error("%s: null pointer argument", who);
+    return VRM_ERR_ARG;
+  }
+  hipLaunchKernelGGL(tq_pool_read_kernel, dim3(NP * 2 * KH * tq::kTokens), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx, bits, radius,
+                     angles, qjl_signs, qjl_norms);
   return launch_status(who);
 }

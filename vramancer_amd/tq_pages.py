@@ -1,0 +1,204 @@
+"""TurboQuant KV pages on MI355X: a paged pool of the reference's TurboQuant
+codes, written by the GPU quantizer and attended in place by the paged decode.
+
+The reference stores TurboQuant-compressed K/V as Python dicts per (page,
+layer, slot) (``write_kv`` + ``flush_compression``, core/paged_attention.py:
+568-675; ``compress_page_bulk``, :1420-1496) and attends them with
+``compute_attention_turbo`` (:1259-1418), which gathers and decompresses on
+the host side per call.  Here the same codes live in a device pool
+
+    tq_pool[P, L, 2, KH, slice]   (uint8, slice = slice_bytes(bits) bytes)
+
+one slice per (page, layer, K/V, kv-head) with the page's 16 tokens: the 127
+angle bins, the fp16 radius and, for K, the 64 QJL sign bits and the fp16
+residual norm.  The codes are those of ``KVCacheCompressor.compress``; the
+decode computes compute_attention_turbo's attention (QJL-corrected scores on
+the rotated query, dense decompressed values) with query head h reading
+kv-head h // (H / KH), the mapping of the paged decode path.
+
+Built for head_dim 128 with the compressor's default qjl_dim (64) and 2, 3 or
+4 bits per angle.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, Optional
+
+from . import _lib
+from .paged_attention_cuda import decode_workspace
+from .turboquant_cuda import angle_lut
+
+__all__ = [
+    "slice_bytes",
+    "allocate_pool",
+    "quantize_append",
+    "quantize_pages",
+    "read_pages",
+    "paged_attention_decode_turbo",
+]
+
+PAGE_SIZE = 16
+
+
+def slice_bytes(bits_per_angle: int, head_dim: int = 128, qjl_dim: int = 64) -> int:
+    n = _lib.load().vrm_tq_slice_bytes(head_dim, bits_per_angle, qjl_dim)
+    if n == 0:
+        raise RuntimeError(f"TurboQuant pages support head_dim 128, qjl_dim 64 and 2-4 bits "
+                           f"(got {head_dim}, {qjl_dim}, {bits_per_angle})")
+    return int(n)
+
+
+def _check_compressor(compressor):
+    if compressor.head_dim != 128 or compressor.qjl_dim != 64 or compressor.bits_per_angle not in (2, 3, 4):
+        raise RuntimeError("TurboQuant pages need a KVCacheCompressor with head_dim 128, qjl_dim 64 and "
+                           f"2-4 bits per angle (got {compressor.head_dim}, {compressor.qjl_dim}, "
+                           f"{compressor.bits_per_angle})")
+
+
+def _buffers(compressor, device):
+    import torch
+
+    signs = compressor._hadamard_signs.to(device=device, dtype=torch.float32).contiguous()
+    jl = compressor.jl_matrix.to(device=device, dtype=torch.float32).contiguous()
+    return signs, jl, angle_lut(compressor.bits_per_angle, device)
+
+
+def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, compressor, device: Any = "cuda"):
+    """Zero-initialised TurboQuant pool for ``compressor``'s settings."""
+    import torch
+
+    _check_compressor(compressor)
+    return torch.zeros((num_pages, num_layers, 2, num_kv_heads, slice_bytes(compressor.bits_per_angle)),
+                       dtype=torch.uint8, device=device)
+
+
+def _pool_dims(tq_pool, compressor):
+    if tq_pool.dim() != 5 or tq_pool.shape[2] != 2 or tq_pool.shape[4] != slice_bytes(compressor.bits_per_angle):
+        raise RuntimeError(f"tq_pool must be [P, L, 2, KH, {slice_bytes(compressor.bits_per_angle)}] uint8")
+    if not tq_pool.is_contiguous():
+        raise RuntimeError("tq_pool must be contiguous (it is written in place)")
+    P, L, _, KH, _ = tq_pool.shape
+    return P, L, KH
+
+
+def quantize_append(tq_pool, layer_idx: int, page_ids, slots, key, value, compressor) -> None:
+    """Compresses N new tokens ([N, KH, 128] K and V) into their (page, slot)
+    of layer ``layer_idx`` (slots from append_token, core/paged_attention.py:
+    431-459)."""
+    import torch
+
+    _check_compressor(compressor)
+    _lib.require_cuda(tq_pool, page_ids, slots, key, value)
+    P, L, KH = _pool_dims(tq_pool, compressor)
+    if key.shape != value.shape or key.dim() != 3 or key.shape[1:] != (KH, 128):
+        raise RuntimeError(f"key/value must be [N, {KH}, 128], got {tuple(key.shape)} / {tuple(value.shape)}")
+    if key.dtype != value.dtype:
+        raise RuntimeError("key and value must share a dtype")
+    N = key.shape[0]
+    page_ids = page_ids.to(torch.int32).contiguous()
+    slots = slots.to(torch.int32).contiguous()
+    if page_ids.shape != (N,) or slots.shape != (N,):
+        raise RuntimeError("page_ids and slots must be [N]")
+    key, value = key.contiguous(), value.contiguous()
+    signs, jl, lut = _buffers(compressor, tq_pool.device)
+    rc = _lib.load().vrm_tq_quant_append(
+        _lib.ptr(key), _lib.ptr(value), _lib.src_dtype_code(key.dtype), _lib.ptr(page_ids), _lib.ptr(slots), N,
+        _lib.ptr(tq_pool), KH, 128, PAGE_SIZE, L, P, int(layer_idx), compressor.bits_per_angle, 64,
+        _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(tq_pool),
+    )
+    _lib.check(rc, "tq quantize_append")
+
+
+def quantize_pages(tq_pool, layer_idx: int, page_ids, key_pages, value_pages, compressor,
+                   n_valid: Optional[Any] = None) -> None:
+    """Bulk write of whole pages ([NP, KH, 16, 128] K and V); page n holds
+    ``n_valid[n]`` tokens (default 16), later slots get zero codes."""
+    import torch
+
+    _check_compressor(compressor)
+    _lib.require_cuda(tq_pool, page_ids, key_pages, value_pages, n_valid)
+    P, L, KH = _pool_dims(tq_pool, compressor)
+    if key_pages.shape != value_pages.shape or key_pages.dim() != 4 or key_pages.shape[1:] != (KH, PAGE_SIZE, 128):
+        raise RuntimeError(f"key/value pages must be [NP, {KH}, 16, 128], got {tuple(key_pages.shape)}")
+    if key_pages.dtype != value_pages.dtype:
+        raise RuntimeError("key and value pages must share a dtype")
+    NP = key_pages.shape[0]
+    page_ids = page_ids.to(torch.int32).contiguous()
+    if n_valid is None:
+        n_valid = torch.full((NP,), PAGE_SIZE, dtype=torch.int32, device=tq_pool.device)
+    n_valid = n_valid.to(torch.int32).contiguous()
+    if page_ids.shape != (NP,) or n_valid.shape != (NP,):
+        raise RuntimeError("page_ids and n_valid must be [NP]")
+    key_pages, value_pages = key_pages.contiguous(), value_pages.contiguous()
+    signs, jl, lut = _buffers(compressor, tq_pool.device)
+    lib = _lib.load()
+    step = 1 << 20  # rows of one launch stay well inside the grid limits
+    for s in range(0, NP, step):
+        e = min(NP, s + step)
+        rc = lib.vrm_tq_quant_pages(
+            _lib.ptr(key_pages[s:e]), _lib.ptr(value_pages[s:e]), _lib.src_dtype_code(key_pages.dtype),
+            _lib.ptr(page_ids[s:e]), _lib.ptr(n_valid[s:e]), e - s, _lib.ptr(tq_pool), KH, 128, PAGE_SIZE, L, P,
+            int(layer_idx), compressor.bits_per_angle, 64, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut),
+            _lib.stream_of(tq_pool),
+        )
+        _lib.check(rc, "tq quantize_pages")
+
+
+def read_pages(tq_pool, layer_idx: int, page_ids, compressor) -> Dict[str, Any]:
+    """Codes of the given pages in the reference's raw format, indexed
+    [n, K/V, kv-head, token]: radius fp16, angles uint8 [.., 127] level-major,
+    qjl_signs uint8 [.., 64], qjl_norms fp16 (zero for V)."""
+    import torch
+
+    _check_compressor(compressor)
+    _lib.require_cuda(tq_pool, page_ids)
+    P, L, KH = _pool_dims(tq_pool, compressor)
+    page_ids = page_ids.to(torch.int32).contiguous()
+    NP = page_ids.shape[0]
+    dev = tq_pool.device
+    shape = (NP, 2, KH, PAGE_SIZE)
+    radius = torch.empty(shape, dtype=torch.float16, device=dev)
+    angles = torch.empty(shape + (127,), dtype=torch.uint8, device=dev)
+    signs = torch.empty(shape + (64,), dtype=torch.uint8, device=dev)
+    norms = torch.empty(shape, dtype=torch.float16, device=dev)
+    rc = _lib.load().vrm_tq_read_pages(
+        _lib.ptr(tq_pool), _lib.ptr(page_ids), NP, KH, 128, PAGE_SIZE, L, P, int(layer_idx),
+        compressor.bits_per_angle, 64, _lib.ptr(radius), _lib.ptr(angles), _lib.ptr(signs), _lib.ptr(norms),
+        _lib.stream_of(tq_pool),
+    )
+    _lib.check(rc, "tq read_pages")
+    return {"radius": radius, "angles": angles, "qjl_signs": signs, "qjl_norms": norms}
+
+
+def paged_attention_decode_turbo(query, tq_pool, page_table, context_lens, layer_idx: int, compressor,
+                                 scale: Optional[float] = None, out=None, workspace=None):
+    """[B, H, 128] float32 attention over TurboQuant pages (compute_attention_turbo
+    with dense values, core/paged_attention.py:1259-1418, for a batch)."""
+    import torch
+
+    _check_compressor(compressor)
+    _lib.require_cuda(query, tq_pool, page_table, context_lens)
+    P, L, KH = _pool_dims(tq_pool, compressor)
+    B, H, D = query.shape
+    if D != 128:
+        raise RuntimeError("TurboQuant pages are built for head_dim 128")
+    if H % KH:
+        raise RuntimeError(f"num_heads {H} is not a multiple of num_kv_heads {KH}")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    query = query.float().contiguous()
+    page_table = page_table.to(torch.int32).contiguous()
+    context_lens = context_lens.to(torch.int32).contiguous()
+    max_pp = page_table.shape[1]
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.float32, device=query.device)
+    if workspace is None:
+        workspace = decode_workspace(B, H, KH, D, max_pp, query.device)
+    signs, jl, lut = _buffers(compressor, query.device)
+    rc = _lib.load().vrm_paged_decode_tq(
+        _lib.ptr(query), _lib.ptr(tq_pool), _lib.ptr(page_table), _lib.ptr(context_lens), _lib.ptr(out),
+        _lib.ptr(workspace), workspace.numel(), B, H, KH, D, PAGE_SIZE, L, P, max_pp, int(layer_idx), float(scale),
+        compressor.bits_per_angle, 64, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(query),
+    )
+    _lib.check(rc, "paged_attention_decode_turbo")
+    return out
