@@ -34,7 +34,7 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from vramancer_amd import _lib, kv_quant, workloads  # noqa: E402
+from vramancer_amd import _lib, kv_quant, tq_pages, workloads  # noqa: E402
 from vramancer_amd.paged_attention_cuda import decode_workspace  # noqa: E402
 
 METRIC = "paged-attn decode µs/layer-step + HBM GB/s (% of peak), 14B-shape quantized KV"
@@ -44,6 +44,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_14b_int8.json")
 KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_BF16, "int8": _lib.VRM_KV_I8,
            "fp8": _lib.VRM_KV_FP8E4M3}
 KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
+          "tq3": "decode_tq_kernel<3> + merge", "tq4": "decode_tq_kernel<4> + merge",
           "bf16": "decode_stream_float_kernel<K_BF16,{D}>", "f16": "decode_stream_float_kernel<K_F16,{D}>",
           "f32": "decode_split_kernel<K_F32,{D},G>"}
 
@@ -77,13 +78,28 @@ def cpu_baseline(inp, layer, n_seq, reps):
     # copy only the pages the sample reads, relabelled 0..n-1
     remap = torch.full((inp["num_pages"],), -1, dtype=torch.long, device=pages.device)
     remap[pages] = torch.arange(pages.numel(), device=pages.device)
+    tbl = remap[table.long()].to(torch.int32).cpu()
+    q = inp["query"][:n_seq].cpu()
+    lens = inp["context_lens"][:n_seq].cpu()
+    comp = inp.get("compressor")
+    if comp is not None:  # TurboQuant pages: the vectorised decompress + dense attention of the oracle
+        from oracle import turboquant as TQ
+
+        codes = {k: v.cpu() for k, v in tq_pages.read_pages(inp["kv_pool"], layer, pages.to(torch.int32),
+                                                               comp).items()}
+        p = TQ.TQParams(128, comp.bits_per_angle, 128, 7, 64, comp._hadamard_signs.cpu(), comp.jl_matrix.cpu())
+        PD.paged_attention_decode_turbo(p, q, codes, tbl, lens)  # warm-up
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            PD.paged_attention_decode_turbo(p, q, codes, tbl, lens)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2] / max(1, int(lens.sum())) * 1e6, threads
     pool = inp["kv_pool"][pages][:, layer:layer + 1].cpu()
     scales = None
     if inp["kv_scales"] is not None:
         scales = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
-    tbl = remap[table.long()].to(torch.int32).cpu()
-    q = inp["query"][:n_seq].cpu()
-    lens = inp["context_lens"][:n_seq].cpu()
     PD.paged_attention_decode(q, pool, tbl, lens, 0, kv_scales=scales)  # warm-up
     times = []
     for _ in range(reps):
@@ -122,19 +138,29 @@ def main():
         # steps rotate over 4 layers so that consecutive steps never hit in the Infinity Cache
         cfg = workloads.scaled(cfg, num_layers=4)
     layers = LAYERS_FILLED if cfg.num_layers > max(LAYERS_FILLED) else tuple(range(4))
-    log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {layers})")
-    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=layers)
+    turbo = cfg.codec in ("tq3", "tq4")
+    # TurboQuant pages are filled on one layer (compression is the slow part of
+    # the set-up); the zero codes of the other layers cost the decode the same.
+    fill = (layers[0],) if turbo else layers
+    log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {fill}, rotating {layers})")
+    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=fill)
     torch.cuda.synchronize()
     q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
     B, H, D = q.shape
-    P, L, _, KH, PS, _ = pool.shape
+    if turbo:
+        P, L, _, KH, _ = pool.shape
+        PS = 16
+        comp = inp["compressor"]
+        tq_signs, tq_jl, tq_lut = tq_pages._buffers(comp, dev)
+    else:
+        P, L, _, KH, PS, _ = pool.shape
     max_pp = table.shape[1]
     scale = 1.0 / math.sqrt(D)
     out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
     ws = decode_workspace(B, H, KH, D, max_pp, dev, PS)
     nsplit = lib.vrm_paged_decode_num_splits(B, H, KH, max_pp, PS)
     stream = _lib.stream_of(q)
-    code = KV_CODE[cfg.codec]
+    code = KV_CODE.get(cfg.codec)
     sc_ptr = sc.data_ptr() if sc is not None else None
     lens_list = lens.tolist()
     ab = workloads.algorithmic_bytes(cfg, lens_list)
@@ -142,6 +168,14 @@ def main():
 
     def full(i):
         layer = layers[i % len(layers)]
+        if turbo:
+            rc = lib.vrm_paged_decode_tq(q.data_ptr(), pool.data_ptr(), table.data_ptr(), lens.data_ptr(),
+                                         out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp,
+                                         layer, scale, comp.bits_per_angle, 64, tq_signs.data_ptr(),
+                                         tq_jl.data_ptr(), tq_lut.data_ptr(), stream)
+            if rc:
+                _lib.check(rc, "turbo decode")
+            return
         rc = lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(), lens.data_ptr(),
                                   out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp, layer,
                                   scale, code, stream)
@@ -162,11 +196,25 @@ def main():
     pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
     log(f"timing {args.steps} layer-steps")
     us_step = time_events(full, args.steps)
-    us_part = time_events(partitions, args.steps)
+    # TurboQuant: no separate partition entry; its kernel time is the whole decode
+    us_part = us_step if turbo else time_events(partitions, args.steps)
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
     us_append = None
-    if sc is not None:
+    if turbo:
+        kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+        vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
+        last = (lens - 1).clamp(min=0)
+        pid = table.gather(1, (last // PS).long()[:, None]).squeeze(1).contiguous()
+        slot = (last % PS).to(torch.int32).contiguous()
+
+        def append(i):
+            tq_pages.quantize_append(pool, layers[0], pid, slot, kn, vn, comp)
+
+        for i in range(5):
+            append(i)
+        us_append = time_events(append, 50)
+    elif sc is not None:
         # append one token per sequence (quantize-on-append), timed separately
         kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
         vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
@@ -213,7 +261,8 @@ def main():
                        f"repeat_interleave + bmm/softmax/bmm, fp32) over the first {min(args.cpu_seqs, B)} of the "
                        f"{B} sequences, median of {args.cpu_reps}, scaled by the batch's total context"),
         }
-    elem = {"f32": "f32", "f16": "f16", "bf16": "bf16", "int8": "int8", "fp8": "fp8e4m3"}[cfg.codec]
+    elem = {"f32": "f32", "f16": "f16", "bf16": "bf16", "int8": "int8", "fp8": "fp8e4m3", "tq3": "tq3-polar",
+            "tq4": "tq4-polar"}[cfg.codec]
     desc = {
         "14b-int8": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
                      "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
@@ -221,6 +270,10 @@ def main():
         "mixed-fp8": ("mixed-fp8 paged decode: 128 sequences lognormal(median 2048, sigma 1) + one of 131072, "
                       "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales"),
         "fp32-plumbing": "fp32-plumbing paged decode: B=4, H=KH=12, D=64, context 512, page 16, fp32 pool",
+        "14b-turbo3": ("14b-turbo3 paged decode over TurboQuant pages: B=16, H=40, KH=8, D=128, context 32768, "
+                       "page 16, 3 bits per angle, Student-t(3) K/V"),
+        "14b-turbo4": ("14b-turbo4 paged decode over TurboQuant pages: B=16, H=40, KH=8, D=128, context 32768, "
+                       "page 16, 4 bits per angle, Student-t(3) K/V"),
     }[cfg.name]
     G = next(g for g in range(16, 0, -1) if (H // KH) % g == 0)
     result = {

@@ -10,6 +10,10 @@ configurations (inputs only; no model weights are involved).
   mixed-fp8      fp8-e4m3 pool (per-page scale), H=64, KH=8, D=128, 128
                  sequences with lognormal context (median 2048, sigma 1,
                  clipped to [16, 131072]) plus one of 131072, L=1
+  14b-turbo3/4   TurboQuant pages (3 / 4 bits per angle), B=16, context
+                 32768, H=40, KH=8, D=128; K/V bf16 from a Student-t (df 3)
+                 per channel scaled to unit variance; the compressor's
+                 rotation comes from torch.manual_seed(seed) before it is built
 
 Every page table is a seeded shuffle of the physical pages.  Tensors are
 generated on ``device`` with a seeded generator; the page table, context
@@ -35,7 +39,7 @@ class DecodeConfig:
     num_kv_heads: int
     head_dim: int
     num_layers: int
-    codec: str                       # "f32" | "f16" | "bf16" | "int8" | "fp8"
+    codec: str                       # "f32" | "f16" | "bf16" | "int8" | "fp8" | "tq3" | "tq4"
     context: str                     # "fixed" | "uniform" | "lognormal"
     ctx_fixed: int = 0
     ctx_low: int = 0
@@ -45,6 +49,7 @@ class DecodeConfig:
     ctx_clip: Sequence[int] = (16, 131072)
     pinned_long: int = 0             # extra sequence of this length (0: none)
     kv_std: float = 1.0
+    kv_dist: str = "normal"          # "normal" | "student_t3" (unit variance)
     outlier_channels: int = 0
     outlier_scale: float = 1.0
     spare_pages: float = 0.0
@@ -60,6 +65,10 @@ CONFIGS: Dict[str, DecodeConfig] = {
                              outlier_channels=2, outlier_scale=20.0),
     "mixed-fp8": DecodeConfig("mixed-fp8", 128, 64, 8, 128, 1, "fp8", "lognormal", ctx_median=2048.0,
                               ctx_sigma=1.0, pinned_long=131072),
+    "14b-turbo3": DecodeConfig("14b-turbo3", 16, 40, 8, 128, 1, "tq3", "fixed", ctx_fixed=32768,
+                               kv_dist="student_t3"),
+    "14b-turbo4": DecodeConfig("14b-turbo4", 16, 40, 8, 128, 1, "tq4", "fixed", ctx_fixed=32768,
+                               kv_dist="student_t3"),
 }
 
 
@@ -110,7 +119,11 @@ def _pool_dtype(codec: str):
 
 def _kv_pages(cfg: DecodeConfig, n: int, gen: torch.Generator, device, outlier_idx) -> torch.Tensor:
     """[n, KH, PS, D] float32 K or V rows of the configured distribution."""
-    x = torch.randn((n, cfg.num_kv_heads, cfg.page_size, cfg.head_dim), generator=gen, device=device)
+    shape = (n, cfg.num_kv_heads, cfg.page_size, cfg.head_dim)
+    x = torch.randn(shape, generator=gen, device=device)
+    if cfg.kv_dist == "student_t3":  # t(3) = z / sqrt(chi2_3 / 3), variance 3
+        chi2 = sum(torch.randn(shape, generator=gen, device=device) ** 2 for _ in range(3))
+        x = x / torch.sqrt(chi2 / 3) / math.sqrt(3.0)
     x = x * cfg.kv_std
     if cfg.outlier_channels:
         x[:, torch.arange(cfg.num_kv_heads, device=device)[:, None], :, outlier_idx] *= cfg.outlier_scale
@@ -149,11 +162,21 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
         outlier_idx = torch.stack([
             torch.randperm(D, generator=g_cpu)[:cfg.outlier_channels] for _ in range(KH)
         ]).to(device)
-    dtype = _pool_dtype(cfg.codec)
     kv_scales = None
-    if cfg.codec in ("int8", "fp8"):
+    compressor = None
+    if cfg.codec in ("tq3", "tq4"):
+        from . import tq_pages
+        from .kv_quantizer import KVCacheCompressor
+
+        torch.manual_seed(seed)  # the rotation and JL matrix are fixed by the seed
+        compressor = KVCacheCompressor(cfg.head_dim, int(cfg.codec[2]))
+        kv_pool = tq_pages.allocate_pool(P, L, KH, compressor, device)
+        dtype = None
+    elif cfg.codec in ("int8", "fp8"):
+        dtype = _pool_dtype(cfg.codec)
         kv_pool, kv_scales = kv_quant.allocate_pool(P, L, KH, D, cfg.codec, PS, device)
     else:
+        dtype = _pool_dtype(cfg.codec)
         kv_pool = torch.zeros((P, L, 2, KH, PS, D), dtype=dtype, device=device)
     page_ids_all = torch.arange(P, dtype=torch.int32, device=device)
     for layer in layers:
@@ -161,7 +184,10 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
             e = min(P, s + chunk_pages)
             k = _kv_pages(cfg, e - s, gen, device, outlier_idx)
             v = _kv_pages(cfg, e - s, gen, device, outlier_idx)
-            if kv_scales is not None:
+            if compressor is not None:
+                tq_pages.quantize_pages(kv_pool, layer, page_ids_all[s:e], k.to(torch.bfloat16),
+                                        v.to(torch.bfloat16), compressor)
+            elif kv_scales is not None:
                 # the quantized pools start from bf16 activations
                 kv_quant.quantize_pages(kv_pool, kv_scales, layer, page_ids_all[s:e], k.to(torch.bfloat16),
                                         v.to(torch.bfloat16))
@@ -177,6 +203,7 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
         "layers": list(layers),
         "num_pages": P,
         "config": cfg,
+        "compressor": compressor,
     }
 
 
@@ -188,6 +215,16 @@ def algorithmic_bytes(cfg: DecodeConfig, lens: Sequence[int]) -> Dict[str, float
     KH, D, H = cfg.num_kv_heads, cfg.head_dim, cfg.num_heads
     tokens = sum(lens)
     pages = sum((n + PS - 1) // PS for n in lens)
+    if cfg.codec in ("tq3", "tq4"):
+        # per token and kv-head: K angles + 64 sign bits + fp16 radius + fp16 norm, V angles + fp16 radius
+        bits = int(cfg.codec[2])
+        angles = (127 * bits + 7) // 8
+        kv = tokens * KH * ((angles + 8 + 2 + 2) + (angles + 2))
+        scales = 0
+        qo = 2 * len(lens) * H * D * 4
+        table = pages * 4
+        return {"kv": kv, "scales": scales, "qo": qo, "table": table, "total": kv + scales + qo + table,
+                "tokens": tokens, "pages": pages}
     elem = {"f32": 4, "f16": 2, "bf16": 2, "int8": 1, "fp8": 1}[cfg.codec]
     kv = tokens * KH * 2 * D * elem
     if cfg.codec == "int8":
