@@ -51,14 +51,13 @@ __device__ __forceinline__ void wave_sync() {
 
 __device__ __forceinline__ float f16_to_f32(uint32_t bits) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits); }
 
-// Bin of slot s of a quarter held in w[0 .. BITS - 1] (little-endian bit
-// stream); s is a constant after unrolling, so the indexing folds away.
-template <int BITS>
-__device__ __forceinline__ int slot_bin(const uint32_t* w, int s) {
-  const int bit = s * BITS, dw = bit / 32, sh = bit % 32;
-  const uint32_t mask = (1u << BITS) - 1;
-  if (sh + BITS <= 32) return (int)((w[dw] >> sh) & mask);
-  return (int)(((w[dw] >> sh) | (w[dw + 1] << (32 - sh))) & mask);
+// WIDTH bits at bit `pos` of the little-endian bit stream w[]; pos is a
+// constant after unrolling, so the indexing folds to one or two ALU ops.
+template <int WIDTH>
+__device__ __forceinline__ uint32_t bit_field(const uint32_t* w, int pos) {
+  const int dw = pos / 32, sh = pos % 32;
+  if (sh + WIDTH <= 32) return __builtin_amdgcn_ubfe(w[dw], sh, WIDTH);
+  return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh), 0, WIDTH);
 }
 
 // In-register Walsh-Hadamard transform of 128 values, element e in lane e % 64,
@@ -97,14 +96,18 @@ struct TqSlot {
 };
 
 template <int BITS>
-__global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G) {
+__global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G) {
   constexpr int NB = 1 << BITS;
   constexpr int RING = 4;
   constexpr int SLICE = T::slice_bytes(BITS);
   constexpr int ABYTES = T::angle_bytes(BITS);
   constexpr int D = T::kPD;
 
-  __shared__ float2 lut[2][NB];             // {cos, sin} of bin centres: level 0, levels >= 1
+  // {cos, sin} of the bin centres (table 0: level 0, table 1: levels >= 1),
+  // singly and for two sibling angles at once (index = bin_a + NB * bin_b)
+  __shared__ float2 lut[2][NB];
+  __shared__ float4 lut2[2][NB * NB];
+  __shared__ uint2 sign_lut[16];             // 4 sign bits -> 4 fp16 +-1 (bit i -> element i)
   __shared__ float qbuf[kWaves][16][D + 4];  // per wave: q_rot rows, later the output columns
 
   const int lane = threadIdx.x & 63;
@@ -120,6 +123,16 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
   for (int i = threadIdx.x; i < 2 * NB; i += blockDim.x) {
     const int tab = i / NB, bin = i % NB;
     lut[tab][bin] = make_float2(tq.lut[(2 * tab) * NB + bin], tq.lut[(2 * tab + 1) * NB + bin]);
+  }
+  for (int i = threadIdx.x; i < 2 * NB * NB; i += blockDim.x) {
+    const int tab = i / (NB * NB), ba = i % NB, bb = (i / NB) % NB;
+    lut2[tab][ba + NB * bb] = make_float4(tq.lut[(2 * tab) * NB + ba], tq.lut[(2 * tab + 1) * NB + ba],
+                                          tq.lut[(2 * tab) * NB + bb], tq.lut[(2 * tab + 1) * NB + bb]);
+  }
+  if (threadIdx.x < 16) {
+    uint32_t h[4];
+    for (int e = 0; e < 4; ++e) h[e] = ((threadIdx.x >> e) & 1) ? 0x3c00u : 0xbc00u;  // fp16 +1 / -1
+    sign_lut[threadIdx.x] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
   __syncthreads();
 
@@ -237,24 +250,29 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
     s.ksign = reinterpret_cast<const uint2*>(ks + T::signs_offset(BITS))[col];
   };
 
-  // dims 32 grp .. 32 grp + 31 of one token, in the reference's order of products
-  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, uint32_t rad_bits, float (&cur)[32]) {
+  // dims 32 grp .. 32 grp + 31 of one token, in the reference's order of
+  // products; sibling angles (slots 2 k + 1, 2 k + 2) are looked up together
+  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&cur)[32]) {
     constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
     const float2 t6 = lut[1][(top0 >> sh31) & (NB - 1)];
     const float2 t5 = lut[1][(topq >> sh31) & (NB - 1)];
-    float p = f16_to_f32(rad_bits);
+    float p = radius;
     p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
     p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
-    cur[0] = p;
+    const float2 c4 = lut[1][bit_field<BITS>(q, 0)];  // level 4: slot 0
+    cur[0] = p * c4.x;
+    cur[1] = p * c4.y;
 #pragma unroll
-    for (int lev = 4; lev >= 0; --lev) {
-      const int n = 1 << (4 - lev);  // nodes of this level in the quarter; slots n - 1 ..
+    for (int lev = 3; lev >= 0; --lev) {
+      const int n = 1 << (4 - lev);  // nodes of this level in the quarter; slots n - 1 .. 2 n - 2
 #pragma unroll
-      for (int i = n - 1; i >= 0; --i) {  // descending: each source is read before it is overwritten
-        const float2 cs = lut[lev == 0 ? 0 : 1][slot_bin<BITS>(q, n - 1 + i)];
-        const float x = cur[i];
-        cur[2 * i] = x * cs.x;
-        cur[2 * i + 1] = x * cs.y;
+      for (int i = n - 2; i >= 0; i -= 2) {  // descending: each source is read before it is overwritten
+        const float4 cs = lut2[lev == 0 ? 0 : 1][bit_field<2 * BITS>(q, (n - 1 + i) * BITS)];
+        const float x0 = cur[i], x1 = cur[i + 1];
+        cur[2 * i] = x0 * cs.x;
+        cur[2 * i + 1] = x0 * cs.y;
+        cur[2 * i + 2] = x1 * cs.z;
+        cur[2 * i + 3] = x1 * cs.w;
       }
     }
   };
@@ -262,7 +280,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
   // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi.
   auto page_scores = [&](const TqSlot<BITS>& s, int pi, float* sc) {
     float kv[32];
-    rebuild(s.kq, s.ktop[0], s.ktop[1], s.krad, kv);
+    rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), kv);
     v4f c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -280,13 +298,11 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
     v4f cq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      v8h sg;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = 16 * (2 * c + e / 4) + 4 * grp + (e % 4);
-        const uint32_t bit = (j < 32 ? s.ksign.x >> j : s.ksign.y >> (j - 32)) & 1u;
-        sg[e] = bit ? (_Float16)1.f : (_Float16)-1.f;
-      }
+      // elements e < 4: JL rows 32 c + 4 grp + e; e >= 4: rows 32 c + 16 + 4 grp + e - 4
+      const uint32_t word = c == 0 ? s.ksign.x : s.ksign.y;
+      const uint2 lo = sign_lut[__builtin_amdgcn_ubfe(word, 4 * grp, 4)];
+      const uint2 hi = sign_lut[__builtin_amdgcn_ubfe(word, 16 + 4 * grp, 4)];
+      const v8h sg = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
       cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][0], cq, 0, 0, 0);
       cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][1], cq, 0, 0, 0);
     }
@@ -300,16 +316,18 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
   };
 
   // V of 16 dims (block 2 c + h) for this lane's 4 tokens of one page, exact
-  // fp16 values in token-per-lane order; absent pages and tokens past the
-  // context read as 0 whatever the page holds.
-  auto v_block = [&](const v8h& vop, int h, int pi, bool ok, float* out4) {
+  // fp16 values in token-per-lane order.
+  auto v_block = [&](const v8h& vop, int h, float* out4) {
     const v4f t = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, onehot[h], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out4[r] = (ok && pi * kPS + grp * 4 + r < tok_end) ? t[r] : 0.f;
+    for (int r = 0; r < 4; ++r) out4[r] = t[r];
   };
-  auto v_operand = [&](const TqSlot<BITS>& s, v8h (&vop)[4]) {
+  // Values of this lane's token; absent pages and tokens past the context get
+  // radius 0 (whatever the page holds), so they contribute exact zeros.
+  auto v_operand = [&](const TqSlot<BITS>& s, int pi, v8h (&vop)[4]) {
     float vv[32];
-    rebuild(s.vq, s.vtop[0], s.vtop[1], s.vrad, vv);
+    const bool live = s.ok && pi * kPS + col < tok_end;
+    rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, vv);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -347,20 +365,15 @@ __global__ void __launch_bounds__(64 * kWaves) decode_tq_kernel(DecodeArgs a, Tq
       Bl[e] = (_Float16)(p - (float)hi);
     }
     v8h vop0[4], vop1[4];
-    v_operand(s0, vop0);
-    if (has1) v_operand(s1, vop1);
+    v_operand(s0, pi, vop0);
+    v_operand(s1, pi + 1, vop1);  // past the partition: radius 0
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float t[8];
-        v_block(vop0[c], h, pi, s0.ok, t);
-        if (has1) {
-          v_block(vop1[c], h, pi + 1, s1.ok, t + 4);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) t[4 + r] = 0.f;
-        }
+        v_block(vop0[c], h, t);
+        v_block(vop1[c], h, t + 4);
         v8h A;
 #pragma unroll
         for (int e = 0; e < 8; ++e) A[e] = (_Float16)t[e];  // exact: fp16 values
