@@ -270,6 +270,18 @@ int vrm_tq_quant_pages(const void* key, const void* value, int src_dtype,
                        const float* angle_lut, vrm_stream_t stream);
 
 /*
+ * compress_page_bulk's device work (core/paged_attention.py:1420-1496): reads
+ * pages page_ids[n] of layer layer_idx from a float pool kv_pool[P][L][2][KH]
+ * [16][D] (kv_dtype f32, f16 or bf16, the manager's raw pool) and writes
+ * their codes into the same (page, layer) of tq_pool; page n holds n_valid[n]
+ * tokens, later slots get zero codes.  Codes as vrm_tq_quant_pages.
+ */
+int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int32_t* page_ids,
+                         const int32_t* n_valid, int NP, uint8_t* tq_pool, int KH, int D, int PS,
+                         int L, int P, int layer_idx, int bits, int qjl_dim, const float* signs,
+                         const float* jl, const float* angle_lut, vrm_stream_t stream);
+
+/*
  * Reads pages back in the reference's raw code format: row
  * ((n * 2 + kv) * KH + h) * 16 + t gets radius (fp16 bits), the 127
  * level-major bins, 64 sign bytes and the norm (V rows: zero signs / norm).
@@ -293,6 +305,34 @@ int vrm_paged_decode_tq(const float* query, const uint8_t* tq_pool, const int32_
                         int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx,
                         float scale, int bits, int qjl_dim, const float* signs, const float* jl,
                         const float* angle_lut, vrm_stream_t stream);
+
+/* --------------------------------------------------------------------------
+ * Paged cache manager support (PagedKVCacheManager, core/paged_attention.py).
+ * -------------------------------------------------------------------------- */
+
+/*
+ * Block-table build of compute_attention_decode (core/paged_attention.py:
+ * 1226-1248): request b's pages are flat_pages[offsets[b] .. offsets[b+1]),
+ * offsets has B + 1 entries.  Writes page_table[b][p] = its p-th page for
+ * p below the count and -1 up to max_pp, and context_lens[b] =
+ * num_tokens[b].  A list that overruns the flat array or max_pp is cut
+ * (entries past max_pp are not written; a malformed (offsets[b],
+ * offsets[b+1]) pair gives a row of -1).
+ */
+int vrm_build_block_table(const int32_t* flat_pages, int n_flat, const int32_t* offsets,
+                          const int32_t* num_tokens, int B, int max_pp, int32_t* page_table,
+                          int32_t* context_lens, vrm_stream_t stream);
+
+/*
+ * Raw write of N tokens into a float pool: replaces write_kv's index-put
+ * (core/paged_attention.py:611-612, pool[page, layer, 0|1, :, slot, :] =
+ * key|value).  key/value are [N][KH][D] of src_dtype; kv_dtype is VRM_KV_F32,
+ * VRM_KV_F16 or VRM_KV_BF16; conversions round to nearest even.  Rows aimed
+ * at pages outside [0, P) or slots outside [0, PS) are dropped.
+ */
+int vrm_kv_write(const void* key, const void* value, int src_dtype, const int32_t* page_ids,
+                 const int32_t* slots, int N, void* kv_pool, int kv_dtype, int KH, int D, int PS,
+                 int L, int P, int layer_idx, vrm_stream_t stream);
 
 #ifdef __cplusplus
 }

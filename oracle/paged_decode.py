@@ -141,15 +141,16 @@ def dense_attention(q, K, V, scale):
     return out
 
 
-def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scale=None):
+def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scale=None, head_map="div"):
     """[B, H, D] float32 attention over TurboQuant pages, as
     PagedKVCacheManager.compute_attention_turbo (core/paged_attention.py:
     1259-1418) evaluates it with dense values (sparse_v_ratio 1.0): per kv-head,
     scores = attention_score(q_group, merged compressed keys) * scale (QJL-
     corrected, on the rotated query; core/kv_quantizer.py:502-535), softmax,
-    then weights @ decompress(values) (core/kv_quantizer.py:481-500).  Query
-    head h reads kv-head h // (H / KH), the paged decode's mapping (the
-    reference's turbo path uses h % KH, an inconsistency of the reference).
+    then weights @ decompress(values) (core/kv_quantizer.py:481-500).  With
+    head_map "div" query head h reads kv-head h // (H / KH), the paged
+    decode's mapping; with "mod" it reads kv-head h % KH, the mapping of
+    compute_attention_turbo itself (core/paged_attention.py:1374).
 
     ``p`` are the compressor's parameters (oracle.turboquant.make_params);
     ``codes`` holds one layer's raw codes indexed [page, K/V, kv-head, token]:
@@ -189,8 +190,14 @@ def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scal
 
         for kvh in range(KH):
             ck, cv = gather(0, kvh), gather(1, kvh)
-            q_group = query[b, kvh * ratio:(kvh + 1) * ratio].float()
+            if head_map == "div":
+                group = list(range(kvh * ratio, (kvh + 1) * ratio))
+            elif head_map == "mod":
+                group = [h for h in range(H) if h % KH == kvh]
+            else:
+                raise ValueError(f"head_map {head_map!r}")
+            q_group = query[b, group].float()
             scores = TQ.attention_score(p, q_group, ck) * scale
             weights = torch.softmax(scores, dim=-1)
-            out[b, kvh * ratio:(kvh + 1) * ratio] = weights @ TQ.decompress(p, cv)
+            out[b, group] = weights @ TQ.decompress(p, cv)
     return out

@@ -359,6 +359,7 @@ def test_turbo_paged_oracle_without_qjl_is_dense_attention_over_decompressed_kv(
     table = torch.tensor([[4, 1, 3], [0, 5, -1]], dtype=torch.int32)
     lens = torch.tensor([40, 20], dtype=torch.int32)
     out = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.09)
+    out_mod = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.09, head_map="mod")
     for b in range(2):
         ks, vs = [], []
         for t in range(int(lens[b])):
@@ -375,6 +376,10 @@ def test_turbo_paged_oracle_without_qjl_is_dense_attention_over_decompressed_kv(
         V = torch.stack(vs, 1).double()
         ref = PD.dense_attention(q[b], K, V, 0.09)
         torch.testing.assert_close(out[b].double(), ref, atol=2e-5, rtol=1e-5)
+        # compute_attention_turbo's own mapping: head h reads kv-head h % KH
+        for h in range(H):
+            w = torch.softmax(0.09 * (K[h % KH] @ q[b, h].double()), 0)
+            torch.testing.assert_close(out_mod[b, h].double(), w @ V[h % KH], atol=2e-5, rtol=1e-5)
 
 
 def test_turbo_paged_oracle_relabel_invariance():

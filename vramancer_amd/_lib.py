@@ -54,6 +54,9 @@ SIGNATURES = {
     "vrm_tq_quant_pages": (_i, [_p, _p, _i, _p, _p, _i, _p] + [_i] * 8 + [_p, _p, _p, _p]),
     "vrm_tq_read_pages": (_i, [_p, _p, _i] + [_i] * 8 + [_p, _p, _p, _p, _p]),
     "vrm_paged_decode_tq": (_i, [_p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _i, _p, _p, _p, _p]),
+    "vrm_tq_compress_pool": (_i, [_p, _i, _p, _p, _i, _p] + [_i] * 8 + [_p, _p, _p, _p]),
+    "vrm_build_block_table": (_i, [_p, _i, _p, _p, _i, _i, _p, _p, _p]),
+    "vrm_kv_write": (_i, [_p, _p, _i, _p, _p, _i, _p] + [_i] * 7 + [_p]),
 }
 
 

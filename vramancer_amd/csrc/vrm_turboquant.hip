@@ -249,6 +249,7 @@ struct TqPoolArgs {
   const int32_t* n_valid;  // pages: valid tokens of each page; append: nullptr
   uint8_t* pool;
   int KH, L, P, layer, bits, head_dim;
+  int from_pool;  // pages: key/value are a float pool [P][L][2][KH][16][head_dim] read at (page_ids[n], layer)
   const float* signs;
   const float* jl;
   const float* lut;
@@ -280,6 +281,7 @@ __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
   }
   const int pid = a.page_ids[n];
   if (pid < 0 || pid >= a.P || t < 0 || t >= L::kTokens) return;  // rows aimed outside the pool are dropped
+  if (a.from_pool) src_first = (((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::kTokens + t) * a.head_dim;
   uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::slice_bytes(a.bits);
   const int abytes = L::angle_bytes(a.bits);
   uint8_t* rec = slice + (size_t)t * abytes;
@@ -522,7 +524,7 @@ int check_tq_pool(int KH, int D, int PS, int L, int P, int layer_idx, int bits, 
 int tq_pool_write(const void* key, const void* value, int src_dtype, const int32_t* page_ids, const int32_t* slots,
                   const int32_t* n_valid, int rows, uint8_t* tq_pool, int KH, int D, int PS, int L, int P,
                   int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl, const float* angle_lut,
-                  vrm_stream_t stream, const char* who) {
+                  vrm_stream_t stream, const char* who, bool from_pool = false) {
   int rc = check_tq_pool(KH, D, PS, L, P, layer_idx, bits, qjl_dim, who);
   if (rc) return rc;
   if (rows < 0) {
@@ -555,6 +557,7 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.layer = layer_idx;
   a.bits = bits;
   a.head_dim = D;
+  a.from_pool = from_pool ? 1 : 0;
   a.signs = signs;
   a.jl = jl;
   a.lut = angle_lut;
@@ -606,6 +609,32 @@ extern "C" int vrm_tq_quant_pages(const void* key, const void* value, int src_dt
   }
   return tq_pool_write(key, value, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D, PS,
                        L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who);
+}
+
+extern "C" int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int32_t* page_ids,
+                                    const int32_t* n_valid, int NP, uint8_t* tq_pool, int KH, int D, int PS, int L,
+                                    int P, int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl,
+                                    const float* angle_lut, vrm_stream_t stream) {
+  const char* who = "vrm_tq_compress_pool";
+  if (NP < 0 || KH <= 0 || (long)NP * KH * tq::kTokens > 0x3fffffff) {
+    set_error("%s: bad sizes (NP=%d KH=%d)", who, NP, KH);
+    return VRM_ERR_ARG;
+  }
+  int src_dtype;
+  switch (kv_dtype) {
+    case VRM_KV_F32: src_dtype = VRM_SRC_F32; break;
+    case VRM_KV_F16: src_dtype = VRM_SRC_F16; break;
+    case VRM_KV_BF16: src_dtype = VRM_SRC_BF16; break;
+    default:
+      set_error("%s: kv_dtype %d is not a float pool", who, kv_dtype);
+      return VRM_ERR_ARG;
+  }
+  if (NP > 0 && !n_valid) {
+    set_error("%s: null n_valid", who);
+    return VRM_ERR_ARG;
+  }
+  return tq_pool_write(kv_pool, kv_pool, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D,
+                       PS, L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who, true);
 }
 
 extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids, int NP, int KH, int D, int PS,

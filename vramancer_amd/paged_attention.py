@@ -1,0 +1,699 @@
+"""Paged KV-cache manager on MI355X: the decode-path part of VRAMancer's
+``PagedKVCacheManager`` (core/paged_attention.py:88-1508).
+
+Host side, as in the reference: a free list of physical pages (allocation
+pops from its end), one page list and token count per request, reference
+counts for forks, and the slot mapping of ``append_token`` (token n of a
+request lives in slot n % page_size of its page n // page_size).
+
+Device side, in this library's kernels:
+
+* ``write_kv`` writes a token's K/V rows into the pool with ``vrm_kv_write``
+  (float16 / bfloat16 / float32 pools, the reference's raw index-put) or
+  quantizes them on append with ``vrm_kv_quant_append`` (int8 / fp8 pools);
+  ``write_kv_batch`` does the same for N tokens in one launch;
+* ``flush_compression`` compresses every pending row of every layer into the
+  TurboQuant pages with one ``vrm_tq_quant_append`` launch (the reference
+  builds per-slot dicts, core/paged_attention.py:623-675);
+* ``compute_attention_decode`` builds the block table on the device
+  (``vrm_build_block_table``) and runs the paged decode;
+* ``compute_attention_turbo`` attends the TurboQuant pages in place
+  (``vrm_paged_decode_tq``) with the reference's head mapping ``h % n_kv``
+  (:1374); pages with no codes for the layer are first compressed from the
+  raw pool, as the reference's lazy ``compress_page_bulk`` call does;
+* ``compress_page_bulk`` compresses a page's raw K/V for every layer that has
+  no codes yet (``vrm_tq_compress_pool``).
+
+Not built (outside the decode path): multi-GPU pools, the VRAM lending pool,
+LRU eviction to other memory tiers (``append_token`` returns ``None`` once
+the pool is exhausted, where the reference would try to evict), prefix
+caching, parity engrams and the Hugging Face cache conversions.
+
+A manager whose ``device`` is not a GPU keeps the host bookkeeping only: it
+allocates no pools, its decode calls return ``None`` (as the reference's do
+without a pool) and writes raise ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import itertools
+import math
+import os
+import threading
+import time
+from dataclasses import dataclass, field
+from typing import Any, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import _lib
+
+__all__ = ["PagedKVConfig", "PhysicalPage", "PageTableEntry", "PagedKVCacheManager"]
+
+# Pool element types: name -> (torch dtype name, bytes per element).
+_POOL_DTYPES = {
+    "float16": ("float16", 2), "fp16": ("float16", 2), "half": ("float16", 2),
+    "bfloat16": ("bfloat16", 2), "bf16": ("bfloat16", 2),
+    "float32": ("float32", 4), "fp32": ("float32", 4), "float": ("float32", 4),
+    "int8": ("int8", 1),
+    "fp8": ("float8_e4m3fn", 1), "float8_e4m3fn": ("float8_e4m3fn", 1),
+}
+
+
+def _pool_dtype(name: str) -> Tuple[str, int]:
+    try:
+        return _POOL_DTYPES[name.lower()]
+    except KeyError:
+        raise ValueError(f"unknown KV dtype {name!r}; expected one of {sorted(_POOL_DTYPES)}") from None
+
+
+@dataclass
+class PagedKVConfig:
+    """Configuration of the paged KV cache (core/paged_attention.py:88-146).
+
+    ``dtype`` names the pool's element type: float16 (default), bfloat16,
+    float32, or the quantized int8 / fp8 codecs of ``vramancer_amd.kv_quant``.
+    """
+
+    page_size: int = 16
+    num_layers: int = 12
+    num_kv_heads: int = 12
+    head_dim: int = 64
+    max_pages: int = 4096
+    device: str = "cuda:0"
+    dtype: str = "float16"
+    kv_compression: Optional[str] = None   # None or "turboquant"
+    compression_bits: int = 3
+    qjl_dim: Optional[int] = None
+    sparse_v_ratio: float = 1.0
+
+    @property
+    def page_size_bytes(self) -> int:
+        """Bytes of one page over all layers: codes of K and V, plus the
+        scales of the int8 (per token and head) and fp8 (per head) pools."""
+        kind, esize = _pool_dtype(self.dtype)
+        per_head = self.page_size * self.head_dim * esize
+        if kind == "int8":
+            per_head += self.page_size * 4
+        elif kind == "float8_e4m3fn":
+            per_head += 4
+        return 2 * self.num_layers * self.num_kv_heads * per_head
+
+    @property
+    def total_memory_bytes(self) -> int:
+        return self.page_size_bytes * self.max_pages
+
+    @classmethod
+    def from_model(cls, model: Any, max_pages: int = 4096, device: str = "cuda:0") -> "PagedKVConfig":
+        """Config from a Hugging Face model's ``config``; compression settings
+        from VRM_KV_COMPRESSION, VRM_KV_COMPRESSION_BITS and VRM_SPARSE_V_RATIO
+        (core/paged_attention.py:117-146)."""
+        kv_comp = os.environ.get("VRM_KV_COMPRESSION", "").lower() or None
+        comp_bits = int(os.environ.get("VRM_KV_COMPRESSION_BITS", "3"))
+        sparse_v = float(os.environ.get("VRM_SPARSE_V_RATIO", "1.0"))
+        config = getattr(model, "config", None)
+        if config is None:
+            return cls(max_pages=max_pages, device=device, kv_compression=kv_comp, compression_bits=comp_bits,
+                       sparse_v_ratio=sparse_v)
+        num_layers = getattr(config, "num_hidden_layers", 12)
+        num_heads = getattr(config, "num_attention_heads", 12)
+        num_kv_heads = getattr(config, "num_key_value_heads", num_heads)
+        hidden_size = getattr(config, "hidden_size", 768)
+        return cls(num_layers=num_layers, num_kv_heads=num_kv_heads, head_dim=hidden_size // num_heads,
+                   max_pages=max_pages, device=device, kv_compression=kv_comp, compression_bits=comp_bits,
+                   sparse_v_ratio=sparse_v)
+
+
+@dataclass
+class PhysicalPage:
+    """One page of the pool (core/paged_attention.py:152-171)."""
+
+    page_id: int
+    ref_count: int = 0
+    allocated: bool = False
+    last_access: float = field(default_factory=time.time)
+
+
+@dataclass
+class PageTableEntry:
+    """A request's physical pages and token count (core/paged_attention.py:178-185)."""
+
+    request_id: str
+    pages: List[int] = field(default_factory=list)
+    num_tokens: int = 0
+    created_at: float = field(default_factory=time.time)
+
+
+def _is_gpu(device: str) -> bool:
+    return str(device).startswith("cuda")
+
+
+class PagedKVCacheManager:
+    """Block-based KV cache with on-demand page allocation and GPU decode."""
+
+    def __init__(self, config: Optional[PagedKVConfig] = None):
+        self.config = cfg = config or PagedKVConfig()
+        self._lock = threading.Lock()
+        self._pages: List[PhysicalPage] = [PhysicalPage(page_id=i) for i in range(cfg.max_pages)]
+        self._free_pages: List[int] = list(range(cfg.max_pages))
+        self._page_tables: Dict[str, PageTableEntry] = {}
+        self._total_allocations = 0
+        self._total_frees = 0
+        self._peak_usage = 0
+        # Bumped by every change of a page list or token count; keys the
+        # device block-table cache of compute_attention_decode.
+        self._epoch = 0
+        self._table_cache: Optional[tuple] = None
+        self._workspaces: Dict[tuple, Any] = {}
+
+        self._gpu_pool: Any = None
+        self._kv_scales: Any = None
+        self._tq_pool: Any = None
+        self._tq_buffers: Optional[tuple] = None
+        # Bit s of _tq_slots[page, layer] is set once slot s of that page and
+        # layer holds TurboQuant codes (the reference's _compressed_pages
+        # entries, core/paged_attention.py:236-238).
+        self._tq_slots: Optional[np.ndarray] = None
+        self._pending_compress: List[tuple] = []
+        self._kv_compressor: Any = None
+        self._init_kv_compression()
+        if _is_gpu(cfg.device):
+            self._init_pools()
+
+    # ------------------------------------------------------------------
+    # Set-up
+    # ------------------------------------------------------------------
+
+    def _init_kv_compression(self) -> None:
+        """TurboQuant compressor built as core/paged_attention.py:366-401 does
+        (same constructor call, so the same draws of torch's global RNG)."""
+        comp = self.config.kv_compression
+        if comp is None:
+            return
+        if comp != "turboquant":
+            raise ValueError(f"unknown kv_compression {comp!r}; expected None or 'turboquant'")
+        from .kv_quantizer import KVCacheCompressor
+
+        self._kv_compressor = KVCacheCompressor(head_dim=self.config.head_dim,
+                                                bits_per_angle=self.config.compression_bits,
+                                                qjl_dim=self.config.qjl_dim)
+
+    def _init_pools(self) -> None:
+        import torch
+
+        cfg = self.config
+        kind, _ = _pool_dtype(cfg.dtype)
+        dev = torch.device(cfg.device)
+        if kind in ("int8", "float8_e4m3fn"):
+            from . import kv_quant
+
+            self._gpu_pool, self._kv_scales = kv_quant.allocate_pool(
+                cfg.max_pages, cfg.num_layers, cfg.num_kv_heads, cfg.head_dim,
+                "int8" if kind == "int8" else "fp8", cfg.page_size, dev)
+        else:
+            self._gpu_pool = torch.zeros((cfg.max_pages, cfg.num_layers, 2, cfg.num_kv_heads, cfg.page_size,
+                                          cfg.head_dim), dtype=getattr(torch, kind), device=dev)
+        if self._kv_compressor is not None:
+            from . import tq_pages
+
+            if kind not in ("float16", "bfloat16", "float32"):
+                raise RuntimeError("TurboQuant compression needs a float16, bfloat16 or float32 raw pool "
+                                   f"(got {cfg.dtype})")
+            if cfg.page_size != tq_pages.PAGE_SIZE:
+                raise RuntimeError(f"TurboQuant pages hold {tq_pages.PAGE_SIZE} tokens (page_size {cfg.page_size})")
+            self._kv_compressor = self._kv_compressor.to(dev)
+            self._tq_pool = tq_pages.allocate_pool(cfg.max_pages, cfg.num_layers, cfg.num_kv_heads,
+                                                   self._kv_compressor, dev)
+            self._tq_buffers = tq_pages._buffers(self._kv_compressor, dev)
+            self._tq_slots = np.zeros((cfg.max_pages, cfg.num_layers), dtype=np.uint32)
+
+    def _require_pool(self, what: str) -> None:
+        if self._gpu_pool is None:
+            raise RuntimeError(f"{what} needs a GPU pool (manager device is {self.config.device!r})")
+
+    # ------------------------------------------------------------------
+    # Allocation (core/paged_attention.py:403-519, 916-931)
+    # ------------------------------------------------------------------
+
+    def _alloc_page(self) -> Optional[int]:
+        if not self._free_pages:
+            return None
+        page_id = self._free_pages.pop()
+        page = self._pages[page_id]
+        page.allocated = True
+        page.ref_count = 1
+        page.last_access = time.time()
+        self._total_allocations += 1
+        return page_id
+
+    def allocate(self, request_id: str, num_tokens: int = 0) -> PageTableEntry:
+        """Page list for a new request, with pages for ``num_tokens`` tokens."""
+        with self._lock:
+            if request_id in self._page_tables:
+                return self._page_tables[request_id]
+            entry = PageTableEntry(request_id=request_id)
+            for _ in range(math.ceil(num_tokens / self.config.page_size) if num_tokens > 0 else 0):
+                page_id = self._alloc_page()
+                if page_id is None:
+                    break
+                entry.pages.append(page_id)
+            entry.num_tokens = num_tokens
+            self._page_tables[request_id] = entry
+            self._peak_usage = max(self._peak_usage, self.config.max_pages - len(self._free_pages))
+            self._epoch += 1
+            return entry
+
+    def _append_locked(self, request_id: str) -> Optional[Tuple[int, int]]:
+        entry = self._page_tables.get(request_id)
+        if entry is None:
+            return None
+        slot = entry.num_tokens % self.config.page_size
+        page_index = entry.num_tokens // self.config.page_size
+        if page_index >= len(entry.pages):
+            page_id = self._alloc_page()
+            if page_id is None:
+                return None
+            entry.pages.append(page_id)
+            self._peak_usage = max(self._peak_usage, self.config.max_pages - len(self._free_pages))
+        physical = entry.pages[page_index]
+        entry.num_tokens += 1
+        self._pages[physical].last_access = time.time()
+        self._epoch += 1
+        return physical, slot
+
+    def append_token(self, request_id: str) -> Optional[Tuple[int, int]]:
+        """(page_id, slot) for a request's next token, allocating a page when
+        the last one is full; ``None`` for an unknown request or a full pool."""
+        with self._lock:
+            return self._append_locked(request_id)
+
+    def append_tokens(self, request_ids: Sequence[str]) -> Tuple[Any, Any]:
+        """``append_token`` for a batch, as two int32 device tensors [N]
+        (page ids, slots) ready for ``write_kv_batch``; a request that gets no
+        slot has page -1 and slot -1, which the writers skip."""
+        import torch
+
+        self._require_pool("append_tokens")
+        out = np.full((2, len(request_ids)), -1, dtype=np.int32)
+        with self._lock:
+            for i, rid in enumerate(request_ids):
+                got = self._append_locked(rid)
+                if got is not None:
+                    out[0, i], out[1, i] = got
+        dev = torch.from_numpy(out).to(self._gpu_pool.device)
+        return dev[0], dev[1]
+
+    def free(self, request_id: str) -> int:
+        """Drops a request; returns how many pages went back to the free list."""
+        with self._lock:
+            entry = self._page_tables.pop(request_id, None)
+            if entry is None:
+                return 0
+            freed = 0
+            for page_id in entry.pages:
+                page = self._pages[page_id]
+                page.ref_count -= 1
+                if page.ref_count <= 0:
+                    page.allocated = False
+                    page.ref_count = 0
+                    self._free_pages.append(page_id)
+                    freed += 1
+                    self._total_frees += 1
+            self._epoch += 1
+            return freed
+
+    def fork(self, src_request_id: str, dst_request_id: str) -> Optional[PageTableEntry]:
+        """New request sharing every page of ``src_request_id`` (ref counts +1)."""
+        with self._lock:
+            src = self._page_tables.get(src_request_id)
+            if src is None:
+                return None
+            entry = PageTableEntry(request_id=dst_request_id, pages=list(src.pages), num_tokens=src.num_tokens)
+            for page_id in entry.pages:
+                self._pages[page_id].ref_count += 1
+            self._page_tables[dst_request_id] = entry
+            self._epoch += 1
+            return entry
+
+    # ------------------------------------------------------------------
+    # Writes (core/paged_attention.py:568-675)
+    # ------------------------------------------------------------------
+
+    def _write_rows(self, layer_idx: int, page_ids, slots, key, value) -> None:
+        cfg = self.config
+        pool = self._gpu_pool
+        KH, D = cfg.num_kv_heads, cfg.head_dim
+        if key.dtype != value.dtype:
+            raise RuntimeError("key and value must share a dtype")
+        if not 0 <= layer_idx < cfg.num_layers:
+            raise RuntimeError(f"layer_idx {layer_idx} outside [0, {cfg.num_layers})")
+        code = _lib.kv_dtype_code(pool.dtype)
+        N = key.shape[0]
+        if code in (_lib.VRM_KV_I8, _lib.VRM_KV_FP8E4M3):
+            from . import kv_quant
+
+            kv_quant.quantize_append(pool, self._kv_scales, layer_idx, page_ids, slots, key, value)
+            return
+        rc = _lib.load().vrm_kv_write(
+            _lib.ptr(key), _lib.ptr(value), _lib.src_dtype_code(key.dtype), _lib.ptr(page_ids), _lib.ptr(slots), N,
+            _lib.ptr(pool), code, KH, D, cfg.page_size, cfg.num_layers, cfg.max_pages, int(layer_idx),
+            _lib.stream_of(pool))
+        _lib.check(rc, "write_kv")
+
+    def _rows(self, t, n: int, what: str):
+        """[n, KH, D] contiguous view of a K or V argument on the pool's device."""
+        cfg = self.config
+        _lib.require_cuda(t, self._gpu_pool)
+        if t.numel() != n * cfg.num_kv_heads * cfg.head_dim:
+            raise RuntimeError(f"{what} must hold {n} x {cfg.num_kv_heads} x {cfg.head_dim} values, "
+                               f"got shape {tuple(t.shape)}")
+        return t.reshape(n, cfg.num_kv_heads, cfg.head_dim).contiguous()
+
+    def write_kv(self, request_id: str, layer_idx: int, page_id: int, slot: int, key: Any, value: Any) -> None:
+        """Writes one token's K/V ([num_kv_heads, head_dim]) to (page_id, slot)
+        of ``layer_idx``; with TurboQuant compression the rows also wait in
+        the queue that ``flush_compression`` empties."""
+        import torch
+
+        self._require_pool("write_kv")
+        key = self._rows(key, 1, "key")
+        value = self._rows(value, 1, "value")
+        ids = torch.tensor([[page_id], [slot]], dtype=torch.int32).to(self._gpu_pool.device)
+        self._write_rows(layer_idx, ids[0], ids[1], key, value)
+        if self._kv_compressor is not None:
+            self._pending_compress.append((layer_idx, ids[0], ids[1], key, value, [(int(page_id), int(slot))]))
+
+    def write_kv_batch(self, layer_idx: int, page_ids: Any, slots: Any, key: Any, value: Any,
+                       host_slots: Optional[Sequence[Tuple[int, int]]] = None) -> None:
+        """Writes N tokens' K/V ([N, num_kv_heads, head_dim]) in one launch;
+        ``page_ids`` / ``slots`` are [N] device tensors (``append_tokens``).
+        ``host_slots`` optionally lists the same (page, slot) pairs on the host,
+        which spares the compression queue a device read-back."""
+        import torch
+
+        self._require_pool("write_kv_batch")
+        N = int(page_ids.shape[0])
+        key = self._rows(key, N, "key")
+        value = self._rows(value, N, "value")
+        page_ids = page_ids.to(torch.int32).contiguous()
+        slots = slots.to(torch.int32).contiguous()
+        if tuple(slots.shape) != (N,):
+            raise RuntimeError("page_ids and slots must both be [N]")
+        self._write_rows(layer_idx, page_ids, slots, key, value)
+        if self._kv_compressor is not None:
+            self._pending_compress.append((layer_idx, page_ids, slots, key, value,
+                                           list(host_slots) if host_slots is not None else None))
+
+    def flush_compression(self) -> None:
+        """Compresses every queued row, all layers at once, into the TurboQuant
+        pages: one launch per source dtype."""
+        import torch
+
+        pending, self._pending_compress = self._pending_compress, []
+        if not pending or self._kv_compressor is None:
+            return
+        cfg = self.config
+        L = cfg.num_layers
+        groups: Dict[Any, list] = {}
+        for item in pending:
+            groups.setdefault(item[3].dtype, []).append(item)
+        signs, jl, lut = self._tq_buffers
+        lib = _lib.load()
+        for dtype, items in groups.items():
+            # (page, layer) pairs flattened to page * L + layer, so that one
+            # launch covers every layer: the pool is viewed as [P * L, 1, ...].
+            flat = torch.cat([it[1].to(torch.int64) * L + it[0] for it in items]).to(torch.int32)
+            slots = torch.cat([it[2] for it in items])
+            key = torch.cat([it[3] for it in items])
+            value = torch.cat([it[4] for it in items])
+            N = key.shape[0]
+            rc = lib.vrm_tq_quant_append(
+                _lib.ptr(key), _lib.ptr(value), _lib.src_dtype_code(dtype), _lib.ptr(flat), _lib.ptr(slots), N,
+                _lib.ptr(self._tq_pool), cfg.num_kv_heads, cfg.head_dim, cfg.page_size, 1, cfg.max_pages * L, 0,
+                cfg.compression_bits, self._kv_compressor.qjl_dim, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut),
+                _lib.stream_of(key))
+            _lib.check(rc, "flush_compression")
+        for layer_idx, pids, slots, _, _, host in pending:
+            pairs = host if host is not None else list(zip(pids.tolist(), slots.tolist()))
+            for pid, slot in pairs:
+                if 0 <= pid < cfg.max_pages and 0 <= slot < cfg.page_size:
+                    self._tq_slots[pid, layer_idx] |= np.uint32(1 << slot)
+
+    def read_kv(self, request_id: str, layer_idx: int) -> Optional[Tuple[Any, Any]]:
+        """(keys, values) of a request for one layer, [num_kv_heads, tokens,
+        head_dim] (core/paged_attention.py:677-712); quantized pools are
+        dequantized to float32."""
+        import torch
+
+        if self._gpu_pool is None:
+            return None
+        with self._lock:
+            entry = self._page_tables.get(request_id)
+            if entry is None or not entry.pages:
+                return None
+            page_ids, tokens = list(entry.pages), entry.num_tokens
+        cfg = self.config
+        ids = torch.tensor(page_ids, dtype=torch.int32).to(self._gpu_pool.device)
+        if self._kv_scales is not None:
+            from . import kv_quant
+
+            pages = kv_quant.dequantize_pages(self._gpu_pool, self._kv_scales, layer_idx, ids)
+        else:
+            pages = self._gpu_pool[ids.long(), layer_idx]
+        # [n, 2, KH, PS, D] -> [KH, n * PS, D] per K/V
+        keys = pages[:, 0].permute(1, 0, 2, 3).reshape(cfg.num_kv_heads, -1, cfg.head_dim)[:, :tokens]
+        values = pages[:, 1].permute(1, 0, 2, 3).reshape(cfg.num_kv_heads, -1, cfg.head_dim)[:, :tokens]
+        return keys, values
+
+    # ------------------------------------------------------------------
+    # Decode (core/paged_attention.py:1193-1418)
+    # ------------------------------------------------------------------
+
+    def _block_table(self, request_ids: Sequence[str], device) -> Optional[tuple]:
+        """Device (page_table [B, max_pp], context_lens [B]) for a batch of
+        requests, rebuilt only when a page list or token count changed."""
+        import torch
+
+        key = (tuple(request_ids), self._epoch, str(device))
+        if self._table_cache is not None and self._table_cache[0] == key:
+            return self._table_cache[1]
+        with self._lock:
+            lists, ntok = [], []
+            for rid in request_ids:
+                entry = self._page_tables.get(rid)
+                lists.append(entry.pages if entry is not None else [])
+                ntok.append(entry.num_tokens if entry is not None else 0)
+            key = (tuple(request_ids), self._epoch, str(device))
+        B = len(request_ids)
+        counts = np.fromiter((len(p) for p in lists), dtype=np.int64, count=B)
+        max_pp = int(counts.max()) if B else 0
+        if max_pp == 0:
+            return None
+        total = int(counts.sum())
+        host = np.empty(2 * B + 1 + total, dtype=np.int32)  # offsets, token counts, pages: one upload
+        host[0] = 0
+        np.cumsum(counts, out=host[1:B + 1])
+        host[B + 1:2 * B + 1] = ntok
+        host[2 * B + 1:] = np.fromiter(itertools.chain.from_iterable(lists), dtype=np.int32, count=total)
+        buf = torch.from_numpy(host).to(device)
+        table = torch.empty((B, max_pp), dtype=torch.int32, device=device)
+        ctx = torch.empty((B,), dtype=torch.int32, device=device)
+        rc = _lib.load().vrm_build_block_table(
+            _lib.ptr(buf[2 * B + 1:]) if total else None, total, _lib.ptr(buf), _lib.ptr(buf[B + 1:]), B, max_pp,
+            _lib.ptr(table), _lib.ptr(ctx), _lib.stream_of(table))
+        _lib.check(rc, "build_block_table")
+        result = (table, ctx)
+        self._table_cache = (key, result, buf)
+        return result
+
+    def _workspace(self, B: int, H: int, max_pp: int, device):
+        from .paged_attention_cuda import decode_workspace
+
+        cfg = self.config
+        key = (B, H, max_pp, str(device))
+        ws = self._workspaces.get(key)
+        if ws is None:
+            if len(self._workspaces) > 8:
+                self._workspaces.clear()
+            ws = decode_workspace(B, H, cfg.num_kv_heads, cfg.head_dim, max_pp, device, cfg.page_size)
+            self._workspaces[key] = ws
+        return ws
+
+    def compute_attention_decode(self, query: Any, request_ids: list, layer_idx: int,
+                                 scale: Optional[float] = None) -> Any:
+        """Decode attention of a batch straight from the pool: query [B, H, D]
+        -> [B, H, D] float32 (core/paged_attention.py:1193-1253).  Returns
+        ``None`` without a pool or when no request has a page."""
+        from .paged_attention_cuda import paged_attention_decode
+
+        if self._gpu_pool is None:
+            return None
+        got = self._block_table(request_ids, query.device)
+        if got is None:
+            return None
+        table, ctx = got
+        B, H = query.shape[0], query.shape[1]
+        return paged_attention_decode(query, self._gpu_pool, table, ctx, layer_idx, scale, kv_scales=self._kv_scales,
+                                      workspace=self._workspace(B, H, table.shape[1], query.device))
+
+    def _ensure_compressed(self, page_ids: Sequence[int], layer_idx: int) -> None:
+        missing = [p for p in dict.fromkeys(page_ids) if self._tq_slots[p, layer_idx] == 0]
+        for pid in missing:
+            self.compress_page_bulk(pid)
+
+    def compute_attention_turbo(self, query: Any, request_id: str, layer_idx: int,
+                                scale: Optional[float] = None) -> Any:
+        """Attention of one request's query [num_heads, head_dim] over its
+        TurboQuant pages (core/paged_attention.py:1259-1418): QJL-corrected
+        scores of the rotated query, softmax, dense decompressed values, with
+        query head h reading kv-head h % num_kv_heads.  Returns [num_heads,
+        head_dim] float32, or ``None`` without compression or data."""
+        if self._kv_compressor is None:
+            return None
+        with self._lock:
+            entry = self._page_tables.get(request_id)
+            if entry is None or not entry.pages:
+                return None
+            page_ids, num_tokens = list(entry.pages), entry.num_tokens
+        if num_tokens <= 0:
+            return None
+        self._require_pool("compute_attention_turbo")
+        self._ensure_compressed(page_ids, layer_idx)
+        num_heads = query.shape[0] if query.dim() >= 2 else 1
+        q = query.reshape(1, num_heads, self.config.head_dim)
+        return self._turbo_decode(q, [page_ids], [num_tokens], layer_idx, scale)[0]
+
+    def compute_attention_turbo_batch(self, query: Any, request_ids: Sequence[str], layer_idx: int,
+                                      scale: Optional[float] = None) -> Any:
+        """``compute_attention_turbo`` for a batch in one launch: query
+        [B, H, D] -> [B, H, D] float32; a request without pages or tokens
+        gets zeros."""
+        import torch
+
+        if self._kv_compressor is None:
+            return None
+        self._require_pool("compute_attention_turbo_batch")
+        with self._lock:
+            lists, ntok = [], []
+            for rid in request_ids:
+                entry = self._page_tables.get(rid)
+                lists.append(list(entry.pages) if entry is not None else [])
+                ntok.append(entry.num_tokens if entry is not None else 0)
+        for pages, n in zip(lists, ntok):
+            if n > 0:
+                self._ensure_compressed(pages[:math.ceil(n / self.config.page_size)], layer_idx)
+        if not any(lists):
+            return torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+        return self._turbo_decode(query, lists, ntok, layer_idx, scale)
+
+    def _turbo_decode(self, query, lists, ntok, layer_idx, scale):
+        """Paged TurboQuant decode with the reference's h % n_kv head mapping.
+
+        The kernel gives query head j kv-head j // (H / KH); the reference's
+        group of kv-head k is heads k, k + KH, k + 2 KH, ..., so query heads
+        are permuted into kernel order (j = k * (H / KH) + g for head
+        g * KH + k) and the output permuted back."""
+        import torch
+
+        cfg = self.config
+        KH, D = cfg.num_kv_heads, cfg.head_dim
+        B, H = query.shape[0], query.shape[1]
+        if H % KH:
+            raise RuntimeError(f"num_heads {H} is not a multiple of num_kv_heads {KH}")
+        if cfg.sparse_v_ratio < 1.0 and any(max(1, math.ceil(cfg.sparse_v_ratio * n)) < n for n in ntok):
+            raise NotImplementedError("sparse V (sparse_v_ratio < 1) is not implemented for TurboQuant pages")
+        dev = self._tq_pool.device
+        ratio = H // KH
+        order = torch.arange(H).reshape(ratio, KH).t().reshape(-1)  # kernel head j <- reference head order[j]
+        q = query.to(dev, torch.float32)[:, order.to(dev)].contiguous()
+        max_pp = max(1, max(len(p) for p in lists))
+        table = np.full((B, max_pp + 1), -1, dtype=np.int32)  # last column: context lengths
+        for b, pages in enumerate(lists):
+            table[b, :len(pages)] = pages
+            table[b, max_pp] = ntok[b]
+        t = torch.from_numpy(table).to(dev)
+        page_table = t[:, :max_pp].contiguous()
+        ctx = t[:, max_pp].contiguous()
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+        ws = self._workspace(B, H, max_pp, dev)
+        signs, jl, lut = self._tq_buffers
+        rc = _lib.load().vrm_paged_decode_tq(
+            _lib.ptr(q), _lib.ptr(self._tq_pool), _lib.ptr(page_table), _lib.ptr(ctx), _lib.ptr(out), _lib.ptr(ws),
+            ws.numel() * ws.element_size(), B, H, KH, D, cfg.page_size, cfg.num_layers, cfg.max_pages, max_pp,
+            int(layer_idx), float(scale), cfg.compression_bits, self._kv_compressor.qjl_dim, _lib.ptr(signs),
+            _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(q))
+        _lib.check(rc, "compute_attention_turbo")
+        inverse = torch.empty_like(order)
+        inverse[order] = torch.arange(H)
+        return out[:, inverse.to(dev)]
+
+    def compress_page_bulk(self, page_id: int, num_valid_slots: int = 0) -> bool:
+        """Compresses a page's raw K/V into TurboQuant codes for every layer
+        that has none yet; slots from ``num_valid_slots`` on (when > 0) get
+        zero codes (core/paged_attention.py:1420-1496).  False without
+        compression, without a pool or for a free page."""
+        import torch
+
+        if self._kv_compressor is None or self._gpu_pool is None:
+            return False
+        cfg = self.config
+        if not 0 <= page_id < cfg.max_pages or not self._pages[page_id].allocated:
+            return False
+        ps = num_valid_slots if num_valid_slots > 0 else cfg.page_size
+        ps = min(ps, cfg.page_size)
+        layers = [l for l in range(cfg.num_layers) if self._tq_slots[page_id, l] == 0]
+        if not layers:
+            return True
+        L = cfg.num_layers
+        host = np.array([[page_id * L + l for l in layers], [ps] * len(layers)], dtype=np.int32)
+        dev = torch.from_numpy(host).to(self._gpu_pool.device)
+        signs, jl, lut = self._tq_buffers
+        rc = _lib.load().vrm_tq_compress_pool(
+            _lib.ptr(self._gpu_pool), _lib.kv_dtype_code(self._gpu_pool.dtype), _lib.ptr(dev[0]), _lib.ptr(dev[1]),
+            len(layers), _lib.ptr(self._tq_pool), cfg.num_kv_heads, cfg.head_dim, cfg.page_size, 1,
+            cfg.max_pages * L, 0, cfg.compression_bits, self._kv_compressor.qjl_dim, _lib.ptr(signs), _lib.ptr(jl),
+            _lib.ptr(lut), _lib.stream_of(self._gpu_pool))
+        _lib.check(rc, "compress_page_bulk")
+        self._tq_slots[page_id, layers] = np.uint32((1 << ps) - 1)
+        return True
+
+    # ------------------------------------------------------------------
+    # Introspection
+    # ------------------------------------------------------------------
+
+    @property
+    def kv_compression_active(self) -> bool:
+        return self._kv_compressor is not None
+
+    @property
+    def compression_ratio(self) -> float:
+        """fp16 bits per dim over the compressor's bits per dim."""
+        if self._kv_compressor is None:
+            return 1.0
+        return 16.0 / self._kv_compressor.bits_per_dim()
+
+    def stats(self) -> Dict[str, Any]:
+        used = self.config.max_pages - len(self._free_pages)
+        compressed = int(np.count_nonzero(self._tq_slots.any(axis=1))) if self._tq_slots is not None else 0
+        return {
+            "total_pages": len(self._pages),
+            "used_pages": used,
+            "free_pages": len(self._free_pages),
+            "utilization": used / max(len(self._pages), 1),
+            "peak_usage": self._peak_usage,
+            "total_allocations": self._total_allocations,
+            "total_frees": self._total_frees,
+            "active_requests": len(self._page_tables),
+            "page_size_tokens": self.config.page_size,
+            "memory_mb": self.config.total_memory_bytes / 1e6,
+            "devices": [self.config.device],
+            "kv_compression": self.config.kv_compression or "none",
+            "compressed_pages": compressed,
+            "compression_ratio": self.compression_ratio,
+        }
+
+    def __repr__(self) -> str:
+        s = self.stats()
+        return (f"PagedKVCache(pages={s['used_pages']}/{s['total_pages']}, "
+                f"requests={s['active_requests']}, mem={s['memory_mb']:.1f}MB)")
