@@ -69,9 +69,16 @@ const char* vrm_last_error(void);
  * Paged decode attention.
  * -------------------------------------------------------------------------- */
 
-/* Number of token partitions (split-K) vrm_paged_decode will use for a call of
- * this shape, and the workspace bytes it needs.  Both depend only on the
- * arguments (no device state).  max_pp is the page-table width. */
+/* Workspace sizing.  The decode cuts every sequence's pages into partitions
+ * whose size the device derives from the context lengths; a batch never has
+ * more than B + 2 * ceil(4096 / KH) partitions (work items).
+ * vrm_paged_decode_num_splits returns that capacity per sequence,
+ * ceil(capacity / B), and vrm_paged_decode_workspace_bytes the bytes for
+ * B * nsplit items: a 256-byte aligned header of 16 + 2B + 1 ints (partition
+ * geometry, written by the partition pass for the merge), then
+ * [items][H][D] float32 accumulators and [items][H][2] (max, sum).  Both
+ * depend only on the arguments (no device state); max_pp is the page-table
+ * width. */
 int vrm_paged_decode_num_splits(int B, int H, int KH, int max_pp, int page_size);
 size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit);
 
