@@ -234,6 +234,42 @@ int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* angles, int
                               const float* signs, const float* angle_lut, float* out,
                               int rotated, vrm_stream_t stream);
 
+/*
+ * scores[M][N] float32 = out_scale * (q_rot . k_polar + QJL correction) for M
+ * query rows q [M][head_dim] float32 against N compressed keys in the raw
+ * format of vrm_turboquant_compress: KVCacheCompressor.attention_score
+ * (core/kv_quantizer.py:502-535; q_rot = rotate(pad(q)), k_polar the polar
+ * decode from the fp16 radius, correction = (q_rot JL^T . (2 s - 1)) *
+ * sqrt(pi / 2) / qjl_dim * norm).  Replaces the tensor-op path of
+ * CUDATurboQuantOps.attention_score_gpu (core/turboquant_cuda.py:208-255),
+ * with the rotated query in both terms as the reference's CPU path has it.
+ * workspace: >= vrm_turboquant_score_workspace_bytes(M, padded_dim, qjl_dim)
+ * bytes (the rotated and projected queries).  M <= 65535.
+ */
+size_t vrm_turboquant_score_workspace_bytes(int M, int padded_dim, int qjl_dim);
+int vrm_turboquant_score(const float* q, int M, const uint16_t* radius, const uint8_t* angles,
+                         const uint8_t* qjl_signs, const uint16_t* qjl_norms, int N, int head_dim,
+                         int padded_dim, int n_levels, int bits, int qjl_dim, const float* signs,
+                         const float* jl, const float* angle_lut, float out_scale, float* workspace,
+                         size_t workspace_bytes, float* scores, vrm_stream_t stream);
+
+/*
+ * Top-k ("sparse V") attention over explicit scores: for each row m of
+ * scores[M][N] (row stride ld_scores), the k largest scores S_m are kept and
+ *   out[m][:] = sum_{n in S_m} e^(s_mn - max) values[n][:] / sum_{n in S_m} e^(s_mn - max),
+ * the renormalised top-k softmax weights of KVCacheCompressor.sparse_v_attend
+ * (core/kv_quantizer.py:537-562) and of compute_attention_turbo with
+ * sparse_v_ratio < 1 (core/paged_attention.py:1384-1400).  Of scores equal to
+ * the k-th largest, the lowest-indexed are kept.  k = N is the dense
+ * softmax(scores) values.  values [N][D] (row stride ld_values), out [M][D]
+ * (row stride ld_out), float32; 1 <= k <= N.
+ * workspace: >= vrm_topk_attend_workspace_bytes(M, k) bytes.
+ */
+size_t vrm_topk_attend_workspace_bytes(int M, int k);
+int vrm_topk_attend(const float* scores, int M, int N, long long ld_scores, int k, const float* values,
+                    int D, long long ld_values, float* out, long long ld_out, void* workspace,
+                    size_t workspace_bytes, vrm_stream_t stream);
+
 /* --------------------------------------------------------------------------
  * TurboQuant pages.  The reference keeps TurboQuant-compressed K/V in Python
  * dicts per (page, layer, slot) (core/paged_attention.py:568-675, 1420-1496)

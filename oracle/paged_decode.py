@@ -141,7 +141,8 @@ def dense_attention(q, K, V, scale):
     return out
 
 
-def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scale=None, head_map="div"):
+def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scale=None, head_map="div",
+                                 sparse_v_ratio=1.0):
     """[B, H, D] float32 attention over TurboQuant pages, as
     PagedKVCacheManager.compute_attention_turbo (core/paged_attention.py:
     1259-1418) evaluates it with dense values (sparse_v_ratio 1.0): per kv-head,
@@ -150,7 +151,9 @@ def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scal
     then weights @ decompress(values) (core/kv_quantizer.py:481-500).  With
     head_map "div" query head h reads kv-head h // (H / KH), the paged
     decode's mapping; with "mod" it reads kv-head h % KH, the mapping of
-    compute_attention_turbo itself (core/paged_attention.py:1374).
+    compute_attention_turbo itself (core/paged_attention.py:1374).  With
+    sparse_v_ratio < 1 each head keeps its top ceil(ratio * seq) softmax
+    weights, renormalised, over the values of those tokens (:1384-1400).
 
     ``p`` are the compressor's parameters (oracle.turboquant.make_params);
     ``codes`` holds one layer's raw codes indexed [page, K/V, kv-head, token]:
@@ -199,5 +202,14 @@ def paged_attention_decode_turbo(p, query, codes, page_table, context_lens, scal
             q_group = query[b, group].float()
             scores = TQ.attention_score(p, q_group, ck) * scale
             weights = torch.softmax(scores, dim=-1)
-            out[b, group] = weights @ TQ.decompress(p, cv)
+            values = TQ.decompress(p, cv)
+            seq = weights.shape[-1]
+            k = max(1, int(math.ceil(sparse_v_ratio * seq)))
+            if k < seq:
+                for gi, h in enumerate(group):
+                    top_w, top_i = weights[gi:gi + 1].topk(k, dim=-1)
+                    top_w = top_w / top_w.sum(dim=-1, keepdim=True)
+                    out[b, h] = (top_w @ values[top_i[0]])[0]
+            else:
+                out[b, group] = weights @ values
     return out

@@ -290,12 +290,3 @@ def test_turbo_batch_matches_single_requests():
     table, ctx = _host_table(m, rids)
     ref = PD.paged_attention_decode_turbo(_params(m._kv_compressor), qb, _codes(m, 0), table, ctx, head_map="mod")
     _assert_close(out, ref, "batch vs oracle")
-
-
-def test_turbo_sparse_v_is_refused_loudly():
-    torch.manual_seed(1)
-    m = _mgr(dtype="bfloat16", kv_compression="turboquant", sparse_v_ratio=0.3, num_layers=1)
-    _fill(m, ["a"], [10], torch.bfloat16, seed=1)
-    m.flush_compression()
-    with pytest.raises(NotImplementedError):
-        m.compute_attention_turbo(torch.randn(2, 128, device=DEV), "a", 0)

@@ -396,3 +396,42 @@ def test_turbo_paged_oracle_relabel_invariance():
     codes2 = {k: v[perm] for k, v in codes.items()}
     out2 = PD.paged_attention_decode_turbo(p, q, codes2, inv[table.long()].to(torch.int32), lens)
     assert torch.equal(out, out2)
+
+
+def test_turbo_paged_oracle_sparse_v_closed_forms():
+    # sparse V keeps the top-k softmax weights of each head and renormalises
+    # them: with zero residual norms this is the fp64 softmax over the k
+    # largest scores of the decompressed keys; k = 1 returns the value row of
+    # the best-scoring token; a ratio reaching every token is the dense path
+    p = TQ.make_params(128, 3, seed=9)
+    P, KH, H = 5, 2, 4
+    codes = _turbo_codes(p, P, KH, 12)
+    codes["qjl_norms"].zero_()
+    q = torch.randn(1, H, 128, generator=torch.Generator().manual_seed(13))
+    table = torch.tensor([[3, 0, 4, 1]], dtype=torch.int32)
+    lens = torch.tensor([57], dtype=torch.int32)
+    dense = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.1, head_map="mod")
+    full = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.1, head_map="mod", sparse_v_ratio=0.999)
+    assert torch.equal(dense, full)  # ceil(0.999 * 57) = 57 keeps every token
+    ks, vs = [], []
+    for t in range(57):
+        pid, s = int(table[0, t // 16]), t % 16
+        rows = []
+        for kv in range(2):
+            c = {"radius": codes["radius"][pid, kv, :, s].reshape(-1, 1),
+                 "angles": list(torch.split(codes["angles"][pid, kv, :, s], [64, 32, 16, 8, 4, 2, 1], -1)),
+                 "shape": (KH, 128)}
+            rows.append(TQ.decompress(p, c).double())
+        ks.append(rows[0])
+        vs.append(rows[1])
+    K, V = torch.stack(ks, 1), torch.stack(vs, 1)
+    for ratio, k in ((0.3, 18), (0.01, 1)):
+        out = PD.paged_attention_decode_turbo(p, q, codes, table, lens, scale=0.1, head_map="mod",
+                                              sparse_v_ratio=ratio)
+        for h in range(H):
+            s = 0.1 * (K[h % KH] @ q[0, h].double())
+            top = torch.argsort(s, descending=True)[:k]
+            w = torch.softmax(s[top], 0)
+            torch.testing.assert_close(out[0, h].double(), w @ V[h % KH][top], atol=2e-5, rtol=1e-5)
+            if k == 1:
+                torch.testing.assert_close(out[0, h].double(), V[h % KH][int(s.argmax())], atol=1e-6, rtol=1e-6)

@@ -33,6 +33,7 @@ _p = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_ll = ctypes.c_longlong
 
 # name -> (restype, argtypes); mirrors include/vrm_paged.h
 SIGNATURES = {
@@ -57,6 +58,10 @@ SIGNATURES = {
     "vrm_tq_compress_pool": (_i, [_p, _i, _p, _p, _i, _p] + [_i] * 8 + [_p, _p, _p, _p]),
     "vrm_build_block_table": (_i, [_p, _i, _p, _p, _i, _i, _p, _p, _p]),
     "vrm_kv_write": (_i, [_p, _p, _i, _p, _p, _i, _p] + [_i] * 7 + [_p]),
+    "vrm_turboquant_score_workspace_bytes": (_sz, [_i, _i, _i]),
+    "vrm_turboquant_score": (_i, [_p, _i, _p, _p, _p, _p] + [_i] * 6 + [_p, _p, _p, _f, _p, _sz, _p, _p]),
+    "vrm_topk_attend_workspace_bytes": (_sz, [_i, _i]),
+    "vrm_topk_attend": (_i, [_p, _i, _i, _ll, _i, _p, _i, _ll, _p, _ll, _p, _sz, _p]),
 }
 
 

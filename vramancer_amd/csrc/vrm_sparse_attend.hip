@@ -1,0 +1,210 @@
+// Top-k ("sparse V") attention over explicit scores.
+//
+// The reference keeps, per query row, the k largest softmax weights,
+// renormalises them and takes their weighted sum of values
+// (KVCacheCompressor.sparse_v_attend, core/kv_quantizer.py:537-562, and
+// compute_attention_turbo with sparse_v_ratio < 1, core/paged_attention.py:
+// 1384-1400).  Softmax is monotonic, so the kept tokens are the k largest
+// scores, and the renormalised weights are the softmax over the kept tokens
+// alone:
+//   out[m] = sum_{n in S_m} e^(s_mn - max) v_n / sum_{n in S_m} e^(s_mn - max).
+// With k = N this is the dense softmax(s) V of the reference's k >= seq_len
+// branch.
+//
+// Selection (topk_select_kernel): the k-th largest score T of each row by a
+// radix select, four passes of 8 bits over an order-preserving integer key,
+// one workgroup per row.  S_m is every score above T plus, of the scores equal
+// to T, the lowest-indexed ones up to k in total (the reference's topk leaves
+// the choice among equal weights unspecified).  topk_attend_kernel compacts
+// S_m in index order, then computes the weights and the weighted sum (one
+// thread per value dimension).
+#include "vrm_common.h"
+
+#include <math.h>
+
+namespace vrm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+// Ascending float order <-> ascending unsigned order.
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* scores, int N, long long ld, int k,
+                                                               uint32_t* sel) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_remaining;
+  const int tid = threadIdx.x;
+  const float* row = scores + (size_t)blockIdx.x * ld;
+  uint32_t prefix = 0, mask = 0, remaining = (uint32_t)k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;  // kThreads == 256 bins
+    __syncthreads();
+    for (int n = tid; n < N; n += kThreads) {
+      const uint32_t key = order_key(row[n]);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      // walk the bins from the largest keys down until the k-th is inside
+      uint32_t r = remaining;
+      int b = 255;
+      for (; b > 0 && r > hist[b]; --b) r -= hist[b];
+      s_prefix = prefix | ((uint32_t)b << shift);
+      s_remaining = r;
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    remaining = s_remaining;
+    mask |= 255u << shift;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    sel[2 * blockIdx.x] = prefix;        // key of T
+    sel[2 * blockIdx.x + 1] = remaining;  // scores equal to T that are kept
+  }
+}
+
+// Exclusive prefix sum over the workgroup; `total` gets the sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int& total, int* lds) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __builtin_amdgcn_ds_bpermute(max(lane - d, 0) << 2, inc);
+    if (lane >= d) inc += t;
+  }
+  if (lane == 63) lds[w] = inc;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const int c = lds[i];
+    base += i < w ? c : 0;
+    total += c;
+  }
+  __syncthreads();
+  return base + inc - v;
+}
+
+__device__ __forceinline__ float block_max(float v, float* lds) {
+  v = group_max<64>(v);
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = lds[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, lds[i]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+  v = group_sum<64>(v);
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r += lds[i];
+  __syncthreads();
+  return r;
+}
+
+// One workgroup per row.  idx_ws / w_ws: [rows][k] scratch (indices, weights).
+__global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scores, int N, long long ld, int k,
+                                                               const uint32_t* sel, const float* values, int D,
+                                                               long long ldv, int32_t* idx_ws, float* w_ws,
+                                                               float* out, long long ldo) {
+  __shared__ int scan_lds[kWaves];
+  __shared__ float red_lds[kWaves];
+  const int tid = threadIdx.x;
+  const int m = blockIdx.x;
+  const float* row = scores + (size_t)m * ld;
+  const uint32_t t_key = sel[2 * m];
+  const int ties = (int)sel[2 * m + 1];
+  int32_t* idx = idx_ws + (size_t)m * k;
+  float* wts = w_ws + (size_t)m * k;
+  int count = 0, ties_seen = 0;
+  float mx = -INFINITY;
+  for (int base = 0; base < N; base += kThreads) {
+    const int n = base + tid;
+    const float s = n < N ? row[n] : 0.f;
+    const uint32_t key = order_key(s);
+    const bool eq = n < N && key == t_key;
+    int eq_total;
+    const int eq_rank = block_exclusive_scan(eq ? 1 : 0, eq_total, scan_lds) + ties_seen;
+    const bool take = n < N && (key > t_key || (eq && eq_rank < ties));
+    int take_total;
+    const int pos = block_exclusive_scan(take ? 1 : 0, take_total, scan_lds) + count;
+    if (take && pos < k) {
+      idx[pos] = n;
+      mx = fmaxf(mx, s);
+    }
+    ties_seen += eq_total;
+    count += take_total;
+  }
+  count = min(count, k);
+  mx = block_max(mx, red_lds);
+  float part = 0.f;
+  for (int i = tid; i < count; i += kThreads) {
+    const float w = expf(row[idx[i]] - mx);
+    wts[i] = w;
+    part += w;
+  }
+  const float l = block_sum(part, red_lds);  // its barriers also publish idx / wts to the workgroup
+  for (int d = tid; d < D; d += kThreads) {
+    float acc = 0.f;
+    for (int i = 0; i < count; ++i) acc = fmaf(wts[i], values[(size_t)idx[i] * ldv + d], acc);
+    out[(size_t)m * ldo + d] = acc / l;
+  }
+}
+
+}  // namespace
+}  // namespace vrm
+
+using namespace vrm;
+
+extern "C" size_t vrm_topk_attend_workspace_bytes(int M, int k) {
+  if (M < 0 || k < 0) return 0;
+  return (size_t)M * 2 * sizeof(uint32_t) + (size_t)M * (size_t)k * (sizeof(int32_t) + sizeof(float));
+}
+
+extern "C" int vrm_topk_attend(const float* scores, int M, int N, long long ld_scores, int k, const float* values,
+                               int D, long long ld_values, float* out, long long ld_out, void* workspace,
+                               size_t workspace_bytes, vrm_stream_t stream) {
+  const char* who = "vrm_topk_attend";
+  if (M < 0 || N <= 0 || D <= 0 || k < 1 || k > N || ld_scores < N || ld_values < D || ld_out < D) {
+    set_error("%s: bad sizes (M=%d N=%d k=%d D=%d ld=%lld/%lld/%lld)", who, M, N, k, D, ld_scores, ld_values,
+              ld_out);
+    return VRM_ERR_ARG;
+  }
+  if (M > 0x7fffffff / 2) {
+    set_error("%s: too many rows (%d)", who, M);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (workspace_bytes < vrm_topk_attend_workspace_bytes(M, k)) {
+    set_error("%s: workspace of %zu bytes, need %zu", who, workspace_bytes, vrm_topk_attend_workspace_bytes(M, k));
+    return VRM_ERR_WORKSPACE;
+  }
+  if (M == 0) {
+    clear_error();
+    return VRM_OK;
+  }
+  if (!scores || !values || !out || !workspace) {
+    set_error("%s: null pointer argument", who);
+    return VRM_ERR_ARG;
+  }
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint32_t* sel = reinterpret_cast<uint32_t*>(ws);
+  int32_t* idx = reinterpret_cast<int32_t*>(ws + (size_t)M * 2 * sizeof(uint32_t));
+  float* wts = reinterpret_cast<float*>(ws + (size_t)M * 2 * sizeof(uint32_t) + (size_t)M * k * sizeof(int32_t));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel);
+  hipLaunchKernelGGL(topk_attend_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel, values, D,
+                     ld_values, idx, wts, out, ld_out);
+  return launch_status(who);
+}

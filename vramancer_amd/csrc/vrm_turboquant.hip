@@ -397,6 +397,76 @@ __global__ void __launch_bounds__(64) tq_decompress_kernel(TqArgs a, int rotated
   }
 }
 
+// Query side of KVCacheCompressor.attention_score (core/kv_quantizer.py:
+// 516-521, 319-321): q_rot = rotate(pad(q)) and q_proj = q_rot JL^T.  One
+// wavefront per query row m; ws row m holds [q_rot (PD) | q_proj (qjl_dim)].
+template <int PD>
+__global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_dim, const float* signs,
+                                                      const float* jl, int qjl_dim, float* ws) {
+  constexpr int PER = PD / 64;
+  __shared__ float rot[PD];
+  const int lane = threadIdx.x;
+  const int m = blockIdx.x;
+  float v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = k * 64 + lane;
+    const float x = e < head_dim ? q[(size_t)m * head_dim + e] : 0.f;
+    v[k] = __fmul_rn(x, signs[e]);
+  }
+  fwht<PD>(v, lane);
+  const float root = (float)sqrt((double)PD);
+  float* out = ws + (size_t)m * (PD + qjl_dim);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    v[k] = __fdiv_rn(v[k], root);
+    rot[k * 64 + lane] = v[k];
+    out[k * 64 + lane] = v[k];
+  }
+  __syncthreads();
+  for (int j = lane; j < qjl_dim; j += 64) {
+    const float* row = jl + (size_t)j * PD;
+    float acc = 0.f;
+    for (int e = 0; e < PD; ++e) acc = __fadd_rn(acc, __fmul_rn(rot[e], row[e]));
+    out[PD + j] = acc;
+  }
+}
+
+// Key side: one wavefront per compressed key n rebuilds k_polar (the polar
+// decode from the fp16 radius, as attention_score does), then each lane
+// scores query rows m = lane, lane + 64, ...:
+//   scores[m][n] = out_scale * (q_rot[m] . k_polar[n] + (q_proj[m] . (2 s_n - 1)) * coef * norm_n)
+// with coef = sqrt(pi / 2) / qjl_dim (core/kv_quantizer.py:523-535).
+template <int PD>
+__global__ void __launch_bounds__(64) tq_score_kernel(const float* ws, int M, int qjl_dim, const uint16_t* radius,
+                                                      const uint8_t* angles, const uint8_t* qjl_signs,
+                                                      const uint16_t* qjl_norms, int N, const float* lut, int bits,
+                                                      float coef, float out_scale, float* scores) {
+  __shared__ float bufA[PD / 2];
+  __shared__ float bufB[PD / 2];
+  __shared__ float recon[PD];
+  __shared__ uint8_t bins[PD];
+  __shared__ float sgn[4 * PD];
+  const int lane = threadIdx.x;
+  const int n = blockIdx.x;
+  for (int i = lane; i < PD - 1; i += 64) bins[i] = angles[(size_t)n * (PD - 1) + i];
+  for (int j = lane; j < qjl_dim; j += 64)
+    sgn[j] = __fsub_rn(__fmul_rn((float)qjl_signs[(size_t)n * qjl_dim + j], 2.f), 1.f);
+  const float r = f16_bits_to_f32(radius[n]);
+  const float norm = f16_bits_to_f32(qjl_norms[n]);
+  __syncthreads();
+  polar_decode<PD>(r, bins, lut, 1 << bits, bufA, bufB, recon, lane);
+  for (int m = lane; m < M; m += 64) {
+    const float* qr = ws + (size_t)m * (PD + qjl_dim);
+    float dot = 0.f;
+    for (int e = 0; e < PD; ++e) dot = __fadd_rn(dot, __fmul_rn(qr[e], recon[e]));
+    float raw = 0.f;
+    for (int j = 0; j < qjl_dim; ++j) raw = __fadd_rn(raw, __fmul_rn(qr[PD + j], sgn[j]));
+    const float corr = __fmul_rn(__fmul_rn(raw, coef), norm);
+    scores[(size_t)m * N + n] = __fmul_rn(__fadd_rn(dot, corr), out_scale);
+  }
+}
+
 int check_tq(int N, int head_dim, int padded_dim, int n_levels, int bits, const char* who) {
   if (N < 0 || head_dim <= 0 || head_dim > padded_dim) {
     set_error("%s: bad sizes (N=%d head_dim=%d padded_dim=%d)", who, N, head_dim, padded_dim);
@@ -609,6 +679,56 @@ extern "C" int vrm_tq_quant_pages(const void* key, const void* value, int src_dt
   }
   return tq_pool_write(key, value, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D, PS,
                        L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who);
+}
+
+extern "C" size_t vrm_turboquant_score_workspace_bytes(int M, int padded_dim, int qjl_dim) {
+  if (M < 0 || padded_dim <= 0 || qjl_dim < 0) return 0;
+  return (size_t)M * (size_t)(padded_dim + qjl_dim) * sizeof(float);
+}
+
+extern "C" int vrm_turboquant_score(const float* q, int M, const uint16_t* radius, const uint8_t* angles,
+                                    const uint8_t* qjl_signs, const uint16_t* qjl_norms, int N, int head_dim,
+                                    int padded_dim, int n_levels, int bits, int qjl_dim, const float* signs,
+                                    const float* jl, const float* angle_lut, float out_scale, float* workspace,
+                                    size_t workspace_bytes, float* scores, vrm_stream_t stream) {
+  const char* who = "vrm_turboquant_score";
+  int rc = check_tq(N, head_dim, padded_dim, n_levels, bits, who);
+  if (rc) return rc;
+  if (M < 0 || M > 65535 || N > 0x7fffffff / 2) {
+    set_error("%s: bad sizes (M=%d N=%d)", who, M, N);
+    return VRM_ERR_ARG;
+  }
+  if (qjl_dim <= 0 || qjl_dim > 4 * padded_dim) {
+    set_error("%s: qjl_dim %d outside [1, %d]", who, qjl_dim, 4 * padded_dim);
+    return VRM_ERR_ARG;
+  }
+  if (workspace_bytes < vrm_turboquant_score_workspace_bytes(M, padded_dim, qjl_dim)) {
+    set_error("%s: workspace of %zu bytes, need %zu", who, workspace_bytes,
+              vrm_turboquant_score_workspace_bytes(M, padded_dim, qjl_dim));
+    return VRM_ERR_WORKSPACE;
+  }
+  if (M == 0 || N == 0) {
+    clear_error();
+    return VRM_OK;
+  }
+  if (!q || !radius || !angles || !qjl_signs || !qjl_norms || !signs || !jl || !angle_lut || !workspace ||
+      !scores) {
+    set_error("%s: null pointer argument", who);
+    return VRM_ERR_ARG;
+  }
+  const float coef = (float)(sqrt(M_PI / 2.0) / qjl_dim);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define VRM_TQ_SCORE(PDV)                                                                                      \
+  hipLaunchKernelGGL(tq_query_kernel<PDV>, dim3(M), dim3(64), 0, st, q, head_dim, signs, jl, qjl_dim, workspace); \
+  hipLaunchKernelGGL(tq_score_kernel<PDV>, dim3(N), dim3(64), 0, st, workspace, M, qjl_dim, radius, angles,       \
+                     qjl_signs, qjl_norms, N, angle_lut, bits, coef, out_scale, scores)
+  switch (padded_dim) {
+    case 64: VRM_TQ_SCORE(64); break;
+    case 128: VRM_TQ_SCORE(128); break;
+    default: VRM_TQ_SCORE(256); break;
+  }
+#undef VRM_TQ_SCORE
+  return launch_status(who);
 }
 
 extern "C" int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int32_t* page_ids,

@@ -239,20 +239,37 @@ class KVCacheCompressor(nn.Module):
             q, compressed_k, *self._ops_args(), self._hadamard_signs, self.jl_matrix, self.qjl_dim)
 
     def sparse_v_attend(self, q, compressed_k, compressed_v_list, scale=None, sparse_v_ratio=0.1):
-        """Scores from compressed keys, then values of the top ceil(ratio * seq)
-        tokens only (core/kv_quantizer.py:537-562)."""
+        """Scores from compressed keys, then the renormalised softmax over the
+        top ceil(ratio * seq) scores applied to their values
+        (core/kv_quantizer.py:537-562); every step runs in gfx950 kernels.
+        The values are decompressed in one batch; rows of several queries are
+        supported (the reference's sparse branch takes one)."""
+        from .turboquant_cuda import topk_attend
+
         if scale is None:
             scale = 1.0 / math.sqrt(self.head_dim)
-        weights = torch.softmax(self.attention_score(q, compressed_k) * scale, dim=-1)
-        seq_len = weights.shape[-1]
+        compressed_k = self._unpack_compressed(compressed_k)
+        scores = CUDATurboQuantOps.attention_score_gpu(
+            q, compressed_k, *self._ops_args(), self._hadamard_signs, self.jl_matrix, self.qjl_dim, scale=scale)
+        seq_len = scores.shape[-1]
         k = max(1, int(math.ceil(sparse_v_ratio * seq_len)))
-        if k >= seq_len:
-            v_mat = torch.cat([self.decompress(cv) for cv in compressed_v_list], dim=0)
-            return weights @ v_mat
-        topk_w, topk_idx = weights.topk(k, dim=-1)
-        topk_w = topk_w / topk_w.sum(dim=-1, keepdim=True)
-        v_mat = torch.cat([self.decompress(compressed_v_list[int(i)]) for i in topk_idx.squeeze(0).tolist()], dim=0)
-        return topk_w @ v_mat
+        v_mat = self._decompress_list(compressed_v_list)
+        if v_mat.shape[0] != seq_len:
+            raise RuntimeError(f"{v_mat.shape[0]} value rows for {seq_len} keys")
+        return topk_attend(scores, min(k, seq_len), v_mat)
+
+    def _decompress_list(self, compressed_list):
+        """Rows of every dict of the list, decompressed in one launch: [rows, head_dim]."""
+        parts = [self._unpack_compressed(c) for c in compressed_list]
+        if not parts:
+            raise RuntimeError("empty value list")
+        merged = {
+            "radius": torch.cat([c["radius"].reshape(-1) for c in parts]),
+            "angles": [torch.cat([c["angles"][l].reshape(-1, c["angles"][l].shape[-1]) for c in parts])
+                       for l in range(len(parts[0]["angles"]))],
+        }
+        merged["shape"] = (merged["radius"].shape[0], self.head_dim)
+        return CUDATurboQuantOps.decompress_gpu(merged, *self._ops_args(), self._hadamard_signs)
 
     def bits_per_dim(self):
         """((padded_dim - 1) * bits + 16 + qjl_dim + 16) / head_dim."""

@@ -20,7 +20,9 @@ Device side, in this library's kernels:
 * ``compute_attention_turbo`` attends the TurboQuant pages in place
   (``vrm_paged_decode_tq``) with the reference's head mapping ``h % n_kv``
   (:1374); pages with no codes for the layer are first compressed from the
-  raw pool, as the reference's lazy ``compress_page_bulk`` call does;
+  raw pool, as the reference's lazy ``compress_page_bulk`` call does; with
+  ``sparse_v_ratio < 1`` each head keeps its top-k softmax weights
+  (``vrm_turboquant_score`` + ``vrm_topk_attend``, :1384-1400);
 * ``compress_page_bulk`` compresses a page's raw K/V for every layer that has
   no codes yet (``vrm_tq_compress_pool``).
 
@@ -560,7 +562,54 @@ class PagedKVCacheManager:
         self._ensure_compressed(page_ids, layer_idx)
         num_heads = query.shape[0] if query.dim() >= 2 else 1
         q = query.reshape(1, num_heads, self.config.head_dim)
+        if self._sparse_k(num_tokens) < num_tokens:
+            return self._turbo_sparse(q[0], page_ids, num_tokens, layer_idx, scale)
         return self._turbo_decode(q, [page_ids], [num_tokens], layer_idx, scale)[0]
+
+    def _sparse_k(self, num_tokens: int) -> int:
+        """Tokens whose values a head keeps: max(1, ceil(sparse_v_ratio * seq))
+        (core/paged_attention.py:1379-1380)."""
+        return max(1, int(math.ceil(self.config.sparse_v_ratio * num_tokens)))
+
+    def _turbo_sparse(self, q, page_ids, num_tokens, layer_idx, scale):
+        """Sparse V of compute_attention_turbo (core/paged_attention.py:
+        1384-1400) for one request: per kv-head, scores of its query heads
+        (h % KH), the renormalised top-k softmax and the weighted sum of those
+        tokens' values, all in library kernels."""
+        import torch
+
+        from . import tq_pages
+        from .turboquant_cuda import CUDATurboQuantOps, topk_attend
+
+        cfg = self.config
+        KH, D = cfg.num_kv_heads, cfg.head_dim
+        H = q.shape[0]
+        comp = self._kv_compressor
+        dev = self._tq_pool.device
+        ids = torch.tensor(page_ids, dtype=torch.int32).to(dev)
+        codes = tq_pages.read_pages(self._tq_pool, layer_idx, ids, comp)  # [NP, K/V, KH, 16, ...]
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        n = num_tokens
+        k = self._sparse_k(n)
+        qf = q.to(dev, torch.float32)
+        signs, jl = comp._hadamard_signs, comp.jl_matrix
+        args = (D, comp._padded_dim, comp._n_levels, comp.bits_per_angle)
+        out = torch.empty((H, D), dtype=torch.float32, device=dev)
+
+        def tokens(name, kv, kvh):  # the request's first n tokens of one kv-head, page-major
+            t = codes[name][:, kv, kvh]
+            return t.reshape(-1, *t.shape[2:])[:n].contiguous()
+
+        for kvh in range(KH):
+            group = torch.arange(kvh, H, KH, device=dev)
+            keys = {"radius": tokens("radius", 0, kvh), "angles": [tokens("angles", 0, kvh)],
+                    "qjl_signs": tokens("qjl_signs", 0, kvh), "qjl_norms": tokens("qjl_norms", 0, kvh)}
+            scores = CUDATurboQuantOps.attention_score_gpu(qf[group], keys, *args, signs, jl, comp.qjl_dim,
+                                                           scale=scale)
+            vals = {"radius": tokens("radius", 1, kvh), "angles": [tokens("angles", 1, kvh)], "shape": (n, D)}
+            out[group] = topk_attend(scores, k, CUDATurboQuantOps.decompress_gpu(vals, *args, signs))
+        return out
 
     def compute_attention_turbo_batch(self, query: Any, request_ids: Sequence[str], layer_idx: int,
                                       scale: Optional[float] = None) -> Any:
@@ -583,7 +632,11 @@ class PagedKVCacheManager:
                 self._ensure_compressed(pages[:math.ceil(n / self.config.page_size)], layer_idx)
         if not any(lists):
             return torch.zeros(query.shape, dtype=torch.float32, device=query.device)
-        return self._turbo_decode(query, lists, ntok, layer_idx, scale)
+        out = self._turbo_decode(query, lists, ntok, layer_idx, scale)
+        for b, (pages, n) in enumerate(zip(lists, ntok)):
+            if n > 0 and pages and self._sparse_k(n) < n:
+                out[b] = self._turbo_sparse(query[b], pages, n, layer_idx, scale)
+        return out
 
     def _turbo_decode(self, query, lists, ntok, layer_idx, scale):
         """Paged TurboQuant decode with the reference's h % n_kv head mapping.
@@ -599,8 +652,6 @@ class PagedKVCacheManager:
         B, H = query.shape[0], query.shape[1]
         if H % KH:
             raise RuntimeError(f"num_heads {H} is not a multiple of num_kv_heads {KH}")
-        if cfg.sparse_v_ratio < 1.0 and any(max(1, math.ceil(cfg.sparse_v_ratio * n)) < n for n in ntok):
-            raise NotImplementedError("sparse V (sparse_v_ratio < 1) is not implemented for TurboQuant pages")
         dev = self._tq_pool.device
         ratio = H // KH
         order = torch.arange(H).reshape(ratio, KH).t().reshape(-1)  # kernel head j <- reference head order[j]

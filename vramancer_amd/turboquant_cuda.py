@@ -18,7 +18,7 @@ from typing import Dict, Tuple
 
 from . import _lib
 
-__all__ = ["CUDATurboQuantOps", "has_cuda_turboquant", "angle_lut"]
+__all__ = ["CUDATurboQuantOps", "has_cuda_turboquant", "angle_lut", "topk_attend"]
 
 _lut_lock = threading.Lock()
 _lut_cache: Dict[Tuple[int, str], "object"] = {}
@@ -170,24 +170,6 @@ class CUDATurboQuantOps:
                                          hadamard_signs, rotated=True)
 
     @staticmethod
-    def rotate_gpu(x, hadamard_signs, padded_dim: int):
-        """Randomized Hadamard rotation of rows of x (zero-padded to padded_dim)."""
-        import torch
-
-        flat = x.reshape(-1, x.shape[-1]).float()
-        if padded_dim > flat.shape[-1]:
-            flat = torch.nn.functional.pad(flat, (0, padded_dim - flat.shape[-1]))
-        result = flat * hadamard_signs.to(device=flat.device, dtype=torch.float32)
-        h = 1
-        n = flat.shape[0]
-        while h < padded_dim:
-            result = result.view(n, -1, 2, h)
-            result = torch.stack([result[:, :, 0] + result[:, :, 1], result[:, :, 0] - result[:, :, 1]],
-                                 dim=2).reshape(n, padded_dim)
-            h *= 2
-        return result / math.sqrt(padded_dim)
-
-    @staticmethod
     def attention_score_gpu(
         q,
         compressed_k: dict,
@@ -198,18 +180,61 @@ class CUDATurboQuantOps:
         hadamard_signs,
         jl_matrix,
         qjl_dim: int,
+        scale: float = 1.0,
     ):
-        """scores = q_rot . k_polar + QJL correction (core/kv_quantizer.py:502-535)."""
+        """[n_queries, N] scores = q_rot . k_polar + QJL correction
+        (core/kv_quantizer.py:502-535), times ``scale``, in two kernels:
+        query rotation and projection, then one wavefront per key."""
         import torch
 
         _lib.require_cuda(q)
-        q_rot = CUDATurboQuantOps.rotate_gpu(q.reshape(-1, head_dim), hadamard_signs, padded_dim)
-        k_polar = CUDATurboQuantOps.polar_keys_gpu(compressed_k, head_dim, padded_dim, n_levels, bits_per_angle,
-                                                   hadamard_signs)
-        scores = q_rot @ k_polar.t()
-        jl_f = jl_matrix.to(device=q.device, dtype=torch.float32)
-        q_proj = q_rot @ jl_f.t()
-        signs_float = compressed_k["qjl_signs"].float() * 2 - 1
-        raw = q_proj @ signs_float.t()
-        scale = math.sqrt(math.pi / 2) / qjl_dim
-        return scores + raw * scale * compressed_k["qjl_norms"].float().reshape(1, -1)
+        device = q.device
+        flat_q = q.reshape(-1, head_dim).float().contiguous()
+        radius = compressed_k["radius"].reshape(-1).to(torch.float16).contiguous()
+        angles = torch.cat([a.to(torch.uint8) for a in compressed_k["angles"]], dim=-1).contiguous()
+        qjl_signs = compressed_k["qjl_signs"].to(torch.uint8).contiguous()
+        qjl_norms = compressed_k["qjl_norms"].reshape(-1).to(torch.float16).contiguous()
+        _lib.require_cuda(flat_q, radius, angles, qjl_signs, qjl_norms)
+        M, N = flat_q.shape[0], radius.shape[0]
+        if angles.shape != (N, padded_dim - 1) or qjl_signs.shape != (N, qjl_dim) or qjl_norms.shape != (N,):
+            raise RuntimeError("compressed key fields do not match padded_dim / qjl_dim")
+        signs_f = hadamard_signs.to(device=device, dtype=torch.float32).contiguous()
+        jl_f = jl_matrix.to(device=device, dtype=torch.float32).contiguous()
+        lib = _lib.load()
+        ws_bytes = lib.vrm_turboquant_score_workspace_bytes(M, padded_dim, qjl_dim)
+        ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=device)
+        scores = torch.empty((M, N), dtype=torch.float32, device=device)
+        rc = lib.vrm_turboquant_score(
+            _lib.ptr(flat_q), M, _lib.ptr(radius), _lib.ptr(angles), _lib.ptr(qjl_signs), _lib.ptr(qjl_norms), N,
+            head_dim, padded_dim, n_levels, bits_per_angle, qjl_dim, _lib.ptr(signs_f), _lib.ptr(jl_f),
+            _lib.ptr(angle_lut(bits_per_angle, device)), float(scale), _lib.ptr(ws), ws.numel() * 4,
+            _lib.ptr(scores), _lib.stream_of(flat_q),
+        )
+        _lib.check(rc, "turboquant attention_score")
+        return scores
+
+
+def topk_attend(scores, k: int, values):
+    """Renormalised top-k softmax attention: for each row of ``scores`` [M, N]
+    the ``k`` largest scores are kept and ``out[m] = softmax(kept) @
+    values[kept]`` ([M, D] float32, values [N, D]).  This is the value step of
+    the reference's sparse V (core/kv_quantizer.py:537-562,
+    core/paged_attention.py:1384-1400); ``k >= N`` is the dense softmax."""
+    import torch
+
+    _lib.require_cuda(scores, values)
+    scores = scores.float().contiguous()
+    values = values.float().contiguous()
+    M, N = scores.shape
+    if values.dim() != 2 or values.shape[0] != N:
+        raise RuntimeError(f"values must be [{N}, D], got {tuple(values.shape)}")
+    D = values.shape[1]
+    k = max(1, min(int(k), N))
+    out = torch.empty((M, D), dtype=torch.float32, device=scores.device)
+    lib = _lib.load()
+    ws_bytes = lib.vrm_topk_attend_workspace_bytes(M, k)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=scores.device)
+    rc = lib.vrm_topk_attend(_lib.ptr(scores), M, N, N, k, _lib.ptr(values), D, D, _lib.ptr(out), D, _lib.ptr(ws),
+                             ws.numel(), _lib.stream_of(scores))
+    _lib.check(rc, "topk_attend")
+    return out
