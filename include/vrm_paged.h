@@ -270,6 +270,19 @@ int vrm_topk_attend(const float* scores, int M, int N, long long ld_scores, int 
                     int D, long long ld_values, float* out, long long ld_out, void* workspace,
                     size_t workspace_bytes, vrm_stream_t stream);
 
+/*
+ * Packed code format of KVCacheCompressor (core/kv_quantizer.py:46-105,
+ * 337-371): each of `rows` rows of M uint8 values contributes the low `bits`
+ * bits of every value, most significant bit first; the row's bit stream fills
+ * ceil(M * bits / 8) bytes from bit 7 of byte 0, the last byte zero-padded.
+ * QJL signs use bits = 1, angle bins bits = bits_per_angle over a row's
+ * level-major bins.  vrm_unpack_bits is the inverse.  1 <= bits <= 8.
+ */
+int vrm_pack_bits(const uint8_t* vals, long long rows, int M, int bits, uint8_t* packed,
+                  vrm_stream_t stream);
+int vrm_unpack_bits(const uint8_t* packed, long long rows, int M, int bits, uint8_t* vals,
+                    vrm_stream_t stream);
+
 /* --------------------------------------------------------------------------
  * TurboQuant pages.  The reference keeps TurboQuant-compressed K/V in Python
  * dicts per (page, layer, slot) (core/paged_attention.py:568-675, 1420-1496)

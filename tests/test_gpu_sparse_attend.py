@@ -121,3 +121,22 @@ def test_manager_sparse_v_matches_oracle(ratio):
     for i, rid in enumerate(("a", "b")):
         single = m.compute_attention_turbo(q[i].to(DEV), rid, 1)
         assert torch.allclose(batch[i], single, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("bits,M", [(1, 64), (1, 13), (3, 127), (4, 127), (2, 5), (8, 9), (5, 31)])
+def test_pack_kernels_match_numpy_packbits(bits, M):
+    """The packed format against numpy's packbits (big bit order), a library
+    routine: each value's low `bits` bits, MSB first, then bytes MSB-first."""
+    import numpy as np
+
+    from vramancer_amd.kv_quantizer import _pack_values, _unpack_values
+
+    _say(f"pack bits {bits} M {M}")
+    g = np.random.default_rng(bits * 100 + M)
+    vals = g.integers(0, 256, size=(37, M), dtype=np.uint8)
+    stream = np.unpackbits(vals[..., None], axis=-1)[..., 8 - bits:].reshape(37, M * bits)
+    want = np.packbits(stream, axis=-1, bitorder="big")
+    got = _pack_values(torch.from_numpy(vals).to(DEV), bits).cpu().numpy()
+    assert np.array_equal(got, want)
+    back = _unpack_values(torch.from_numpy(want).to(DEV), M, bits).cpu().numpy()
+    assert np.array_equal(back, vals & ((1 << bits) - 1))

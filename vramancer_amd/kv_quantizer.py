@@ -21,59 +21,61 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
+from . import _lib
 from .turboquant_cuda import CUDATurboQuantOps
 
 __all__ = ["KVCacheCompressor", "TurboQuantCompressor", "BatchedCompressedRef"]
 
 
-# ---------------------------------------------------------------------------
-# Bit packing (MSB first) — same byte layout as core/kv_quantizer.py:46-105
-# ---------------------------------------------------------------------------
+# Bit packing (MSB first): the byte layout of core/kv_quantizer.py:46-105.
+
+def _pack_values(vals, bits: int):
+    """[..., M] uint8 -> [..., ceil(M * bits / 8)] bytes: the low ``bits``
+    bits of each value, most significant first, packed MSB-first
+    (core/kv_quantizer.py:46-83), by the gfx950 pack kernel."""
+    *batch, M = vals.shape
+    flat = vals.reshape(-1, M).to(torch.uint8).contiguous()
+    _lib.require_cuda(flat)
+    nbytes = (M * bits + 7) // 8
+    out = torch.empty((flat.shape[0], nbytes), dtype=torch.uint8, device=flat.device)
+    rc = _lib.load().vrm_pack_bits(_lib.ptr(flat), flat.shape[0], M, bits, _lib.ptr(out), _lib.stream_of(flat))
+    _lib.check(rc, "pack")
+    return out.reshape(*batch, nbytes)
+
+
+def _unpack_values(packed, M: int, bits: int):
+    """Inverse of _pack_values: [..., nbytes] -> [..., M] uint8."""
+    *batch, nbytes = packed.shape
+    flat = packed.reshape(-1, nbytes).to(torch.uint8).contiguous()
+    _lib.require_cuda(flat)
+    if nbytes * 8 < M * bits:
+        raise RuntimeError(f"{nbytes} bytes cannot hold {M} values of {bits} bits")
+    out = torch.empty((flat.shape[0], M), dtype=torch.uint8, device=flat.device)
+    rc = _lib.load().vrm_unpack_bits(_lib.ptr(flat), flat.shape[0], M, bits, _lib.ptr(out), _lib.stream_of(flat))
+    _lib.check(rc, "unpack")
+    return out.reshape(*batch, M)
+
 
 def _pack_bits(signs):
     """[..., M] 0/1 uint8 -> [..., ceil(M/8)] bytes, first element in the MSB."""
-    *batch, M = signs.shape
-    pad = (8 - M % 8) % 8
-    if pad:
-        signs = F.pad(signs, (0, pad))
-    weights = torch.tensor([128, 64, 32, 16, 8, 4, 2, 1], dtype=torch.uint8, device=signs.device)
-    grouped = signs.reshape(*batch, signs.shape[-1] // 8, 8)
-    return (grouped * weights).sum(dim=-1).to(torch.uint8)
+    return _pack_values(signs, 1)
 
 
 def _unpack_bits(packed, M):
-    """Inverse of _pack_bits: [..., ceil(M/8)] -> [..., M] uint8 of 0/1."""
-    *batch, nbytes = packed.shape
-    shifts = torch.tensor([7, 6, 5, 4, 3, 2, 1, 0], dtype=torch.uint8, device=packed.device)
-    bits = (packed.unsqueeze(-1) >> shifts) & 1
-    return bits.reshape(*batch, nbytes * 8)[..., :M]
+    return _unpack_values(packed, M, 1)
 
 
 def _pack_angles(angles_list, bits_per_angle):
-    """Concatenates per-level [N, cols] angle bins and packs bits_per_angle bits
-    per value, most significant bit first."""
+    """Level-major concatenation of a row's angle bins, bits_per_angle bits each."""
     if not angles_list:
         return torch.tensor([], dtype=torch.uint8)
-    flat = torch.cat(angles_list, dim=-1)
-    N = flat.shape[0]
-    shifts = torch.arange(bits_per_angle - 1, -1, -1, device=flat.device, dtype=torch.uint8)
-    bits = ((flat.unsqueeze(-1) >> shifts) & 1).reshape(N, -1)
-    return _pack_bits(bits)
+    return _pack_values(torch.cat(angles_list, dim=-1), bits_per_angle)
 
 
 def _unpack_angles(packed, N, level_dims, bits_per_angle):
-    total = sum(level_dims)
-    bits = _unpack_bits(packed, total * bits_per_angle).reshape(N, total, bits_per_angle)
-    shifts = torch.arange(bits_per_angle - 1, -1, -1, device=packed.device, dtype=torch.uint8)
-    flat = (bits * (1 << shifts)).sum(dim=-1).to(torch.uint8)
-    out = []
-    offset = 0
-    for d in level_dims:
-        out.append(flat[:, offset:offset + d])
-        offset += d
-    return out
+    flat = _unpack_values(packed, sum(level_dims), bits_per_angle).reshape(N, -1)
+    return list(torch.split(flat, list(level_dims), dim=-1))
 
 
 class BatchedCompressedRef(dict):
