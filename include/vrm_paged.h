@@ -131,6 +131,30 @@ int vrm_paged_decode_merge(const int32_t* context_lens, float* out,
                            int B, int H, int KH, int D, int PS, int max_pp, vrm_stream_t stream);
 
 /*
+ * vrm_paged_decode that also writes lse[b][h] = ln sum_t exp(scale q.k_t)
+ * over the attended tokens (-inf when none), so that attentions over
+ * disjoint token sets can be merged (vrm_attn_combine).  No counterpart in
+ * the reference; used by the Hugging Face cache integration to merge the
+ * compressed pages with the uncompressed recent tokens
+ * (core/turboquant_cache.py:176-196 concatenates them instead).
+ */
+int vrm_paged_decode_lse(const float* query, const void* kv_pool, const float* kv_scales,
+                         const int32_t* page_table, const int32_t* context_lens, float* out,
+                         float* lse, void* workspace, size_t workspace_bytes, int B, int H, int KH,
+                         int D, int PS, int L, int P, int max_pp, int layer_idx, float scale,
+                         int kv_dtype, vrm_stream_t stream);
+
+/*
+ * out = (e^(lse1 - m) out1 + e^(lse2 - m) out2) / (e^(lse1 - m) + e^(lse2 - m)),
+ * m = max(lse1, lse2), row by row ([rows][D] float32 outputs, [rows] lse):
+ * the attention over the union of two disjoint token sets from the
+ * attentions over each.  A row with both lse = -inf gives zeros; lse_out
+ * (optional) gets the union's lse.  No counterpart in the reference.
+ */
+int vrm_attn_combine(const float* out1, const float* lse1, const float* out2, const float* lse2,
+                     long long rows, int D, float* out, float* lse_out, vrm_stream_t stream);
+
+/*
  * Same attention over the reference's asymmetric 4-bit pool:
  *   value(d) = (nibble(d) - zero[g]) * scale[g],  g = d / 32,
  *   byte j of a row holds d = 2j in its low nibble and d = 2j+1 in its high one.
@@ -389,6 +413,20 @@ int vrm_build_block_table(const int32_t* flat_pages, int n_flat, const int32_t* 
 int vrm_kv_write(const void* key, const void* value, int src_dtype, const int32_t* page_ids,
                  const int32_t* slots, int N, void* kv_pool, int kv_dtype, int KH, int D, int PS,
                  int L, int P, int layer_idx, vrm_stream_t stream);
+
+/*
+ * vrm_paged_decode_tq plus the lse output of vrm_paged_decode_lse.  With
+ * with_qjl != 0 the scores are compute_attention_turbo's (QJL-corrected);
+ * with with_qjl == 0 they are q . decompress(k), the keys the reference's
+ * Hugging Face cache hands to the model's attention
+ * (core/turboquant_cache.py:135-138, 176-186).
+ */
+int vrm_paged_decode_tq_lse(const float* query, const uint8_t* tq_pool, const int32_t* page_table,
+                            const int32_t* context_lens, float* out, float* lse, void* workspace,
+                            size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,
+                            int max_pp, int layer_idx, float scale, int bits, int qjl_dim,
+                            const float* signs, const float* jl, const float* angle_lut,
+                            int with_qjl, vrm_stream_t stream);
 
 #ifdef __cplusplus
 }

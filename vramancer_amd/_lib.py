@@ -62,6 +62,9 @@ SIGNATURES = {
     "vrm_turboquant_score": (_i, [_p, _i, _p, _p, _p, _p] + [_i] * 6 + [_p, _p, _p, _f, _p, _sz, _p, _p]),
     "vrm_topk_attend_workspace_bytes": (_sz, [_i, _i]),
     "vrm_topk_attend": (_i, [_p, _i, _i, _ll, _i, _p, _i, _ll, _p, _ll, _p, _sz, _p]),
+    "vrm_paged_decode_lse": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _p]),
+    "vrm_paged_decode_tq_lse": (_i, [_p, _p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _i, _p, _p, _p, _i, _p]),
+    "vrm_attn_combine": (_i, [_p, _p, _p, _p, _ll, _i, _p, _p, _p]),
     "vrm_pack_bits": (_i, [_p, _ll, _i, _i, _p, _p]),
     "vrm_unpack_bits": (_i, [_p, _ll, _i, _i, _p, _p]),
 }

@@ -33,6 +33,7 @@ struct DecodeArgs {
   int B, H, KH, L, P, max_pp, layer;
   float qscale;               // scale * log2(e): scores live in the log2 domain
   int target;                 // work items the partition size aims for
+  float* lse;                 // optional [B][H] natural-log sum of exp(scale * q.k), written by the merge
 };
 
 // ---------------------------------------------------------------------------

@@ -328,7 +328,8 @@ template <int D>
 __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restrict__ part_acc,
                                                             const float* __restrict__ part_ml,
                                                             const int32_t* __restrict__ header,
-                                                            float* __restrict__ out, int H, int B) {
+                                                            float* __restrict__ out, float* __restrict__ lse, int H,
+                                                            int B) {
   constexpr int PER = D / 64;
   constexpr int BATCH = 4;
   constexpr int WAVES = 4;
@@ -418,7 +419,31 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
     float* dst = out + ((size_t)b * H + h) * D;
 #pragma unroll
     for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = o[i] * inv;
+    // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
+    if (lse && lane == 0) lse[(size_t)b * H + h] = L > 0.f ? (gm + log2f(L)) * 0.6931471805599453f : -INFINITY;
   }
+}
+
+// out = (e^(lse1 - m) o1 + e^(lse2 - m) o2) / (e^(lse1 - m) + e^(lse2 - m)),
+// m = max(lse1, lse2): two attentions over disjoint token sets merged into
+// the attention over their union; lse_out (optional) gets the union's lse.
+__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ o1, const float* __restrict__ lse1,
+                                                           const float* __restrict__ o2, const float* __restrict__ lse2,
+                                                           long long rows, int D, float* __restrict__ out,
+                                                           float* __restrict__ lse_out) {
+  const long long x = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (x >= rows * D) return;
+  const long long r = x / D;
+  const float a = lse1[r], c = lse2[r];
+  const float m = fmaxf(a, c);
+  float w1 = 0.f, w2 = 0.f;
+  if (m != -INFINITY) {
+    w1 = a == -INFINITY ? 0.f : expf(a - m);
+    w2 = c == -INFINITY ? 0.f : expf(c - m);
+  }
+  const float den = w1 + w2;
+  out[x] = den > 0.f ? (w1 * o1[x] + w2 * o2[x]) / den : 0.f;
+  if (lse_out && x % D == 0) lse_out[r] = den > 0.f ? m + logf(den) : -INFINITY;
 }
 
 template <int KIND, int D, int G>
@@ -469,15 +494,15 @@ hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStrea
   const dim3 block(256);
   switch (D) {
     case 64:
-      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
                          a.H, B);
       break;
     case 128:
-      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
                          a.H, B);
       break;
     default:
-      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
                          a.H, B);
       break;
   }
@@ -619,7 +644,7 @@ int kind_of(int kv_dtype) {
 int decode_entry(const float* query, const void* kv_pool, const float* kv_scales, const int32_t* page_table,
                  const int32_t* context_lens, float* out, void* workspace, size_t workspace_bytes, int B, int H,
                  int KH, int D, int PS, int L, int P, int max_pp, int layer_idx, float scale, int kv_dtype,
-                 vrm_stream_t stream, int passes) {
+                 vrm_stream_t stream, int passes, float* lse = nullptr) {
   int rc = check_common(query, kv_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
                         scale);
   if (rc) return rc;
@@ -648,8 +673,48 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
   a.P = P;
   a.max_pp = max_pp;
   a.layer = layer_idx;
+  a.lse = lse;
   return run_decode(a, kind, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
                     passes);
+}
+
+constexpr float kQjlCoef = (float)(1.2533141373155003 / 64.0);  // sqrt(pi / 2) / qjl_dim
+
+int tq_entry(const float* query, const uint8_t* tq_pool, const int32_t* page_table, const int32_t* context_lens,
+             float* out, void* workspace, size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,
+             int max_pp, int layer_idx, float scale, int bits, int qjl_dim, const float* signs, const float* jl,
+             const float* angle_lut, float* lse, float qjl_coef, vrm_stream_t stream) {
+  int rc = check_common(query, tq_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  if (D != 128 || qjl_dim != 64) {
+    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128 and qjl_dim 64 (got %d, %d)", D,
+              qjl_dim);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (bits < 2 || bits > 4) {
+    set_error("vrm_paged_decode_tq: bits_per_angle %d unsupported (2, 3, 4)", bits);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (!signs || !jl || !angle_lut) {
+    set_error("vrm_paged_decode_tq: null compressor buffer");
+    return VRM_ERR_ARG;
+  }
+  DecodeArgs a{};
+  a.query = query;
+  a.pool = tq_pool;
+  a.page_table = page_table;
+  a.ctx_lens = context_lens;
+  a.H = H;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.max_pp = max_pp;
+  a.layer = layer_idx;
+  a.lse = lse;
+  TqDecodeArgs tq{signs, jl, angle_lut, qjl_coef};
+  return run_tq_decode(a, tq, bits, out, workspace, workspace_bytes, B, D, scale,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -757,34 +822,56 @@ extern "C" int vrm_paged_decode_tq(const float* query, const uint8_t* tq_pool, c
                                    int B, int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx,
                                    float scale, int bits, int qjl_dim, const float* signs, const float* jl,
                                    const float* angle_lut, vrm_stream_t stream) {
-  int rc = check_common(query, tq_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
-                        scale);
-  if (rc) return rc;
-  if (D != 128 || qjl_dim != 64) {
-    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128 and qjl_dim 64 (got %d, %d)", D,
-              qjl_dim);
-    return VRM_ERR_UNSUPPORTED;
-  }
-  if (bits < 2 || bits > 4) {
-    set_error("vrm_paged_decode_tq: bits_per_angle %d unsupported (2, 3, 4)", bits);
-    return VRM_ERR_UNSUPPORTED;
-  }
-  if (!signs || !jl || !angle_lut) {
-    set_error("vrm_paged_decode_tq: null compressor buffer");
+  return tq_entry(query, tq_pool, page_table, context_lens, out, workspace, workspace_bytes, B, H, KH, D, PS, L, P,
+                  max_pp, layer_idx, scale, bits, qjl_dim, signs, jl, angle_lut, nullptr, kQjlCoef, stream);
+}
+
+extern "C" int vrm_paged_decode_tq_lse(const float* query, const uint8_t* tq_pool, const int32_t* page_table,
+                                       const int32_t* context_lens, float* out, float* lse, void* workspace,
+                                       size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,
+                                       int max_pp, int layer_idx, float scale, int bits, int qjl_dim,
+                                       const float* signs, const float* jl, const float* angle_lut, int with_qjl,
+                                       vrm_stream_t stream) {
+  if (!lse) {
+    set_error("vrm_paged_decode_tq_lse: null lse");
     return VRM_ERR_ARG;
   }
-  DecodeArgs a{};
-  a.query = query;
-  a.pool = tq_pool;
-  a.page_table = page_table;
-  a.ctx_lens = context_lens;
-  a.H = H;
-  a.KH = KH;
-  a.L = L;
-  a.P = P;
-  a.max_pp = max_pp;
-  a.layer = layer_idx;
-  TqDecodeArgs tq{signs, jl, angle_lut, (float)(1.2533141373155003 / 64.0)};
-  return run_tq_decode(a, tq, bits, out, workspace, workspace_bytes, B, D, scale,
-                       reinterpret_cast<hipStream_t>(stream));
+  // without the QJL term the scores are q_rot . k_polar = q . decompress(k)
+  return tq_entry(query, tq_pool, page_table, context_lens, out, workspace, workspace_bytes, B, H, KH, D, PS, L, P,
+                  max_pp, layer_idx, scale, bits, qjl_dim, signs, jl, angle_lut, lse, with_qjl ? kQjlCoef : 0.f,
+                  stream);
+}
+
+extern "C" int vrm_paged_decode_lse(const float* query, const void* kv_pool, const float* kv_scales,
+                                    const int32_t* page_table, const int32_t* context_lens, float* out, float* lse,
+                                    void* workspace, size_t workspace_bytes, int B, int H, int KH, int D, int PS,
+                                    int L, int P, int max_pp, int layer_idx, float scale, int kv_dtype,
+                                    vrm_stream_t stream) {
+  if (!lse) {
+    set_error("vrm_paged_decode_lse: null lse");
+    return VRM_ERR_ARG;
+  }
+  return decode_entry(query, kv_pool, kv_scales, page_table, context_lens, out, workspace, workspace_bytes, B, H, KH,
+                      D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth, lse);
+}
+
+extern "C" int vrm_attn_combine(const float* out1, const float* lse1, const float* out2, const float* lse2,
+                                long long rows, int D, float* out, float* lse_out, vrm_stream_t stream) {
+  const char* who = "vrm_attn_combine";
+  if (rows < 0 || D <= 0 || rows * D / 256 > 0x7fffffffLL) {
+    set_error("%s: bad sizes (rows=%lld D=%d)", who, rows, D);
+    return VRM_ERR_ARG;
+  }
+  if (rows == 0) {
+    clear_error();
+    return VRM_OK;
+  }
+  if (!out1 || !lse1 || !out2 || !lse2 || !out) {
+    set_error("%s: null pointer argument", who);
+    return VRM_ERR_ARG;
+  }
+  const long long n = rows * D;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), out1, lse1, out2, lse2, rows, D, out, lse_out);
+  return launch_status(who);
 }

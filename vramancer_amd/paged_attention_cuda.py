@@ -28,6 +28,7 @@ from . import _lib
 
 __all__ = [
     "paged_attention_decode",
+    "combine_attention",
     "paged_attention_decode_q4",
     "has_cuda_paged_attention",
     "decode_workspace",
@@ -79,6 +80,7 @@ def paged_attention_decode(
     kv_scales: Any = None,  # int8: [P, L, 2, KH, PS] / fp8: [P, L, 2, KH] float32
     out: Any = None,
     workspace: Any = None,
+    lse: Any = None,        # optional [B, H] float32 output: ln sum_t exp(scale q.k_t)
 ) -> Any:
     """Single-token attention straight from the paged KV pool.
 
@@ -113,12 +115,51 @@ def paged_attention_decode(
     lib = _lib.load()
     if workspace is None:
         workspace = decode_workspace(B, H, KH, D, max_pp, query.device, PS)
-    rc = lib.vrm_paged_decode(
-        _lib.ptr(query), _lib.ptr(kv_pool), _lib.ptr(kv_scales), _lib.ptr(page_table), _lib.ptr(context_lens),
-        _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
-        B, H, KH, D, PS, L, P, max_pp, int(layer_idx), scale, code, _lib.stream_of(query),
-    )
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if lse is None:
+        rc = lib.vrm_paged_decode(
+            _lib.ptr(query), _lib.ptr(kv_pool), _lib.ptr(kv_scales), _lib.ptr(page_table), _lib.ptr(context_lens),
+            _lib.ptr(out), _lib.ptr(workspace), ws_bytes, B, H, KH, D, PS, L, P, max_pp, int(layer_idx), scale, code,
+            _lib.stream_of(query),
+        )
+    else:
+        _check_lse(lse, B, H, query.device)
+        rc = lib.vrm_paged_decode_lse(
+            _lib.ptr(query), _lib.ptr(kv_pool), _lib.ptr(kv_scales), _lib.ptr(page_table), _lib.ptr(context_lens),
+            _lib.ptr(out), _lib.ptr(lse), _lib.ptr(workspace), ws_bytes, B, H, KH, D, PS, L, P, max_pp,
+            int(layer_idx), scale, code, _lib.stream_of(query),
+        )
     _lib.check(rc, "paged_attention_decode")
+    return out
+
+
+def _check_lse(lse, B: int, H: int, device) -> None:
+    import torch
+
+    if tuple(lse.shape) != (B, H) or lse.dtype != torch.float32 or not lse.is_contiguous() or lse.device != device:
+        raise RuntimeError(f"lse must be a contiguous float32 [{B}, {H}] tensor on {device}")
+
+
+def combine_attention(out1: Any, lse1: Any, out2: Any, lse2: Any, lse_out: Any = None) -> Any:
+    """Attention over the union of two disjoint token sets from the
+    attentions over each ([..., D] float32 outputs with their [...] log-sum-exp
+    of the scaled scores); rows where both sets are empty give zeros."""
+    import torch
+
+    _lib.require_cuda(out1, lse1, out2, lse2, lse_out)
+    if out1.shape != out2.shape or lse1.shape != lse2.shape or tuple(out1.shape[:-1]) != tuple(lse1.shape):
+        raise RuntimeError("combine_attention: mismatched shapes")
+    o1, o2 = out1.float().contiguous(), out2.float().contiguous()
+    l1, l2 = lse1.float().contiguous(), lse2.float().contiguous()
+    D = o1.shape[-1]
+    rows = o1.numel() // D
+    out = torch.empty_like(o1)
+    if lse_out is not None and (lse_out.shape != l1.shape or lse_out.dtype != torch.float32 or
+                                not lse_out.is_contiguous()):
+        raise RuntimeError("lse_out must be a contiguous float32 tensor shaped like lse1")
+    rc = _lib.load().vrm_attn_combine(_lib.ptr(o1), _lib.ptr(l1), _lib.ptr(o2), _lib.ptr(l2), rows, D, _lib.ptr(out),
+                                      _lib.ptr(lse_out), _lib.stream_of(o1))
+    _lib.check(rc, "combine_attention")
     return out
 
 

@@ -25,7 +25,7 @@ import math
 from typing import Any, Dict, Optional
 
 from . import _lib
-from .paged_attention_cuda import decode_workspace
+from .paged_attention_cuda import _check_lse, decode_workspace
 from .turboquant_cuda import angle_lut
 
 __all__ = [
@@ -171,9 +171,14 @@ def read_pages(tq_pool, layer_idx: int, page_ids, compressor) -> Dict[str, Any]:
 
 
 def paged_attention_decode_turbo(query, tq_pool, page_table, context_lens, layer_idx: int, compressor,
-                                 scale: Optional[float] = None, out=None, workspace=None):
+                                 scale: Optional[float] = None, out=None, workspace=None, lse=None,
+                                 qjl: bool = True):
     """[B, H, 128] float32 attention over TurboQuant pages (compute_attention_turbo
-    with dense values, core/paged_attention.py:1259-1418, for a batch)."""
+    with dense values, core/paged_attention.py:1259-1418, for a batch).
+
+    ``lse`` ([B, H] float32) receives ln sum_t exp(scale score_t); with
+    ``qjl=False`` (only together with ``lse``) the scores are q . decompress(k)
+    without the QJL correction, as the Hugging Face cache path attends."""
     import torch
 
     _check_compressor(compressor)
@@ -195,10 +200,23 @@ def paged_attention_decode_turbo(query, tq_pool, page_table, context_lens, layer
     if workspace is None:
         workspace = decode_workspace(B, H, KH, D, max_pp, query.device)
     signs, jl, lut = _buffers(compressor, query.device)
-    rc = _lib.load().vrm_paged_decode_tq(
-        _lib.ptr(query), _lib.ptr(tq_pool), _lib.ptr(page_table), _lib.ptr(context_lens), _lib.ptr(out),
-        _lib.ptr(workspace), workspace.numel(), B, H, KH, D, PAGE_SIZE, L, P, max_pp, int(layer_idx), float(scale),
-        compressor.bits_per_angle, 64, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(query),
-    )
+    lib = _lib.load()
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if lse is None:
+        if not qjl:
+            raise RuntimeError("qjl=False needs an lse output")
+        rc = lib.vrm_paged_decode_tq(
+            _lib.ptr(query), _lib.ptr(tq_pool), _lib.ptr(page_table), _lib.ptr(context_lens), _lib.ptr(out),
+            _lib.ptr(workspace), ws_bytes, B, H, KH, D, PAGE_SIZE, L, P, max_pp, int(layer_idx), float(scale),
+            compressor.bits_per_angle, 64, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(query),
+        )
+    else:
+        _check_lse(lse, B, H, query.device)
+        rc = lib.vrm_paged_decode_tq_lse(
+            _lib.ptr(query), _lib.ptr(tq_pool), _lib.ptr(page_table), _lib.ptr(context_lens), _lib.ptr(out),
+            _lib.ptr(lse), _lib.ptr(workspace), ws_bytes, B, H, KH, D, PAGE_SIZE, L, P, max_pp, int(layer_idx),
+            float(scale), compressor.bits_per_angle, 64, _lib.ptr(signs), _lib.ptr(jl), _lib.ptr(lut),
+            1 if qjl else 0, _lib.stream_of(query),
+        )
     _lib.check(rc, "paged_attention_decode_turbo")
     return out
