@@ -537,12 +537,20 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
     for (int r = 0; r < 4; ++r) sc[r] = (s.ok && pi * kPS + grp * 4 + r < tok_end) ? c4[r] : -INFINITY;
   };
 
-  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page; tokens
-  // that are absent or past the context read as 0 (whatever the page holds).
-  auto v_block = [&](const FloatSlot<D>& s, int pi, int blk, bool valid_page, float* out4) {
-    const v4f t = Ops::mma(__builtin_bit_cast(vec, s.v[blk >> 1]), onehot[blk & 1], v4f{0.f, 0.f, 0.f, 0.f});
+  // V rows of this lane's token (col) with absent pages and tokens past the
+  // context zeroed bitwise, whatever the page holds (NaN included), so that
+  // their transposed values are exact zeros; one mask per page, no branch.
+  auto v_rows = [&](const FloatSlot<D>& s, int pi, bool page_live, uint4 (&out)[NC]) {
+    const uint32_t keep = (page_live && pi * kPS + col < tok_end) ? 0xffffffffu : 0u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out4[r] = (valid_page && pi * kPS + grp * 4 + r < tok_end) ? t[r] : 0.f;
+    for (int c = 0; c < NC; ++c)
+      out[c] = make_uint4(s.v[c].x & keep, s.v[c].y & keep, s.v[c].z & keep, s.v[c].w & keep);
+  };
+  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page.
+  auto v_block = [&](const uint4 (&rows)[NC], int blk, float* out4) {
+    const v4f t = Ops::mma(__builtin_bit_cast(vec, rows[blk >> 1]), onehot[blk & 1], v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out4[r] = t[r];
   };
 
   auto process_pair = [&](const FloatSlot<D>& s0, const FloatSlot<D>& s1, int pi, bool has1) {
@@ -575,13 +583,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
       Bh[e] = hi;
       Bl[e] = (el)(p - (float)hi);
     }
-    const bool ok0 = s0.ok;
-    const bool ok1 = has1 && s1.ok;
+    uint4 rows0[NC], rows1[NC];
+    v_rows(s0, pi, s0.ok, rows0);
+    v_rows(s1, pi + 1, has1 && s1.ok, rows1);
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       float t[8];
-      v_block(s0, pi, blk, ok0, t);
-      v_block(s1, pi + 1, blk, ok1, t + 4);
+      v_block(rows0, blk, t);
+      v_block(rows1, blk, t + 4);
       vec A;
 #pragma unroll
       for (int e = 0; e < 8; ++e) A[e] = (el)t[e];  // exact: the values came from the pool
