@@ -102,6 +102,66 @@ def test_turboquant_rejects_bad_arguments(lib):
     assert c(1, 0, 0, 128, 128, 7, 3, 64, 1, 1, 1, 1, 1, 1, 1, None) == 0   # N == 0
 
 
+def test_manager_and_attend_entries_reject_bad_arguments(lib):
+    """Argument checks of the block table, raw write, pool compression, score,
+    top-k, pack and merge entries: rejected on the host, nothing launched."""
+    bt = lib.vrm_build_block_table
+    assert bt(1, 4, 1, 1, -1, 8, 1, 1, None) == -1
+    assert bt(1, 4, 1, 1, 70000, 8, 1, 1, None) == -2
+    assert bt(1, 4, None, 1, 2, 8, 1, 1, None) == -1 and b"null" in lib.vrm_last_error()
+    assert bt(None, 0, None, None, 0, 0, None, None, None) == 0
+
+    w = lib.vrm_kv_write
+    args = [1, 1, _lib.VRM_SRC_F32, 1, 1, 2, 1, _lib.VRM_KV_F16, 2, 64, 16, 3, 9, 0, None]
+
+    def kw(i, v):
+        a = list(args)
+        a[i] = v
+        return w(*a)
+
+    assert kw(7, _lib.VRM_KV_I8) == -1 and b"float pool" in lib.vrm_last_error()
+    assert kw(2, 7) == -1
+    assert kw(13, 3) == -1 and b"layer_idx" in lib.vrm_last_error()
+    assert kw(0, None) == -1
+    assert kw(5, 0) == 0
+
+    cp = lib.vrm_tq_compress_pool
+    assert cp(1, _lib.VRM_KV_I8, 1, 1, 2, 1, 2, 128, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == -1
+    assert cp(1, _lib.VRM_KV_F16, 1, 1, 2, 1, 2, 64, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == -2
+    assert cp(1, _lib.VRM_KV_F16, 1, 1, 0, 1, 2, 128, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == 0
+
+    sb = lib.vrm_turboquant_score_workspace_bytes(5, 128, 64)
+    assert sb == 5 * 192 * 4
+    sc = lib.vrm_turboquant_score
+    assert sc(1, 5, 1, 1, 1, 1, 9, 128, 128, 7, 3, 0, 1, 1, 1, 1.0, 1, sb, 1, None) == -1
+    assert sc(1, 5, 1, 1, 1, 1, 9, 128, 128, 7, 3, 64, 1, 1, 1, 1.0, 1, sb - 4, 1, None) == -3
+    assert sc(1, 5, 1, 1, 1, 1, 9, 100, 100, 7, 3, 64, 1, 1, 1, 1.0, 1, sb, 1, None) == -2
+    assert sc(None, 0, None, None, None, None, 9, 128, 128, 7, 3, 64, None, None, None, 1.0, None, 0, None,
+              None) == 0
+
+    tb = lib.vrm_topk_attend_workspace_bytes(3, 10)
+    assert tb == 3 * 8 + 3 * 10 * 8
+    tk = lib.vrm_topk_attend
+    assert tk(1, 3, 10, 10, 11, 1, 64, 64, 1, 64, 1, tb, None) == -1  # k > N
+    assert tk(1, 3, 10, 10, 0, 1, 64, 64, 1, 64, 1, tb, None) == -1   # k < 1
+    assert tk(1, 3, 10, 9, 5, 1, 64, 64, 1, 64, 1, tb, None) == -1    # row stride below N
+    assert tk(1, 3, 10, 10, 10, 1, 64, 64, 1, 64, 1, tb - 1, None) == -3
+    assert tk(1, 0, 10, 10, 5, 1, 64, 64, 1, 64, None, 0, None) == 0
+
+    assert lib.vrm_pack_bits(1, 4, 8, 9, 1, None) == -1
+    assert lib.vrm_unpack_bits(None, 4, 8, 3, 1, None) == -1
+    assert lib.vrm_pack_bits(None, 0, 8, 3, None, None) == 0
+
+    assert lib.vrm_attn_combine(1, 1, 1, 1, -1, 64, 1, None, None) == -1
+    assert lib.vrm_attn_combine(None, 1, 1, 1, 4, 64, 1, None, None) == -1
+    assert lib.vrm_attn_combine(None, None, None, None, 0, 64, None, None, None) == 0
+
+    assert lib.vrm_paged_decode_lse(1, 1, None, 1, 1, 1, None, 1, 1 << 30, 2, 8, 8, 64, 16, 1, 4, 4, 0, 0.125,
+                                    _lib.VRM_KV_F32, None) == -1
+    assert lib.vrm_paged_decode_tq_lse(1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 8, 8, 128, 16, 1, 4, 4, 0, 0.1, 3, 64,
+                                       1, 1, 1, 0, None) == -1
+
+
 def test_python_api_refuses_cpu_tensors():
     import torch
     from vramancer_amd.paged_attention_cuda import paged_attention_decode
