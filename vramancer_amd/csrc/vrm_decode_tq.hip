@@ -103,12 +103,25 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   constexpr int ABYTES = T::angle_bytes(BITS);
   constexpr int D = T::kPD;
 
-  // {cos, sin} of the bin centres (table 0: level 0, table 1: levels >= 1),
-  // singly and for two sibling angles at once (index = bin_a + NB * bin_b)
-  __shared__ float2 lut[2][NB];
-  __shared__ float4 lut2[2][NB * NB];
-  __shared__ uint2 sign_lut[16];             // 4 sign bits -> 4 fp16 +-1 (bit i -> element i)
-  __shared__ float qbuf[kWaves][16][D + 4];  // per wave: q_rot rows, later the output columns
+  // {cos, sin} of the bin centres of levels >= 1, singly and, at 4 bits
+  // (levels 3 and 2), for two sibling angles at once (index bin_a + NB bin_b)
+  __shared__ float2 lut[NB];
+  __shared__ float4 lut2[BITS <= 3 ? 1 : NB * NB];
+  __shared__ uint2 sign_lut[16];  // 4 sign bits -> 4 fp16 +-1 (bit i -> element i)
+  // Two levels per lookup: for a node angle a and the angles b, c of its two
+  // children (index a + NB (b + NB c)), the products (cos a cos b, cos a sin b,
+  // sin a cos c, sin a sin c); t10 for levels 1/0 (level 0 has its own bin
+  // centres) and, at 2 and 3 bits, t32 for levels 3/2.  They share LDS with
+  // qbuf (per wave: q_rot rows before the stream, the output columns after
+  // it), which is dead while the tables are read.
+  constexpr bool kT32 = BITS <= 3;
+  constexpr int NT = NB * NB * NB;
+  constexpr int QBUF_BYTES = kWaves * 16 * (D + 4) * 4;
+  constexpr int TAB_BYTES = (kT32 ? 2 : 1) * NT * 16;
+  __shared__ __attribute__((aligned(16))) unsigned char shbuf[QBUF_BYTES > TAB_BYTES ? QBUF_BYTES : TAB_BYTES];
+  float(*qbuf)[16][D + 4] = reinterpret_cast<float(*)[16][D + 4]>(shbuf);
+  float4* t10 = reinterpret_cast<float4*>(shbuf);
+  float4* t32 = t10 + NT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -120,14 +133,12 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   const int kvh = unit / chunks;
   const int h0 = kvh * group + (unit % chunks) * G;
 
-  for (int i = threadIdx.x; i < 2 * NB; i += blockDim.x) {
-    const int tab = i / NB, bin = i % NB;
-    lut[tab][bin] = make_float2(tq.lut[(2 * tab) * NB + bin], tq.lut[(2 * tab + 1) * NB + bin]);
-  }
-  for (int i = threadIdx.x; i < 2 * NB * NB; i += blockDim.x) {
-    const int tab = i / (NB * NB), ba = i % NB, bb = (i / NB) % NB;
-    lut2[tab][ba + NB * bb] = make_float4(tq.lut[(2 * tab) * NB + ba], tq.lut[(2 * tab + 1) * NB + ba],
-                                          tq.lut[(2 * tab) * NB + bb], tq.lut[(2 * tab + 1) * NB + bb]);
+  for (int i = threadIdx.x; i < NB; i += blockDim.x) lut[i] = make_float2(tq.lut[2 * NB + i], tq.lut[3 * NB + i]);
+  if constexpr (BITS > 3) {
+    for (int i = threadIdx.x; i < NB * NB; i += blockDim.x) {
+      const int ba = i % NB, bb = i / NB;
+      lut2[i] = make_float4(tq.lut[2 * NB + ba], tq.lut[3 * NB + ba], tq.lut[2 * NB + bb], tq.lut[3 * NB + bb]);
+    }
   }
   if (threadIdx.x < 16) {
     uint32_t h[4];
@@ -216,6 +227,23 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       onehot[h][e] = (grp == 2 * h + (col >> 3) && e == (col & 7)) ? (_Float16)1.f : (_Float16)0.f;
   const float qjl_scale = a.qscale * tq.qjl_coef;
 
+  // every wave of the workgroup is done with qbuf (all share the work item,
+  // so all reach this point): its LDS now holds the two-level tables
+  __syncthreads();
+  {
+    const float* cos1 = tq.lut + 2 * NB;  // levels >= 1
+    const float* sin1 = tq.lut + 3 * NB;
+    const float* cos0 = tq.lut;           // level 0
+    const float* sin0 = tq.lut + NB;
+    for (int i = threadIdx.x; i < NT; i += blockDim.x) {
+      const int ia = i % NB, ib = (i / NB) % NB, ic = i / (NB * NB);
+      t10[i] = make_float4(cos1[ia] * cos0[ib], cos1[ia] * sin0[ib], sin1[ia] * cos0[ic], sin1[ia] * sin0[ic]);
+      if constexpr (kT32)
+        t32[i] = make_float4(cos1[ia] * cos1[ib], cos1[ia] * sin1[ib], sin1[ia] * cos1[ic], sin1[ia] * sin1[ic]);
+    }
+  }
+  __syncthreads();
+
   // ---------------- streaming state ----------------
   float m_run = kNoMax, l_run = 0.f;
   // O^T block 2 c + h: row 4 grp + r <-> dim 32 (2 h + (4 grp + r) / 8) + 8 c + (4 grp + r) % 8
@@ -250,30 +278,51 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     s.ksign = reinterpret_cast<const uint2*>(ks + T::signs_offset(BITS))[col];
   };
 
-  // dims 32 grp .. 32 grp + 31 of one token, in the reference's order of
-  // products; sibling angles (slots 2 k + 1, 2 k + 2) are looked up together
+  // dims 32 grp .. 32 grp + 31 of one token: the reference's tree of
+  // products, two levels per lookup from the product tables below level 4
+  // (4 bits: levels 3 and 2 one at a time with sibling angles together), so
+  // each value is the reference's within a float32 rounding or two.
   auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&cur)[32]) {
     constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
-    const float2 t6 = lut[1][(top0 >> sh31) & (NB - 1)];
-    const float2 t5 = lut[1][(topq >> sh31) & (NB - 1)];
+    const float2 t6 = lut[(top0 >> sh31) & (NB - 1)];
+    const float2 t5 = lut[(topq >> sh31) & (NB - 1)];
     float p = radius;
     p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
     p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
-    const float2 c4 = lut[1][bit_field<BITS>(q, 0)];  // level 4: slot 0
-    cur[0] = p * c4.x;
-    cur[1] = p * c4.y;
+    const float2 c4 = lut[bit_field<BITS>(q, 0)];  // level 4: slot 0
+    const float x3[2] = {p * c4.x, p * c4.y};
+    float y[8];  // the level-1 nodes
+    if constexpr (kT32) {
+      // levels 3 and 2: node j (slot 1 + j), children slots 3 + 2 j, 4 + 2 j
 #pragma unroll
-    for (int lev = 3; lev >= 0; --lev) {
-      const int n = 1 << (4 - lev);  // nodes of this level in the quarter; slots n - 1 .. 2 n - 2
-#pragma unroll
-      for (int i = n - 2; i >= 0; i -= 2) {  // descending: each source is read before it is overwritten
-        const float4 cs = lut2[lev == 0 ? 0 : 1][bit_field<2 * BITS>(q, (n - 1 + i) * BITS)];
-        const float x0 = cur[i], x1 = cur[i + 1];
-        cur[2 * i] = x0 * cs.x;
-        cur[2 * i + 1] = x0 * cs.y;
-        cur[2 * i + 2] = x1 * cs.z;
-        cur[2 * i + 3] = x1 * cs.w;
+      for (int j = 0; j < 2; ++j) {
+        const float4 t = t32[bit_field<BITS>(q, (1 + j) * BITS) + NB * bit_field<2 * BITS>(q, (3 + 2 * j) * BITS)];
+        y[4 * j] = x3[j] * t.x;
+        y[4 * j + 1] = x3[j] * t.y;
+        y[4 * j + 2] = x3[j] * t.z;
+        y[4 * j + 3] = x3[j] * t.w;
       }
+    } else {
+      // level 3 (slots 1, 2), then level 2 (slots 3 .. 6), sibling angles together
+      const float4 a3 = lut2[bit_field<2 * BITS>(q, 1 * BITS)];
+      const float x2[4] = {x3[0] * a3.x, x3[0] * a3.y, x3[1] * a3.z, x3[1] * a3.w};
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const float4 a2 = lut2[bit_field<2 * BITS>(q, (3 + i) * BITS)];
+        y[2 * i] = x2[i] * a2.x;
+        y[2 * i + 1] = x2[i] * a2.y;
+        y[2 * i + 2] = x2[i + 1] * a2.z;
+        y[2 * i + 3] = x2[i + 1] * a2.w;
+      }
+    }
+    // levels 1 and 0: node j (slot 7 + j), children slots 15 + 2 j, 16 + 2 j
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float4 t = t10[bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
+      cur[4 * j] = y[j] * t.x;
+      cur[4 * j + 1] = y[j] * t.y;
+      cur[4 * j + 2] = y[j] * t.z;
+      cur[4 * j + 3] = y[j] * t.w;
     }
   };
 
@@ -402,6 +451,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   }
 
   // ---------------- partition result: columns to natural dims, unrotate ----------------
+  __syncthreads();  // the tables are dead once every wave has streamed its pages
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
