@@ -257,9 +257,13 @@ def main():
             "unit": "us/layer-step",
             "cores": threads,
             "kind": "port",
-            "sample": (f"oracle restatement of the reference's PyTorch decode ({cfg.codec} dequant + gather + "
-                       f"repeat_interleave + bmm/softmax/bmm, fp32) over the first {min(args.cpu_seqs, B)} of the "
-                       f"{B} sequences, median of {args.cpu_reps}, scaled by the batch's total context"),
+            "sample": ((f"oracle restatement of compute_attention_turbo (per kv-head: QJL-corrected scores "
+                        f"of the rotated query, softmax, decompressed values; fp32) over the first "
+                        if cfg.codec.startswith("tq") else
+                        f"oracle restatement of the reference's PyTorch decode ({cfg.codec} dequant + gather + "
+                        f"repeat_interleave + bmm/softmax/bmm, fp32) over the first ")
+                       + f"{min(args.cpu_seqs, B)} of the {B} sequences, median of {args.cpu_reps}, scaled by the "
+                         "batch's total context"),
         }
     elem = {"f32": "f32", "f16": "f16", "bf16": "bf16", "int8": "int8", "fp8": "fp8e4m3", "tq3": "tq3-polar",
             "tq4": "tq4-polar"}[cfg.codec]
