@@ -18,7 +18,9 @@ and the reference's CPU path (the oracle restatement) timed on a sample.
 ``--workload`` measures one of the other decode shapes the same way (7b-bf16:
 B=32, 28/4 heads, bf16 pool, context ~U[1024, 8192]; mixed-fp8: 129
 sequences, 64/8 heads, fp8 pool, lognormal contexts plus one of 131072;
-fp32-plumbing); the default line is 14b-int8.
+fp32-plumbing); the default line is 14b-int8.  ``--batcher`` times one layer
+of a batched decode step of the 7b-bf16 batch through the pages against the
+reference batcher's pad-and-concat step, on the same GPU.
 """
 from __future__ import annotations
 
@@ -111,6 +113,131 @@ def cpu_baseline(inp, layer, n_seq, reps):
     return per_token_us, threads
 
 
+def batcher_step(args):
+    """``--batcher``: one layer of a continuous-batching decode step over the
+    7b-bf16 batch (B=32, H=28, KH=4, D=128, context ~U[1024, 8192]), two ways
+    on the GPU, with the same K/V:
+
+    * paged: the new token's K/V rows written into the pages
+      (``vrm_kv_write``), then the paged decode (``vrm_paged_decode``), bf16;
+    * pad-and-concat, the reference batcher's step
+      (core/continuous_batcher.py:711-756, 828-867): each request's cache
+      [1, KH, len, D] left-padded with zeros to the longest and concatenated
+      into the batch, the new token appended (``DynamicCache.update``'s
+      ``torch.cat``), then transformers' SDPA attention with the padding mask,
+      which repeats K/V to H heads.  Run in float16, the same bytes per
+      element as bfloat16.
+
+    The manager's bookkeeping, once per step for all layers, is timed on its
+    own: the slot mapping of one new token per request (``append_tokens``)
+    and the device block table, patched with the new token counts and pages
+    (``manager_step_us``); a full rebuild of the table from every page list
+    (``vrm_build_block_table``) for comparison."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cfg = workloads.CONFIGS["7b-bf16"]
+    inp = workloads.make_decode_inputs(cfg, dev, seed=0)
+    q, pool, table, lens = inp["query"], inp["kv_pool"], inp["page_table"], inp["context_lens"]
+    B, H, D = q.shape
+    P, L, _, KH, PS, _ = pool.shape
+    max_pp = table.shape[1]
+    scale = 1.0 / math.sqrt(D)
+    lens_list = lens.tolist()
+    stream = _lib.stream_of(q)
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+    ws = decode_workspace(B, H, KH, D, max_pp, dev, PS)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    knew = torch.randn((B, KH, D), generator=gen, device=dev).to(torch.bfloat16)
+    vnew = torch.randn((B, KH, D), generator=gen, device=dev).to(torch.bfloat16)
+    last = (lens - 1).clamp(min=0)
+    pid = table.gather(1, (last // PS).long()[:, None]).squeeze(1).contiguous()
+    slot = (last % PS).to(torch.int32).contiguous()
+
+    def paged(i):
+        rc = lib.vrm_kv_write(knew.data_ptr(), vnew.data_ptr(), _lib.VRM_SRC_BF16, pid.data_ptr(), slot.data_ptr(),
+                              B, pool.data_ptr(), _lib.VRM_KV_BF16, KH, D, PS, L, P, 0, stream)
+        rc = rc or lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), None, table.data_ptr(), lens.data_ptr(),
+                                        out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp, 0,
+                                        scale, _lib.VRM_KV_BF16, stream)
+        if rc:
+            _lib.check(rc, "paged step")
+
+    # the manager's per-step bookkeeping for the same batch: slot mapping of
+    # one new token per request, then the device block table (patched)
+    from vramancer_amd.paged_attention import PagedKVCacheManager, PagedKVConfig
+
+    mgr = PagedKVCacheManager(PagedKVConfig(page_size=PS, num_layers=1, num_kv_heads=KH, head_dim=D,
+                                            max_pages=P + B * 8, device="cuda:0", dtype="bfloat16"))
+    rids = [f"r{b}" for b in range(B)]
+    for rid, n in zip(rids, lens_list):
+        mgr.allocate(rid, num_tokens=n)
+
+    def bookkeeping(i):
+        mgr.append_tokens(rids)
+        mgr._block_table(rids, dev)
+
+    def rebuild(i):
+        mgr._table_cache = None
+        mgr._block_table(rids, dev)
+
+    # per-request caches of layer 0, [1, KH, len, D] float16
+    caches = []
+    for b, n in enumerate(lens_list):
+        pages = pool[table[b, :(n + PS - 1) // PS].long(), 0]  # [np, 2, KH, PS, D]
+        kv = pages.permute(1, 2, 0, 3, 4).reshape(2, KH, -1, D)[:, :, :n].to(torch.float16)
+        caches.append((kv[0].unsqueeze(0).contiguous(), kv[1].unsqueeze(0).contiguous()))
+    maxlen = max(lens_list)
+    keep = torch.zeros((B, maxlen + 1), dtype=torch.bool, device=dev)
+    for b, n in enumerate(lens_list):
+        keep[b, maxlen - n:] = True
+    mask = keep[:, None, None, :]  # [B, 1, 1, maxlen + 1], True = attend
+    q16 = q.to(torch.float16).unsqueeze(2)  # [B, H, 1, D]
+    k16, v16 = knew.to(torch.float16).unsqueeze(2), vnew.to(torch.float16).unsqueeze(2)
+
+    class _Attn:  # what sdpa_attention_forward reads from the attention module
+        num_key_value_groups = H // KH
+        is_causal = True
+
+    def pad_concat(i):
+        ks, vs = [], []
+        for (k, v), n in zip(caches, lens_list):
+            if n < maxlen:
+                z = torch.zeros((1, KH, maxlen - n, D), dtype=k.dtype, device=dev)
+                k, v = torch.cat([z, k], dim=2), torch.cat([z, v], dim=2)
+            ks.append(k)
+            vs.append(v)
+        K = torch.cat([torch.cat(ks, dim=0), k16], dim=2)
+        V = torch.cat([torch.cat(vs, dim=0), v16], dim=2)
+        sdpa_attention_forward(_Attn, q16, K, V, mask, scaling=scale)
+
+    for fn in (paged, rebuild, bookkeeping, pad_concat):
+        for i in range(3):
+            fn(i)
+    torch.cuda.synchronize()
+    log("timing the batcher step")
+    us_paged = time_events(paged, args.steps)
+    us_rebuild = time_events(rebuild, 20)
+    us_book = time_events(bookkeeping, 100)  # 100 steps: every request opens 6 or 7 pages
+    us_pad = time_events(pad_concat, 10)
+    result = {
+        "metric": "batched decode step, attention of one layer: paged vs pad-and-concat",
+        "value": round(us_paged, 3),
+        "unit": "us/layer-step",
+        "higher_is_better": False,
+        "pad_concat_us": round(us_pad, 1),
+        "speedup": round(us_pad / us_paged, 1),
+        "manager_step_us": round(us_book, 2),
+        "block_table_rebuild_us": round(us_rebuild, 2),
+        "dtype": "bf16 (pad-and-concat: f16)",
+        "data": "synthetic",
+        "config": {"workload": "7b-bf16 batch: B=32, H=28, KH=4, D=128, context ~U[1024, 8192], page 16",
+                   "context_tokens": int(sum(lens_list)), "max_context": maxlen},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +248,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="14b-int8", choices=sorted(workloads.CONFIGS),
                     help="decode shape to measure (the headline line is 14b-int8)")
+    ap.add_argument("--batcher", action="store_true",
+                    help="time one layer of a batched decode step, paged vs the reference's pad-and-concat")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -131,6 +260,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.batcher:
+        batcher_step(args)
+        return
     lib = _lib.load()
     dev = torch.device("cuda:0")
     cfg = workloads.CONFIGS[args.workload]

@@ -143,7 +143,9 @@ def test_compute_attention_decode_matches_oracle(dtype):
     out = m.compute_attention_decode(q.to(DEV), order, 1)
     table, ctx = m._block_table(order, torch.device(DEV))
     want_t, want_c = _host_table(m, order)
-    assert torch.equal(table.cpu(), want_t) and torch.equal(ctx.cpu(), want_c)
+    w = want_t.shape[1]
+    assert table.shape[1] >= w and (table[:, w:] == -1).all()
+    assert torch.equal(table[:, :w].cpu(), want_t) and torch.equal(ctx.cpu(), want_c)
     # unchanged page lists: the device table is reused, not rebuilt
     assert m._block_table(order, torch.device(DEV))[0] is table
     torch.cuda.synchronize()
@@ -154,6 +156,46 @@ def test_compute_attention_decode_matches_oracle(dtype):
     # one more token changes the table
     m.append_token("r2")
     assert m._block_table(order, torch.device(DEV))[1].cpu().tolist() == [200, 0, 37, 2]
+
+
+def test_block_table_patched_on_growth():
+    """Decode-style growth (token counts + 1, a page appended now and then)
+    patches the kept device table in place; a shrink, a freed request or a
+    list past the width rebuilds it.  Every state is compared with the table
+    built on the host from the page lists."""
+    _say("block table growth patches")
+    m = _mgr(num_kv_heads=2, max_pages=400, num_layers=1)
+    rids = ["a", "b", "c"]
+    for rid, n in zip(rids, [15, 16, 40]):
+        m.allocate(rid, num_tokens=n)
+    dev = torch.device(DEV)
+
+    def check(order):
+        table, ctx = m._block_table(order, dev)
+        want_t, want_c = _host_table(m, order)
+        w = want_t.shape[1]
+        assert (table[:, w:] == -1).all()
+        assert torch.equal(table[:, :w].cpu(), want_t) and torch.equal(ctx.cpu(), want_c)
+        return table
+
+    first = check(rids)
+    width = first.shape[1]
+    for step in range(40):  # pages appended by a, b and c at different steps
+        for rid in rids:
+            m.append_token(rid)
+        assert check(rids) is first
+    m.allocate("d", num_tokens=3)
+    assert check(rids + ["d"]) is not first  # another batch: rebuilt
+    assert check(rids) is not first
+    again = check(rids)
+    m.free("b")
+    m.allocate("b", num_tokens=5)  # a new entry under the same id
+    assert check(rids) is not again
+    grown = check(rids)
+    while len(m._page_tables["c"].pages) <= grown.shape[1]:  # past the width
+        m.append_token("c")
+    assert check(rids) is not grown
+    assert width >= 16
 
 
 def test_compute_attention_decode_without_pages_is_none():

@@ -1,0 +1,246 @@
+"""Batched decode of a Hugging Face model over the paged KV cache, and the
+manager's Hugging Face cache conversions, on the GPU.
+
+Model: a tiny random Llama (head_dim 128, GQA 2:1, two layers).  Requests of
+ragged lengths (5, 16, 33 prompt tokens: inside a page, exactly one page,
+past two pages) are prefilled one at a time into the pages, then decoded
+together for 20 teacher-forced steps, one forward per step.
+
+The reference is the same model in float32 on the CPU with eager attention,
+each request decoded alone with its own ``DynamicCache`` (what the reference
+batcher's ``_forward_single`` computes).  Logits agree within
+2e-2 + 2e-2 |ref| for float32, float16 and bfloat16 pools (the paged decode's
+bar on attention outputs, 2e-3 + 1e-2 |ref|, carried through two layers and
+the output projection; bfloat16 storage alone moves these logits by at most
+4e-3).  Quantized pools add their codec's error: on the CPU, rounding the
+cached K/V as int8 (amax / 127 per token and head) moves these logits by up
+to 1.4e-2 and as e4m3 by up to 5.7e-2, so their bars are 5e-2 and 0.15
+absolute.  Batching itself must not change a request's result: the same
+requests decoded one at a time through the pages agree within 5e-3 (float32
+reassociation, and the odd code that rounds the other way when the model's
+products differ in the last bit between batch sizes).
+"""
+import copy
+
+import pytest
+import torch
+from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+
+from vramancer_amd.paged_attention import PagedKVCacheManager, PagedKVConfig
+from vramancer_amd.paged_batch import PagedBatchCache, decode_step, enable_paged_attention, prefill
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+PROMPTS = (5, 16, 33)
+STEPS = 20
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _model():
+    cfg = LlamaConfig(vocab_size=256, hidden_size=512, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=512)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).eval()
+
+
+def _manager(dtype, max_pages=64):
+    return PagedKVCacheManager(PagedKVConfig(page_size=16, num_layers=2, num_kv_heads=2, head_dim=128,
+                                             max_pages=max_pages, device=DEV, dtype=dtype))
+
+
+@pytest.fixture(scope="module")
+def setting():
+    model = _model()
+    gen = torch.Generator().manual_seed(5)
+    streams = [torch.randint(0, 256, (1, n + STEPS), generator=gen) for n in PROMPTS]
+    ref = []
+    with torch.no_grad():
+        for ids, n in zip(streams, PROMPTS):
+            cache = DynamicCache()
+            rows = [model(ids[:, :n], past_key_values=cache, use_cache=True).logits[0, -1]]
+            for s in range(STEPS):
+                rows.append(model(ids[:, n + s:n + s + 1], past_key_values=cache, use_cache=True).logits[0, -1])
+            ref.append(torch.stack(rows))
+    gpu_model = copy.deepcopy(model).to(DEV)
+    enable_paged_attention(gpu_model)
+    return gpu_model, streams, torch.stack(ref, 1)  # [STEPS + 1, R, V]
+
+
+@torch.no_grad()
+def _run(model, mgr, streams, rids, batched=True):
+    rows = [torch.cat([prefill(model, mgr, rid, ids[:, :n].to(DEV)) for rid, ids, n in zip(rids, streams, PROMPTS)])]
+    caches = [PagedBatchCache(mgr, rids)] if batched else [PagedBatchCache(mgr, [r]) for r in rids]
+    for s in range(STEPS):
+        tok = [ids[0, n + s] for ids, n in zip(streams, PROMPTS)]
+        if batched:
+            rows.append(decode_step(model, mgr, rids, torch.stack(tok).to(DEV), caches[0]))
+        else:
+            rows.append(torch.cat([decode_step(model, mgr, [r], t.reshape(1).to(DEV), c)
+                                   for r, t, c in zip(rids, tok, caches)]))
+    return torch.stack(rows).float().cpu()
+
+
+def _close(got, want, atol, rtol, what):
+    err = (got - want).abs()
+    bad = err > atol + rtol * want.abs()
+    assert not bad.any(), f"{what}: {int(bad.sum())} logits off, max err {err.max():.3e}"
+
+
+TOL = {"float32": 2e-2, "float16": 2e-2, "bfloat16": 2e-2, "int8": 5e-2, "fp8": 0.15}
+
+
+@pytest.mark.parametrize("dtype", list(TOL))
+def test_batched_decode_matches_sequential_hf(setting, dtype):
+    model, streams, ref = setting
+    _say(f"paged batch decode vs HF sequential, pool {dtype}")
+    mgr = _manager(dtype)
+    rids = [f"r{i}" for i in range(len(PROMPTS))]
+    for rid in rids:
+        mgr.allocate(rid)
+    got = _run(model, mgr, streams, rids)
+    _close(got, ref, TOL[dtype], 2e-2, f"pool {dtype}")
+    assert [mgr._page_tables[r].num_tokens for r in rids] == [n + STEPS for n in PROMPTS]
+    assert [len(mgr._page_tables[r].pages) for r in rids] == [-(-(n + STEPS) // 16) for n in PROMPTS]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "int8", "fp8"])
+def test_batched_decode_matches_one_at_a_time(setting, dtype):
+    model, streams, _ = setting
+    _say(f"paged batch decode vs one-at-a-time paged decode, pool {dtype}")
+    rids = [f"r{i}" for i in range(len(PROMPTS))]
+    outs = []
+    for batched in (True, False):
+        mgr = _manager(dtype)
+        for rid in rids:
+            mgr.allocate(rid)
+        outs.append(_run(model, mgr, streams, rids, batched))
+    _close(outs[0], outs[1], 5e-3, 5e-3, f"pool {dtype}")
+
+
+def test_batch_with_forked_request(setting):
+    """A fork shares its source's pages (ref counts), so the block table
+    holds the same physical pages in two rows.  Both decode the same tokens:
+    their writes to the shared last page agree, and each then allocates its
+    own page when that one is full (33 + 15 tokens)."""
+    model, streams, ref = setting
+    _say("paged batch decode with a forked request")
+    mgr = _manager("float32")
+    mgr.allocate("a")
+    with torch.no_grad():
+        prefill(model, mgr, "a", streams[2][:, :PROMPTS[2]].to(DEV))
+    mgr.fork("a", "b")
+    cache = PagedBatchCache(mgr, ["a", "b"])
+    rows = []
+    with torch.no_grad():
+        for s in range(STEPS):
+            t = streams[2][0, PROMPTS[2] + s].to(DEV)
+            rows.append(decode_step(model, mgr, ["a", "b"], torch.stack([t, t]), cache).float().cpu())
+    got = torch.stack(rows)
+    _close(got[:, 0], ref[1:, 2], 2e-2, 2e-2, "source")
+    _close(got[:, 1], got[:, 0], 1e-5, 1e-5, "fork")
+    pa, pb = mgr._page_tables["a"].pages, mgr._page_tables["b"].pages
+    assert pa[:3] == pb[:3] and pa[3] != pb[3]
+
+
+def test_fp8_forks_cannot_share_a_step(setting):
+    model, streams, _ = setting
+    mgr = _manager("fp8")
+    mgr.allocate("a")
+    with torch.no_grad():
+        prefill(model, mgr, "a", streams[0][:, :5].to(DEV))
+        mgr.fork("a", "b")
+        with pytest.raises(RuntimeError, match="share their last page"):
+            decode_step(model, mgr, ["a", "b"], torch.tensor([1, 1], device=DEV))
+
+
+def test_decode_step_pool_exhausted_raises(setting):
+    model, streams, _ = setting
+    _say("paged batch decode, pool exhausted")
+    mgr = _manager("float16", max_pages=3)
+    mgr.allocate("x")
+    with torch.no_grad():
+        prefill(model, mgr, "x", streams[1][:, :16].to(DEV))
+        mgr.allocate("y")
+        prefill(model, mgr, "y", streams[0][:, :32].to(DEV))
+        assert not mgr._free_pages
+        with pytest.raises(RuntimeError, match="no page left"):
+            decode_step(model, mgr, ["x", "y"], torch.tensor([1, 2], device=DEV))
+
+
+def test_multi_token_update_raises(setting):
+    model, streams, _ = setting
+    mgr = _manager("float16")
+    mgr.allocate("x")
+    with torch.no_grad():
+        prefill(model, mgr, "x", streams[0][:, :5].to(DEV))
+        with pytest.raises(RuntimeError, match="one token per request"):
+            model(streams[0][:, 5:8].to(DEV), past_key_values=PagedBatchCache(mgr, ["x"]), use_cache=True)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int8", "fp8"])
+@pytest.mark.parametrize("seq_len", [1, 16, 37])
+def test_from_to_hf_cache_roundtrip(dtype, seq_len):
+    """from_hf_cache then to_hf_cache returns the states as the pool stores
+    them: exactly the cast for float pools, within half a quantization step
+    for int8 (scale amax / 127 per token and head) and within the e4m3
+    rounding of the page scale for fp8."""
+    _say(f"from/to_hf_cache {dtype} seq_len {seq_len}")
+    mgr = _manager(dtype)
+    g = torch.Generator(device=DEV).manual_seed(seq_len)
+    past = tuple((torch.randn(1, 2, seq_len, 128, device=DEV, generator=g),
+                  torch.randn(1, 2, seq_len, 128, device=DEV, generator=g)) for _ in range(2))
+    mgr.allocate("r")
+    mgr.from_hf_cache("r", past)
+    entry = mgr._page_tables["r"]
+    assert entry.num_tokens == seq_len and len(entry.pages) == -(-seq_len // 16)
+    back = mgr.to_hf_cache("r")
+    assert len(back) == 2
+    for (k, v), (k2, v2) in zip(past, back):
+        for a, b in ((k, k2), (v, v2)):
+            assert tuple(b.shape) == (1, 2, seq_len, 128)
+            if dtype in ("float32", "float16", "bfloat16"):
+                assert b.dtype == getattr(torch, dtype)
+                assert torch.equal(b, a.to(b.dtype))
+            elif dtype == "int8":
+                step = a.abs().amax(-1, keepdim=True) / 127
+                assert ((b - a).abs() <= 0.5 * step * (1 + 1e-5) + 1e-7).all()
+            else:
+                # one scale per (page, kv-head): e4m3 keeps 3 mantissa bits
+                assert ((b - a).abs() <= a.abs() * 2.0 ** -4 + 2.0 ** -9 * a.abs().amax()).all()
+
+
+def test_from_hf_cache_accepts_dynamic_cache():
+    _say("from_hf_cache of a DynamicCache")
+    mgr = _manager("float32")
+    cache = DynamicCache()
+    g = torch.Generator(device=DEV).manual_seed(1)
+    states = [(torch.randn(1, 2, 20, 128, device=DEV, generator=g),
+               torch.randn(1, 2, 20, 128, device=DEV, generator=g)) for _ in range(2)]
+    for i, (k, v) in enumerate(states):
+        cache.update(k, v, i)
+    mgr.from_hf_cache("new", cache)  # allocates the request
+    back = mgr.to_hf_cache("new")
+    for (k, v), (k2, v2) in zip(states, back):
+        assert torch.equal(k, k2) and torch.equal(v, v2)
+
+
+def test_prefix_cache_pages_read_back():
+    """A request that hits the prefix cache shares the pages the first one
+    wrote: to_hf_cache of the second request returns the first one's K/V."""
+    _say("prefix cache hit reads the shared pages")
+    mgr = _manager("float32")
+    tokens = list(range(40))
+    assert mgr.try_prefix_cache("a", tokens) == 0
+    g = torch.Generator(device=DEV).manual_seed(2)
+    past = tuple((torch.randn(1, 2, 32, 128, device=DEV, generator=g),
+                  torch.randn(1, 2, 32, 128, device=DEV, generator=g)) for _ in range(2))
+    mgr.from_hf_cache("a", past)
+    assert mgr.try_prefix_cache("b", tokens) == 32
+    assert mgr._page_tables["b"].pages == mgr._page_tables["a"].pages
+    back = mgr.to_hf_cache("b")
+    for (k, v), (k2, v2) in zip(past, back):
+        assert torch.equal(k, k2) and torch.equal(v, v2)

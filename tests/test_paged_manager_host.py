@@ -132,3 +132,72 @@ def test_pages_needed_is_ceil_division():
     for n in (1, 15, 16, 17, 47, 48):
         m = _mgr()
         assert len(m.allocate("a", num_tokens=n).pages) == math.ceil(n / 16)
+
+
+def test_prefix_cache_miss_then_hit():
+    """core/paged_attention.py:521-566: full pages only; a first request
+    registers its pages, a second with the same prefix shares them."""
+    m = _mgr(page_size=4, max_pages=16)
+    tokens = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10]  # two full pages and a partial one
+    assert m.try_prefix_cache("a", tokens) == 0
+    assert m._page_tables["a"].pages == [15, 14] and m._page_tables["a"].num_tokens == 8
+    assert m.try_prefix_cache("b", tokens) == 8
+    assert m._page_tables["b"].pages == [15, 14]
+    assert [m._pages[p].ref_count for p in (15, 14)] == [2, 2]
+    s = m.stats()
+    assert s["prefix_cache_entries"] == 2 and s["prefix_cache_hits"] == 2 and s["active_requests"] == 2
+    assert m.free("a") == 0 and m.free("b") == 2
+
+
+def test_prefix_cache_hits_count_only_a_run_to_the_last_page():
+    m = _mgr(page_size=4, max_pages=16)
+    m.try_prefix_cache("a", [1, 2, 3, 4, 5, 6, 7, 8])
+    # first page hits, second misses: the count restarts at the miss
+    assert m.try_prefix_cache("b", [1, 2, 3, 4, 0, 0, 0, 0]) == 0
+    assert m._page_tables["b"].pages == [15, 13]
+    # a miss then a hit counts the hit
+    assert m.try_prefix_cache("c", [9, 9, 9, 9, 5, 6, 7, 8]) == 4
+    assert m._page_tables["c"].pages == [12, 14]
+
+
+def test_prefix_cache_skips_freed_pages_and_stops_when_full():
+    m = _mgr(page_size=4, max_pages=3)
+    m.try_prefix_cache("a", [1, 2, 3, 4])
+    m.free("a")
+    # the registered page is free again: a miss, which re-registers the page popped
+    assert m.try_prefix_cache("b", [1, 2, 3, 4]) == 0
+    assert m._page_tables["b"].pages == [2]
+    assert m.try_prefix_cache("c", list(range(100, 116))) == 0
+    assert m._page_tables["c"].pages == [1, 0] and m._page_tables["c"].num_tokens == 8
+
+
+def test_hf_conversions_without_a_pool():
+    """Without a GPU pool from_hf_cache does nothing and to_hf_cache returns
+    None (core/paged_attention.py:728-729, 825-826)."""
+    torch = pytest.importorskip("torch")
+    m = _mgr()
+    m.allocate("a")
+    m.from_hf_cache("a", ((torch.zeros(1, 2, 3, 128), torch.zeros(1, 2, 3, 128)),))
+    assert m._page_tables["a"].num_tokens == 0 and m.to_hf_cache("a") is None
+
+
+def test_hf_layers_reads_each_cache_form():
+    torch = pytest.importorskip("torch")
+    from transformers import DynamicCache
+
+    from vramancer_amd.paged_attention import hf_layers
+
+    k = [torch.full((1, 2, 3, 4), float(i)) for i in range(3)]
+    v = [t + 10 for t in k]
+    legacy = tuple(zip(k, v))
+    dyn = DynamicCache()
+    for i in range(3):
+        dyn.update(k[i], v[i], i)
+
+    class Old:  # transformers 4.36-4.x attribute form
+        key_cache, value_cache = k, v
+
+    for form in (legacy, dyn, Old()):
+        got = hf_layers(form)
+        assert len(got) == 3
+        assert all(torch.equal(a, b) and torch.equal(c, d) for (a, c), b, d in zip(got, k, v))

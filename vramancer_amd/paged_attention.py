@@ -24,12 +24,16 @@ Device side, in this library's kernels:
   ``sparse_v_ratio < 1`` each head keeps its top-k softmax weights
   (``vrm_turboquant_score`` + ``vrm_topk_attend``, :1384-1400);
 * ``compress_page_bulk`` compresses a page's raw K/V for every layer that has
-  no codes yet (``vrm_tq_compress_pool``).
+  no codes yet (``vrm_tq_compress_pool``);
+* ``from_hf_cache`` stores a prefilled Hugging Face cache in a request's
+  pages with one ``vrm_kv_write`` launch per layer, ``to_hf_cache`` gathers
+  it back; ``try_prefix_cache`` shares full pages of a token prefix between
+  requests (host bookkeeping, :521-566).
 
 Not built (outside the decode path): multi-GPU pools, the VRAM lending pool,
 LRU eviction to other memory tiers (``append_token`` returns ``None`` once
-the pool is exhausted, where the reference would try to evict), prefix
-caching, parity engrams and the Hugging Face cache conversions.
+the pool is exhausted, where the reference would try to evict) and parity
+engrams.
 
 A manager whose ``device`` is not a GPU keeps the host bookkeeping only: it
 allocates no pools, its decode calls return ``None`` (as the reference's do
@@ -49,7 +53,7 @@ import numpy as np
 
 from . import _lib
 
-__all__ = ["PagedKVConfig", "PhysicalPage", "PageTableEntry", "PagedKVCacheManager"]
+__all__ = ["PagedKVConfig", "PhysicalPage", "PageTableEntry", "PagedKVCacheManager", "hf_layers"]
 
 # Pool element types: name -> (torch dtype name, bytes per element).
 _POOL_DTYPES = {
@@ -149,6 +153,20 @@ def _is_gpu(device: str) -> bool:
     return str(device).startswith("cuda")
 
 
+def hf_layers(past_key_values: Any) -> List[Tuple[Any, Any]]:
+    """(key, value) per layer of a Hugging Face cache: a ``Cache`` whose
+    ``layers`` hold ``keys``/``values``, one with ``key_cache`` /
+    ``value_cache`` lists (transformers 4.36-4.x), or a tuple of pairs.  For
+    a ``Cache``, the layers up to the first one that holds nothing."""
+    layers = getattr(past_key_values, "layers", None)
+    if layers is not None:
+        filled = itertools.takewhile(lambda l: getattr(l, "keys", None) is not None and l.keys.numel() > 0, layers)
+        return [(layer.keys, layer.values) for layer in filled]
+    if hasattr(past_key_values, "key_cache"):
+        return list(zip(past_key_values.key_cache, past_key_values.value_cache))
+    return [(kv[0], kv[1]) for kv in past_key_values]
+
+
 class PagedKVCacheManager:
     """Block-based KV cache with on-demand page allocation and GPU decode."""
 
@@ -164,8 +182,11 @@ class PagedKVCacheManager:
         # Bumped by every change of a page list or token count; keys the
         # device block-table cache of compute_attention_decode.
         self._epoch = 0
-        self._table_cache: Optional[tuple] = None
+        self._table_cache: Optional[dict] = None
         self._workspaces: Dict[tuple, Any] = {}
+        # hash(tuple of a full page's token ids) -> page id (:216, :540-558).
+        self._prefix_cache: Dict[int, int] = {}
+        self._cache_hits = 0
 
         self._gpu_pool: Any = None
         self._kv_scales: Any = None
@@ -336,6 +357,44 @@ class PagedKVCacheManager:
             self._epoch += 1
             return entry
 
+    def try_prefix_cache(self, request_id: str, token_ids: Sequence[int]) -> int:
+        """Prefix caching over full pages (core/paged_attention.py:521-566).
+
+        Walks ``token_ids`` a full page at a time (a trailing partial page is
+        not looked at): a page whose token tuple hashes to an entry of the
+        prefix cache that is still allocated is shared (ref count + 1) and
+        counts ``page_size`` hits; otherwise a new page is allocated and
+        registered under that hash, and the hit count restarts at 0 (only a
+        run of hits ending at the last full page counts).  The walk stops when
+        the pool is empty.  The request's token count becomes pages *
+        page_size.  Returns the hit count."""
+        PS = self.config.page_size
+        with self._lock:
+            entry = self._page_tables.get(request_id)
+            if entry is None:
+                entry = self._page_tables[request_id] = PageTableEntry(request_id=request_id)
+            hits = 0
+            for start in range(0, len(token_ids) - PS + 1, PS):
+                key = hash(tuple(token_ids[start:start + PS]))
+                cached = self._prefix_cache.get(key)
+                if cached is not None and self._pages[cached].allocated:
+                    entry.pages.append(cached)
+                    self._pages[cached].ref_count += 1
+                    self._pages[cached].last_access = time.time()
+                    hits += PS
+                    self._cache_hits += 1
+                else:
+                    page_id = self._alloc_page()
+                    if page_id is None:
+                        break
+                    entry.pages.append(page_id)
+                    self._prefix_cache[key] = page_id
+                    hits = 0
+            entry.num_tokens = len(entry.pages) * PS
+            self._peak_usage = max(self._peak_usage, self.config.max_pages - len(self._free_pages))
+            self._epoch += 1
+            return hits
+
     # ------------------------------------------------------------------
     # Writes (core/paged_attention.py:568-675)
     # ------------------------------------------------------------------
@@ -467,45 +526,170 @@ class PagedKVCacheManager:
         return keys, values
 
     # ------------------------------------------------------------------
+    # Hugging Face caches (core/paged_attention.py:716-912)
+    # ------------------------------------------------------------------
+
+    def from_hf_cache(self, request_id: str, past_key_values: Any) -> None:
+        """Stores a prefilled Hugging Face cache in a request's pages
+        (core/paged_attention.py:716-805).
+
+        ``past_key_values`` is a ``Cache`` or a tuple of (key, value) pairs,
+        keys/values [batch, num_kv_heads, seq_len, head_dim]; batch row 0 is
+        stored, as in the reference.  Pages are added until seq_len tokens
+        fit (fewer when the pool runs out), the token count becomes seq_len,
+        and each of the first num_layers layers is written with one
+        ``vrm_kv_write`` launch (for int8 / fp8 pools, one
+        ``vrm_kv_quant_pages`` launch over whole pages).  TurboQuant codes are not written here: as in the reference they are
+        made when a turbo decode or ``compress_page_bulk`` needs them.  Does
+        nothing without a pool."""
+        import torch
+
+        if self._gpu_pool is None or past_key_values is None:
+            return
+        if self._page_tables.get(request_id) is None:
+            self.allocate(request_id)
+        layers = hf_layers(past_key_values)
+        if not layers:
+            return
+        cfg = self.config
+        seq_len = int(layers[0][0].shape[2])
+        for k, v in layers[:cfg.num_layers]:
+            for t in (k, v):
+                if t.dim() != 4 or t.shape[1] != cfg.num_kv_heads or t.shape[2] != seq_len \
+                        or t.shape[3] != cfg.head_dim:
+                    raise RuntimeError(f"cache states must be [batch, {cfg.num_kv_heads}, {seq_len}, "
+                                       f"{cfg.head_dim}], got {tuple(t.shape)}")
+        with self._lock:
+            entry = self._page_tables[request_id]
+            while len(entry.pages) < math.ceil(seq_len / cfg.page_size):
+                page_id = self._alloc_page()
+                if page_id is None:
+                    break
+                entry.pages.append(page_id)
+            entry.num_tokens = seq_len
+            self._peak_usage = max(self._peak_usage, cfg.max_pages - len(self._free_pages))
+            self._epoch += 1
+            pages = np.asarray(entry.pages, dtype=np.int64)
+        PS, KH, D = cfg.page_size, cfg.num_kv_heads, cfg.head_dim
+        n = min(seq_len, len(pages) * PS)
+        if n == 0:
+            return
+        dev = self._gpu_pool.device
+        nl = min(len(layers), cfg.num_layers)
+        if self._kv_scales is not None:
+            # Quantized pools take whole pages (the fp8 scale is one per page).
+            from . import kv_quant
+
+            NP = -(-n // PS)
+            ids = torch.from_numpy(pages[:NP].astype(np.int32)).to(dev)
+            n_valid = torch.from_numpy(np.minimum(PS, n - PS * np.arange(NP)).astype(np.int32)).to(dev)
+
+            def page_major(t):  # [1, KH, S, D] -> [NP, KH, PS, D], zero past n
+                rows = torch.zeros((KH, NP * PS, D), dtype=t.dtype, device=dev)
+                rows[:, :n] = t[0, :, :n]
+                return rows.view(KH, NP, PS, D).transpose(0, 1)
+
+            for layer_idx in range(nl):
+                k, v = layers[layer_idx]
+                _lib.require_cuda(k, v, self._gpu_pool)
+                kv_quant.quantize_pages(self._gpu_pool, self._kv_scales, layer_idx, ids, page_major(k),
+                                        page_major(v), n_valid)
+            return
+        t = np.arange(n)
+        ids = torch.from_numpy(np.stack([pages[t // PS], t % PS]).astype(np.int32)).to(dev)
+        for layer_idx in range(nl):
+            k, v = layers[layer_idx]
+            key = self._rows(k[0, :, :n].transpose(0, 1), n, "key")
+            value = self._rows(v[0, :, :n].transpose(0, 1), n, "value")
+            self._write_rows(layer_idx, ids[0], ids[1], key, value)
+
+    def to_hf_cache(self, request_id: str) -> Optional[tuple]:
+        """A request's pages as a Hugging Face legacy cache
+        (core/paged_attention.py:807-912): a tuple over num_layers of (key,
+        value), each [1, num_kv_heads, tokens, head_dim] in the pool's dtype
+        (float32 for int8 / fp8 pools, dequantized).  ``None`` without a pool
+        or for a request with no page."""
+        if self._gpu_pool is None:
+            return None
+        out = []
+        for layer_idx in range(self.config.num_layers):
+            got = self.read_kv(request_id, layer_idx)
+            if got is None:
+                return None
+            out.append((got[0].unsqueeze(0), got[1].unsqueeze(0)))
+        return tuple(out)
+
+    # ------------------------------------------------------------------
     # Decode (core/paged_attention.py:1193-1418)
     # ------------------------------------------------------------------
 
     def _block_table(self, request_ids: Sequence[str], device) -> Optional[tuple]:
-        """Device (page_table [B, max_pp], context_lens [B]) for a batch of
-        requests, rebuilt only when a page list or token count changed."""
+        """Device (page_table [B, width], context_lens [B]) for a batch of
+        requests; ``None`` when no request has a page.
+
+        ``width`` is the longest page list plus headroom (entries past a
+        request's pages are -1; the decode reads only ctx's pages).  The
+        table is kept for the next call with the same requests: reused as is
+        while no page list or token count changed; when the requests only
+        grew within the width (decode steps: every count + 1, now and then a
+        new page) the new token counts and page ids are uploaded and patched
+        in place on the current stream, an upload of O(B) values instead of
+        every page id; anything else rebuilds it with
+        ``vrm_build_block_table``."""
         import torch
 
-        key = (tuple(request_ids), self._epoch, str(device))
-        if self._table_cache is not None and self._table_cache[0] == key:
-            return self._table_cache[1]
+        rids, dev = tuple(request_ids), str(device)
+        c = self._table_cache
+        if c is not None and c["key"] == (rids, dev) and c["epoch"] == self._epoch:
+            return c["result"]
+        B = len(rids)
         with self._lock:
-            lists, ntok = [], []
-            for rid in request_ids:
-                entry = self._page_tables.get(rid)
-                lists.append(entry.pages if entry is not None else [])
-                ntok.append(entry.num_tokens if entry is not None else 0)
-            key = (tuple(request_ids), self._epoch, str(device))
-        B = len(request_ids)
-        counts = np.fromiter((len(p) for p in lists), dtype=np.int64, count=B)
-        max_pp = int(counts.max()) if B else 0
+            epoch = self._epoch
+            entries = [self._page_tables.get(rid) for rid in rids]
+            lists = [e.pages if e is not None else [] for e in entries]
+            counts = np.fromiter((len(p) for p in lists), dtype=np.int64, count=B)
+            ntok = np.fromiter((e.num_tokens if e is not None else 0 for e in entries), dtype=np.int64, count=B)
+            max_pp = int(counts.max()) if B else 0
+            grow = (c is not None and c["key"] == (rids, dev) and max_pp <= c["width"]
+                    and all(a is b for a, b in zip(entries, c["entries"])) and bool((counts >= c["counts"]).all()))
+            if grow:
+                old = c["counts"]
+                new = [(b * c["width"] + j, lists[b][j]) for b in np.flatnonzero(counts > old).tolist()
+                       for j in range(int(old[b]), int(counts[b]))]
+            elif max_pp:
+                total = int(counts.sum())
+                flat = np.fromiter(itertools.chain.from_iterable(lists), dtype=np.int32, count=total)
         if max_pp == 0:
             return None
-        total = int(counts.sum())
+        if grow:
+            n = len(new)
+            host = np.empty(B + 2 * n, dtype=np.int64)  # token counts, flat table indices, page ids: one upload
+            host[:B] = ntok
+            if n:
+                host[B:] = np.asarray(new, dtype=np.int64).T.reshape(-1)
+            buf = torch.from_numpy(host).to(device)
+            table, ctx = c["result"]
+            ctx.copy_(buf[:B])
+            if n:
+                table.view(-1).index_copy_(0, buf[B:B + n], buf[B + n:].to(torch.int32))
+            c.update(epoch=epoch, counts=counts, buf=buf)
+            return c["result"]
+        width = max_pp + max(16, max_pp // 8)
         host = np.empty(2 * B + 1 + total, dtype=np.int32)  # offsets, token counts, pages: one upload
         host[0] = 0
         np.cumsum(counts, out=host[1:B + 1])
         host[B + 1:2 * B + 1] = ntok
-        host[2 * B + 1:] = np.fromiter(itertools.chain.from_iterable(lists), dtype=np.int32, count=total)
+        host[2 * B + 1:] = flat
         buf = torch.from_numpy(host).to(device)
-        table = torch.empty((B, max_pp), dtype=torch.int32, device=device)
+        table = torch.empty((B, width), dtype=torch.int32, device=device)
         ctx = torch.empty((B,), dtype=torch.int32, device=device)
         rc = _lib.load().vrm_build_block_table(
-            _lib.ptr(buf[2 * B + 1:]) if total else None, total, _lib.ptr(buf), _lib.ptr(buf[B + 1:]), B, max_pp,
+            _lib.ptr(buf[2 * B + 1:]) if total else None, total, _lib.ptr(buf), _lib.ptr(buf[B + 1:]), B, width,
             _lib.ptr(table), _lib.ptr(ctx), _lib.stream_of(table))
         _lib.check(rc, "build_block_table")
-        result = (table, ctx)
-        self._table_cache = (key, result, buf)
-        return result
+        self._table_cache = dict(key=(rids, dev), epoch=epoch, entries=entries, counts=counts, width=width,
+                                 result=(table, ctx), buf=buf)
+        return table, ctx
 
     def _workspace(self, B: int, H: int, max_pp: int, device):
         from .paged_attention_cuda import decode_workspace
@@ -736,6 +920,8 @@ class PagedKVCacheManager:
             "total_allocations": self._total_allocations,
             "total_frees": self._total_frees,
             "active_requests": len(self._page_tables),
+            "prefix_cache_entries": len(self._prefix_cache),
+            "prefix_cache_hits": self._cache_hits,
             "page_size_tokens": self.config.page_size,
             "memory_mb": self.config.total_memory_bytes / 1e6,
             "devices": [self.config.device],
