@@ -125,7 +125,7 @@ def _codes(pool, comp, layer):
     return {k: t.cpu() for k, t in c.items()}
 
 
-@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("H,KH", [(40, 8), (16, 2), (8, 8)])
 def test_decode_turbo_matches_oracle(bits, H, KH):
     _say(f"turbo decode bits {bits} H {H} KH {KH}")

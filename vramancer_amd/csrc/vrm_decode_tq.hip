@@ -289,14 +289,14 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     float p = radius;
     p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
     p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
-    const float2 c4 = lut[bit_field<BITS>(q, 0)];  // level 4: slot 0
+    const float2 c4 = lut[bit_field<BITS>(q, (kT32 ? 30 : 0) * BITS)];  // level 4
     const float x3[2] = {p * c4.x, p * c4.y};
     float y[8];  // the level-1 nodes
     if constexpr (kT32) {
-      // levels 3 and 2: node j (slot 1 + j), children slots 3 + 2 j, 4 + 2 j
+      // levels 3 and 2: node j and its children in slots 24 + 3 j .. 26 + 3 j
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float4 t = t32[bit_field<BITS>(q, (1 + j) * BITS) + NB * bit_field<2 * BITS>(q, (3 + 2 * j) * BITS)];
+        const float4 t = t32[bit_field<3 * BITS>(q, (24 + 3 * j) * BITS)];
         y[4 * j] = x3[j] * t.x;
         y[4 * j + 1] = x3[j] * t.y;
         y[4 * j + 2] = x3[j] * t.z;
@@ -315,10 +315,12 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
         y[2 * i + 3] = x2[i + 1] * a2.w;
       }
     }
-    // levels 1 and 0: node j (slot 7 + j), children slots 15 + 2 j, 16 + 2 j
+    // levels 1 and 0: node j and its children in slots 3 j .. 3 j + 2 (4 bits:
+    // node slot 7 + j, children slots 15 + 2 j, 16 + 2 j)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float4 t = t10[bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
+      const float4 t = t10[kT32 ? bit_field<3 * BITS>(q, 3 * j * BITS)
+                                : bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
       cur[4 * j] = y[j] * t.x;
       cur[4 * j + 1] = y[j] * t.y;
       cur[4 * j + 2] = y[j] * t.z;

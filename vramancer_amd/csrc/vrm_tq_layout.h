@@ -13,14 +13,22 @@
 // Angle record of one token: four quarters of 4 * bits bytes.  Quarter g holds
 // the 31 angles of the subtree over dims 32 g .. 32 g + 31 plus one spare slot
 // that carries a top-level angle, so that a decode lane owning those dims
-// reads one aligned 4 * bits-byte word:
-//   slot 0            level 4, angle g
-//   slots 1 .. 2      level 3, angles 2 g .. 2 g + 1
-//   slots 3 .. 6      level 2, angles 4 g .. 4 g + 3
-//   slots 7 .. 14     level 1, angles 8 g .. 8 g + 7
-//   slots 15 .. 30    level 0, angles 16 g .. 16 g + 15
-//   slot 31           quarter 0: level 6 angle; quarter 1: level 5 angle 0;
-//                     quarter 2: level 5 angle 1; quarter 3: 0
+// reads one aligned 4 * bits-byte word.  For bits <= 3 a node's angle is
+// followed by its two children's, so that the index of a two-level product
+// table (node bin + NB * child-0 bin + NB^2 * child-1 bin, NB = 2^bits) is one
+// contiguous 3 * bits-bit field:
+//   slots 3 j, 3 j + 1, 3 j + 2       (j = 0 .. 7) level 1 angle 8 g + j,
+//                                     then level 0 angles 16 g + 2 j, 16 g + 2 j + 1
+//   slots 24 + 3 j .. 26 + 3 j        (j = 0, 1) level 3 angle 2 g + j, then
+//                                     level 2 angles 4 g + 2 j, 4 g + 2 j + 1
+//   slot 30                           level 4 angle g
+// For bits == 4 the levels are in order (the decode reads siblings in pairs):
+//   slot 0 level 4 angle g; slots 1, 2 level 3 angles 2 g, 2 g + 1; slots
+//   3 .. 6 level 2 angles 4 g ..; slots 7 .. 14 level 1 angles 8 g ..; slots
+//   15 .. 30 level 0 angles 16 g ..
+// For every bits:
+//   slot 31   quarter 0: level 6 angle; quarter 1: level 5 angle 0;
+//             quarter 2: level 5 angle 1; quarter 3: 0
 // Slot s occupies bits [s * bits, (s + 1) * bits) of its quarter, bit i of a
 // quarter being bit i % 8 of its byte i / 8 (little-endian).  The record has
 // exactly the 127 * bits bits of the reference's packed angles (plus bits
@@ -49,11 +57,22 @@ __host__ __device__ constexpr int slice_bytes(int bits) { return norms_offset(bi
 __host__ __device__ constexpr int level_offset(int l) { return kPD - (kPD >> l); }
 
 // (quarter, slot) of angle i of level l.
-__host__ __device__ inline void slot_of(int l, int i, int& quarter, int& slot) {
+__host__ __device__ inline void slot_of(int l, int i, int bits, int& quarter, int& slot) {
   if (l <= 4) {
     const int per = 1 << (4 - l);  // angles of level l per quarter
     quarter = i / per;
-    slot = (per - 1) + (i % per);
+    const int a = i % per;  // angle within the quarter
+    if (bits == 4) {
+      slot = (per - 1) + a;
+      return;
+    }
+    switch (l) {
+      case 0: slot = 3 * (a >> 1) + 1 + (a & 1); break;
+      case 1: slot = 3 * a; break;
+      case 2: slot = 24 + 3 * (a >> 1) + 1 + (a & 1); break;
+      case 3: slot = 24 + 3 * a; break;
+      default: slot = 30; break;
+    }
   } else if (l == 5) {
     quarter = 1 + i;
     slot = 31;
@@ -65,15 +84,23 @@ __host__ __device__ inline void slot_of(int l, int i, int& quarter, int& slot) {
 
 // Level-major bin index (reference order) of slot s of quarter g, or -1 for
 // the unused spare of quarter 3.
-__host__ __device__ inline int bin_index_of(int g, int s) {
+__host__ __device__ inline int bin_index_of(int g, int s, int bits) {
   if (s == 31) return g == 0 ? level_offset(6) : (g <= 2 ? level_offset(5) + (g - 1) : -1);
-  int l = 4, first = 0;
-  while (s >= first + (1 << (4 - l))) {
-    first += 1 << (4 - l);
-    --l;
+  if (bits == 4) {
+    int l = 4, first = 0;
+    while (s >= first + (1 << (4 - l))) {
+      first += 1 << (4 - l);
+      --l;
+    }
+    return level_offset(l) + g * (1 << (4 - l)) + (s - first);
   }
-  const int per = 1 << (4 - l);
-  return level_offset(l) + g * per + (s - first);
+  if (s == 30) return level_offset(4) + g;
+  if (s >= 24) {
+    const int k = (s - 24) / 3, r = (s - 24) % 3;
+    return r == 0 ? level_offset(3) + 2 * g + k : level_offset(2) + 4 * g + 2 * k + (r - 1);
+  }
+  const int j = s / 3, r = s % 3;
+  return r == 0 ? level_offset(1) + 8 * g + j : level_offset(0) + 16 * g + 2 * j + (r - 1);
 }
 
 }  // namespace tq

@@ -304,7 +304,7 @@ __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
     const int g = lane / qdw, k = lane % qdw;
     uint32_t word = 0;
     for (int slot = (32 * k) / a.bits; slot < 32 && slot * a.bits < 32 * k + 32; ++slot) {
-      const int bi = L::bin_index_of(g, slot);
+      const int bi = L::bin_index_of(g, slot, a.bits);
       if (bi < 0) continue;
       const int shift = slot * a.bits - 32 * k;  // may be negative for a slot straddling the dword start
       const uint32_t val = w.bins[bi];
@@ -352,7 +352,7 @@ __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, c
     int l = 0;
     while (i >= L::level_offset(l + 1)) ++l;
     int g, s;
-    L::slot_of(l, i - L::level_offset(l), g, s);
+    L::slot_of(l, i - L::level_offset(l), bits, g, s);
     const int bit = g * 32 * bits + s * bits;
     uint32_t x = rec[bit / 8] | ((bit / 8 + 1 < L::angle_bytes(bits)) ? (uint32_t)rec[bit / 8 + 1] << 8 : 0u);
     angles[(size_t)row * L::kAngles + i] = (uint8_t)((x >> (bit % 8)) & ((1u << bits) - 1));
