@@ -60,6 +60,27 @@ __device__ __forceinline__ uint32_t bit_field(const uint32_t* w, int pos) {
   return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh), 0, WIDTH);
 }
 
+// fp16 pair {fp16(a0 b0), fp16(a1 b1)}, each product rounded once to fp16
+// (v_fma_mix with float32 sources).
+__device__ __forceinline__ uint32_t mul_f16x2(float a0, float b0, float a1, float b1) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0\n\tv_fma_mixhi_f16 %0, %3, %4, 0"
+      : "=&v"(r)
+      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+  return r;
+}
+
+// fp16 pair {fp16(a0 b0 - h.lo), fp16(a1 b1 - h.hi)}: the residuals of the
+// products against their fp16 roundings h, each one fused multiply-add.
+__device__ __forceinline__ uint32_t residual_f16x2(float a0, float b0, float a1, float b1, uint32_t h) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(r)
+      : "v"(a0), "v"(b0), "v"(a1), "v"(b1), "v"(h));
+  return r;
+}
+
 // In-register Walsh-Hadamard transform of 128 values, element e in lane e % 64,
 // register e / 64, in the reference's butterfly order.
 __device__ __forceinline__ void fwht128(float (&v)[2], int lane) {
@@ -282,7 +303,9 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // products, two levels per lookup from the product tables below level 4
   // (4 bits: levels 3 and 2 one at a time with sibling angles together), so
   // each value is the reference's within a float32 rounding or two.
-  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&cur)[32]) {
+  // Leaves the last level's products to the caller: value 4 j + k of the
+  // group is y[j] * t[j][k].
+  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&y)[8], float4 (&t)[8]) {
     constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
     const float2 t6 = lut[(top0 >> sh31) & (NB - 1)];
     const float2 t5 = lut[(topq >> sh31) & (NB - 1)];
@@ -291,7 +314,6 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
     const float2 c4 = lut[bit_field<BITS>(q, (kT32 ? 30 : 0) * BITS)];  // level 4
     const float x3[2] = {p * c4.x, p * c4.y};
-    float y[8];  // the level-1 nodes
     if constexpr (kT32) {
       // levels 3 and 2: node j and its children in slots 24 + 3 j .. 26 + 3 j
 #pragma unroll
@@ -318,30 +340,30 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     // levels 1 and 0: node j and its children in slots 3 j .. 3 j + 2 (4 bits:
     // node slot 7 + j, children slots 15 + 2 j, 16 + 2 j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float4 t = t10[kT32 ? bit_field<3 * BITS>(q, 3 * j * BITS)
-                                : bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
-      cur[4 * j] = y[j] * t.x;
-      cur[4 * j + 1] = y[j] * t.y;
-      cur[4 * j + 2] = y[j] * t.z;
-      cur[4 * j + 3] = y[j] * t.w;
-    }
+    for (int j = 0; j < 8; ++j)
+      t[j] = t10[kT32 ? bit_field<3 * BITS>(q, 3 * j * BITS)
+                      : bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
   };
+  auto comp = [](const float4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; };
 
   // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi.
   auto page_scores = [&](const TqSlot<BITS>& s, int pi, float* sc) {
-    float kv[32];
-    rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), kv);
+    float y[8];
+    float4 t[8];
+    rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), y, t);
     v4f c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      v8h kh, kl;
+      // k = y t as hi = fp16(k) and lo = fp16(k - hi)
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = kv[8 * c + e];
-        kh[e] = (_Float16)x;
-        kl[e] = (_Float16)(x - (float)kh[e]);
+      for (int e = 0; e < 8; e += 2) {
+        const int j = (8 * c + e) >> 2, k = e & 3;
+        hw[e / 2] = mul_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1));
+        lw[e / 2] = residual_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1), hw[e / 2]);
       }
+      const v8h kh = __builtin_bit_cast(v8h, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+      const v8h kl = __builtin_bit_cast(v8h, make_uint4(lw[0], lw[1], lw[2], lw[3]));
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][0], c4, 0, 0, 0);
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][1], c4, 0, 0, 0);
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, QH[c][0], c4, 0, 0, 0);
@@ -376,13 +398,20 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // Values of this lane's token; absent pages and tokens past the context get
   // radius 0 (whatever the page holds), so they contribute exact zeros.
   auto v_operand = [&](const TqSlot<BITS>& s, int pi, v8h (&vop)[4]) {
-    float vv[32];
+    float y[8];
+    float4 t[8];
     const bool live = s.ok && pi * kPS + col < tok_end;
-    rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, vv);
+    rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, y, t);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c) {
+      uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vop[c][e] = (_Float16)vv[8 * c + e];
+      for (int e = 0; e < 8; e += 2) {
+        const int j = (8 * c + e) >> 2, k = e & 3;
+        w[e / 2] = mul_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1));
+      }
+      vop[c] = __builtin_bit_cast(v8h, make_uint4(w[0], w[1], w[2], w[3]));
+    }
   };
 
   auto process_pair = [&](const TqSlot<BITS>& s0, const TqSlot<BITS>& s1, int pi, bool has1) {
