@@ -296,6 +296,37 @@ def test_turbo_lazy_bulk_compression_from_raw_pool():
     assert m.compress_page_bulk(0) is False
 
 
+def test_turbo_reused_pages_are_compressed_afresh():
+    """A freed page goes back with its compression state cleared: when
+    from_hf_cache fills it for a new request (compression deferred), the turbo
+    decode compresses the new contents instead of reading the old codes."""
+    _say("turbo page reuse after free")
+    torch.manual_seed(9)
+    m = _mgr(dtype="float16", kv_compression="turboquant", compression_bits=3, num_kv_heads=2, num_layers=2)
+    _fill(m, ["a"], [40], torch.float32, seed=6)
+    m.flush_compression()
+    old_pages = list(m._page_tables["a"].pages)
+    assert all(m._tq_slots[p, 0] != 0 for p in old_pages)
+    m.free("a")
+    assert all(m._tq_slots[p].sum() == 0 for p in old_pages)
+    g = torch.Generator().manual_seed(10)
+    past = tuple((torch.randn(1, 2, 40, 128, generator=g).to(DEV), torch.randn(1, 2, 40, 128, generator=g).to(DEV))
+                 for _ in range(2))
+    m.from_hf_cache("b", past)
+    assert set(m._page_tables["b"].pages) == set(old_pages)
+    q = torch.randn(4, 128, generator=torch.Generator().manual_seed(11))
+    out = m.compute_attention_turbo(q.to(DEV), "b", 1)
+    torch.cuda.synchronize()
+    raw = m._gpu_pool.cpu()
+    pages = m._page_tables["b"].pages
+    _check_codes(m, {(l, p, s): (raw[p, l, 0, :, s], raw[p, l, 1, :, s]) for p in pages[:2] for l in range(2)
+                     for s in range(16)})
+    table, ctx = _host_table(m, ["b"])
+    ref = PD.paged_attention_decode_turbo(_params(m._kv_compressor), q[None], _codes(m, 1), table, ctx,
+                                          head_map="mod")
+    _assert_close(out, ref[0], "reused pages")
+
+
 def test_compress_page_bulk_valid_slots():
     _say("compress_page_bulk num_valid_slots")
     torch.manual_seed(8)

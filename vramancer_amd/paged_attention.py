@@ -338,6 +338,10 @@ class PagedKVCacheManager:
                 if page.ref_count <= 0:
                     page.allocated = False
                     page.ref_count = 0
+                    if self._tq_slots is not None:
+                        # its codes belong to the old request: the next owner's
+                        # tokens are compressed afresh
+                        self._tq_slots[page_id] = 0
                     self._free_pages.append(page_id)
                     freed += 1
                     self._total_frees += 1
