@@ -157,6 +157,63 @@ def test_fp8_forks_cannot_share_a_step(setting):
             decode_step(model, mgr, ["a", "b"], torch.tensor([1, 1], device=DEV))
 
 
+def test_continuous_batching_churn(setting):
+    """A continuous batcher's life: requests arrive and finish at different
+    steps, every step decodes the active set in one forward (the batch changes
+    shape, so the block table is rebuilt, or patched while it holds), and the
+    pages of finished requests go to newcomers.  Every request's logits match
+    the HF reference decoding it alone."""
+    model, _, _ = setting
+    _say("paged batch decode under churn")
+    plan = [(0, 5, 12), (0, 30, 6), (2, 16, 10), (4, 1, 8), (5, 47, 5), (7, 20, 9)]  # (arrival, prompt, new)
+    gen = torch.Generator().manual_seed(21)
+    streams = [torch.randint(0, 256, (1, n + g), generator=gen) for _, n, g in plan]
+    cpu_model = _model()
+    ref = []
+    with torch.no_grad():
+        for ids, (_, n, g) in zip(streams, plan):
+            cache = DynamicCache()
+            rows = [cpu_model(ids[:, :n], past_key_values=cache, use_cache=True).logits[0, -1]]
+            for t in range(g - 1):
+                rows.append(cpu_model(ids[:, n + t:n + t + 1], past_key_values=cache, use_cache=True).logits[0, -1])
+            ref.append(torch.stack(rows))
+    mgr = _manager("float32", max_pages=16)
+    got = {i: [] for i in range(len(plan))}
+    active, seen_pages, reused = {}, set(), False
+    cache = None
+    with torch.no_grad():
+        for step in range(64):
+            for i, (arr, n, _) in enumerate(plan):
+                if arr == step:
+                    mgr.allocate(f"q{i}")
+                    got[i].append(prefill(model, mgr, f"q{i}", streams[i][:, :n].to(DEV))[0].float().cpu())
+                    active[i] = 0
+                    pages = set(mgr._page_tables[f"q{i}"].pages)
+                    reused |= bool(pages & seen_pages)
+                    seen_pages |= pages
+            ids = sorted(active)
+            if ids:
+                rids = [f"q{i}" for i in ids]
+                if cache is None or cache.request_ids != rids:
+                    cache = PagedBatchCache(mgr, rids)
+                toks = torch.stack([streams[i][0, plan[i][1] + active[i]] for i in ids]).to(DEV)
+                logits = decode_step(model, mgr, rids, toks, cache).float().cpu()
+                for k, i in enumerate(ids):
+                    active[i] += 1
+                    if active[i] < plan[i][2]:
+                        got[i].append(logits[k])
+                    else:  # its last token is in: the request finishes
+                        mgr.free(f"q{i}")
+                        del active[i]
+            if all(arr <= step for arr, _, _ in plan) and not active:
+                break
+    assert not active and all(len(got[i]) == g for i, (_, _, g) in enumerate(plan))
+    assert reused, "no page of a finished request was handed to a newcomer"
+    for i in range(len(plan)):
+        _close(torch.stack(got[i]), ref[i], 2e-2, 2e-2, f"request {i}")
+    assert not mgr._page_tables and len(mgr._free_pages) == 16
+
+
 def test_decode_step_pool_exhausted_raises(setting):
     model, streams, _ = setting
     _say("paged batch decode, pool exhausted")
