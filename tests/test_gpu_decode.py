@@ -267,3 +267,24 @@ def test_decode_full_size_bf16_sampled_parity():
         sub_table = torch.arange(n, dtype=torch.int32)[None]
         ref = PD.paged_attention_decode(q[b:b + 1].cpu(), sub_pool, sub_table, lens[b:b + 1].cpu(), 0)
         _assert_close(out[b:b + 1], ref, f"7b seq {b} ctx {int(lens[b])}")
+
+
+def test_decode_full_size_fp8_sampled_parity():
+    """Mixed-length fp8 at its full size (128 lognormal contexts plus one of
+    131072 tokens, 64/8 heads): the longest, the shortest and a median
+    sequence match the oracle on their own pages."""
+    cfg = workloads.CONFIGS["mixed-fp8"]
+    _say("mixed-fp8 full size")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=9, layers=(0,))
+    q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
+    out = paged_attention_decode(q, pool, table, lens, 0, kv_scales=sc)
+    torch.cuda.synchronize()
+    order = torch.argsort(lens.cpu())
+    picks = [int(order[-1]), int(order[0]), int(order[len(order) // 2])]
+    assert int(lens[picks[0]]) == 131072
+    for b in picks:
+        n = (int(lens[b]) + 15) // 16
+        pages = table[b, :n].long()
+        ref = PD.paged_attention_decode(q[b:b + 1].cpu(), pool[pages].cpu(), torch.arange(n, dtype=torch.int32)[None],
+                                        lens[b:b + 1].cpu(), 0, kv_scales=sc[pages].cpu())
+        _assert_close(out[b:b + 1], ref, f"fp8 seq {b} ctx {int(lens[b])}")

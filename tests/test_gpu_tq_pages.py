@@ -159,3 +159,25 @@ def test_decode_turbo_long_contexts_many_partitions():
     torch.cuda.synchronize()
     ref = PD.paged_attention_decode_turbo(_params(comp), q, _codes(pool, comp, 0), table, lens)
     _assert_close(out, ref, "long contexts")
+
+
+@pytest.mark.parametrize("name", ["14b-turbo3", "14b-turbo4"])
+def test_decode_turbo_full_size_sampled_parity(name):
+    """The TurboQuant benchmark at its full size (B=16 x 32768 tokens, 40/8
+    heads): two sequences match the oracle on the codes read back from their
+    own pages."""
+    from vramancer_amd import workloads
+
+    cfg = workloads.CONFIGS[name]
+    _say(f"{name} full size")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=4, layers=(0,))
+    q, pool, table, lens, comp = (inp["query"], inp["kv_pool"], inp["page_table"], inp["context_lens"],
+                                  inp["compressor"])
+    out = tq_pages.paged_attention_decode_turbo(q, pool, table, lens, 0, comp)
+    torch.cuda.synchronize()
+    for b in (0, 11):
+        n = (int(lens[b]) + 15) // 16
+        codes = {k: t.cpu() for k, t in tq_pages.read_pages(pool, 0, table[b, :n].contiguous(), comp).items()}
+        ref = PD.paged_attention_decode_turbo(_params(comp), q[b:b + 1].cpu(), codes,
+                                              torch.arange(n, dtype=torch.int32)[None], lens[b:b + 1].cpu())
+        _assert_close(out[b:b + 1], ref, f"{name} seq {b}")
