@@ -20,7 +20,9 @@ B=32, 28/4 heads, bf16 pool, context ~U[1024, 8192]; mixed-fp8: 129
 sequences, 64/8 heads, fp8 pool, lognormal contexts plus one of 131072;
 fp32-plumbing); the default line is 14b-int8.  ``--batcher`` times one layer
 of a batched decode step of the 7b-bf16 batch through the pages against the
-reference batcher's pad-and-concat step, on the same GPU.
+reference batcher's pad-and-concat step, on the same GPU.  ``--codecs`` times
+the codec kernels beside the decode (fp8 append, TurboQuant compress, pack,
+decompress, scores, sparse V) with the oracle's CPU time on a sample.
 """
 from __future__ import annotations
 
@@ -238,6 +240,120 @@ def batcher_step(args):
     print(json.dumps(result), flush=True)
 
 
+def codec_bench(args):
+    """``--codecs``: the codec kernels beside the decode, each timed with HIP
+    events on its stream at a size taken from the decode workloads, with its
+    algorithmic bytes (inputs read + outputs written) and the oracle's CPU
+    time on a bounded sample scaled to the same size:
+
+    * fp8 append: one bf16 token per sequence and kv-head into the last page
+      of each of the 129 mixed-fp8 sequences (8 kv-heads, D=128);
+    * TurboQuant (3 bits, D=128) over 65,536 bf16 rows (16 sequences x 512
+      tokens x 8 kv-heads): compress to the raw codes; pack angles and QJL
+      signs; decompress;
+    * attention_score: 40 query heads against 32,768 compressed keys;
+    * sparse V: the same scores, softmax over the top 10 %, decompressed
+      values.
+    """
+    from oracle import kv_codecs as KC
+    from oracle import turboquant as TQ
+    from vramancer_amd.kv_quantizer import KVCacheCompressor, _pack_angles, _pack_bits
+    from vramancer_amd.turboquant_cuda import CUDATurboQuantOps
+
+    dev = torch.device("cuda:0")
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    threads = torch.get_num_threads()
+    g = torch.Generator(device=dev).manual_seed(3)
+    rows = []
+
+    def gpu_us(fn, reps=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        return time_events(lambda i: fn(), reps)
+
+    def cpu_us(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2] * 1e6
+
+    def add(name, us, nbytes, cpu, scale_cpu, sample):
+        rows.append({"name": name, "us": round(us, 2), "bytes": int(nbytes),
+                     "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_of_8TBs": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                     "cpu_us": round(cpu * scale_cpu, 1), "cpu_sample": sample})
+        log(f"{name}: {us:.2f} us, cpu {cpu * scale_cpu:.0f} us")
+
+    # fp8 append, mixed-fp8 shape
+    Bq, KH, D, PS = 129, 8, 128, 16
+    pool, scales = kv_quant.allocate_pool(Bq, 1, KH, D, "fp8", PS, dev)
+    kn = torch.randn((Bq, KH, D), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((Bq, KH, D), generator=g, device=dev).to(torch.bfloat16)
+    pid = torch.arange(Bq, dtype=torch.int32, device=dev)
+    slot = torch.full((Bq,), 7, dtype=torch.int32, device=dev)
+    us = gpu_us(lambda: kv_quant.quantize_append(pool, scales, 0, pid, slot, kn, vn))
+    page0 = torch.zeros((PS, D), dtype=torch.uint8)
+    kc = kn.cpu()
+
+    def cpu_fp8():
+        for b in range(16):
+            for h in range(KH):
+                KC.fp8_append(page0, torch.tensor(0.1), 7, kc[b, h])
+
+    add("fp8_append", us, 2 * Bq * KH * D * (2 + 1) + 2 * Bq * KH * 4, cpu_us(cpu_fp8), 2 * Bq / 16,
+        "oracle fp8_append of 16 of the 129 K rows (all 8 heads), scaled to K and V of 129")
+
+    # TurboQuant over 65,536 rows
+    torch.manual_seed(0)
+    comp = KVCacheCompressor(128, 3).to(dev)
+    p = TQ.TQParams(128, 3, 128, 7, 64, comp._hadamard_signs.cpu(), comp.jl_matrix.cpu())
+    N = 65536
+    x = torch.randn((N, 128), generator=g, device=dev).to(torch.bfloat16)
+    args_ = (128, 128, 7, 3, comp._hadamard_signs, comp.jl_matrix)
+    raw = CUDATurboQuantOps.compress_gpu(x, *args_)
+    S = 2048
+    xs = x[:S].float().cpu()
+    add("tq_compress", gpu_us(lambda: CUDATurboQuantOps.compress_gpu(x, *args_)), N * (256 + 195),
+        cpu_us(lambda: TQ.compress(p, xs, pack=False)), N / S, f"oracle compress of {S} rows, scaled")
+    raw_s = TQ.compress(p, xs, pack=False)
+    add("tq_pack", gpu_us(lambda: (_pack_angles(raw["angles"], 3), _pack_bits(raw["qjl_signs"]))),
+        N * (127 + 64 + 48 + 8),
+        cpu_us(lambda: (TQ.pack_angles(raw_s["angles"], 3), TQ.pack_bits(raw_s["qjl_signs"]))), N / S,
+        f"oracle pack_angles + pack_bits of {S} rows, scaled")
+    add("tq_decompress", gpu_us(lambda: CUDATurboQuantOps.decompress_gpu(raw, 128, 128, 7, 3, comp._hadamard_signs)),
+        N * (2 + 127 + 512), cpu_us(lambda: TQ.decompress(p, raw_s)), N / S,
+        f"oracle decompress of {S} rows, scaled")
+
+    # scores and sparse V: 40 heads against 32,768 keys
+    Nk, M = 32768, 40
+    ck = {k: (v[:Nk] if torch.is_tensor(v) else [a[:Nk] for a in v] if isinstance(v, list) else v)
+          for k, v in raw.items()}
+    ck["shape"] = (Nk, 128)
+    cv = {k: (v[Nk:2 * Nk] if torch.is_tensor(v) else [a[Nk:2 * Nk] for a in v] if isinstance(v, list) else v)
+          for k, v in raw.items()}
+    cv["shape"] = (Nk, 128)
+    q = torch.randn((M, 128), generator=g, device=dev)
+    ks = TQ.compress(p, x[:4096].float().cpu(), pack=False)
+    qc = q.cpu()
+    add("tq_attention_score",
+        gpu_us(lambda: CUDATurboQuantOps.attention_score_gpu(q, ck, *args_, 64)),
+        Nk * 195 + M * Nk * 4 + M * 128 * 4, cpu_us(lambda: TQ.attention_score(p, qc, ks)), Nk / 4096,
+        "oracle attention_score of the 40 heads against 4096 keys, scaled")
+    vs = [TQ.compress(p, r[None], pack=False) for r in x[4096:4096 + 4096].float().cpu()]
+    add("tq_sparse_v_attend",
+        gpu_us(lambda: comp.sparse_v_attend(q, ck, [cv], sparse_v_ratio=0.1)),
+        Nk * (195 + 129) + M * Nk * 4 + M * 128 * 4,
+        cpu_us(lambda: TQ.sparse_v_attend(p, qc[:1], ks, vs, sparse_v_ratio=0.1), reps=1), M * Nk / 4096,
+        "oracle sparse_v_attend of 1 head over 4096 keys (per-token value dicts), scaled to 40 x 32768")
+    print(json.dumps({"metric": "codec kernels: us, algorithmic GB/s, and the oracle on the CPU",
+                      "n_gpus": 1, "data": "synthetic", "cpu_threads": threads, "rows": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,6 +364,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default="14b-int8", choices=sorted(workloads.CONFIGS),
                     help="decode shape to measure (the headline line is 14b-int8)")
+    ap.add_argument("--codecs", action="store_true",
+                    help="time the codec kernels (fp8 append, TurboQuant compress / pack / decompress / scores / "
+                         "sparse V) beside the oracle on the CPU")
     ap.add_argument("--batcher", action="store_true",
                     help="time one layer of a batched decode step, paged vs the reference's pad-and-concat")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -262,6 +381,9 @@ def main():
         sys.exit(2)
     if args.batcher:
         batcher_step(args)
+        return
+    if args.codecs:
+        codec_bench(args)
         return
     lib = _lib.load()
     dev = torch.device("cuda:0")
