@@ -287,7 +287,8 @@ int vrm_turboquant_score(const float* q, int M, const uint16_t* radius, const ui
  * the k-th largest, the lowest-indexed are kept.  k = N is the dense
  * softmax(scores) values.  values [N][D] (row stride ld_values), out [M][D]
  * (row stride ld_out), float32; 1 <= k <= N.
- * workspace: >= vrm_topk_attend_workspace_bytes(M, k) bytes.
+ * workspace: >= vrm_topk_attend_workspace_bytes(M, k) bytes (selection,
+ * kept indices and weights, and the partial sums of the weighted sum).
  */
 size_t vrm_topk_attend_workspace_bytes(int M, int k);
 int vrm_topk_attend(const float* scores, int M, int N, long long ld_scores, int k, const float* values,

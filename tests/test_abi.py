@@ -140,7 +140,10 @@ def test_manager_and_attend_entries_reject_bad_arguments(lib):
               None) == 0
 
     tb = lib.vrm_topk_attend_workspace_bytes(3, 10)
-    assert tb == 3 * 8 + 3 * 10 * 8
+    # selection [M][2] u32, indices and weights [M][k], row meta [M] (16-byte
+    # aligned), partial sums [M][16 splits][256] f32
+    r16 = lambda x: (x + 15) // 16 * 16  # noqa: E731
+    assert tb == r16(r16(3 * 8 + 3 * 10 * 8) + 3 * 8) + 3 * 16 * 256 * 4
     tk = lib.vrm_topk_attend
     assert tk(1, 3, 10, 10, 11, 1, 64, 64, 1, 64, 1, tb, None) == -1  # k > N
     assert tk(1, 3, 10, 10, 0, 1, 64, 64, 1, 64, 1, tb, None) == -1   # k < 1

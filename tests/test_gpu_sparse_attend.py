@@ -61,7 +61,7 @@ def _topk_reference(s, k, v):
 
 
 @pytest.mark.parametrize("M,N,D,k", [(3, 1000, 128, 100), (2, 77, 7, 1), (4, 300, 256, 300), (1, 5000, 64, 4999),
-                                     (70, 40, 128, 13)])
+                                     (70, 40, 128, 13), (2, 600, 300, 57), (40, 32768, 128, 3277)])
 def test_topk_attend_matches_float64(M, N, D, k):
     _say(f"topk M{M} N{N} D{D} k{k}")
     g = torch.Generator().manual_seed(N + k)

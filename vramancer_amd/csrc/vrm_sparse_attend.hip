@@ -16,8 +16,7 @@
 // one workgroup per row.  S_m is every score above T plus, of the scores equal
 // to T, the lowest-indexed ones up to k in total (the reference's topk leaves
 // the choice among equal weights unspecified).  topk_attend_kernel compacts
-// S_m in index order, then computes the weights and the weighted sum (one
-// thread per value dimension).
+// S_m in index order, then computes the weights and the weighted sum.
 #include "vrm_common.h"
 
 #include <math.h>
@@ -115,10 +114,24 @@ __device__ __forceinline__ float block_sum(float v, float* lds) {
 }
 
 // One workgroup per row.  idx_ws / w_ws: [rows][k] scratch (indices, weights).
+// Compaction reads kElems consecutive scores per thread per pass, so one pass
+// (two workgroup scans) covers kThreads * kElems scores in index order.  For
+// D <= kMaxFastD the weighted sum is left to topk_pv_kernel (meta gets the
+// row's kept count and weight sum); wider rows are summed here, one thread
+// per value dimension.
+constexpr int kElems = 4;
+constexpr int kMaxFastD = 256;
+constexpr int kSplits = 16;  // workgroups per row in the weighted sum
+
+struct RowMeta {
+  int count;
+  float l;
+};
+
 __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scores, int N, long long ld, int k,
                                                                const uint32_t* sel, const float* values, int D,
                                                                long long ldv, int32_t* idx_ws, float* w_ws,
-                                                               float* out, long long ldo) {
+                                                               RowMeta* meta, float* out, long long ldo) {
   __shared__ int scan_lds[kWaves];
   __shared__ float red_lds[kWaves];
   const int tid = threadIdx.x;
@@ -130,19 +143,41 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
   float* wts = w_ws + (size_t)m * k;
   int count = 0, ties_seen = 0;
   float mx = -INFINITY;
-  for (int base = 0; base < N; base += kThreads) {
-    const int n = base + tid;
-    const float s = n < N ? row[n] : 0.f;
-    const uint32_t key = order_key(s);
-    const bool eq = n < N && key == t_key;
+  for (int base = 0; base < N; base += kThreads * kElems) {
+    const int n0 = base + tid * kElems;
+    float s[kElems];
+    bool gt[kElems], eq[kElems];
+    int n_eq = 0;
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) {
+      const int n = n0 + e;
+      s[e] = n < N ? row[n] : 0.f;
+      const uint32_t key = order_key(s[e]);
+      gt[e] = n < N && key > t_key;
+      eq[e] = n < N && key == t_key;
+      n_eq += eq[e] ? 1 : 0;
+    }
     int eq_total;
-    const int eq_rank = block_exclusive_scan(eq ? 1 : 0, eq_total, scan_lds) + ties_seen;
-    const bool take = n < N && (key > t_key || (eq && eq_rank < ties));
+    int eq_rank = block_exclusive_scan(n_eq, eq_total, scan_lds) + ties_seen;
+    bool take[kElems];
+    int n_take = 0;
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) {
+      take[e] = gt[e] || (eq[e] && eq_rank < ties);
+      eq_rank += eq[e] ? 1 : 0;
+      n_take += take[e] ? 1 : 0;
+    }
     int take_total;
-    const int pos = block_exclusive_scan(take ? 1 : 0, take_total, scan_lds) + count;
-    if (take && pos < k) {
-      idx[pos] = n;
-      mx = fmaxf(mx, s);
+    int pos = block_exclusive_scan(n_take, take_total, scan_lds) + count;
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) {
+      if (take[e]) {
+        if (pos < k) {
+          idx[pos] = n0 + e;
+          mx = fmaxf(mx, s[e]);
+        }
+        ++pos;
+      }
     }
     ties_seen += eq_total;
     count += take_total;
@@ -156,10 +191,80 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
     part += w;
   }
   const float l = block_sum(part, red_lds);  // its barriers also publish idx / wts to the workgroup
+  if (D <= kMaxFastD) {
+    if (tid == 0) meta[m] = RowMeta{count, l};
+    return;
+  }
   for (int d = tid; d < D; d += kThreads) {
     float acc = 0.f;
     for (int i = 0; i < count; ++i) acc = fmaf(wts[i], values[(size_t)idx[i] * ldv + d], acc);
     out[(size_t)m * ldo + d] = acc / l;
+  }
+}
+
+// Weighted sum of the kept values of row m = blockIdx.x, split s = blockIdx.y
+// of kSplits: the split's tokens (a contiguous range of the kept list) are
+// dealt to the wavefronts in turn, 8 tokens' loads issued together; each lane
+// holds dims lane, lane + 64, ... of its wavefront's sum, and the wavefronts'
+// sums are added through LDS into part[m][s][:].
+__global__ void __launch_bounds__(kThreads) topk_pv_kernel(const int32_t* idx_ws, const float* w_ws,
+                                                           const RowMeta* meta, int k, const float* values, int D,
+                                                           long long ldv, float* part) {
+  __shared__ float part_lds[kWaves][kMaxFastD];
+  const int m = blockIdx.x, sp = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int count = meta[m].count;
+  const int chunk = (count + kSplits - 1) / kSplits;
+  const int lo = min(sp * chunk, count), hi = min(lo + chunk, count);
+  const int32_t* idx = idx_ws + (size_t)m * k;
+  const float* wts = w_ws + (size_t)m * k;
+  float acc[kMaxFastD / 64];
+#pragma unroll
+  for (int c = 0; c < kMaxFastD / 64; ++c) acc[c] = 0.f;
+  constexpr int U = 8;  // tokens whose loads are issued together
+  int i = lo + wave;
+  for (; i + (U - 1) * kWaves < hi; i += U * kWaves) {
+    float wt[U], v[U][kMaxFastD / 64];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      wt[u] = wts[i + u * kWaves];
+      const float* vr = values + (size_t)idx[i + u * kWaves] * ldv;
+#pragma unroll
+      for (int c = 0; c < kMaxFastD / 64; ++c) v[u][c] = c * 64 + lane < D ? vr[c * 64 + lane] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int c = 0; c < kMaxFastD / 64; ++c) acc[c] = fmaf(wt[u], v[u][c], acc[c]);
+  }
+  for (; i < hi; i += kWaves) {
+    const float wt = wts[i];
+    const float* vr = values + (size_t)idx[i] * ldv;
+#pragma unroll
+    for (int c = 0; c < kMaxFastD / 64; ++c)
+      if (c * 64 + lane < D) acc[c] = fmaf(wt, vr[c * 64 + lane], acc[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < kMaxFastD / 64; ++c) part_lds[wave][c * 64 + lane] = acc[c];
+  __syncthreads();
+  float* dst = part + ((size_t)m * kSplits + sp) * kMaxFastD;
+  for (int d = threadIdx.x; d < D; d += kThreads) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) sum += part_lds[w][d];
+    dst[d] = sum;
+  }
+}
+
+// out[m][:] = (sum over the splits of part[m][s][:]) / l_m, splits in order.
+__global__ void __launch_bounds__(kThreads) topk_combine_kernel(const float* part, const RowMeta* meta, int D,
+                                                                float* out, long long ldo) {
+  const int m = blockIdx.x;
+  const float l = meta[m].l;
+  for (int d = threadIdx.x; d < D; d += kThreads) {
+    float sum = 0.f;
+    for (int sp = 0; sp < kSplits; ++sp) sum += part[((size_t)m * kSplits + sp) * kMaxFastD + d];
+    out[(size_t)m * ldo + d] = sum / l;
   }
 }
 
@@ -168,9 +273,26 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
 
 using namespace vrm;
 
+// Workspace: sel [M][2] u32, idx [M][k] i32, weights [M][k] f32, row meta
+// [M], weighted-sum partials [M][kSplits][kMaxFastD] f32.
+static size_t topk_ws_offsets(int M, int k, size_t* idx_off, size_t* w_off, size_t* meta_off, size_t* part_off) {
+  size_t o = (size_t)M * 2 * sizeof(uint32_t);
+  *idx_off = o;
+  o += (size_t)M * (size_t)k * sizeof(int32_t);
+  *w_off = o;
+  o += (size_t)M * (size_t)k * sizeof(float);
+  o = (o + 15) / 16 * 16;
+  *meta_off = o;
+  o += (size_t)M * sizeof(RowMeta);
+  o = (o + 15) / 16 * 16;
+  *part_off = o;
+  return o + (size_t)M * kSplits * kMaxFastD * sizeof(float);
+}
+
 extern "C" size_t vrm_topk_attend_workspace_bytes(int M, int k) {
   if (M < 0 || k < 0) return 0;
-  return (size_t)M * 2 * sizeof(uint32_t) + (size_t)M * (size_t)k * (sizeof(int32_t) + sizeof(float));
+  size_t a, b, c, d;
+  return topk_ws_offsets(M, k, &a, &b, &c, &d);
 }
 
 extern "C" int vrm_topk_attend(const float* scores, int M, int N, long long ld_scores, int k, const float* values,
@@ -199,12 +321,21 @@ extern "C" int vrm_topk_attend(const float* scores, int M, int N, long long ld_s
     return VRM_ERR_ARG;
   }
   uint8_t* ws = static_cast<uint8_t*>(workspace);
+  size_t idx_off, w_off, meta_off, part_off;
+  topk_ws_offsets(M, k, &idx_off, &w_off, &meta_off, &part_off);
   uint32_t* sel = reinterpret_cast<uint32_t*>(ws);
-  int32_t* idx = reinterpret_cast<int32_t*>(ws + (size_t)M * 2 * sizeof(uint32_t));
-  float* wts = reinterpret_cast<float*>(ws + (size_t)M * 2 * sizeof(uint32_t) + (size_t)M * k * sizeof(int32_t));
+  int32_t* idx = reinterpret_cast<int32_t*>(ws + idx_off);
+  float* wts = reinterpret_cast<float*>(ws + w_off);
+  RowMeta* meta = reinterpret_cast<RowMeta*>(ws + meta_off);
+  float* part = reinterpret_cast<float*>(ws + part_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel);
   hipLaunchKernelGGL(topk_attend_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel, values, D,
-                     ld_values, idx, wts, out, ld_out);
+                     ld_values, idx, wts, meta, out, ld_out);
+  if (D <= kMaxFastD) {
+    hipLaunchKernelGGL(topk_pv_kernel, dim3(M, kSplits), dim3(kThreads), 0, st, idx, wts, meta, k, values, D,
+                       ld_values, part);
+    hipLaunchKernelGGL(topk_combine_kernel, dim3(M), dim3(kThreads), 0, st, part, meta, D, out, ld_out);
+  }
   return launch_status(who);
 }
