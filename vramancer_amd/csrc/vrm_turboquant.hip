@@ -467,6 +467,74 @@ __global__ void __launch_bounds__(64) tq_score_kernel(const float* ws, int M, in
   }
 }
 
+// The same scores, for up to kScoreMaxLds bytes of staged queries: one
+// wavefront per kScoreKeys keys, the query rows (q_rot, q_proj) staged in LDS
+// once (row stride PD + qjl_dim + 1 floats, so lane m reads a bank of its
+// own), kScoreBatch keys rebuilt at a time and scored together; each score
+// is summed in the same order as tq_score_kernel's.
+constexpr int kScoreKeys = 16;
+constexpr int kScoreBatch = 4;
+constexpr int kScoreMaxLds = 60 * 1024;
+
+template <int PD>
+__global__ void __launch_bounds__(64) tq_score_lds_kernel(const float* ws, int M, int qjl_dim,
+                                                          const uint16_t* radius, const uint8_t* angles,
+                                                          const uint8_t* qjl_signs, const uint16_t* qjl_norms, int N,
+                                                          const float* lut, int bits, float coef, float out_scale,
+                                                          float* scores) {
+  extern __shared__ float dyn[];  // [M][W] queries, then [kScoreBatch][qjl_dim] signs
+  __shared__ float bufA[PD / 2];
+  __shared__ float bufB[PD / 2];
+  __shared__ float recon[kScoreBatch][PD];
+  __shared__ uint8_t bins[PD];
+  const int lane = threadIdx.x;
+  const int W = PD + qjl_dim + 1;
+  float* qs = dyn;
+  float* sgn = dyn + (size_t)M * W;
+  for (int i = lane; i < M * (PD + qjl_dim); i += 64) {
+    const int m = i / (PD + qjl_dim), e = i - m * (PD + qjl_dim);
+    qs[m * W + e] = ws[i];
+  }
+  const int first = blockIdx.x * kScoreKeys;
+  const int last = min(N, first + kScoreKeys);
+  for (int n0 = first; n0 < last; n0 += kScoreBatch) {
+    const int nb = min(kScoreBatch, last - n0);
+    float norm[kScoreBatch];
+    for (int kb = 0; kb < nb; ++kb) {
+      const int n = n0 + kb;
+      for (int i = lane; i < PD - 1; i += 64) bins[i] = angles[(size_t)n * (PD - 1) + i];
+      for (int j = lane; j < qjl_dim; j += 64)
+        sgn[kb * qjl_dim + j] = __fsub_rn(__fmul_rn((float)qjl_signs[(size_t)n * qjl_dim + j], 2.f), 1.f);
+      norm[kb] = f16_bits_to_f32(qjl_norms[n]);
+      polar_decode<PD>(f16_bits_to_f32(radius[n]), bins, lut, 1 << bits, bufA, bufB, recon[kb], lane);
+    }
+    for (int m = lane; m < M; m += 64) {
+      const float* qr = qs + m * W;
+      float dot[kScoreBatch], raw[kScoreBatch];
+#pragma unroll
+      for (int kb = 0; kb < kScoreBatch; ++kb) dot[kb] = raw[kb] = 0.f;
+      for (int e = 0; e < PD; ++e) {
+        const float qv = qr[e];
+#pragma unroll
+        for (int kb = 0; kb < kScoreBatch; ++kb) dot[kb] = __fadd_rn(dot[kb], __fmul_rn(qv, recon[kb][e]));
+      }
+      for (int j = 0; j < qjl_dim; ++j) {
+        const float qv = qr[PD + j];
+#pragma unroll
+        for (int kb = 0; kb < kScoreBatch; ++kb) raw[kb] = __fadd_rn(raw[kb], __fmul_rn(qv, sgn[kb * qjl_dim + j]));
+      }
+#pragma unroll
+      for (int kb = 0; kb < kScoreBatch; ++kb) {
+        if (kb < nb) {
+          const float corr = __fmul_rn(__fmul_rn(raw[kb], coef), norm[kb]);
+          scores[(size_t)m * N + n0 + kb] = __fmul_rn(__fadd_rn(dot[kb], corr), out_scale);
+        }
+      }
+    }
+    __syncthreads();  // recon / sgn / bins are rewritten for the next keys
+  }
+}
+
 int check_tq(int N, int head_dim, int padded_dim, int n_levels, int bits, const char* who) {
   if (N < 0 || head_dim <= 0 || head_dim > padded_dim) {
     set_error("%s: bad sizes (N=%d head_dim=%d padded_dim=%d)", who, N, head_dim, padded_dim);
@@ -718,10 +786,17 @@ extern "C" int vrm_turboquant_score(const float* q, int M, const uint16_t* radiu
   }
   const float coef = (float)(sqrt(M_PI / 2.0) / qjl_dim);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t lds = ((size_t)M * (padded_dim + qjl_dim + 1) + (size_t)kScoreBatch * qjl_dim) * sizeof(float);
+  const bool staged = lds <= (size_t)kScoreMaxLds;
 #define VRM_TQ_SCORE(PDV)                                                                                      \
   hipLaunchKernelGGL(tq_query_kernel<PDV>, dim3(M), dim3(64), 0, st, q, head_dim, signs, jl, qjl_dim, workspace); \
-  hipLaunchKernelGGL(tq_score_kernel<PDV>, dim3(N), dim3(64), 0, st, workspace, M, qjl_dim, radius, angles,       \
-                     qjl_signs, qjl_norms, N, angle_lut, bits, coef, out_scale, scores)
+  if (staged)                                                                                                  \
+    hipLaunchKernelGGL(tq_score_lds_kernel<PDV>, dim3((N + kScoreKeys - 1) / kScoreKeys), dim3(64), lds, st,   \
+                       workspace, M, qjl_dim, radius, angles, qjl_signs, qjl_norms, N, angle_lut, bits, coef,   \
+                       out_scale, scores);                                                                     \
+  else                                                                                                         \
+    hipLaunchKernelGGL(tq_score_kernel<PDV>, dim3(N), dim3(64), 0, st, workspace, M, qjl_dim, radius, angles,     \
+                       qjl_signs, qjl_norms, N, angle_lut, bits, coef, out_scale, scores)
   switch (padded_dim) {
     case 64: VRM_TQ_SCORE(64); break;
     case 128: VRM_TQ_SCORE(128); break;
