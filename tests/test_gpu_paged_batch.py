@@ -153,7 +153,7 @@ def test_fp8_forks_cannot_share_a_step(setting):
     with torch.no_grad():
         prefill(model, mgr, "a", streams[0][:, :5].to(DEV))
         mgr.fork("a", "b")
-        with pytest.raises(RuntimeError, match="share their last page"):
+        with pytest.raises(RuntimeError, match="share the page"):
             decode_step(model, mgr, ["a", "b"], torch.tensor([1, 1], device=DEV))
 
 
@@ -224,8 +224,11 @@ def test_decode_step_pool_exhausted_raises(setting):
         mgr.allocate("y")
         prefill(model, mgr, "y", streams[0][:, :32].to(DEV))
         assert not mgr._free_pages
+        before = list(mgr.token_counts(["x", "y"]))
         with pytest.raises(RuntimeError, match="no page left"):
             decode_step(model, mgr, ["x", "y"], torch.tensor([1, 2], device=DEV))
+    # the failed step changed nothing: the batch can go on once a page is free
+    assert list(mgr.token_counts(["x", "y"])) == before
 
 
 def test_multi_token_update_raises(setting):

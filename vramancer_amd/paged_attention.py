@@ -309,21 +309,59 @@ class PagedKVCacheManager:
         with self._lock:
             return self._append_locked(request_id)
 
-    def append_tokens(self, request_ids: Sequence[str]) -> Tuple[Any, Any]:
+    def append_tokens(self, request_ids: Sequence[str], strict: bool = False) -> Tuple[Any, Any]:
         """``append_token`` for a batch, as two int32 device tensors [N]
         (page ids, slots) ready for ``write_kv_batch``; a request that gets no
-        slot has page -1 and slot -1, which the writers skip."""
+        slot has page -1 and slot -1, which the writers skip.
+
+        With ``strict`` the batch is checked first and nothing changes when
+        it fails: an unknown request id raises ``KeyError``; too few free
+        pages for the requests whose last page is full, or (fp8 pools)
+        requests sharing the page their token goes to, raise
+        ``RuntimeError``.  An fp8 append rescales its page, so one launch may
+        write a page once only."""
         import torch
 
         self._require_pool("append_tokens")
         out = np.full((2, len(request_ids)), -1, dtype=np.int32)
+        PS = self.config.page_size
         with self._lock:
+            if strict:
+                entries = [self._page_tables.get(rid) for rid in request_ids]
+                missing = [rid for rid, e in zip(request_ids, entries) if e is None]
+                if missing:
+                    raise KeyError(f"unknown request ids {missing}")
+                opening = [rid for rid, e in zip(request_ids, entries) if e.num_tokens // PS >= len(e.pages)]
+                if len(opening) > len(self._free_pages):
+                    raise RuntimeError(f"no page left for requests {opening[len(self._free_pages):]} "
+                                       f"(pool of {self.config.max_pages} pages)")
+                if self._gpu_pool.dtype == torch.float8_e4m3fn:
+                    tails = [e.pages[e.num_tokens // PS] for e in entries if e.num_tokens // PS < len(e.pages)]
+                    if len(set(tails)) < len(tails):
+                        raise RuntimeError("requests of an fp8 pool that share the page their next token goes to "
+                                           "(forks) cannot append in one launch")
             for i, rid in enumerate(request_ids):
                 got = self._append_locked(rid)
                 if got is not None:
                     out[0, i], out[1, i] = got
         dev = torch.from_numpy(out).to(self._gpu_pool.device)
         return dev[0], dev[1]
+
+    @property
+    def gpu_pool(self) -> Any:
+        """The device K/V pool, or ``None`` for a host-only manager."""
+        return self._gpu_pool
+
+    def request_ids(self) -> set:
+        """Ids of the requests that hold a page table."""
+        with self._lock:
+            return set(self._page_tables)
+
+    def token_counts(self, request_ids: Sequence[str]) -> np.ndarray:
+        """Token count of each request (0 for an unknown id), int64 on the host."""
+        with self._lock:
+            return np.array([e.num_tokens if (e := self._page_tables.get(rid)) is not None else 0
+                             for rid in request_ids], dtype=np.int64)
 
     def free(self, request_id: str) -> int:
         """Drops a request; returns how many pages went back to the free list."""

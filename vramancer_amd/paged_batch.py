@@ -105,9 +105,10 @@ class PagedBatchCache(Cache):
     stays the same."""
 
     def __init__(self, manager: PagedKVCacheManager, request_ids: Sequence[str]):
-        if manager._gpu_pool is None:
+        if manager.gpu_pool is None:
             raise RuntimeError("PagedBatchCache needs a manager with a GPU pool")
-        missing = [rid for rid in request_ids if rid not in manager._page_tables]
+        known = manager.request_ids()
+        missing = [rid for rid in request_ids if rid not in known]
         if missing:
             raise KeyError(f"unknown request ids {missing}")
         self.manager = manager
@@ -117,30 +118,10 @@ class PagedBatchCache(Cache):
 
     def token_counts(self) -> np.ndarray:
         """Each request's token count (the position of its next token)."""
-        with self.manager._lock:
-            return np.array([self.manager._page_tables[rid].num_tokens for rid in self.request_ids], dtype=np.int64)
+        return self.manager.token_counts(self.request_ids)
 
     def _begin_step(self) -> None:
-        m = self.manager
-        host = np.full((2, len(self.request_ids)), -1, dtype=np.int32)
-        PS = m.config.page_size
-        with m._lock:
-            if m._gpu_pool.dtype == torch.float8_e4m3fn:
-                # fp8 appends rescale a page's codes: one token per page per launch
-                tails = [e.pages[e.num_tokens // PS] for e in (m._page_tables[r] for r in self.request_ids)
-                         if e.num_tokens // PS < len(e.pages)]
-                if len(set(tails)) < len(tails):
-                    raise RuntimeError("requests of an fp8 pool that share their last page (forks) cannot "
-                                       "decode in one step")
-            for i, rid in enumerate(self.request_ids):
-                got = m._append_locked(rid)
-                if got is not None:
-                    host[0, i], host[1, i] = got
-        if (host[0] < 0).any():
-            full = [rid for rid, p in zip(self.request_ids, host[0]) if p < 0]
-            raise RuntimeError(f"no page left for requests {full} (pool of {m.config.max_pages} pages)")
-        dev = torch.from_numpy(host).to(m._gpu_pool.device)
-        self._slots = (dev[0], dev[1])
+        self._slots = self.manager.append_tokens(self.request_ids, strict=True)
 
     def _step_slots(self) -> Tuple[torch.Tensor, torch.Tensor]:
         if self._slots is None:
