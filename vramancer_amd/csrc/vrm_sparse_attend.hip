@@ -26,6 +26,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kSelLoads = 8;  // scores per thread per load round of the radix select
 
 // Ascending float order <-> ascending unsigned order.
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -43,9 +44,20 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* scor
   for (int shift = 24; shift >= 0; shift -= 8) {
     hist[tid] = 0;  // kThreads == 256 bins
     __syncthreads();
-    for (int n = tid; n < N; n += kThreads) {
-      const uint32_t key = order_key(row[n]);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    // kSelLoads scores per thread are loaded before any histogram update, so
+    // the loads of a pass are not serialised behind the LDS atomics.
+    for (int base = 0; base < N; base += kThreads * kSelLoads) {
+      float x[kSelLoads];
+#pragma unroll
+      for (int e = 0; e < kSelLoads; ++e) {
+        const int n = base + e * kThreads + tid;
+        x[e] = n < N ? row[n] : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < kSelLoads; ++e) {
+        const uint32_t key = order_key(x[e]);
+        if (base + e * kThreads + tid < N && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
     if (tid == 0) {
