@@ -100,6 +100,30 @@ def test_append_equals_page_write():
     assert torch.equal(a.cpu(), b.cpu())
 
 
+def test_device_buffers_cached_and_refreshed():
+    """The compressor's signs and JL matrix are uploaded once per device and
+    uploaded again after an in-place change or a replacement; pages written
+    after the change carry codes of the changed matrix."""
+    _say("device buffer cache")
+    comp = _compressor(3)
+    s1, j1, _ = tq_pages._buffers(comp, DEV)
+    s2, j2, _ = tq_pages._buffers(comp, DEV)
+    assert s1 is s2 and j1 is j2
+    comp.jl_matrix.neg_()
+    _, j3, _ = tq_pages._buffers(comp, DEV)
+    assert j3 is not j1 and torch.equal(j3.cpu(), comp.jl_matrix)
+    comp.jl_matrix = torch.flip(comp.jl_matrix, [0]).contiguous()
+    _, j4, _ = tq_pages._buffers(comp, DEV)
+    assert torch.equal(j4.cpu(), comp.jl_matrix)
+    k = _student_t((1, 2, 16, 128), 5)
+    pool = tq_pages.allocate_pool(1, 1, 2, comp, DEV)
+    tq_pages.quantize_pages(pool, 0, torch.zeros(1, dtype=torch.int32, device=DEV), k.to(DEV), k.to(DEV), comp)
+    got = tq_pages.read_pages(pool, 0, torch.zeros(1, dtype=torch.int32, device=DEV), comp)["qjl_signs"][0, 0].cpu()
+    ref = CUDATurboQuantOps.compress_gpu(k.to(DEV).reshape(-1, 128), 128, 128, 7, 3, comp._hadamard_signs,
+                                         comp.jl_matrix)["qjl_signs"].cpu().reshape(2, 16, 64)
+    assert torch.equal(got, ref)
+
+
 def _turbo_case(comp, B, H, KH, ctxs, seed, L=1, layer=0, spare=2):
     g = torch.Generator().manual_seed(seed)
     npages = [(c + 15) // 16 for c in ctxs]

@@ -86,13 +86,9 @@ __host__ __device__ inline void slot_of(int l, int i, int bits, int& quarter, in
 // the unused spare of quarter 3.
 __host__ __device__ inline int bin_index_of(int g, int s, int bits) {
   if (s == 31) return g == 0 ? level_offset(6) : (g <= 2 ? level_offset(5) + (g - 1) : -1);
-  if (bits == 4) {
-    int l = 4, first = 0;
-    while (s >= first + (1 << (4 - l))) {
-      first += 1 << (4 - l);
-      --l;
-    }
-    return level_offset(l) + g * (1 << (4 - l)) + (s - first);
+  if (bits == 4) {  // slots 2^m - 1 .. 2^(m+1) - 2 hold the 2^m angles of level 4 - m
+    const int m = 31 - __builtin_clz(s + 1);
+    return level_offset(4 - m) + g * (1 << m) + (s + 1 - (1 << m));
   }
   if (s == 30) return level_offset(4) + g;
   if (s >= 24) {

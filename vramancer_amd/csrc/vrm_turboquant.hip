@@ -95,44 +95,41 @@ struct TqArgs {
   float* out;        // decompress output
 };
 
-// Polar decode of one row into `recon` (LDS, PD floats) from the fp32 radius
-// and the level-major bins in `bins`.  Levels run from the top (one angle)
-// down to level 0, interleaving (r cos, r sin) pairs.
+// Element e of the polar decode of one row from the fp32 radius and the
+// level-major bins (level l at offset PD - (PD >> l)).  The reference decodes
+// level by level from the top, each value r of level l becoming the pair
+// (r cos, r sin) of level l - 1; element e is therefore the product chain
+//   ((radius * f_{NL-1}) * f_{NL-2}) ... * f_0,
+// f_l the cos (bit l of e clear) or sin (set) of angle e >> (l + 1) of level
+// l, the same roundings in the same order, with no exchange between lanes.
+template <int PD>
+__device__ __forceinline__ float polar_element(float radius, const uint8_t* bins, const float* lut, int nb, int e) {
+  constexpr int NL = __builtin_ctz(PD);
+  float r = radius;
+#pragma unroll
+  for (int l = NL - 1; l >= 0; --l) {
+    const int idx = min((int)bins[PD - (PD >> l) + (e >> (l + 1))], nb - 1);  // caller-supplied bins stay in the table
+    r = __fmul_rn(r, lut[(l == 0 ? 0 : 2 * nb) + (((e >> l) & 1) ? nb : 0) + idx]);
+  }
+  return r;
+}
+
+// Polar decode of one row into `recon` (LDS, PD floats); bins may have been
+// written by any lane before the call, recon is visible to every lane after.
 template <int PD>
 __device__ __forceinline__ void polar_decode(float radius, const uint8_t* bins, const float* lut, int nb,
-                                             float* bufA, float* bufB, float* recon, int lane) {
-  constexpr int NL = __builtin_ctz(PD);
-  float* cur = bufA;
-  float* nxt = bufB;
-  if (lane == 0) cur[0] = radius;
+                                             float* recon, int lane) {
   __syncthreads();
-  // level_offset(l) = sum_{i<l} PD >> (i + 1) = PD - (PD >> l)
-  for (int level = NL - 1; level >= 0; --level) {
-    const int count = PD >> (level + 1);
-    const int off = PD - (PD >> level);
-    const float* cos_t = lut + (level == 0 ? 0 : 2 * nb);
-    const float* sin_t = cos_t + nb;
-    float* dst = level == 0 ? recon : nxt;
-    for (int i = lane; i < count; i += 64) {
-      const int idx = min((int)bins[off + i], nb - 1);  // caller-supplied bins stay inside the table
-      const float r = cur[i];
-      dst[2 * i] = __fmul_rn(r, cos_t[idx]);
-      dst[2 * i + 1] = __fmul_rn(r, sin_t[idx]);
-    }
-    __syncthreads();
-    float* t = cur;
-    cur = nxt;
-    nxt = t;
-  }
+#pragma unroll
+  for (int k = 0; k < PD / 64; ++k) recon[k * 64 + lane] = polar_element<PD>(radius, bins, lut, nb, k * 64 + lane);
+  __syncthreads();
 }
 
 // LDS working set of one row.
 template <int PD>
 struct RowLds {
-  float rot[PD];  // rotated row, then the residual
-  float bufA[PD / 2];
-  float bufB[PD / 2];
-  float recon[PD];
+  alignas(16) float rot[PD];  // rotated row, then the residual (read as float4)
+  float rad[PD];              // radius of each polar node, level-major like the bins
   uint8_t bins[PD];
   float norm_acc[8];
 };
@@ -162,29 +159,36 @@ __device__ __forceinline__ float encode_row(const void* src, size_t first, int h
   }
   __syncthreads();
 
+  // The radii only need square roots, level after level: node i of level l
+  // (w.rad[PD - (PD >> l) + i]) over children 2 i, 2 i + 1 of level l - 1
+  // (the rotated row below level 0).
+  for (int level = 0; level < NL; ++level) {
+    const float* child = level == 0 ? w.rot : w.rad + (PD - (PD >> (level - 1)));
+    float* rad = w.rad + (PD - (PD >> level));
+    for (int i = lane; i < (PD >> (level + 1)); i += 64) {
+      const float x0 = child[2 * i], x1 = child[2 * i + 1];
+      rad[i] = sqrt_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), 1e-12f));
+    }
+    __syncthreads();
+  }
+  // With every child known, the angles of all levels are independent: lane
+  // takes bins b = lane, lane + 64, ... of the level-major order.
   const float lo0 = (float)-3.141592653589793, range0 = (float)6.283185307179586;
   const float range1 = (float)1.5707963267948966;
   const float nbf = (float)nb;
-  const float* cur = w.rot;
-  float* nxt = w.bufA;
-  for (int level = 0; level < NL; ++level) {
-    const int count = PD >> (level + 1);
-    const int off = PD - (PD >> level);
-    for (int i = lane; i < count; i += 64) {
-      const float x0 = cur[2 * i], x1 = cur[2 * i + 1];
-      const float r = sqrt_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), 1e-12f));
-      const float th = vrm_fdlibm::atan2f(x1, x0);
-      float nrm = level == 0 ? __fdiv_rn(__fsub_rn(th, lo0), range0) : __fdiv_rn(th, range1);
-      int idx = (int)__fmul_rn(nrm, nbf);  // truncation toward zero, as .long()
-      idx = min(max(idx, 0), nb - 1);
-      w.bins[off + i] = (uint8_t)idx;
-      nxt[i] = r;
-    }
-    __syncthreads();
-    cur = nxt;
-    nxt = (nxt == w.bufA) ? w.bufB : w.bufA;
+  for (int b = lane; b < PD - 1; b += 64) {
+    const int level = NL - 1 - (31 - __builtin_clz(PD - b - 1));  // PD >> (level + 1) < PD - b <= PD >> level
+    const int i = b - (PD - (PD >> level));
+    const float* child = level == 0 ? w.rot : w.rad + (PD - (PD >> (level - 1)));
+    const float x0 = child[2 * i], x1 = child[2 * i + 1];
+    const float th = vrm_fdlibm::atan2f(x1, x0);
+    const float nrm = level == 0 ? __fdiv_rn(__fsub_rn(th, lo0), range0) : __fdiv_rn(th, range1);
+    int idx = (int)__fmul_rn(nrm, nbf);  // truncation toward zero, as .long()
+    idx = min(max(idx, 0), nb - 1);
+    w.bins[b] = (uint8_t)idx;
   }
-  return cur[0];
+  __syncthreads();
+  return w.rad[PD - 2];
 }
 
 // Residual against the reconstruction from the fp32 radius, its QJL signs
@@ -195,22 +199,44 @@ template <int PD, typename PutSign>
 __device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius, const float* lut, int bits,
                                          const float* jl, int qjl_dim, RowLds<PD>& w, int lane, PutSign put_sign) {
   constexpr int PER = PD / 64;
-  polar_decode<PD>(radius, w.bins, lut, 1 << bits, w.bufA, w.bufB, w.recon, lane);
+  float res[PER];
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int e = k * 64 + lane;
-    w.rot[e] = __fsub_rn(v[k], w.recon[e]);  // rot now holds the residual
-  }
+  for (int k = 0; k < PER; ++k) res[k] = __fsub_rn(v[k], polar_element<PD>(radius, w.bins, lut, 1 << bits, k * 64 + lane));
+#pragma unroll
+  for (int k = 0; k < PER; ++k) w.rot[k * 64 + lane] = res[k];  // rot now holds the residual
   __syncthreads();
+  // Lane j walks row j of the JL matrix.  With a 16-byte aligned matrix (every
+  // row is then aligned, PD being a multiple of 4) it reads four floats per
+  // load and four residual elements per LDS broadcast; the accumulation order
+  // is the same element order either way.
+  const bool vec = (reinterpret_cast<uintptr_t>(jl) & 15) == 0;
   for (int j = lane; j < qjl_dim; j += 64) {
     const float* jr = jl + (size_t)j * PD;
     double s = 0.0;
-    for (int e = 0; e < PD; ++e) s = fma((double)w.rot[e], (double)jr[e], s);
+    if (vec) {
+      const float4* jr4 = reinterpret_cast<const float4*>(jr);
+      const float4* r4 = reinterpret_cast<const float4*>(w.rot);
+#pragma unroll 8
+      for (int m = 0; m < PD / 4; ++m) {
+        const float4 x = jr4[m];
+        const float4 r = r4[m];
+        s = fma((double)r.x, (double)x.x, s);
+        s = fma((double)r.y, (double)x.y, s);
+        s = fma((double)r.z, (double)x.z, s);
+        s = fma((double)r.w, (double)x.w, s);
+      }
+    } else {
+      for (int e = 0; e < PD; ++e) s = fma((double)w.rot[e], (double)jr[e], s);
+    }
     put_sign(j, s > 0.0);
   }
   if (lane < 8) {
+    float x[PD / 8];
+#pragma unroll
+    for (int m = 0; m < PD / 8; ++m) x[m] = w.rot[lane + 8 * m];
     float acc = 0.f;
-    for (int e = lane; e < PD; e += 8) acc = fmaf(w.rot[e], w.rot[e], acc);
+#pragma unroll
+    for (int m = 0; m < PD / 8; ++m) acc = fmaf(x[m], x[m], acc);
     w.norm_acc[lane] = acc;
   }
   __syncthreads();
@@ -255,7 +281,7 @@ struct TqPoolArgs {
   const float* lut;
 };
 
-template <int SRC>
+template <int SRC, int BITS>
 __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
   namespace L = vrm::tq;
   constexpr int PD = L::kPD;
@@ -282,33 +308,37 @@ __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
   const int pid = a.page_ids[n];
   if (pid < 0 || pid >= a.P || t < 0 || t >= L::kTokens) return;  // rows aimed outside the pool are dropped
   if (a.from_pool) src_first = (((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::kTokens + t) * a.head_dim;
-  uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::slice_bytes(a.bits);
-  const int abytes = L::angle_bytes(a.bits);
+  uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::slice_bytes(BITS);
+  const int abytes = L::angle_bytes(BITS);
   uint8_t* rec = slice + (size_t)t * abytes;
-  uint16_t* radius_out = reinterpret_cast<uint16_t*>(slice + L::radius_offset(a.bits)) + t;
+  uint16_t* radius_out = reinterpret_cast<uint16_t*>(slice + L::radius_offset(BITS)) + t;
   if (!live) {  // slots past the page's valid tokens hold zero records
     for (int i = lane; i < abytes; i += 64) rec[i] = 0;
     if (lane == 0) *radius_out = 0;
     if (kv == 0) {
-      if (lane < 8) slice[L::signs_offset(a.bits) + t * 8 + lane] = 0;
-      if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(a.bits))[t] = 0;
+      if (lane < 8) slice[L::signs_offset(BITS) + t * 8 + lane] = 0;
+      if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = 0;
     }
     return;
   }
   float v[PD / 64];
   const void* src = kv ? a.value : a.key;
-  const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, a.bits, v, w, lane);
-  // angle record: dword k of quarter g covers quarter bits [32 k, 32 k + 32)
-  const int qdw = a.bits;  // dwords per quarter (4 * bits bytes)
-  if (lane < 4 * qdw) {
-    const int g = lane / qdw, k = lane % qdw;
+  const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, BITS, v, w, lane);
+  // angle record: dword k of quarter g covers quarter bits [32 k, 32 k + 32),
+  // i.e. at most 32 / BITS + 2 slots from the one holding bit 32 k
+  if (lane < 4 * BITS) {  // BITS dwords per quarter
+    const int g = lane / BITS, k = lane % BITS;
+    const int s0 = (32 * k) / BITS;
     uint32_t word = 0;
-    for (int slot = (32 * k) / a.bits; slot < 32 && slot * a.bits < 32 * k + 32; ++slot) {
-      const int bi = L::bin_index_of(g, slot, a.bits);
-      if (bi < 0) continue;
-      const int shift = slot * a.bits - 32 * k;  // may be negative for a slot straddling the dword start
-      const uint32_t val = w.bins[bi];
-      word |= shift >= 0 ? (val << shift) : (val >> -shift);
+#pragma unroll
+    for (int m = 0; m < 32 / BITS + 2; ++m) {
+      const int slot = s0 + m;
+      const int bi = slot < 32 && slot * BITS < 32 * k + 32 ? L::bin_index_of(g, slot, BITS) : -1;
+      if (bi >= 0) {
+        const int shift = slot * BITS - 32 * k;  // negative for a slot straddling the dword start
+        const uint32_t val = w.bins[bi];
+        word |= shift >= 0 ? (val << shift) : (val >> -shift);
+      }
     }
     reinterpret_cast<uint32_t*>(rec)[lane] = word;
   }
@@ -316,12 +346,12 @@ __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
   if (kv == 1) return;
   if (lane < L::kQjl / 32) sign_bits[lane] = 0;
   __syncthreads();
-  const float norm = qjl_row<PD>(v, radius, a.lut, a.bits, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
+  const float norm = qjl_row<PD>(v, radius, a.lut, BITS, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
     if (pos) atomicOr(&sign_bits[j >> 5], 1u << (j & 31));
   });
   __syncthreads();
-  if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(a.bits) + t * 8)[lane] = sign_bits[lane];
-  if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(a.bits))[t] = f32_to_f16_bits(norm);
+  if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(BITS) + t * 8)[lane] = sign_bits[lane];
+  if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = f32_to_f16_bits(norm);
 }
 
 // Reads a TurboQuant pool back into the reference's raw code format, for
@@ -368,8 +398,6 @@ __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, c
 template <int PD>
 __global__ void __launch_bounds__(64) tq_decompress_kernel(TqArgs a, int rotated) {
   constexpr int PER = PD / 64;
-  __shared__ float bufA[PD / 2];
-  __shared__ float bufB[PD / 2];
   __shared__ float recon[PD];
   __shared__ uint8_t bins[PD];
   const int lane = threadIdx.x;
@@ -378,7 +406,7 @@ __global__ void __launch_bounds__(64) tq_decompress_kernel(TqArgs a, int rotated
   for (int i = lane; i < PD - 1; i += 64) bins[i] = a.angles[(size_t)row * (PD - 1) + i];
   const float radius = f16_bits_to_f32(a.radius[row]);
   __syncthreads();
-  polar_decode<PD>(radius, bins, a.lut, nb, bufA, bufB, recon, lane);
+  polar_decode<PD>(radius, bins, a.lut, nb, recon, lane);
   float v[PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) v[k] = recon[k * 64 + lane];
@@ -442,8 +470,6 @@ __global__ void __launch_bounds__(64) tq_score_kernel(const float* ws, int M, in
                                                       const uint8_t* angles, const uint8_t* qjl_signs,
                                                       const uint16_t* qjl_norms, int N, const float* lut, int bits,
                                                       float coef, float out_scale, float* scores) {
-  __shared__ float bufA[PD / 2];
-  __shared__ float bufB[PD / 2];
   __shared__ float recon[PD];
   __shared__ uint8_t bins[PD];
   __shared__ float sgn[4 * PD];
@@ -455,7 +481,7 @@ __global__ void __launch_bounds__(64) tq_score_kernel(const float* ws, int M, in
   const float r = f16_bits_to_f32(radius[n]);
   const float norm = f16_bits_to_f32(qjl_norms[n]);
   __syncthreads();
-  polar_decode<PD>(r, bins, lut, 1 << bits, bufA, bufB, recon, lane);
+  polar_decode<PD>(r, bins, lut, 1 << bits, recon, lane);
   for (int m = lane; m < M; m += 64) {
     const float* qr = ws + (size_t)m * (PD + qjl_dim);
     float dot = 0.f;
@@ -483,8 +509,6 @@ __global__ void __launch_bounds__(64) tq_score_lds_kernel(const float* ws, int M
                                                           const float* lut, int bits, float coef, float out_scale,
                                                           float* scores) {
   extern __shared__ float dyn[];  // [M][W] queries, then [kScoreBatch][qjl_dim] signs
-  __shared__ float bufA[PD / 2];
-  __shared__ float bufB[PD / 2];
   __shared__ float recon[kScoreBatch][PD];
   __shared__ uint8_t bins[PD];
   const int lane = threadIdx.x;
@@ -506,7 +530,7 @@ __global__ void __launch_bounds__(64) tq_score_lds_kernel(const float* ws, int M
       for (int j = lane; j < qjl_dim; j += 64)
         sgn[kb * qjl_dim + j] = __fsub_rn(__fmul_rn((float)qjl_signs[(size_t)n * qjl_dim + j], 2.f), 1.f);
       norm[kb] = f16_bits_to_f32(qjl_norms[n]);
-      polar_decode<PD>(f16_bits_to_f32(radius[n]), bins, lut, 1 << bits, bufA, bufB, recon[kb], lane);
+      polar_decode<PD>(f16_bits_to_f32(radius[n]), bins, lut, 1 << bits, recon[kb], lane);
     }
     for (int m = lane; m < M; m += 64) {
       const float* qr = qs + m * W;
@@ -701,11 +725,18 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.lut = angle_lut;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(rows, 2);
-  switch (src_dtype) {
-    case VRM_SRC_F32: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_F32>, grid, dim3(64), 0, st, a); break;
-    case VRM_SRC_F16: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_F16>, grid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL(tq_pool_write_kernel<VRM_SRC_BF16>, grid, dim3(64), 0, st, a); break;
+#define VRM_TQ_WRITE(SRC)                                                                          \
+  switch (bits) {                                                                                  \
+    case 2: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 2>), grid, dim3(64), 0, st, a); break; \
+    case 3: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 3>), grid, dim3(64), 0, st, a); break; \
+    default: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 4>), grid, dim3(64), 0, st, a); break; \
   }
+  switch (src_dtype) {
+    case VRM_SRC_F32: VRM_TQ_WRITE(VRM_SRC_F32); break;
+    case VRM_SRC_F16: VRM_TQ_WRITE(VRM_SRC_F16); break;
+    default: VRM_TQ_WRITE(VRM_SRC_BF16); break;
+  }
+#undef VRM_TQ_WRITE
   return launch_status(who);
 }
 }  // namespace

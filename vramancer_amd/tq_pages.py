@@ -21,6 +21,7 @@ Built for head_dim 128 with the compressor's default qjl_dim (64) and 2, 3 or
 """
 from __future__ import annotations
 
+import functools
 import math
 from typing import Any, Dict, Optional
 
@@ -40,6 +41,7 @@ __all__ = [
 PAGE_SIZE = 16
 
 
+@functools.lru_cache(maxsize=None)
 def slice_bytes(bits_per_angle: int, head_dim: int = 128, qjl_dim: int = 64) -> int:
     n = _lib.load().vrm_tq_slice_bytes(head_dim, bits_per_angle, qjl_dim)
     if n == 0:
@@ -56,11 +58,28 @@ def _check_compressor(compressor):
 
 
 def _buffers(compressor, device):
+    """Float32 device copies of the compressor's Hadamard signs and JL matrix,
+    and the angle table.  The copies are kept on the compressor per device and
+    made again when either source tensor is replaced or changed in place, so a
+    compressor that stays on the host costs one upload, not two per call."""
     import torch
 
-    signs = compressor._hadamard_signs.to(device=device, dtype=torch.float32).contiguous()
-    jl = compressor.jl_matrix.to(device=device, dtype=torch.float32).contiguous()
-    return signs, jl, angle_lut(compressor.bits_per_angle, device)
+    src_s, src_j = compressor._hadamard_signs, compressor.jl_matrix
+    cache = compressor.__dict__.setdefault("_vrm_device_buffers", {})
+    hit = cache.get(device)
+    if (hit is None or hit[0] is not src_s or hit[1] is not src_j or hit[2] != (src_s._version, src_j._version)
+            or hit[3] != compressor.bits_per_angle):
+        dev = torch.device(device)
+        follows_current = dev.type == "cuda" and dev.index is None  # not cached: the current device may change
+        if follows_current:
+            dev = torch.device("cuda", torch.cuda.current_device())
+        signs = src_s.to(device=dev, dtype=torch.float32).contiguous()
+        jl = src_j.to(device=dev, dtype=torch.float32).contiguous()
+        hit = (src_s, src_j, (src_s._version, src_j._version), compressor.bits_per_angle,
+               (signs, jl, angle_lut(compressor.bits_per_angle, dev)))
+        if not follows_current:
+            cache[device] = hit
+    return hit[4]
 
 
 def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, compressor, device: Any = "cuda"):
