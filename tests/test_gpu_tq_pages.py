@@ -100,6 +100,26 @@ def test_append_equals_page_write():
     assert torch.equal(a.cpu(), b.cpu())
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_bulk_page_write_equals_small_writes(bits):
+    """40 pages of 8 kv-heads (5,120 rows per side, several rows per
+    workgroup) written at once equal the same pages written 5 at a time."""
+    _say(f"bulk page write bits {bits}")
+    comp = _compressor(bits)
+    P, L, KH, NP = 48, 2, 8, 40
+    k = _student_t((NP, KH, 16, 128), 11).to(DEV)
+    v = _student_t((NP, KH, 16, 128), 12).to(DEV)
+    ids = torch.randperm(P, generator=torch.Generator().manual_seed(3))[:NP].to(torch.int32).to(DEV)
+    n_valid = torch.randint(1, 17, (NP,), generator=torch.Generator().manual_seed(4)).to(torch.int32).to(DEV)
+    a = tq_pages.allocate_pool(P, L, KH, comp, DEV)
+    b = tq_pages.allocate_pool(P, L, KH, comp, DEV)
+    tq_pages.quantize_pages(a, 1, ids, k, v, comp, n_valid)
+    for s in range(0, NP, 5):
+        tq_pages.quantize_pages(b, 1, ids[s:s + 5], k[s:s + 5], v[s:s + 5], comp, n_valid[s:s + 5])
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())
+
+
 def test_device_buffers_cached_and_refreshed():
     """The compressor's signs and JL matrix are uploaded once per device and
     uploaded again after an in-place change or a replacement; pages written

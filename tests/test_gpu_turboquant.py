@@ -132,6 +132,24 @@ def test_compress_other_shapes(head_dim, bits):
     assert torch.equal(dec, TQ.decompress(p, ref))
 
 
+@pytest.mark.parametrize("head_dim,bits", [(128, 3), (96, 2), (256, 4)])
+def test_compress_bulk_launch_equals_small_launches(head_dim, bits):
+    """A launch of 4,097 rows (several rows per workgroup, the last group
+    partial) gives the codes of the same rows compressed 1,000 at a time."""
+    _say(f"bulk vs small d{head_dim} b{bits}")
+    p = TQ.make_params(head_dim, bits, seed=7 * head_dim + bits)
+    kv = _student_t(4097, head_dim, 5 + bits).to(DEV)
+    args = (head_dim, p.padded_dim, p.n_levels, bits, p.signs.to(DEV), p.jl_matrix.to(DEV))
+    bulk = CUDATurboQuantOps.compress_gpu(kv, *args)
+    parts = [CUDATurboQuantOps.compress_gpu(kv[s:s + 1000].contiguous(), *args) for s in range(0, 4097, 1000)]
+    for key in ("radius", "qjl_signs", "qjl_norms"):
+        want = torch.cat([c[key].reshape(c[key].shape[0], -1) for c in parts])
+        assert torch.equal(bulk[key].reshape(want.shape).view(torch.uint8), want.view(torch.uint8)), key
+    got_angles = torch.cat(list(bulk["angles"]), -1)
+    want_angles = torch.cat([torch.cat(list(c["angles"]), -1) for c in parts])
+    assert torch.equal(got_angles, want_angles)
+
+
 def test_compressor_api_roundtrip_and_batch():
     _say("compressor api")
     torch.manual_seed(42)

@@ -49,6 +49,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
   return __builtin_bit_cast(unsigned short, (_Float16)x);  // round to nearest even
 }
 
+// Each row of the codec belongs to one wavefront, whose LDS working set no
+// other wavefront touches.  A wavefront's LDS operations complete in program
+// order, so a wavefront-scope fence is what orders one lane's LDS writes
+// before another lane's later reads: no s_barrier, and workgroups can carry
+// several rows whose wavefronts never wait for each other.
+__device__ __forceinline__ void row_sync() { __syncwarp(); }
+
 // In-register Walsh-Hadamard transform of a PD-element row spread as element
 // e -> (lane e % 64, register e / 64); same butterfly order as the reference.
 template <int PD>
@@ -119,17 +126,18 @@ __device__ __forceinline__ float polar_element(float radius, const uint8_t* bins
 template <int PD>
 __device__ __forceinline__ void polar_decode(float radius, const uint8_t* bins, const float* lut, int nb,
                                              float* recon, int lane) {
-  __syncthreads();
+  row_sync();
 #pragma unroll
   for (int k = 0; k < PD / 64; ++k) recon[k * 64 + lane] = polar_element<PD>(radius, bins, lut, nb, k * 64 + lane);
-  __syncthreads();
+  row_sync();
 }
 
 // LDS working set of one row.
 template <int PD>
 struct RowLds {
-  alignas(16) float rot[PD];  // rotated row, then the residual (read as float4)
-  float rad[PD];              // radius of each polar node, level-major like the bins
+  float rot[PD];               // rotated row
+  float rad[PD];               // radius of each polar node, level-major like the bins
+  alignas(16) double res[PD];  // QJL residual, widened once by the lane that owns it
   uint8_t bins[PD];
   float norm_acc[8];
 };
@@ -157,7 +165,7 @@ __device__ __forceinline__ float encode_row(const void* src, size_t first, int h
     v[k] = __fdiv_rn(v[k], root);
     w.rot[k * 64 + lane] = v[k];
   }
-  __syncthreads();
+  row_sync();
 
   // The radii only need square roots, level after level: node i of level l
   // (w.rad[PD - (PD >> l) + i]) over children 2 i, 2 i + 1 of level l - 1
@@ -169,7 +177,7 @@ __device__ __forceinline__ float encode_row(const void* src, size_t first, int h
       const float x0 = child[2 * i], x1 = child[2 * i + 1];
       rad[i] = sqrt_rn(__fadd_rn(__fadd_rn(__fmul_rn(x0, x0), __fmul_rn(x1, x1)), 1e-12f));
     }
-    __syncthreads();
+    row_sync();
   }
   // With every child known, the angles of all levels are independent: lane
   // takes bins b = lane, lane + 64, ... of the level-major order.
@@ -187,7 +195,7 @@ __device__ __forceinline__ float encode_row(const void* src, size_t first, int h
     idx = min(max(idx, 0), nb - 1);
     w.bins[b] = (uint8_t)idx;
   }
-  __syncthreads();
+  row_sync();
   return w.rad[PD - 2];
 }
 
@@ -203,54 +211,63 @@ __device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius
 #pragma unroll
   for (int k = 0; k < PER; ++k) res[k] = __fsub_rn(v[k], polar_element<PD>(radius, w.bins, lut, 1 << bits, k * 64 + lane));
 #pragma unroll
-  for (int k = 0; k < PER; ++k) w.rot[k * 64 + lane] = res[k];  // rot now holds the residual
-  __syncthreads();
+  for (int k = 0; k < PER; ++k) w.res[k * 64 + lane] = (double)res[k];
+  row_sync();
   // Lane j walks row j of the JL matrix.  With a 16-byte aligned matrix (every
   // row is then aligned, PD being a multiple of 4) it reads four floats per
-  // load and four residual elements per LDS broadcast; the accumulation order
-  // is the same element order either way.
+  // load; the residual comes as doubles, two per LDS broadcast.  The
+  // accumulation order is the element order either way.
   const bool vec = (reinterpret_cast<uintptr_t>(jl) & 15) == 0;
+  const double2* r2 = reinterpret_cast<const double2*>(w.res);
   for (int j = lane; j < qjl_dim; j += 64) {
     const float* jr = jl + (size_t)j * PD;
     double s = 0.0;
     if (vec) {
       const float4* jr4 = reinterpret_cast<const float4*>(jr);
-      const float4* r4 = reinterpret_cast<const float4*>(w.rot);
 #pragma unroll 8
       for (int m = 0; m < PD / 4; ++m) {
         const float4 x = jr4[m];
-        const float4 r = r4[m];
-        s = fma((double)r.x, (double)x.x, s);
-        s = fma((double)r.y, (double)x.y, s);
-        s = fma((double)r.z, (double)x.z, s);
-        s = fma((double)r.w, (double)x.w, s);
+        const double2 ra = r2[2 * m], rb = r2[2 * m + 1];
+        s = fma(ra.x, (double)x.x, s);
+        s = fma(ra.y, (double)x.y, s);
+        s = fma(rb.x, (double)x.z, s);
+        s = fma(rb.y, (double)x.w, s);
       }
     } else {
-      for (int e = 0; e < PD; ++e) s = fma((double)w.rot[e], (double)jr[e], s);
+      for (int e = 0; e < PD; ++e) s = fma(w.res[e], (double)jr[e], s);
     }
     put_sign(j, s > 0.0);
   }
   if (lane < 8) {
     float x[PD / 8];
 #pragma unroll
-    for (int m = 0; m < PD / 8; ++m) x[m] = w.rot[lane + 8 * m];
+    for (int m = 0; m < PD / 8; ++m) x[m] = (float)w.res[lane + 8 * m];  // exact: widened from a float
     float acc = 0.f;
 #pragma unroll
     for (int m = 0; m < PD / 8; ++m) acc = fmaf(x[m], x[m], acc);
     w.norm_acc[lane] = acc;
   }
-  __syncthreads();
+  row_sync();
   float s = w.norm_acc[0];
 #pragma unroll
   for (int k = 1; k < 8; ++k) s = __fadd_rn(s, w.norm_acc[k]);
   return sqrt_rn(s);
 }
 
-template <int SRC, int PD>
-__global__ void __launch_bounds__(64) tq_compress_kernel(TqArgs a) {
-  __shared__ RowLds<PD> w;
-  const int lane = threadIdx.x;
-  const int row = blockIdx.x;
+// Launch shape of the row kernels: a launch of at least kBulkMinRows rows
+// packs kBulkRows rows (one wavefront each) per workgroup, so a compute unit
+// holds more rows at once than its workgroup slots allow at one row each;
+// smaller launches keep one row per workgroup, spread over more units.
+constexpr int kBulkRows = 4;
+constexpr int kBulkMinRows = 4096;
+
+template <int SRC, int PD, int ROWS>
+__global__ void __launch_bounds__(64 * ROWS) tq_compress_kernel(TqArgs a) {
+  __shared__ RowLds<PD> rows_lds[ROWS];
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
+  if (row >= a.N) return;  // whole wavefront: no workgroup barrier follows
+  RowLds<PD>& w = rows_lds[threadIdx.x >> 6];
   float v[PD / 64];
   const float radius = encode_row<SRC, PD>(a.kv, (size_t)row * a.head_dim, a.head_dim, a.signs, a.bits, v, w, lane);
   for (int i = lane; i < PD - 1; i += 64) a.angles[(size_t)row * (PD - 1) + i] = w.bins[i];
@@ -274,6 +291,7 @@ struct TqPoolArgs {
   const int32_t* slots;    // append: slot of each token; pages: nullptr
   const int32_t* n_valid;  // pages: valid tokens of each page; append: nullptr
   uint8_t* pool;
+  int rows;  // rows of one K/V side: tokens * KH (append) or pages * KH * 16 (pages)
   int KH, L, P, layer, bits, head_dim;
   int from_pool;  // pages: key/value are a float pool [P][L][2][KH][16][head_dim] read at (page_ids[n], layer)
   const float* signs;
@@ -281,29 +299,33 @@ struct TqPoolArgs {
   const float* lut;
 };
 
-template <int SRC, int BITS>
-__global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
+template <int SRC, int BITS, int ROWS>
+__global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) {
   namespace L = vrm::tq;
   constexpr int PD = L::kPD;
-  __shared__ RowLds<PD> w;
-  __shared__ uint32_t sign_bits[L::kQjl / 32];
-  const int lane = threadIdx.x;
+  __shared__ RowLds<PD> rows_lds[ROWS];
+  __shared__ uint32_t rows_signs[ROWS][L::kQjl / 32];
+  const int lane = threadIdx.x & 63;
+  const int x = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
+  if (x >= a.rows) return;  // whole wavefront: no workgroup barrier follows
+  RowLds<PD>& w = rows_lds[threadIdx.x >> 6];
+  uint32_t* sign_bits = rows_signs[threadIdx.x >> 6];
   const int kv = blockIdx.y;
   // append: x = n * KH + h (token n); pages: x = (np * KH + h) * 16 + t
   int n, h, t;
   size_t src_first;
   bool live = true;
   if (a.slots) {
-    n = blockIdx.x / a.KH;
-    h = blockIdx.x % a.KH;
+    n = x / a.KH;
+    h = x % a.KH;
     t = a.slots[n];
-    src_first = (size_t)blockIdx.x * a.head_dim;
+    src_first = (size_t)x * a.head_dim;
   } else {
-    t = blockIdx.x % L::kTokens;
-    h = (blockIdx.x / L::kTokens) % a.KH;
-    n = blockIdx.x / (L::kTokens * a.KH);
+    t = x % L::kTokens;
+    h = (x / L::kTokens) % a.KH;
+    n = x / (L::kTokens * a.KH);
     live = t < a.n_valid[n];
-    src_first = (size_t)blockIdx.x * a.head_dim;
+    src_first = (size_t)x * a.head_dim;
   }
   const int pid = a.page_ids[n];
   if (pid < 0 || pid >= a.P || t < 0 || t >= L::kTokens) return;  // rows aimed outside the pool are dropped
@@ -345,11 +367,11 @@ __global__ void __launch_bounds__(64) tq_pool_write_kernel(TqPoolArgs a) {
   if (lane == 0) *radius_out = f32_to_f16_bits(radius);
   if (kv == 1) return;
   if (lane < L::kQjl / 32) sign_bits[lane] = 0;
-  __syncthreads();
+  row_sync();
   const float norm = qjl_row<PD>(v, radius, a.lut, BITS, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
     if (pos) atomicOr(&sign_bits[j >> 5], 1u << (j & 31));
   });
-  __syncthreads();
+  row_sync();
   if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(BITS) + t * 8)[lane] = sign_bits[lane];
   if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = f32_to_f16_bits(norm);
 }
@@ -618,8 +640,13 @@ extern "C" int vrm_turboquant_compress(const void* kv, int src_dtype, int N, int
   a.qjl_signs = qjl_signs;
   a.qjl_norms = qjl_norms;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define VRM_TQ_LAUNCH(SRC, PDV) \
-  hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV>), dim3(N), dim3(64), 0, st, a)
+  const bool bulk = N >= kBulkMinRows;
+#define VRM_TQ_LAUNCH(SRC, PDV)                                                                                     \
+  if (bulk)                                                                                                         \
+    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, kBulkRows>), dim3((N + kBulkRows - 1) / kBulkRows),            \
+                       dim3(64 * kBulkRows), 0, st, a);                                                             \
+  else                                                                                                              \
+    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, 1>), dim3(N), dim3(64), 0, st, a)
 #define VRM_TQ_PD(SRC)                                  \
   switch (padded_dim) {                                 \
     case 64: VRM_TQ_LAUNCH(SRC, 64); break;             \
@@ -713,6 +740,7 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.slots = slots;
   a.n_valid = n_valid;
   a.pool = tq_pool;
+  a.rows = rows;
   a.KH = KH;
   a.L = L;
   a.P = P;
@@ -724,12 +752,19 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.jl = jl;
   a.lut = angle_lut;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(rows, 2);
-#define VRM_TQ_WRITE(SRC)                                                                          \
-  switch (bits) {                                                                                  \
-    case 2: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 2>), grid, dim3(64), 0, st, a); break; \
-    case 3: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 3>), grid, dim3(64), 0, st, a); break; \
-    default: hipLaunchKernelGGL((tq_pool_write_kernel<SRC, 4>), grid, dim3(64), 0, st, a); break; \
+  // bulk writes pack kBulkRows rows (wavefronts) per workgroup, small ones one
+  const bool bulk = rows >= kBulkMinRows;
+  const dim3 grid(bulk ? (rows + kBulkRows - 1) / kBulkRows : rows, 2);
+#define VRM_TQ_WRITE_R(SRC, B)                                                                               \
+  if (bulk)                                                                                                  \
+    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, kBulkRows>), grid, dim3(64 * kBulkRows), 0, st, a);     \
+  else                                                                                                       \
+    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, 1>), grid, dim3(64), 0, st, a);
+#define VRM_TQ_WRITE(SRC)                          \
+  switch (bits) {                                  \
+    case 2: VRM_TQ_WRITE_R(SRC, 2); break;         \
+    case 3: VRM_TQ_WRITE_R(SRC, 3); break;         \
+    default: VRM_TQ_WRITE_R(SRC, 4); break;        \
   }
   switch (src_dtype) {
     case VRM_SRC_F32: VRM_TQ_WRITE(VRM_SRC_F32); break;
@@ -737,6 +772,7 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
     default: VRM_TQ_WRITE(VRM_SRC_BF16); break;
   }
 #undef VRM_TQ_WRITE
+#undef VRM_TQ_WRITE_R
   return launch_status(who);
 }
 }  // namespace

@@ -23,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .turboquant_cuda import CUDATurboQuantOps
+from .turboquant_cuda import CUDATurboQuantOps, level_bins
 
 __all__ = ["KVCacheCompressor", "TurboQuantCompressor", "BatchedCompressedRef"]
 
@@ -70,7 +70,7 @@ def _pack_angles(angles_list, bits_per_angle):
     """Level-major concatenation of a row's angle bins, bits_per_angle bits each."""
     if not angles_list:
         return torch.tensor([], dtype=torch.uint8)
-    return _pack_values(torch.cat(angles_list, dim=-1), bits_per_angle)
+    return _pack_values(level_bins(angles_list, sum(a.shape[-1] for a in angles_list)), bits_per_angle)
 
 
 def _unpack_angles(packed, N, level_dims, bits_per_angle):

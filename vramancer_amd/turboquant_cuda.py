@@ -79,6 +79,30 @@ def _split_levels(angles, padded_dim: int, n_levels: int):
     return out
 
 
+def level_bins(levels, width: int):
+    """The [N, width] uint8 bin array of a per-level list of [N, n_l] bins.
+
+    When the list is the column views of one [N, width] array, as
+    ``compress_gpu`` returns it, that array is used as is; any other list is
+    concatenated into a new one.
+    """
+    import torch
+
+    first = levels[0]
+    N = first.shape[0] if first.dim() == 2 else -1
+    if N > 0 and sum(t.shape[-1] for t in levels) == width:
+        ptr = first.data_ptr()
+        base = first.untyped_storage().data_ptr()
+        for t in levels:
+            if (t.dtype != torch.uint8 or t.dim() != 2 or t.shape[0] != N or t.stride() != (width, 1)
+                    or t.device != first.device or t.untyped_storage().data_ptr() != base or t.data_ptr() != ptr):
+                break
+            ptr += t.shape[1]
+        else:
+            return torch.as_strided(first, (N, width), (width, 1))
+    return torch.cat([a.to(torch.uint8) for a in levels], dim=-1).contiguous()
+
+
 class CUDATurboQuantOps:
     """Fused gfx950 TurboQuant ops: one kernel launch per compress / decompress."""
 
@@ -134,7 +158,7 @@ class CUDATurboQuantOps:
         radius = compressed["radius"].reshape(-1).to(torch.float16).contiguous()
         _lib.require_cuda(radius)
         device = radius.device
-        angles = torch.cat([a.to(torch.uint8) for a in compressed["angles"]], dim=-1).contiguous()
+        angles = level_bins(compressed["angles"], padded_dim - 1)
         N = radius.shape[0]
         if angles.shape != (N, padded_dim - 1):
             raise RuntimeError(f"angles {tuple(angles.shape)} do not match padded_dim {padded_dim}")
@@ -191,7 +215,7 @@ class CUDATurboQuantOps:
         device = q.device
         flat_q = q.reshape(-1, head_dim).float().contiguous()
         radius = compressed_k["radius"].reshape(-1).to(torch.float16).contiguous()
-        angles = torch.cat([a.to(torch.uint8) for a in compressed_k["angles"]], dim=-1).contiguous()
+        angles = level_bins(compressed_k["angles"], padded_dim - 1)
         qjl_signs = compressed_k["qjl_signs"].to(torch.uint8).contiguous()
         qjl_norms = compressed_k["qjl_norms"].reshape(-1).to(torch.float16).contiguous()
         _lib.require_cuda(flat_q, radius, angles, qjl_signs, qjl_norms)
