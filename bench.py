@@ -23,6 +23,9 @@ of a batched decode step of the 7b-bf16 batch through the pages against the
 reference batcher's pad-and-concat step, on the same GPU.  ``--codecs`` times
 the codec kernels beside the decode (fp8 append, TurboQuant compress, pack,
 decompress, scores, sparse V) with the oracle's CPU time on a sample.
+``--hf-cache`` times one layer of a decode step through the Hugging Face
+TurboQuant cache at the 14b-turbo3 shape, paged attention against the
+materialised keys/values + SDPA the reference's cache hands a model.
 """
 from __future__ import annotations
 
@@ -354,6 +357,96 @@ def codec_bench(args):
                       "n_gpus": 1, "data": "synthetic", "cpu_threads": threads, "rows": rows}), flush=True)
 
 
+def hf_cache_step(args):
+    """``--hf-cache``: one layer of a decode step through the Hugging Face
+    TurboQuant cache (``TurboQuantLayer``, core/turboquant_cache.py:78-299) at
+    the 14b-turbo3 shape: B=16, H=40, KH=8, D=128, 3 bits per angle, 32,768
+    compressed tokens per sequence, a residual of 256, float16 activations.
+    Two layers are filled with the same tokens and stepped two ways:
+
+    * paged: ``update`` writes the new token into the residual pages, then
+      ``turbo_paged_attention`` (the function ``enable_paged_attention``
+      registers) runs the TurboQuant decode over the compressed pages and the
+      float decode over the residual, merged by log-sum-exp;
+    * materialised, what the reference's cache hands the model
+      (core/turboquant_cache.py:176-230): ``update`` returns the full keys and
+      values with the compressed part decompressed, and transformers' SDPA
+      attends over them (K/V repeated to H heads, all-true padding mask).
+
+    Steps are timed between spills; the spill (256 residual tokens of every
+    sequence compressed into pages, once per 256 steps) is timed on its own."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    from vramancer_amd.kv_quantizer import KVCacheCompressor
+    from vramancer_amd.turboquant_cache import TurboQuantLayer, turbo_paged_attention
+
+    dev = torch.device("cuda:0")
+    B, H, KH, D, ctx, bits, R = 16, 40, 8, 128, 32768, 3, 256
+    dt = torch.float16
+    scale = 1.0 / math.sqrt(D)
+    torch.manual_seed(0)
+    comp = KVCacheCompressor(D, bits).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    paged_layer = TurboQuantLayer(comp, R, paged_attention=True)
+    mat_layer = TurboQuantLayer(comp, R, paged_attention=False)
+    log(f"filling two cache layers with {ctx} tokens of {B} sequences")
+    chunk = 4096
+    for s in range(0, ctx, chunk):
+        k = torch.randn((B, KH, chunk, D), generator=gen, device=dev).to(dt)
+        v = torch.randn((B, KH, chunk, D), generator=gen, device=dev).to(dt)
+        paged_layer.update(k, v)
+        mat_layer.update(k, v)
+        del k, v
+    q = torch.randn((B, H, 1, D), generator=gen, device=dev).to(dt)
+    kn = torch.randn((B, KH, 1, D), generator=gen, device=dev).to(dt)
+    vn = torch.randn((B, KH, 1, D), generator=gen, device=dev).to(dt)
+
+    class _Attn:  # what the attention functions read from the attention module
+        num_key_value_groups = H // KH
+        is_causal = True
+
+    def paged(i):
+        k, v = paged_layer.update(kn, vn)
+        turbo_paged_attention(_Attn, q, k, v, None, scaling=scale)
+
+    def materialised(i):
+        k, v = mat_layer.update(kn, vn)
+        mask = torch.ones((B, 1, 1, k.shape[2]), dtype=torch.bool, device=dev)
+        sdpa_attention_forward(_Attn, q, k, v, mask, scaling=scale)
+
+    # the first step of each spills the last prefill chunk; the residual then
+    # holds 1 token and grows by one per step
+    warm_p, warm_m = 4, 3
+    for i in range(warm_p):
+        paged(i)
+    for i in range(warm_m):
+        materialised(i)
+    torch.cuda.synchronize()
+    n_paged = min(args.steps, R - warm_p - 1)
+    log(f"timing {n_paged} paged steps and 5 materialised steps")
+    us_paged = time_events(paged, n_paged)
+    us_mat = time_events(materialised, 5)
+    for i in range(R - warm_p - n_paged):  # up to a full residual: the next update spills
+        paged(i)
+    us_spill = time_events(lambda i: paged_layer.update(kn, vn), 1)
+    result = {
+        "metric": "HF TurboQuant cache decode step, one layer: paged attention vs materialised K/V + SDPA",
+        "value": round(us_paged, 3),
+        "unit": "us/layer-step",
+        "higher_is_better": False,
+        "materialised_us": round(us_mat, 1),
+        "speedup": round(us_mat / us_paged, 1),
+        "spill_us": round(us_spill, 1),
+        "spill_per_step_us": round(us_spill / R, 2),
+        "dtype": "tq3-polar codes, f16 activations",
+        "data": "synthetic",
+        "config": {"workload": "14b-turbo3 shape through the HF cache: B=16, H=40, KH=8, D=128, 32,768 "
+                               "compressed tokens per sequence, residual 256, 3 bits per angle",
+                   "compressed_tokens": ctx, "residual_length": R},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +462,9 @@ def main():
                          "sparse V) beside the oracle on the CPU")
     ap.add_argument("--batcher", action="store_true",
                     help="time one layer of a batched decode step, paged vs the reference's pad-and-concat")
+    ap.add_argument("--hf-cache", action="store_true",
+                    help="time one layer of a decode step through the HF TurboQuant cache, paged attention vs "
+                         "materialised K/V + SDPA")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -384,6 +480,9 @@ def main():
         return
     if args.codecs:
         codec_bench(args)
+        return
+    if args.hf_cache:
+        hf_cache_step(args)
         return
     lib = _lib.load()
     dev = torch.device("cuda:0")

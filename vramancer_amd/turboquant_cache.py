@@ -85,6 +85,9 @@ class TurboQuantLayer(CacheLayerMixin):
 
     def _clear(self) -> None:
         self._res_pool = None   # [B * rp, 1, 2, KH, 16, D] residual pages, sequence b owns b * rp ..
+        self._res_ids = None    # [2, rp * 16, B] int32 page / slot of each residual position
+        self._len_rows = None   # [rp * 16 + 1, B] int32, row n all n
+        self._len_last = None   # (n, [B] int32 all n) for the compressed count
         self._rp = 0
         self._res_len = 0
         self._tq_pool = None    # [rows, 1, 2, KH, slice] TurboQuant pages, page j of sequence b at j * B + b
@@ -123,6 +126,12 @@ class TurboQuantLayer(CacheLayerMixin):
         if self._res_pool is not None:
             pool.view(B, rp, -1)[:, :self._rp] = self._res_pool.view(B, self._rp, -1)
         self._res_pool, self._rp = pool, rp
+        # page b * rp + t // 16 and slot t % 16 of residual position t of
+        # sequence b, token-major ([2, rp * 16, B]): the ids of any run of
+        # positions are one contiguous slice
+        t = np.arange(rp * PAGE)[:, None]
+        self._res_ids = _int32(np.stack(np.broadcast_arrays(np.arange(B)[None, :] * rp + t // PAGE, t % PAGE)),
+                               self.device)
         self._tables.clear()
 
     def _ensure_pages(self, pages_per_seq: int) -> None:
@@ -140,16 +149,17 @@ class TurboQuantLayer(CacheLayerMixin):
     # -- writes ------------------------------------------------------------
 
     def _write_residual(self, key_states, value_states, start: int) -> None:
+        """Writes [B, KH, S, D] at residual positions start .. start + S - 1,
+        token-major (row t * B + b), with the ids sliced from the residual
+        table: no host round trip and no index kernels per step."""
         B, KH, S, D = key_states.shape
-        t = start + np.arange(S)
-        pages = (np.arange(B)[:, None] * self._rp + t[None, :] // PAGE).reshape(-1)
-        slots = np.broadcast_to(t[None, :] % PAGE, (B, S)).reshape(-1)
-        ids = _int32(np.stack([pages, slots]), self.device)
-        k = key_states.permute(0, 2, 1, 3).reshape(B * S, KH, D).contiguous()
-        v = value_states.permute(0, 2, 1, 3).reshape(B * S, KH, D).contiguous()
+        ids = self._res_ids[:, start:start + S].reshape(2, S * B)
+        pages, slots = ids[0], ids[1]
+        k = key_states.permute(2, 0, 1, 3).reshape(S * B, KH, D).contiguous()
+        v = value_states.permute(2, 0, 1, 3).reshape(S * B, KH, D).contiguous()
         pool = self._res_pool
         rc = _lib.load().vrm_kv_write(
-            _lib.ptr(k), _lib.ptr(v), _lib.src_dtype_code(k.dtype), _lib.ptr(ids[0]), _lib.ptr(ids[1]), B * S,
+            _lib.ptr(k), _lib.ptr(v), _lib.src_dtype_code(k.dtype), _lib.ptr(pages), _lib.ptr(slots), B * S,
             _lib.ptr(pool), _lib.kv_dtype_code(pool.dtype), KH, D, PAGE, 1, pool.shape[0], 0, _lib.stream_of(pool))
         _lib.check(rc, "TurboQuantLayer residual write")
 
@@ -169,14 +179,16 @@ class TurboQuantLayer(CacheLayerMixin):
         k, v = self._residual_rows()
         k = k.permute(0, 2, 1, 3).reshape(B * n, KH, D).contiguous()
         v = v.permute(0, 2, 1, 3).reshape(B * n, KH, D).contiguous()
-        t = self._n_comp + np.arange(n)
-        pages = ((t[None, :] // PAGE) * B + np.arange(B)[:, None]).reshape(-1)
-        slots = np.broadcast_to(t[None, :] % PAGE, (B, n)).reshape(-1)
-        ids = _int32(np.stack([pages, slots]), self.device)
+        # TurboQuant page (t // 16) * B + b, slot t % 16, sequence-major like k
+        # and v; computed on the device (once per residual_length steps)
+        t = torch.arange(self._n_comp, self._n_comp + n, dtype=torch.int32, device=self.device)
+        pages = ((t // PAGE)[None, :] * B + torch.arange(B, dtype=torch.int32, device=self.device)[:, None])
+        pages = pages.reshape(-1).contiguous()
+        slots = (t % PAGE)[None, :].expand(B, n).reshape(-1).contiguous()
         signs, jl, lut = self._buffers
         pool = self._tq_pool
         rc = _lib.load().vrm_tq_quant_append(
-            _lib.ptr(k), _lib.ptr(v), _lib.src_dtype_code(k.dtype), _lib.ptr(ids[0]), _lib.ptr(ids[1]), B * n,
+            _lib.ptr(k), _lib.ptr(v), _lib.src_dtype_code(k.dtype), _lib.ptr(pages), _lib.ptr(slots), B * n,
             _lib.ptr(pool), KH, D, PAGE, 1, pool.shape[0], 0, self.compressor.bits_per_angle, 64, _lib.ptr(signs),
             _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(pool))
         _lib.check(rc, "TurboQuantLayer spill")
@@ -250,6 +262,18 @@ class TurboQuantLayer(CacheLayerMixin):
             self._tables[key] = t
         return t
 
+    def _lengths(self, n: int):
+        """[B] int32 device array of n: a row of a cached table for residual
+        lengths (one table per residual pool size), a cached array otherwise."""
+        if n < self._rp * PAGE + 1:
+            if self._len_rows is None or self._len_rows.shape[0] != self._rp * PAGE + 1:
+                rows = np.broadcast_to(np.arange(self._rp * PAGE + 1)[:, None], (self._rp * PAGE + 1, self._B))
+                self._len_rows = _int32(rows, self.device)
+            return self._len_rows[n]
+        if self._len_last is None or self._len_last[0] != n:  # the compressed count: changes once per spill
+            self._len_last = (n, torch.full((self._B,), n, dtype=torch.int32, device=self.device))
+        return self._len_last[1]
+
     def _workspace(self, H: int, pages: int):
         key = (H, pages)
         ws = self._ws.get(key)
@@ -270,7 +294,7 @@ class TurboQuantLayer(CacheLayerMixin):
         results = []
         if n_c:
             pj = -(-n_c // PAGE)
-            ctx = torch.full((B,), n_c, dtype=torch.int32, device=self.device)
+            ctx = self._lengths(n_c)
             lse = torch.empty((B, H), dtype=torch.float32, device=self.device)
             out = tq_pages.paged_attention_decode_turbo(q, self._tq_pool, self._table("tq", pj), ctx, 0,
                                                         self.compressor, scale=scale,
@@ -278,7 +302,7 @@ class TurboQuantLayer(CacheLayerMixin):
             results.append((out, lse))
         if n_r:
             pr = -(-n_r // PAGE)
-            ctx = torch.full((B,), n_r, dtype=torch.int32, device=self.device)
+            ctx = self._lengths(n_r)
             lse = torch.empty((B, H), dtype=torch.float32, device=self.device)
             out = paged_attention_decode(q, self._res_pool, self._table("res", pr), ctx, 0, scale=scale,
                                          workspace=self._workspace(H, pr), lse=lse)
