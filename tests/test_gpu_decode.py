@@ -175,10 +175,14 @@ def test_partitions_then_merge_equals_fused_call():
     assert torch.equal(out, out2)
 
 
-def test_decode_q4_matches_oracle():
-    _say("q4")
+@pytest.mark.parametrize("H,KH,D", [(16, 4, 128), (40, 8, 128), (12, 2, 128), (14, 2, 128), (10, 2, 64),
+                                    (12, 2, 256)])
+def test_decode_q4_matches_oracle(H, KH, D):
+    """Head groups per wave: 4, 5, 6, 1 (7 heads per kv-head), 5 and 6 at the
+    other head dims."""
+    _say(f"q4 H={H} KH={KH} D={D}")
     g = torch.Generator().manual_seed(12)
-    B, H, KH, D, PS, L = 3, 16, 4, 128, 16, 2
+    B, PS, L = 3, 16, 2
     ctxs = [70, 1, 400]
     npages = [(c + PS - 1) // PS for c in ctxs]
     P = sum(npages) + 2

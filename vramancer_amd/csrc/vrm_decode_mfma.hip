@@ -632,11 +632,328 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q4 pools at head_dim 128: the reference's asymmetric 4-bit layout (per token
+// and kv-head D/2 bytes of nibbles, byte j holding dims 2j (low) and 2j + 1
+// (high); per 32-dim group a float16 scale and zero point in arrays of their
+// own; value = (nibble - zero) * scale), in the same single-pass stream.
+//   S^T = K Q^T     per group g, v_mfma_i32_16x16x32_i8 of the nibbles against
+//                   the query's three signed 8-bit digits (exact integer dot
+//                   products, as in the int8 kernel), then
+//                   score = sum_g s_g (q.n_g - z_g sum_{d in g} q_d).
+//                   A lane's 8 dims of a group enter as its low nibbles, then
+//                   its high nibbles (dims 0 2 4 6 1 3 5 7 of the slice); the
+//                   query digits are packed in the same order.
+//   V transpose     the one-hot product of the float kernel on the i8 matrix
+//                   cores: token col's nibbles move to lane (col, grp) as
+//                   tokens 4 grp .. + 3 of one dim, exactly.
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_f16 per 16-dim block, the B operand of
+//                   the block's group g holding p s_g (hi + lo float16); the
+//                   zero points' share, sum_t p s_g z_g per (group, head), is
+//                   accumulated beside it and subtracted at the end.
+// Scales and zeros (4 x 128 bytes per page and head: K s, K z, V s, V z)
+// arrive as one 8-byte load per lane and pass through 1 KB of LDS per wave,
+// from which each lane reads the 4 tokens x 4 groups its rows need.
+// ---------------------------------------------------------------------------
+struct Q4Slot {
+  uint32_t k[4];  // token col: dims 32 c + 8 grp .. + 7 (4 bytes of nibbles), group c
+  uint32_t v[4];  // the same positions of V
+  uint2 sz;       // this lane's 8 bytes of the page's scales / zeros
+  bool ok;        // page id inside the pool (wave-uniform)
+};
+
+// 8 nibbles (one dword, byte j = dims 2j, 2j + 1) -> i8 operand: low nibbles,
+// then high nibbles.
+__device__ __forceinline__ long q4_operand(uint32_t w) {
+  const uint32_t lo = w & 0x0f0f0f0fu;
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;
+  return (long)(((uint64_t)hi << 32) | lo);
+}
+
+// Dim offset (0 .. 7) inside a lane's 8-dim slice of operand element e.
+__device__ __forceinline__ constexpr int q4_dim_of(int e) { return e < 4 ? 2 * e : 2 * (e - 4) + 1; }
+// Operand element of dim offset o.
+__device__ __forceinline__ constexpr int q4_elem_of(int o) { return (o & 1) ? 4 + (o >> 1) : (o >> 1); }
+
+__device__ __forceinline__ float half_of(uint32_t w, int hi) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : (w & 0xffffu)));
+}
+
+__global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(DecodeArgs a, int G) {
+  constexpr int D = 128;
+  constexpr int RING = 4;
+  constexpr int ROW = D / 2;             // nibble bytes per token row
+  constexpr int HEAD_BYTES = kPS * ROW;  // one (page, layer, K/V, head) slice of codes
+  constexpr int NG = D / 32;             // 32-dim groups
+  constexpr int NB = D / 16;             // 16-dim blocks of the output column
+  constexpr int SZH = kPS * NG * 2;      // bytes of one (page, layer, K/V, head) slice of scales (or zeros)
+  static_assert(SZH == 16 * 8, "16 lanes load one slice, 8 bytes each");
+  __shared__ __align__(16) uint2 sz_lds[kMaxWaves][2][64];  // [wave][page of the pair][array * 16 + token]
+
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int group = a.H / a.KH;
+  const int chunks = group / G;
+  const int unit = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int kvh = unit / chunks;
+  const int h0 = kvh * group + (unit % chunks) * G;
+
+  const int item = blockIdx.x;
+  WorkItem wi;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  const int b = wi.b;
+  const int n_pages = wi.n_pages;
+  const int last = n_pages - 1;
+  const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);
+  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
+  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
+
+  const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
+  const size_t page_stride = kv_stride * 2 * a.L;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
+  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+  // lane (col, grp) fetches token col of array grp: K scales, K zeros, V scales, V zeros
+  const uint8_t* sz_base = reinterpret_cast<const uint8_t*>((grp & 1) ? a.q4_zero : a.q4_scale) + col * 8;
+  const int sz_kv = grp >> 1;
+
+  // ---------------- query: digits per group, group sums ----------------
+  const float* qrow = a.query + ((size_t)b * a.H + h0 + min(col, G - 1)) * D;
+  float qv[NG][8];  // dims 32 c + 8 grp + o
+#pragma unroll
+  for (int c = 0; c < NG; ++c) {
+    const float4 f0 = ldf4(qrow + 32 * c + 8 * grp);
+    const float4 f1 = ldf4(qrow + 32 * c + 8 * grp + 4);
+    qv[c][0] = f0.x; qv[c][1] = f0.y; qv[c][2] = f0.z; qv[c][3] = f0.w;
+    qv[c][4] = f1.x; qv[c][5] = f1.y; qv[c][6] = f1.z; qv[c][7] = f1.w;
+  }
+  float qmax = 0.f;
+  float qsum[NG];  // sum over the group of q * qscale (this head)
+#pragma unroll
+  for (int c = 0; c < NG; ++c) {
+    float s = 0.f;
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+      qmax = fmaxf(qmax, fabsf(qv[c][o]));
+      s += qv[c][o] * a.qscale;
+    }
+    s += xor_shfl<16>(s);
+    s += xor_shfl<32>(s);
+    qsum[c] = s;
+  }
+  qmax = fmaxf(qmax, xor_shfl<16>(qmax));
+  qmax = fmaxf(qmax, xor_shfl<32>(qmax));
+  const float inv = qmax > 0.f ? 127.f / qmax : 0.f;
+  const float qunit = qmax * (1.f / 127.f) * a.qscale;
+  long QA[NG][3];
+#pragma unroll
+  for (int c = 0; c < NG; ++c) {
+    int d[8][3];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) digits3(qv[c][q4_dim_of(e)] * inv, d[e][0], d[e][1], d[e][2]);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const uint32_t lo = pack4(d[0][k], d[1][k], d[2][k], d[3][k]);
+      const uint32_t hi = pack4(d[4][k], d[5][k], d[6][k], d[7][k]);
+      QA[c][k] = (long)(((uint64_t)hi << 32) | lo);
+    }
+  }
+  // one-hot operands of the V transpose: element e of lane (col, grp) is
+  // E_h[8 grp + e][col] = 1 when operand row 8 grp + e carries dim 16 h + col
+  long onehot[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e1 = grp == 2 * h + (col >> 3) ? q4_elem_of(col & 7) : -1;
+    uint64_t bits = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bits |= (uint64_t)(e == e1 ? 1 : 0) << (8 * e);
+    onehot[h] = (long)bits;
+  }
+
+  float m_run = kNoMax;
+  float l_run = 0.f;
+  float corr[NG];  // this lane's share of sum_t p s_g z_g for its head, per group
+  v4f acc[NB];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) corr[g] = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) acc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto load_page = [&](Q4Slot& s, int pid) {
+    s.ok = page_ok(pid);
+    const int pc = s.ok ? pid : 0;
+    const uint8_t* kb = layer_base + (size_t)pc * page_stride + col * ROW + grp * 4;
+#pragma unroll
+    for (int c = 0; c < NG; ++c) {
+      s.k[c] = *reinterpret_cast<const uint32_t*>(kb + c * 16);
+      s.v[c] = *reinterpret_cast<const uint32_t*>(kb + kv_stride + c * 16);
+    }
+    const size_t head = (((size_t)pc * a.L + a.layer) * 2 + sz_kv) * a.KH + kvh;
+    s.sz = *reinterpret_cast<const uint2*>(sz_base + head * SZH);
+  };
+
+  // scales / zeros of this lane's tokens 4 grp .. + 3 of one staged page:
+  // arr[r] = the 4 groups of token 4 grp + r as two dwords of float16 pairs
+  auto staged = [&](int u, int array, uint2 (&arr)[4]) {
+    const uint4* p = reinterpret_cast<const uint4*>(&sz_lds[wave][u][array * 16 + 4 * grp]);
+    const uint4 x = p[0], y = p[1];
+    arr[0] = make_uint2(x.x, x.y);
+    arr[1] = make_uint2(x.z, x.w);
+    arr[2] = make_uint2(y.x, y.y);
+    arr[3] = make_uint2(y.z, y.w);
+  };
+  auto group_half = [&](const uint2& v, int g) { return half_of(g < 2 ? v.x : v.y, g & 1); };
+
+  auto page_scores = [&](const Q4Slot& s, int u, int pi, float* sc) {
+    uint2 ks[4], kz[4];
+    staged(u, 0, ks);
+    staged(u, 1, kz);
+    float tot[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NG; ++c) {
+      const long kop = q4_operand(s.k[c]);
+      v4i c1 = {0, 0, 0, 0}, c2 = {0, 0, 0, 0}, c3 = {0, 0, 0, 0};
+      c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kop, QA[c][0], c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kop, QA[c][1], c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kop, QA[c][2], c3, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float dot = qunit * ((float)c1[r] + ((float)c2[r] + (float)c3[r] * kInv254) * kInv254);
+        tot[r] += group_half(ks[r], c) * (dot - group_half(kz[r], c) * qsum[c]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = (s.ok && pi * kPS + grp * 4 + r < tok_end) ? tot[r] : -INFINITY;
+  };
+
+  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page, exact.
+  auto v_block = [&](const Q4Slot& s, int blk, float* out4) {
+    v4i t = {0, 0, 0, 0};
+    t = __builtin_amdgcn_mfma_i32_16x16x32_i8(q4_operand(s.v[blk >> 1]), onehot[blk & 1], t, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out4[r] = (float)t[r];
+  };
+
+  auto process_pair = [&](const Q4Slot& s0, const Q4Slot& s1, int pi, bool has1) {
+    // stage both pages' scales / zeros; the wave's LDS operations complete in
+    // order, and the previous pair's reads came before these writes
+    sz_lds[wave][0][lane] = s0.sz;
+    sz_lds[wave][1][lane] = s1.sz;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float sc[8];
+    page_scores(s0, 0, pi, sc);
+    if (has1) {
+      page_scores(s1, 1, pi + 1, sc + 4);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
+    }
+    float pm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
+    pm = fmaxf(pm, xor_shfl<16>(pm));
+    pm = fmaxf(pm, xor_shfl<32>(pm));
+    if (pm > m_run + kLazyRescale) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
+      l_run *= alpha;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) corr[g] *= alpha;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) acc[blk] *= alpha;
+      m_run = pm;
+    }
+    uint2 vs[2][4], vz[2][4];
+    staged(0, 2, vs[0]);
+    staged(0, 3, vz[0]);
+    staged(1, 2, vs[1]);
+    staged(1, 3, vz[1]);
+    // B operands per group: element e <-> token 4 grp + e % 4 of page pi + e / 4
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = __builtin_amdgcn_exp2f(sc[e] - m_run);
+      l_run += p[e];
+    }
+    v8h Bh[NG], Bl[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool live = sc[e] != -INFINITY;  // scales of dead tokens may hold anything
+        const float w = live ? p[e] * group_half(vs[e >> 2][e & 3], g) : 0.f;
+        corr[g] += live ? w * group_half(vz[e >> 2][e & 3], g) : 0.f;
+        const _Float16 hi = (_Float16)w;
+        Bh[g][e] = hi;
+        Bl[g][e] = (_Float16)(w - (float)hi);
+      }
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      float t[8];
+      v_block(s0, blk, t);
+      v_block(s1, blk, t + 4);
+      v8h A;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] = (_Float16)t[e];  // nibbles: exact
+      acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bh[blk >> 1], acc[blk], 0, 0, 0);
+      acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bl[blk >> 1], acc[blk], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // staged reads before the next pair's writes
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  {
+    Q4Slot ring[RING];
+    const int ids0 = ids_at(0);
+    int ids_next = ids_at(RING);
+#pragma unroll
+    for (int u = 0; u < RING; ++u) load_page(ring[u], __builtin_amdgcn_readlane(ids0, u));
+    for (int base = 0; base < n_pages; base += RING) {
+      const int ids_ahead = ids_at(base + 2 * RING);
+#pragma unroll
+      for (int u = 0; u < RING; u += 2) {
+        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
+        load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
+        load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
+      }
+      ids_next = ids_ahead;
+    }
+  }
+
+  float l_tot = l_run + xor_shfl<16>(l_run);
+  l_tot += xor_shfl<32>(l_tot);
+  float corr_tot[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    corr_tot[g] = corr[g] + xor_shfl<16>(corr[g]);
+    corr_tot[g] += xor_shfl<32>(corr_tot[g]);
+  }
+  if (col < G) {
+    float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      const float z = corr_tot[blk >> 1];
+      *reinterpret_cast<float4*>(out + blk * 16 + grp * 4) =
+          make_float4(acc[blk][0] - z, acc[blk][1] - z, acc[blk][2] - z, acc[blk][3] - z);
+    }
+    if (grp == 0) {
+      ml_base[col * 2] = l_tot > 0.f ? m_run : -INFINITY;
+      ml_base[col * 2 + 1] = l_tot;
+    }
+  }
+}
+
 template <int KIND, int D>
 void launch_kernel(const DecodeArgs& a0, int B, int units, int W, int G, hipStream_t st) {
   const void* fn;
   if constexpr (KIND == K_I8 || KIND == K_FP8)
     fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D>);
+  else if constexpr (KIND == K_Q4)
+    fn = reinterpret_cast<const void*>(&decode_stream_q4_kernel);
   else
     fn = reinterpret_cast<const void*>(&decode_stream_float_kernel<KIND, D <= 128 ? D : 128>);
   DecodeArgs a = a0;
@@ -645,6 +962,8 @@ void launch_kernel(const DecodeArgs& a0, int B, int units, int W, int G, hipStre
   dim3 block(64 * W);
   if constexpr (KIND == K_I8 || KIND == K_FP8)
     hipLaunchKernelGGL((decode_stream_kernel<KIND, D>), grid, block, 0, st, a, G);
+  else if constexpr (KIND == K_Q4)
+    hipLaunchKernelGGL(decode_stream_q4_kernel, grid, block, 0, st, a, G);
   else if constexpr (D <= 128)
     hipLaunchKernelGGL((decode_stream_float_kernel<KIND, D>), grid, block, 0, st, a, G);
 }
@@ -662,6 +981,14 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   return hipGetLastError();
 }
 
+hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
+  const int units = a.KH * ((a.H / a.KH) / G);
+  int W = kMaxWaves;
+  while (units % W) --W;
+  launch_kernel<K_Q4, 128>(a, B, units, W, G, st);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
@@ -671,6 +998,7 @@ hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G
     case K_FP8: return launch_d<K_FP8>(a, B, D, G, st);
     case K_BF16: return D <= 128 ? launch_d<K_BF16>(a, B, D, G, st) : hipErrorInvalidValue;
     case K_F16: return D <= 128 ? launch_d<K_F16>(a, B, D, G, st) : hipErrorInvalidValue;
+    case K_Q4: return D == 128 ? launch_q4(a, B, G, st) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

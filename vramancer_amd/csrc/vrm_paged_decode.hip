@@ -459,12 +459,14 @@ hipError_t launch_split(const DecodeArgs& a0, int B, hipStream_t st) {
 
 template <int KIND, int D>
 hipError_t dispatch_g(const DecodeArgs& a, int B, int G, hipStream_t st) {
-  if constexpr (KIND == K_Q4) {  // 32 elements per lane chunk: at most 4 heads per wave
+  if constexpr (KIND == K_Q4) {  // 32 elements per lane chunk: at most 6 heads per wave (7 spill at D = 128)
     switch (G) {
       case 1: return launch_split<KIND, D, 1>(a, B, st);
       case 2: return launch_split<KIND, D, 2>(a, B, st);
       case 3: return launch_split<KIND, D, 3>(a, B, st);
-      default: return launch_split<KIND, D, 4>(a, B, st);
+      case 4: return launch_split<KIND, D, 4>(a, B, st);
+      case 5: return launch_split<KIND, D, 5>(a, B, st);
+      default: return launch_split<KIND, D, 6>(a, B, st);
     }
   } else {
     switch (G) {
@@ -556,11 +558,16 @@ enum Passes { kBoth = 3, kPartitionsOnly = 1, kMergeOnly = 2 };
 
 int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D,
                float scale, hipStream_t st, int passes) {
-  // The matrix-core stream kernels take the quantized pools at every head_dim
-  // and the 16-bit float pools at D <= 128 (at D = 256 their registers
-  // spill); the rest runs on the VALU kernel.
-  const bool mfma = kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128);
-  const int max_tile = kind == K_Q4 ? 4 : mfma ? 16 : 8;
+  // The matrix-core stream kernels take the int8 / fp8 pools at every
+  // head_dim, the 16-bit float pools at D <= 128 (at D = 256 their registers
+  // spill) and the Q4 pool at D = 128 when its codes are 4-byte and its scales
+  // and zeros 8-byte aligned (the widths of their loads); the rest runs on
+  // the VALU kernel.
+  const bool q4_aligned = ((reinterpret_cast<uintptr_t>(a.pool) & 3) | (reinterpret_cast<uintptr_t>(a.q4_scale) & 7) |
+                           (reinterpret_cast<uintptr_t>(a.q4_zero) & 7)) == 0;
+  const bool mfma = kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128) ||
+                    (kind == K_Q4 && D == 128 && q4_aligned);
+  const int max_tile = mfma ? 16 : kind == K_Q4 ? 6 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
   (void)units;
@@ -583,7 +590,7 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
       case K_BF16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_BF16>(a, B, D, G, st); break;
       case K_I8:
       case K_FP8: e = launch_stream_mfma(a, kind, B, D, G, st); break;
-      default: e = dispatch_d<K_Q4>(a, B, D, G, st); break;
+      default: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_Q4>(a, B, D, G, st); break;
     }
     if (e != hipSuccess) {
       set_error("vrm_paged_decode: partition kernel launch failed: %s", hipGetErrorString(e));
