@@ -53,7 +53,7 @@ KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_B
 KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
           "tq3": "decode_tq_kernel<3> + merge", "tq4": "decode_tq_kernel<4> + merge",
           "bf16": "decode_stream_float_kernel<K_BF16,{D}>", "f16": "decode_stream_float_kernel<K_F16,{D}>",
-          "f32": "decode_split_kernel<K_F32,{D},G>"}
+          "f32": "decode_split_kernel<K_F32,{D},G>", "q4": "decode_stream_q4_kernel + merge"}
 
 
 def log(msg):
@@ -104,6 +104,17 @@ def cpu_baseline(inp, layer, n_seq, reps):
         times.sort()
         return times[len(times) // 2] / max(1, int(lens.sum())) * 1e6, threads
     pool = inp["kv_pool"][pages][:, layer:layer + 1].cpu()
+    if inp.get("kv_zeros") is not None:  # Q4: the oracle's dequantize-then-attend path
+        sc = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
+        zp = inp["kv_zeros"][pages][:, layer:layer + 1].cpu()
+        PD.paged_attention_decode_q4(q, pool, sc, zp, tbl, lens, 0)  # warm-up
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            PD.paged_attention_decode_q4(q, pool, sc, zp, tbl, lens, 0)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2] / max(1, int(lens.sum())) * 1e6, threads
     scales = None
     if inp["kv_scales"] is not None:
         scales = inp["kv_scales"][pages][:, layer:layer + 1].cpu()
@@ -492,6 +503,7 @@ def main():
         cfg = workloads.scaled(cfg, num_layers=4)
     layers = LAYERS_FILLED if cfg.num_layers > max(LAYERS_FILLED) else tuple(range(4))
     turbo = cfg.codec in ("tq3", "tq4")
+    q4 = cfg.codec == "q4"
     # TurboQuant pages are filled on one layer (compression is the slow part of
     # the set-up); the zero codes of the other layers cost the decode the same.
     fill = (layers[0],) if turbo else layers
@@ -499,6 +511,7 @@ def main():
     inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=fill)
     torch.cuda.synchronize()
     q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
+    zp = inp["kv_zeros"]
     B, H, D = q.shape
     if turbo:
         P, L, _, KH, _ = pool.shape
@@ -529,6 +542,13 @@ def main():
             if rc:
                 _lib.check(rc, "turbo decode")
             return
+        if q4:
+            rc = lib.vrm_paged_decode_q4(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), zp.data_ptr(), table.data_ptr(),
+                                         lens.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS,
+                                         L, P, max_pp, layer, scale, stream)
+            if rc:
+                _lib.check(rc, "q4 decode")
+            return
         rc = lib.vrm_paged_decode(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(), lens.data_ptr(),
                                   out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp, layer,
                                   scale, code, stream)
@@ -549,8 +569,8 @@ def main():
     pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
     log(f"timing {args.steps} layer-steps")
     us_step = time_events(full, args.steps)
-    # TurboQuant: no separate partition entry; its kernel time is the whole decode
-    us_part = us_step if turbo else time_events(partitions, args.steps)
+    # TurboQuant and Q4: no separate partition entry; the kernel time is the whole decode
+    us_part = us_step if (turbo or q4) else time_events(partitions, args.steps)
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
     us_append = None
@@ -567,7 +587,7 @@ def main():
         for i in range(5):
             append(i)
         us_append = time_events(append, 50)
-    elif sc is not None:
+    elif sc is not None and not q4:  # the reference has no Q4 writer
         # append one token per sequence (quantize-on-append), timed separately
         kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
         vn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
@@ -619,10 +639,12 @@ def main():
                          "batch's total context"),
         }
     elem = {"f32": "f32", "f16": "f16", "bf16": "bf16", "int8": "int8", "fp8": "fp8e4m3", "tq3": "tq3-polar",
-            "tq4": "tq4-polar"}[cfg.codec]
+            "tq4": "tq4-polar", "q4": "u4-asym"}[cfg.codec]
     desc = {
         "14b-int8": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
                      "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
+        "14b-q4": ("14b-q4 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, 48-layer pool of "
+                   "16384 pages, 4-bit asymmetric codes + per-32-dim-group fp16 scale and zero"),
         "7b-bf16": "7b-bf16 paged decode: B=32, H=28, KH=4, D=128, context ~U[1024, 8192], page 16, bf16 pool",
         "mixed-fp8": ("mixed-fp8 paged decode: 128 sequences lognormal(median 2048, sigma 1) + one of 131072, "
                       "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales"),
@@ -664,7 +686,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": KERNEL[cfg.codec].format(D=D) + f" (G={G}, partition pass)",
+            "kernel": KERNEL[cfg.codec].format(D=D) + (f" (G={G}, whole decode)" if (turbo or q4)
+                                                       else f" (G={G}, partition pass)"),
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,

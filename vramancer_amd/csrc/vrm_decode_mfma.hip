@@ -675,9 +675,7 @@ __device__ __forceinline__ constexpr int q4_dim_of(int e) { return e < 4 ? 2 * e
 // Operand element of dim offset o.
 __device__ __forceinline__ constexpr int q4_elem_of(int o) { return (o & 1) ? 4 + (o >> 1) : (o >> 1); }
 
-__device__ __forceinline__ float half_of(uint32_t w, int hi) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? (w >> 16) : (w & 0xffffu)));
-}
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(DecodeArgs a, int G) {
   constexpr int D = 128;
@@ -746,7 +744,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   qmax = fmaxf(qmax, xor_shfl<16>(qmax));
   qmax = fmaxf(qmax, xor_shfl<32>(qmax));
   const float inv = qmax > 0.f ? 127.f / qmax : 0.f;
-  const float qunit = qmax * (1.f / 127.f) * a.qscale;
+  const float qunit = qmax * (1.f / 127.f) * a.qscale * kInv254;  // per unit of 254 d1 + d2 + d3 / 254
+  float nqsum[NG];
+#pragma unroll
+  for (int c = 0; c < NG; ++c) nqsum[c] = -qsum[c];
   long QA[NG][3];
 #pragma unroll
   for (int c = 0; c < NG; ++c) {
@@ -795,19 +796,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   };
 
   // scales / zeros of this lane's tokens 4 grp .. + 3 of one staged page:
-  // arr[r] = the 4 groups of token 4 grp + r as two dwords of float16 pairs
-  auto staged = [&](int u, int array, uint2 (&arr)[4]) {
+  // arr[r][g] = group g of token 4 grp + r
+  auto staged = [&](int u, int array, v4h (&arr)[4]) {
     const uint4* p = reinterpret_cast<const uint4*>(&sz_lds[wave][u][array * 16 + 4 * grp]);
     const uint4 x = p[0], y = p[1];
-    arr[0] = make_uint2(x.x, x.y);
-    arr[1] = make_uint2(x.z, x.w);
-    arr[2] = make_uint2(y.x, y.y);
-    arr[3] = make_uint2(y.z, y.w);
+    arr[0] = __builtin_bit_cast(v4h, make_uint2(x.x, x.y));
+    arr[1] = __builtin_bit_cast(v4h, make_uint2(x.z, x.w));
+    arr[2] = __builtin_bit_cast(v4h, make_uint2(y.x, y.y));
+    arr[3] = __builtin_bit_cast(v4h, make_uint2(y.z, y.w));
   };
-  auto group_half = [&](const uint2& v, int g) { return half_of(g < 2 ? v.x : v.y, g & 1); };
 
   auto page_scores = [&](const Q4Slot& s, int u, int pi, float* sc) {
-    uint2 ks[4], kz[4];
+    v4h ks[4], kz[4];
     staged(u, 0, ks);
     staged(u, 1, kz);
     float tot[4] = {0.f, 0.f, 0.f, 0.f};
@@ -820,8 +820,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
       c3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kop, QA[c][2], c3, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float dot = qunit * ((float)c1[r] + ((float)c2[r] + (float)c3[r] * kInv254) * kInv254);
-        tot[r] += group_half(ks[r], c) * (dot - group_half(kz[r], c) * qsum[c]);
+        // |254 c1 + c2| <= 255 * 127 * 15 * 32 < 2^24: exact as a float
+        const float d12 = (float)(c1[r] * 254 + c2[r]);
+        const float dot = fmaf((float)c3[r], kInv254, d12) * qunit;
+        tot[r] = fmaf((float)ks[r][c], fmaf((float)kz[r][c], nqsum[c], dot), tot[r]);
       }
     }
 #pragma unroll
@@ -837,10 +839,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   };
 
   auto process_pair = [&](const Q4Slot& s0, const Q4Slot& s1, int pi, bool has1) {
-    // stage both pages' scales / zeros; the wave's LDS operations complete in
-    // order, and the previous pair's reads came before these writes
-    sz_lds[wave][0][lane] = s0.sz;
-    sz_lds[wave][1][lane] = s1.sz;
+    // stage both pages' scales / zeros, zeroed for tokens past the context
+    // and absent pages (whatever they hold), so that their weights and zero
+    // points are exact zeros; the wave's LDS operations complete in order,
+    // and the previous pair's reads came before these writes
+    const bool live0 = s0.ok && pi * kPS + col < tok_end;
+    const bool live1 = has1 && s1.ok && (pi + 1) * kPS + col < tok_end;
+    sz_lds[wave][0][lane] = live0 ? s0.sz : make_uint2(0u, 0u);
+    sz_lds[wave][1][lane] = live1 ? s1.sz : make_uint2(0u, 0u);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -866,7 +872,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
       for (int blk = 0; blk < NB; ++blk) acc[blk] *= alpha;
       m_run = pm;
     }
-    uint2 vs[2][4], vz[2][4];
+    v4h vs[2][4], vz[2][4];
     staged(0, 2, vs[0]);
     staged(0, 3, vz[0]);
     staged(1, 2, vs[1]);
@@ -883,9 +889,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const bool live = sc[e] != -INFINITY;  // scales of dead tokens may hold anything
-        const float w = live ? p[e] * group_half(vs[e >> 2][e & 3], g) : 0.f;
-        corr[g] += live ? w * group_half(vz[e >> 2][e & 3], g) : 0.f;
+        const float w = p[e] * (float)vs[e >> 2][e & 3][g];  // 0 for dead tokens (staged zero scale)
+        corr[g] = fmaf(w, (float)vz[e >> 2][e & 3][g], corr[g]);
         const _Float16 hi = (_Float16)w;
         Bh[g][e] = hi;
         Bl[g][e] = (_Float16)(w - (float)hi);

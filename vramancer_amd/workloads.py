@@ -10,6 +10,10 @@ configurations (inputs only; no model weights are involved).
   mixed-fp8      fp8-e4m3 pool (per-page scale), H=64, KH=8, D=128, 128
                  sequences with lognormal context (median 2048, sigma 1,
                  clipped to [16, 131072]) plus one of 131072, L=1
+  14b-q4         the 14b-int8 shape and K/V over the reference's asymmetric
+                 4-bit pool (nibble codes, per 32-dim group an fp16 scale and
+                 zero point); the reference ships no Q4 writer, so the codes
+                 come from a plain per-group min / max quantizer
   14b-turbo3/4   TurboQuant pages (3 / 4 bits per angle), B=16, context
                  32768, H=40, KH=8, D=128; K/V bf16 from a Student-t (df 3)
                  per channel scaled to unit variance; the compressor's
@@ -39,7 +43,7 @@ class DecodeConfig:
     num_kv_heads: int
     head_dim: int
     num_layers: int
-    codec: str                       # "f32" | "f16" | "bf16" | "int8" | "fp8" | "tq3" | "tq4"
+    codec: str                       # "f32" | "f16" | "bf16" | "int8" | "fp8" | "q4" | "tq3" | "tq4"
     context: str                     # "fixed" | "uniform" | "lognormal"
     ctx_fixed: int = 0
     ctx_low: int = 0
@@ -63,6 +67,8 @@ CONFIGS: Dict[str, DecodeConfig] = {
                             kv_std=0.5, spare_pages=0.10),
     "14b-int8": DecodeConfig("14b-int8", 64, 40, 8, 128, 48, "int8", "fixed", ctx_fixed=4096,
                              outlier_channels=2, outlier_scale=20.0),
+    "14b-q4": DecodeConfig("14b-q4", 64, 40, 8, 128, 48, "q4", "fixed", ctx_fixed=4096,
+                           outlier_channels=2, outlier_scale=20.0),
     "mixed-fp8": DecodeConfig("mixed-fp8", 128, 64, 8, 128, 1, "fp8", "lognormal", ctx_median=2048.0,
                               ctx_sigma=1.0, pinned_long=131072),
     "14b-turbo3": DecodeConfig("14b-turbo3", 16, 40, 8, 128, 1, "tq3", "fixed", ctx_fixed=32768,
@@ -117,6 +123,21 @@ def _pool_dtype(codec: str):
     }[codec]
 
 
+def q4_quantize(x: torch.Tensor):
+    """Codes of the reference's asymmetric 4-bit pool for float rows
+    [..., D]: per 32-dim group scale = (max - min) / 15 and zero = -min / scale
+    (float16), nibble = clamp(round(x / scale + zero), 0, 15), byte j holding
+    dims 2j (low nibble) and 2j + 1 (high).  Returns (codes [..., D/2] uint8,
+    scales [..., D/32] float16, zeros [..., D/32] float16)."""
+    g = x.float().reshape(*x.shape[:-1], -1, 32)
+    lo, hi = g.amin(-1), g.amax(-1)
+    scale = ((hi - lo) / 15).clamp(min=1e-6).to(torch.float16)
+    zero = (-lo / scale.float()).to(torch.float16)
+    n = torch.clamp(torch.round(g / scale.float()[..., None] + zero.float()[..., None]), 0, 15).to(torch.uint8)
+    n = n.reshape(x.shape)
+    return n[..., 0::2] | (n[..., 1::2] << 4), scale, zero
+
+
 def _kv_pages(cfg: DecodeConfig, n: int, gen: torch.Generator, device, outlier_idx) -> torch.Tensor:
     """[n, KH, PS, D] float32 K or V rows of the configured distribution."""
     shape = (n, cfg.num_kv_heads, cfg.page_size, cfg.head_dim)
@@ -163,8 +184,13 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
             torch.randperm(D, generator=g_cpu)[:cfg.outlier_channels] for _ in range(KH)
         ]).to(device)
     kv_scales = None
+    kv_zeros = None
     compressor = None
-    if cfg.codec in ("tq3", "tq4"):
+    if cfg.codec == "q4":
+        kv_pool = torch.zeros((P, L, 2, KH, PS, D // 2), dtype=torch.uint8, device=device)
+        kv_scales = torch.zeros((P, L, 2, KH, PS, D // 32), dtype=torch.float16, device=device)
+        kv_zeros = torch.zeros_like(kv_scales)
+    elif cfg.codec in ("tq3", "tq4"):
         from . import tq_pages
         from .kv_quantizer import KVCacheCompressor
 
@@ -184,7 +210,13 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
             e = min(P, s + chunk_pages)
             k = _kv_pages(cfg, e - s, gen, device, outlier_idx)
             v = _kv_pages(cfg, e - s, gen, device, outlier_idx)
-            if compressor is not None:
+            if cfg.codec == "q4":
+                for kv, x in ((0, k), (1, v)):
+                    codes, sc, zp = q4_quantize(x.to(torch.bfloat16))
+                    kv_pool[s:e, layer, kv] = codes
+                    kv_scales[s:e, layer, kv] = sc
+                    kv_zeros[s:e, layer, kv] = zp
+            elif compressor is not None:
                 tq_pages.quantize_pages(kv_pool, layer, page_ids_all[s:e], k.to(torch.bfloat16),
                                         v.to(torch.bfloat16), compressor)
             elif kv_scales is not None:
@@ -198,6 +230,7 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
         "query": query,
         "kv_pool": kv_pool,
         "kv_scales": kv_scales,
+        "kv_zeros": kv_zeros,
         "page_table": table.to(device),
         "context_lens": torch.tensor(lens, dtype=torch.int32, device=device),
         "layers": list(layers),
@@ -221,6 +254,13 @@ def algorithmic_bytes(cfg: DecodeConfig, lens: Sequence[int]) -> Dict[str, float
         angles = (127 * bits + 7) // 8
         kv = tokens * KH * ((angles + 8 + 2 + 2) + (angles + 2))
         scales = 0
+        qo = 2 * len(lens) * H * D * 4
+        table = pages * 4
+        return {"kv": kv, "scales": scales, "qo": qo, "table": table, "total": kv + scales + qo + table,
+                "tokens": tokens, "pages": pages}
+    if cfg.codec == "q4":
+        kv = tokens * KH * 2 * (D // 2)
+        scales = tokens * KH * 2 * (D // 32) * 2 * 2  # float16 scale and zero per 32-dim group
         qo = 2 * len(lens) * H * D * 4
         table = pages * 4
         return {"kv": kv, "scales": scales, "qo": qo, "table": table, "total": kv + scales + qo + table,
