@@ -452,7 +452,7 @@ __global__ void __launch_bounds__(64) tq_decompress_kernel(TqArgs a, int rotated
 // wavefront per query row m; ws row m holds [q_rot (PD) | q_proj (qjl_dim)].
 template <int PD>
 __global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_dim, const float* signs,
-                                                      const float* jl, int qjl_dim, float* ws) {
+                                                      const float* jl, int qjl_dim, float* ws, int permuted) {
   constexpr int PER = PD / 64;
   __shared__ float rot[PD];
   const int lane = threadIdx.x;
@@ -467,18 +467,21 @@ __global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_d
   fwht<PD>(v, lane);
   const float root = (float)sqrt((double)PD);
   float* out = ws + (size_t)m * (PD + qjl_dim);
+  // feature f at f, or (matrix-core scores) at (f % 4) * F / 4 + f / 4
+  const int F4 = (PD + qjl_dim) / 4;
+  auto at = [&](int f) { return permuted ? (f & 3) * F4 + (f >> 2) : f; };
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     v[k] = __fdiv_rn(v[k], root);
     rot[k * 64 + lane] = v[k];
-    out[k * 64 + lane] = v[k];
+    out[at(k * 64 + lane)] = v[k];
   }
   __syncthreads();
   for (int j = lane; j < qjl_dim; j += 64) {
     const float* row = jl + (size_t)j * PD;
     float acc = 0.f;
     for (int e = 0; e < PD; ++e) acc = __fadd_rn(acc, __fmul_rn(rot[e], row[e]));
-    out[PD + j] = acc;
+    out[at(PD + j)] = acc;
   }
 }
 
@@ -512,6 +515,118 @@ __global__ void __launch_bounds__(64) tq_score_kernel(const float* ws, int M, in
     for (int j = 0; j < qjl_dim; ++j) raw = __fadd_rn(raw, __fmul_rn(qr[PD + j], sgn[j]));
     const float corr = __fmul_rn(__fmul_rn(raw, coef), norm);
     scores[(size_t)m * N + n] = __fmul_rn(__fadd_rn(dot, corr), out_scale);
+  }
+}
+
+
+// Scores on the matrix cores, for the page format (padded_dim 128, qjl_dim
+// 64): scores = out_scale * [k_polar | coef norm (2 s - 1)] . [q_rot | q_proj],
+// a [keys x 192] x [192 x queries] product on v_mfma_f32_16x16x4_f32, 16
+// keys per wavefront against every 16-query tile in turn.  Lane (key, g)
+// holds key features f = 4 j + g (A[key][f] of MFMA step j):
+//   * dims 4 j + g of k_polar: the radii top-down to the level-1 angles (the
+//     reference's products in its order, so each dim is the value polar
+//     decode gives), then the level-1 and level-0 factors of the dim;
+//   * QJL features 4 j + g: (2 s - 1) coef norm.
+// The query kernel writes row m of the workspace feature-permuted (feature f
+// at (f % 4) * 48 + f / 4), so a lane's 48 query features are contiguous.
+// Sums run in the matrix cores' order; the result is float32 all through.
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kMfmaKeys = 16;   // keys per wavefront
+constexpr int kMfmaWaves = 4;   // wavefronts per workgroup
+
+__global__ void __launch_bounds__(64 * kMfmaWaves) tq_score_mfma_kernel(const float* ws, int M, const uint16_t* radius,
+                                                                      const uint8_t* angles, const uint8_t* qjl_signs,
+                                                                      const uint16_t* qjl_norms, int N,
+                                                                      const float* lut, int bits, float coef,
+                                                                      float out_scale, float* scores) {
+  constexpr int PD = 128, QJ = 64, F = PD + QJ, J = F / 4, NP = PD / 4;  // 48 steps, 32 of them polar
+  constexpr int ROWB = PD - 1;  // angle bytes per key
+  __shared__ __align__(16) uint8_t bins_lds[kMfmaWaves][kMfmaKeys * ROWB + 16];
+  __shared__ float lut_lds[64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = lane & 15;
+  const int g = lane >> 4;
+  const int nb = 1 << bits;
+  if (threadIdx.x < 4 * nb) lut_lds[threadIdx.x] = lut[threadIdx.x];
+  __syncthreads();  // the workgroup's only barrier, before any wavefront leaves
+  const int n0 = (blockIdx.x * kMfmaWaves + wave) * kMfmaKeys;
+  if (n0 >= N) return;
+  const int nk = min(kMfmaKeys, N - n0);
+
+  // this wavefront's keys' angle bytes into LDS (n0 * 127 is a multiple of 16)
+  {
+    const int total = nk * ROWB;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(angles + (size_t)n0 * ROWB);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(bins_lds[wave]);
+    for (int i = lane; i < total / 4; i += 64) dst[i] = src[i];
+    if (lane < (total & 3)) bins_lds[wave][(total & ~3) + lane] = angles[(size_t)n0 * ROWB + (total & ~3) + lane];
+  }
+  row_sync();
+
+  const bool valid = row < nk;
+  const int kr = min(row, nk - 1);
+  const int key = n0 + kr;
+  const uint8_t* kb = bins_lds[wave] + kr * ROWB;
+  auto factor = [&](int level, int angle, int sine) {
+    const int b = min((int)kb[PD - (PD >> level) + angle], nb - 1);
+    return lut_lds[(level == 0 ? 0 : 2 * nb) + (sine ? nb : 0) + b];
+  };
+  float A[J];
+  {
+    // radii top-down: after level l the value of node i is r * f_6 * ... * f_l
+    float cur[NP];
+    cur[0] = f16_bits_to_f32(radius[key]);
+#pragma unroll
+    for (int level = 6, cnt = 1; level >= 2; --level, cnt *= 2) {
+#pragma unroll
+      for (int i = cnt - 1; i >= 0; --i) {  // downwards, so cur[i] is read before cur[2 i], cur[2 i + 1] are written
+        const float r = cur[i];
+        cur[2 * i] = __fmul_rn(r, factor(level, i, 0));
+        cur[2 * i + 1] = __fmul_rn(r, factor(level, i, 1));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {  // dim 4 j + g
+      const float r0 = __fmul_rn(cur[j], factor(1, j, g >> 1));
+      A[j] = valid ? __fmul_rn(r0, factor(0, 2 * j + (g >> 1), g & 1)) : 0.f;
+    }
+  }
+  {
+    const float cn = valid ? coef * f16_bits_to_f32(qjl_norms[key]) : 0.f;
+    const uint4* sg = reinterpret_cast<const uint4*>(qjl_signs + (size_t)key * QJ);
+#pragma unroll
+    for (int t = 0; t < QJ / 16; ++t) {
+      const uint4 w = sg[t];  // sign bytes 16 t .. 16 t + 15
+      const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {  // feature 4 (4 t + u) + g: byte g of dword u
+        const float s = (float)((d[u] >> (8 * g)) & 0xffu);
+        A[NP + 4 * t + u] = __fmul_rn(__fsub_rn(__fmul_rn(s, 2.f), 1.f), cn);
+      }
+    }
+  }
+
+  for (int m0 = 0; m0 < M; m0 += 16) {
+    const int m = min(m0 + row, M - 1);
+    const float4* qb = reinterpret_cast<const float4*>(ws + (size_t)m * F + g * J);
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < J / 4; ++t) {
+      const float4 b = qb[t];
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[4 * t], b.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[4 * t + 1], b.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[4 * t + 2], b.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[4 * t + 3], b.w, acc, 0, 0, 0);
+    }
+    // C[key 4 g + r][query row]
+    if (m0 + row < M) {
+      float* out = scores + (size_t)(m0 + row) * N + n0 + 4 * g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (4 * g + r < nk) out[r] = __fmul_rn(acc[r], out_scale);
+    }
   }
 }
 
@@ -853,10 +968,23 @@ extern "C" int vrm_turboquant_score(const float* q, int M, const uint16_t* radiu
   }
   const float coef = (float)(sqrt(M_PI / 2.0) / qjl_dim);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the matrix-core kernel: page format (its angle table holds 4 x 2^bits
+  // <= 64 entries), with its code arrays and the workspace aligned for its 4-
+  // and 16-byte loads
+  const bool mfma = padded_dim == 128 && qjl_dim == 64 && bits <= 4 &&
+                    ((reinterpret_cast<uintptr_t>(angles) & 3) | (reinterpret_cast<uintptr_t>(qjl_signs) & 15) |
+                     (reinterpret_cast<uintptr_t>(workspace) & 15)) == 0;
+  if (mfma) {
+    hipLaunchKernelGGL(tq_query_kernel<128>, dim3(M), dim3(64), 0, st, q, head_dim, signs, jl, qjl_dim, workspace, 1);
+    hipLaunchKernelGGL(tq_score_mfma_kernel, dim3((N + kMfmaWaves * kMfmaKeys - 1) / (kMfmaWaves * kMfmaKeys)),
+                       dim3(64 * kMfmaWaves), 0, st, workspace, M, radius, angles, qjl_signs, qjl_norms, N,
+                       angle_lut, bits, coef, out_scale, scores);
+    return launch_status(who);
+  }
   const size_t lds = ((size_t)M * (padded_dim + qjl_dim + 1) + (size_t)kScoreBatch * qjl_dim) * sizeof(float);
   const bool staged = lds <= (size_t)kScoreMaxLds;
 #define VRM_TQ_SCORE(PDV)                                                                                      \
-  hipLaunchKernelGGL(tq_query_kernel<PDV>, dim3(M), dim3(64), 0, st, q, head_dim, signs, jl, qjl_dim, workspace); \
+  hipLaunchKernelGGL(tq_query_kernel<PDV>, dim3(M), dim3(64), 0, st, q, head_dim, signs, jl, qjl_dim, workspace, 0); \
   if (staged)                                                                                                  \
     hipLaunchKernelGGL(tq_score_lds_kernel<PDV>, dim3((N + kScoreKeys - 1) / kScoreKeys), dim3(64), lds, st,   \
                        workspace, M, qjl_dim, radius, angles, qjl_signs, qjl_norms, N, angle_lut, bits, coef,   \
