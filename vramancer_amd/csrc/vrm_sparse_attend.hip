@@ -26,6 +26,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+// The row kernels (select, compaction) give each row one workgroup of
+// kRowThreads: the passes over a row are chains of dependent steps, and with
+// tens of rows per call the wider workgroup is what keeps the units busy.
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kSelLoads = 8;  // scores per thread per load round of the radix select
 
 // Ascending float order <-> ascending unsigned order.
@@ -34,7 +39,7 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* scores, int N, long long ld, int k,
+__global__ void __launch_bounds__(kRowThreads) topk_select_kernel(const float* scores, int N, long long ld, int k,
                                                                uint32_t* sel) {
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_prefix, s_remaining;
@@ -42,21 +47,21 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* scor
   const float* row = scores + (size_t)blockIdx.x * ld;
   uint32_t prefix = 0, mask = 0, remaining = (uint32_t)k;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;  // kThreads == 256 bins
+    if (tid < 256) hist[tid] = 0;
     __syncthreads();
     // kSelLoads scores per thread are loaded before any histogram update, so
     // the loads of a pass are not serialised behind the LDS atomics.
-    for (int base = 0; base < N; base += kThreads * kSelLoads) {
+    for (int base = 0; base < N; base += kRowThreads * kSelLoads) {
       float x[kSelLoads];
 #pragma unroll
       for (int e = 0; e < kSelLoads; ++e) {
-        const int n = base + e * kThreads + tid;
+        const int n = base + e * kRowThreads + tid;
         x[e] = n < N ? row[n] : 0.f;
       }
 #pragma unroll
       for (int e = 0; e < kSelLoads; ++e) {
         const uint32_t key = order_key(x[e]);
-        if (base + e * kThreads + tid < N && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        if (base + e * kRowThreads + tid < N && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
     }
     __syncthreads();
@@ -81,6 +86,7 @@ __global__ void __launch_bounds__(kThreads) topk_select_kernel(const float* scor
 }
 
 // Exclusive prefix sum over the workgroup; `total` gets the sum.
+template <int W>
 __device__ __forceinline__ int block_exclusive_scan(int v, int& total, int* lds) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int inc = v;
@@ -94,7 +100,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int& total, int* lds)
   int base = 0;
   total = 0;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
+  for (int i = 0; i < W; ++i) {
     const int c = lds[i];
     base += i < w ? c : 0;
     total += c;
@@ -103,31 +109,33 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int& total, int* lds)
   return base + inc - v;
 }
 
+template <int W>
 __device__ __forceinline__ float block_max(float v, float* lds) {
   v = group_max<64>(v);
   if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = lds[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, lds[i]);
+  for (int i = 1; i < W; ++i) r = fmaxf(r, lds[i]);
   __syncthreads();
   return r;
 }
 
+template <int W>
 __device__ __forceinline__ float block_sum(float v, float* lds) {
   v = group_sum<64>(v);
   if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = 0.f;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) r += lds[i];
+  for (int i = 0; i < W; ++i) r += lds[i];
   __syncthreads();
   return r;
 }
 
 // One workgroup per row.  idx_ws / w_ws: [rows][k] scratch (indices, weights).
 // Compaction reads kElems consecutive scores per thread per pass, so one pass
-// (two workgroup scans) covers kThreads * kElems scores in index order.  For
+// (two workgroup scans) covers kRowThreads * kElems scores in index order.  For
 // D <= kMaxFastD the weighted sum is left to topk_pv_kernel (meta gets the
 // row's kept count and weight sum); wider rows are summed here, one thread
 // per value dimension.
@@ -140,12 +148,12 @@ struct RowMeta {
   float l;
 };
 
-__global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scores, int N, long long ld, int k,
+__global__ void __launch_bounds__(kRowThreads) topk_attend_kernel(const float* scores, int N, long long ld, int k,
                                                                const uint32_t* sel, const float* values, int D,
                                                                long long ldv, int32_t* idx_ws, float* w_ws,
                                                                RowMeta* meta, float* out, long long ldo) {
-  __shared__ int scan_lds[kWaves];
-  __shared__ float red_lds[kWaves];
+  __shared__ int scan_lds[kRowWaves];
+  __shared__ float red_lds[kRowWaves];
   const int tid = threadIdx.x;
   const int m = blockIdx.x;
   const float* row = scores + (size_t)m * ld;
@@ -155,7 +163,7 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
   float* wts = w_ws + (size_t)m * k;
   int count = 0, ties_seen = 0;
   float mx = -INFINITY;
-  for (int base = 0; base < N; base += kThreads * kElems) {
+  for (int base = 0; base < N; base += kRowThreads * kElems) {
     const int n0 = base + tid * kElems;
     float s[kElems];
     bool gt[kElems], eq[kElems];
@@ -170,7 +178,7 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
       n_eq += eq[e] ? 1 : 0;
     }
     int eq_total;
-    int eq_rank = block_exclusive_scan(n_eq, eq_total, scan_lds) + ties_seen;
+    int eq_rank = block_exclusive_scan<kRowWaves>(n_eq, eq_total, scan_lds) + ties_seen;
     bool take[kElems];
     int n_take = 0;
 #pragma unroll
@@ -180,7 +188,7 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
       n_take += take[e] ? 1 : 0;
     }
     int take_total;
-    int pos = block_exclusive_scan(n_take, take_total, scan_lds) + count;
+    int pos = block_exclusive_scan<kRowWaves>(n_take, take_total, scan_lds) + count;
 #pragma unroll
     for (int e = 0; e < kElems; ++e) {
       if (take[e]) {
@@ -195,19 +203,19 @@ __global__ void __launch_bounds__(kThreads) topk_attend_kernel(const float* scor
     count += take_total;
   }
   count = min(count, k);
-  mx = block_max(mx, red_lds);
+  mx = block_max<kRowWaves>(mx, red_lds);
   float part = 0.f;
-  for (int i = tid; i < count; i += kThreads) {
+  for (int i = tid; i < count; i += kRowThreads) {
     const float w = expf(row[idx[i]] - mx);
     wts[i] = w;
     part += w;
   }
-  const float l = block_sum(part, red_lds);  // its barriers also publish idx / wts to the workgroup
+  const float l = block_sum<kRowWaves>(part, red_lds);  // its barriers also publish idx / wts to the workgroup
   if (D <= kMaxFastD) {
     if (tid == 0) meta[m] = RowMeta{count, l};
     return;
   }
-  for (int d = tid; d < D; d += kThreads) {
+  for (int d = tid; d < D; d += kRowThreads) {
     float acc = 0.f;
     for (int i = 0; i < count; ++i) acc = fmaf(wts[i], values[(size_t)idx[i] * ldv + d], acc);
     out[(size_t)m * ldo + d] = acc / l;
@@ -341,8 +349,8 @@ extern "C" int vrm_topk_attend(const float* scores, int M, int N, long long ld_s
   RowMeta* meta = reinterpret_cast<RowMeta*>(ws + meta_off);
   float* part = reinterpret_cast<float*>(ws + part_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel);
-  hipLaunchKernelGGL(topk_attend_kernel, dim3(M), dim3(kThreads), 0, st, scores, N, ld_scores, k, sel, values, D,
+  hipLaunchKernelGGL(topk_select_kernel, dim3(M), dim3(kRowThreads), 0, st, scores, N, ld_scores, k, sel);
+  hipLaunchKernelGGL(topk_attend_kernel, dim3(M), dim3(kRowThreads), 0, st, scores, N, ld_scores, k, sel, values, D,
                      ld_values, idx, wts, meta, out, ld_out);
   if (D <= kMaxFastD) {
     hipLaunchKernelGGL(topk_pv_kernel, dim3(M, kSplits), dim3(kThreads), 0, st, idx, wts, meta, k, values, D,
