@@ -305,9 +305,12 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
   constexpr int PD = L::kPD;
   __shared__ RowLds<PD> rows_lds[ROWS];
   __shared__ uint32_t rows_signs[ROWS][L::kQjl / 32];
+  __shared__ float lut_lds[4 << BITS];  // the angle table ({level 0, levels >= 1} x {cos, sin} x 2^BITS)
   const int lane = threadIdx.x & 63;
+  if (threadIdx.x < (4 << BITS)) lut_lds[threadIdx.x] = a.lut[threadIdx.x];
+  __syncthreads();  // the workgroup's only barrier, before any wavefront leaves
   const int x = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
-  if (x >= a.rows) return;  // whole wavefront: no workgroup barrier follows
+  if (x >= a.rows) return;
   RowLds<PD>& w = rows_lds[threadIdx.x >> 6];
   uint32_t* sign_bits = rows_signs[threadIdx.x >> 6];
   const int kv = blockIdx.y;
@@ -368,7 +371,7 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
   if (kv == 1) return;
   if (lane < L::kQjl / 32) sign_bits[lane] = 0;
   row_sync();
-  const float norm = qjl_row<PD>(v, radius, a.lut, BITS, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
+  const float norm = qjl_row<PD>(v, radius, lut_lds, BITS, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
     if (pos) atomicOr(&sign_bits[j >> 5], 1u << (j & 31));
   });
   row_sync();
@@ -417,21 +420,30 @@ __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, c
   if (lane == 0) norms[row] = kv == 0 ? reinterpret_cast<const uint16_t*>(slice + L::norms_offset(bits))[t] : 0;
 }
 
-template <int PD>
-__global__ void __launch_bounds__(64) tq_decompress_kernel(TqArgs a, int rotated) {
+template <int PD, int ROWS>
+__global__ void __launch_bounds__(64 * ROWS) tq_decompress_kernel(TqArgs a, int rotated) {
   constexpr int PER = PD / 64;
-  __shared__ float recon[PD];
-  __shared__ uint8_t bins[PD];
-  const int lane = threadIdx.x;
-  const int row = blockIdx.x;
+  __shared__ uint8_t bins_rows[ROWS][PD];
+  __shared__ float lut_lds[64];  // the angle table for up to 4 bits (4 x 16 entries)
+  const int lane = threadIdx.x & 63;
   const int nb = 1 << a.bits;
+  const bool lut_in_lds = nb <= 16;
+  if (lut_in_lds && threadIdx.x < 4 * nb) lut_lds[threadIdx.x] = a.lut[threadIdx.x];
+  __syncthreads();  // the workgroup's only barrier, before any wavefront leaves
+  const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
+  if (row >= a.N) return;
+  uint8_t* bins = bins_rows[threadIdx.x >> 6];
   for (int i = lane; i < PD - 1; i += 64) bins[i] = a.angles[(size_t)row * (PD - 1) + i];
   const float radius = f16_bits_to_f32(a.radius[row]);
-  __syncthreads();
-  polar_decode<PD>(radius, bins, a.lut, nb, recon, lane);
+  row_sync();
   float v[PER];
+  if (lut_in_lds) {  // two copies of the loop, each with the table's address space known
 #pragma unroll
-  for (int k = 0; k < PER; ++k) v[k] = recon[k * 64 + lane];
+    for (int k = 0; k < PER; ++k) v[k] = polar_element<PD>(radius, bins, lut_lds, nb, k * 64 + lane);
+  } else {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = polar_element<PD>(radius, bins, a.lut, nb, k * 64 + lane);
+  }
   if (rotated) {
 #pragma unroll
     for (int k = 0; k < PER; ++k) a.out[(size_t)row * PD + k * 64 + lane] = v[k];
@@ -799,11 +811,19 @@ extern "C" int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* 
   a.angles = const_cast<uint8_t*>(angles);
   a.out = out;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool bulk = N >= kBulkMinRows;
+#define VRM_TQ_DECOMP(PDV)                                                                                   \
+  if (bulk)                                                                                                  \
+    hipLaunchKernelGGL((tq_decompress_kernel<PDV, kBulkRows>), dim3((N + kBulkRows - 1) / kBulkRows),        \
+                       dim3(64 * kBulkRows), 0, st, a, rotated);                                             \
+  else                                                                                                       \
+    hipLaunchKernelGGL((tq_decompress_kernel<PDV, 1>), dim3(N), dim3(64), 0, st, a, rotated)
   switch (padded_dim) {
-    case 64: hipLaunchKernelGGL(tq_decompress_kernel<64>, dim3(N), dim3(64), 0, st, a, rotated); break;
-    case 128: hipLaunchKernelGGL(tq_decompress_kernel<128>, dim3(N), dim3(64), 0, st, a, rotated); break;
-    default: hipLaunchKernelGGL(tq_decompress_kernel<256>, dim3(N), dim3(64), 0, st, a, rotated); break;
+    case 64: VRM_TQ_DECOMP(64); break;
+    case 128: VRM_TQ_DECOMP(128); break;
+    default: VRM_TQ_DECOMP(256); break;
   }
+#undef VRM_TQ_DECOMP
   return launch_status(who);
 }
 
