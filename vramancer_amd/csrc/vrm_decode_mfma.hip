@@ -82,22 +82,15 @@ __device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& 
   hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, bhi) - bias);
 }
 
-// Eight e4m3fn codes (two dwords) -> eight fp16 values (exact).
+// Eight e4m3fn codes (two dwords) -> eight fp16 values (exact: every e4m3fn
+// value, NaN included, is an fp16 value, and the scale is 1), two codes per
+// v_cvt_scalef32_pk_f16_fp8.
 __device__ __forceinline__ v8h fp8x8_to_f16(uint32_t w0, uint32_t w1) {
-  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, false);
-  const auto b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, true);
-  const auto c = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, false);
-  const auto d = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, true);
-  v8h r;
-  r[0] = (_Float16)a[0];
-  r[1] = (_Float16)a[1];
-  r[2] = (_Float16)b[0];
-  r[3] = (_Float16)b[1];
-  r[4] = (_Float16)c[0];
-  r[5] = (_Float16)c[1];
-  r[6] = (_Float16)d[0];
-  r[7] = (_Float16)d[1];
-  return r;
+  const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, false);  // bytes 0, 1
+  const v2h b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w0, 1.0f, true);   // bytes 2, 3
+  const v2h c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w1, 1.0f, false);
+  const v2h d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w1, 1.0f, true);
+  return v8h{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 __device__ __forceinline__ v8h dwords_to_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
