@@ -12,25 +12,43 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// One thread per packed byte; global byte x = row * nbytes + j.
+// Row and column of flat element x of a [rows][width] array; 32-bit division
+// when the whole array indexes in 31 bits (the caller's uniform choice).
+__device__ __forceinline__ void split_index(long long x, int width, bool narrow, long long& row, int& col) {
+  if (narrow) {
+    const uint32_t r = (uint32_t)x / (uint32_t)width;
+    row = r;
+    col = (int)((uint32_t)x - r * (uint32_t)width);
+  } else {
+    row = x / width;
+    col = (int)(x - row * width);
+  }
+}
+
+// One thread per packed byte; global byte x = row * nbytes + j.  The byte's
+// 8 bits walk the stream from bit 8 j: one division finds the first value,
+// then the position inside the value advances bit by bit.
 __global__ void __launch_bounds__(kThreads) pack_kernel(const uint8_t* vals, long long rows, int M, int bits,
                                                         int nbytes, uint8_t* out) {
   const long long x = (long long)blockIdx.x * kThreads + threadIdx.x;
-  if (x >= rows * nbytes) return;
-  const long long row = x / nbytes;
-  const int j = (int)(x - row * nbytes);
+  const long long n = rows * nbytes;
+  if (x >= n) return;
+  long long row;
+  int j;
+  split_index(x, nbytes, n <= 0x7fffffffLL, row, j);
   const uint8_t* v = vals + row * M;
   const int total = M * bits;
+  int pos = 8 * j;  // bit position in the row's stream
+  int i = pos / bits;
+  int from_msb = pos - i * bits;
   uint32_t byte = 0;
-  for (int k = 0; k < 8; ++k) {
-    const int pos = 8 * j + k;  // bit position in the row's stream
-    uint32_t bit = 0;
-    if (pos < total) {
-      const int i = pos / bits;
-      const int from_msb = pos - i * bits;
-      bit = (v[i] >> (bits - 1 - from_msb)) & 1u;
-    }
+  for (int k = 0; k < 8; ++k, ++pos) {
+    const uint32_t bit = pos < total ? (v[i] >> (bits - 1 - from_msb)) & 1u : 0u;
     byte |= bit << (7 - k);
+    if (++from_msb == bits) {
+      from_msb = 0;
+      ++i;
+    }
   }
   out[x] = (uint8_t)byte;
 }
@@ -39,9 +57,11 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const uint8_t* vals, lon
 __global__ void __launch_bounds__(kThreads) unpack_kernel(const uint8_t* packed, long long rows, int M, int bits,
                                                           int nbytes, uint8_t* vals) {
   const long long x = (long long)blockIdx.x * kThreads + threadIdx.x;
-  if (x >= rows * M) return;
-  const long long row = x / M;
-  const int i = (int)(x - row * M);
+  const long long n = rows * M;
+  if (x >= n) return;
+  long long row;
+  int i;
+  split_index(x, M, n <= 0x7fffffffLL, row, i);
   const uint8_t* p = packed + row * nbytes;
   uint32_t v = 0;
   for (int b = 0; b < bits; ++b) {
