@@ -261,18 +261,25 @@ __device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius
 constexpr int kBulkRows = 4;
 constexpr int kBulkMinRows = 4096;
 
-template <int SRC, int PD, int ROWS>
+// LUT_LDS: the angle table (4 x 2^bits floats, bits <= 4) is read from LDS.
+template <int SRC, int PD, int ROWS, bool LUT_LDS>
 __global__ void __launch_bounds__(64 * ROWS) tq_compress_kernel(TqArgs a) {
   __shared__ RowLds<PD> rows_lds[ROWS];
+  __shared__ float lut_lds[LUT_LDS ? 64 : 1];
   const int lane = threadIdx.x & 63;
+  if constexpr (LUT_LDS) {
+    if (threadIdx.x < (4 << a.bits)) lut_lds[threadIdx.x] = a.lut[threadIdx.x];
+    __syncthreads();  // the workgroup's only barrier, before any wavefront leaves
+  }
   const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
-  if (row >= a.N) return;  // whole wavefront: no workgroup barrier follows
+  if (row >= a.N) return;
   RowLds<PD>& w = rows_lds[threadIdx.x >> 6];
   float v[PD / 64];
   const float radius = encode_row<SRC, PD>(a.kv, (size_t)row * a.head_dim, a.head_dim, a.signs, a.bits, v, w, lane);
   for (int i = lane; i < PD - 1; i += 64) a.angles[(size_t)row * (PD - 1) + i] = w.bins[i];
   if (lane == 0) a.radius[row] = f32_to_f16_bits(radius);
-  const float norm = qjl_row<PD>(v, radius, a.lut, a.bits, a.jl, a.qjl_dim, w, lane, [&](int j, bool pos) {
+  const float* lut = LUT_LDS ? lut_lds : a.lut;
+  const float norm = qjl_row<PD>(v, radius, lut, a.bits, a.jl, a.qjl_dim, w, lane, [&](int j, bool pos) {
     a.qjl_signs[(size_t)row * a.qjl_dim + j] = pos ? 1 : 0;
   });
   if (lane == 0) a.qjl_norms[row] = f32_to_f16_bits(norm);
@@ -768,12 +775,16 @@ extern "C" int vrm_turboquant_compress(const void* kv, int src_dtype, int N, int
   a.qjl_norms = qjl_norms;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool bulk = N >= kBulkMinRows;
+  const bool lut_lds = bits <= 4;
 #define VRM_TQ_LAUNCH(SRC, PDV)                                                                                     \
-  if (bulk)                                                                                                         \
-    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, kBulkRows>), dim3((N + kBulkRows - 1) / kBulkRows),            \
+  if (bulk && lut_lds)                                                                                              \
+    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, kBulkRows, true>), dim3((N + kBulkRows - 1) / kBulkRows),      \
+                       dim3(64 * kBulkRows), 0, st, a);                                                             \
+  else if (bulk)                                                                                                    \
+    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, kBulkRows, false>), dim3((N + kBulkRows - 1) / kBulkRows),     \
                        dim3(64 * kBulkRows), 0, st, a);                                                             \
   else                                                                                                              \
-    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, 1>), dim3(N), dim3(64), 0, st, a)
+    hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, 1, false>), dim3(N), dim3(64), 0, st, a)
 #define VRM_TQ_PD(SRC)                                  \
   switch (padded_dim) {                                 \
     case 64: VRM_TQ_LAUNCH(SRC, 64); break;             \
