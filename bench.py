@@ -480,8 +480,8 @@ def main():
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(sharding of the decode is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: the decode here has no multi-GPU path "
+              "(it would shard by sequence or by kv-head, with no exchange); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

@@ -1,7 +1,7 @@
 """Writes golden vectors of the reference's TurboQuant CPU codec.
 
-Run from the repository root in a container that holds the reference at
-/root/reference (never on the GPU box):
+Run from the repository root on a machine that holds the reference at
+/root/reference (the tests only read the fixtures it writes):
 
     python tests/golden/make_golden.py
 
