@@ -233,6 +233,65 @@ def test_decode_full_size_int8_sampled_parity_and_relabel_invariance():
     assert torch.equal(out, out2)
 
 
+def test_decode_full_size_q4_sampled_parity_and_relabel_invariance():
+    """The 14B shape over the 4-bit pool at full size (B=64, context 4096,
+    16384 pages): sampled sequences match the oracle, and relabelling the
+    physical pages leaves the output bit-identical."""
+    cfg = workloads.scaled(workloads.CONFIGS["14b-q4"], num_layers=2)
+    _say("14b-q4 full size, L=2")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=23, layers=(1,))
+    q, pool, sc, zp = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["kv_zeros"]
+    table, lens = inp["page_table"], inp["context_lens"]
+    out = paged_attention_decode_q4(q, pool, sc, zp, table, lens, 1)
+    torch.cuda.synchronize()
+    for b in (0, 29, 63):
+        pages = table[b].long()
+        sub_table = torch.arange(pages.numel(), dtype=torch.int32)[None]
+        ref = PD.paged_attention_decode_q4(q[b:b + 1].cpu(), pool[pages].cpu(), sc[pages].cpu(), zp[pages].cpu(),
+                                           sub_table, lens[b:b + 1].cpu(), 1)
+        _assert_close(out[b:b + 1], ref, f"q4 full-size seq {b}")
+    P = pool.shape[0]
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(4)).to(DEV)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(P, device=DEV)
+    out2 = paged_attention_decode_q4(q, pool[perm], sc[perm], zp[perm], inv[table.long()].to(torch.int32), lens, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_decode_q4_ignores_garbage_past_context():
+    """Scales and zeros of slots past the context, and of a page the table
+    marks absent, may hold anything (here NaN and inf); the output must equal
+    the oracle's, which never reads them."""
+    _say("q4 garbage past context")
+    g = torch.Generator().manual_seed(41)
+    B, H, KH, D, PS, L = 3, 40, 8, 128, 16, 1
+    ctxs = [37, 160, 5]
+    npages = [(c + PS - 1) // PS for c in ctxs]
+    P = sum(npages) + 1
+    packed = torch.randint(0, 256, (P, L, 2, KH, PS, D // 2), generator=g, dtype=torch.uint8)
+    sc = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 0.1 + 0.01).half()
+    zp = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 15).half()
+    table = torch.full((B, max(npages)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = torch.arange(off, off + n, dtype=torch.int32)
+        off += n
+    for b, c in enumerate(ctxs):
+        last = int(table[b, (c - 1) // PS])
+        sc[last, 0, :, :, c % PS or PS:] = float("nan")
+        zp[last, 0, :, :, c % PS or PS:] = float("inf")
+    sc[P - 1] = float("nan")  # a page the table never references
+    table[1, 3] = -1  # an absent page in the middle of sequence 1
+    q = torch.randn(B, H, D, generator=g)
+    lens = torch.tensor(ctxs, dtype=torch.int32)
+    out = paged_attention_decode_q4(q.to(DEV), packed.to(DEV), sc.to(DEV), zp.to(DEV), table.to(DEV), lens.to(DEV), 0)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = PD.paged_attention_decode_q4(q, packed, sc, zp, table, lens, 0)
+    _assert_close(out.cpu(), ref, "q4 garbage")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_decode_float_pool_ignores_garbage_past_context(dtype):
     """Slots past the context in the last page, and pages the table marks
