@@ -292,6 +292,37 @@ def test_decode_q4_ignores_garbage_past_context():
     _assert_close(out.cpu(), ref, "q4 garbage")
 
 
+def test_decode_q4_unaligned_scales_take_the_valu_kernel():
+    """Scales and zeros that start 2 bytes off an 8-byte boundary (views into
+    larger buffers) are decoded by the VALU kernel, to the same bar."""
+    _say("q4 unaligned scales")
+    g = torch.Generator().manual_seed(43)
+    B, H, KH, D, PS, L = 2, 40, 8, 128, 16, 1
+    ctxs = [70, 300]
+    npages = [(c + PS - 1) // PS for c in ctxs]
+    P = sum(npages)
+    packed = torch.randint(0, 256, (P, L, 2, KH, PS, D // 2), generator=g, dtype=torch.uint8)
+    sc = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 0.1 + 0.01).half()
+    zp = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 15).half()
+    table = torch.full((B, max(npages)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = torch.arange(off, off + n, dtype=torch.int32)
+        off += n
+    q = torch.randn(B, H, D, generator=g)
+    lens = torch.tensor(ctxs, dtype=torch.int32)
+
+    def shifted(t):  # the same values, one float16 past an aligned start
+        buf = torch.zeros(t.numel() + 1, dtype=t.dtype, device=DEV)
+        buf[1:] = t.reshape(-1).to(DEV)
+        return buf[1:].view(t.shape)
+
+    out = paged_attention_decode_q4(q.to(DEV), packed.to(DEV), shifted(sc), shifted(zp), table.to(DEV),
+                                    lens.to(DEV), 0)
+    torch.cuda.synchronize()
+    _assert_close(out.cpu(), PD.paged_attention_decode_q4(q, packed, sc, zp, table, lens, 0), "q4 unaligned")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_decode_float_pool_ignores_garbage_past_context(dtype):
     """Slots past the context in the last page, and pages the table marks

@@ -50,6 +50,31 @@ def test_native_score_matches_oracle(head_dim, bits, qjl, M, N):
     assert (err <= 1e-4 * (1 + (0.5 * want).abs())).all(), f"max err {err.max():.3e}"
 
 
+def test_native_score_unaligned_codes_take_the_serial_kernel():
+    """Angle bytes and sign bytes that start off their 4- / 16-byte alignment
+    (views into a larger buffer) are scored by the serial-order kernels, to
+    the same bar."""
+    _say("score unaligned codes")
+    p = TQ.make_params(128, 3, seed=5)
+    g = torch.Generator().manual_seed(6)
+    keys = torch.randn(300, 128, generator=g)
+    q = torch.randn(7, 128, generator=g)
+    ck = TQ.compress(p, keys, pack=False)
+    want = TQ.attention_score(p, q, ck)
+    ang = torch.cat(ck["angles"], -1)
+    buf = torch.zeros(ang.numel() + 1, dtype=torch.uint8, device=DEV)
+    buf[1:] = ang.reshape(-1).to(DEV)
+    ang_off = buf[1:].view(300, 127)  # one byte past an aligned start
+    sbuf = torch.zeros(ck["qjl_signs"].numel() + 4, dtype=torch.uint8, device=DEV)
+    sbuf[4:] = ck["qjl_signs"].reshape(-1).to(DEV)
+    gk = {"radius": ck["radius"].to(DEV), "angles": [ang_off], "qjl_signs": sbuf[4:].view(300, 64),
+          "qjl_norms": ck["qjl_norms"].to(DEV)}
+    got = CUDATurboQuantOps.attention_score_gpu(q.to(DEV), gk, 128, 128, 7, 3, p.signs.to(DEV), p.jl_matrix.to(DEV),
+                                                64).cpu()
+    err = (got - want).abs()
+    assert (err <= 1e-4 * (1 + want.abs())).all(), f"max err {err.max():.3e}"
+
+
 def _topk_reference(s, k, v):
     """float64: the k largest of each row (lowest index first among ties)."""
     out = torch.zeros(s.shape[0], v.shape[1], dtype=torch.float64)
