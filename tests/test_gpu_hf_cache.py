@@ -90,7 +90,9 @@ def test_turboquant_cache_decode_attention_matches_materialised(setting):
     cache = TurboQuantCache(2, 128, bits_per_angle=3, residual_length=32, device=DEV, paged_attention=True)
     layer = cache.layers[0]
     g = torch.Generator().manual_seed(4)
-    for s in (40, 1, 1, 30, 1):  # prompt, then steps that spill and refill the residual
+    # prompt, then steps that spill and refill the residual; the 60-token update grows the
+    # residual pool while it holds a token (copy, new page / slot table), the next one spills it
+    for s in (40, 1, 1, 30, 1, 60, 1):
         k = torch.randn(2, 2, s, 128, generator=g).to(DEV)
         layer.update(k, torch.randn(2, 2, s, 128, generator=g).to(DEV))
         q = torch.randn(2, 4, 1, 128, generator=g).to(DEV)
