@@ -6,7 +6,13 @@
   codes reconstruct every input within half a quantisation step.
 * Algorithmic bytes of the Q4 workload count 64 B of codes and 16 B of
   scales and zeros per token, kv-head and K/V side.
+* bench.py refuses more than one GPU with a message and exit status 2, and
+  lists its workloads and modes in --help.
 """
+import os
+import subprocess
+import sys
+
 import torch
 
 from oracle import paged_decode as PD
@@ -42,3 +48,22 @@ def test_q4_algorithmic_bytes():
     assert ab["kv"] == tokens * 8 * 2 * 64
     assert ab["scales"] == tokens * 8 * 2 * 4 * 2 * 2
     assert ab["total"] == ab["kv"] + ab["scales"] + ab["qo"] + ab["table"]
+
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300, cwd=ROOT)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout == ""
+
+
+def test_bench_help_lists_workloads_and_modes():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--help"], capture_output=True, text=True,
+                       timeout=300, cwd=ROOT)
+    assert r.returncode == 0
+    for word in ("14b-q4", "14b-turbo3", "mixed-fp8", "--batcher", "--codecs", "--hf-cache"):
+        assert word in r.stdout, word
