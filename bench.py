@@ -72,6 +72,18 @@ def time_events(fn, steps):
     return start.elapsed_time(end) * 1e3 / steps  # microseconds per call
 
 
+def host_us(fn, n):
+    """Host microseconds per call to enqueue fn n times (no synchronisation
+    inside the loop), the Python and ctypes cost a decode loop pays per layer."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(n):
+        fn(i)
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) * 1e6 / n
+
+
 def cpu_baseline(inp, layer, n_seq, reps):
     """The reference's PyTorch decode path (restated in oracle/) on the host
     cores, over the first n_seq sequences of the same workload.  Returns
@@ -573,6 +585,34 @@ def main():
     us_part = us_step if (turbo or q4) else time_events(partitions, args.steps)
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
+    # The drop-in Python call: the same decode through the module API, with the
+    # wrapper allocating out + workspace per call, and with both preallocated.
+    from vramancer_amd.paged_attention_cuda import paged_attention_decode, paged_attention_decode_q4
+
+    def api(i, prealloc):
+        layer = layers[i % len(layers)]
+        kw = dict(out=out, workspace=ws) if prealloc else {}
+        if turbo:
+            tq_pages.paged_attention_decode_turbo(q, pool, table, lens, layer, comp, **kw)
+        elif q4:
+            paged_attention_decode_q4(q, pool, sc, zp, table, lens, layer, **kw)
+        else:
+            paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc, **kw)
+
+    for i in range(5):
+        api(i, False)
+        api(i, True)
+    n_host = 50
+    python_api = {
+        "host_us_per_call": {
+            "c_abi": round(host_us(full, n_host), 2),
+            "python": round(host_us(lambda i: api(i, False), n_host), 2),
+            "python_preallocated": round(host_us(lambda i: api(i, True), n_host), 2),
+        },
+        "us_per_layer_step_python_preallocated": round(time_events(lambda i: api(i, True), args.steps), 3),
+    }
+    log(f"python API: {python_api}")
+
     us_append = None
     if turbo:
         kn = torch.randn((B, KH, D), device=dev).to(torch.bfloat16)
@@ -691,6 +731,7 @@ def main():
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,
+        "python_api": python_api,
     }
     print(json.dumps(result), flush=True)
 

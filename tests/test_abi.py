@@ -173,3 +173,35 @@ def test_python_api_refuses_cpu_tensors():
     pool = torch.randn(2, 1, 2, 4, 16, 64)
     with pytest.raises(RuntimeError, match="GPU"):
         paged_attention_decode(q, pool, torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32), 0)
+
+
+def test_decode_wrappers_validate_out_workspace_and_table():
+    """The Python wrappers check the tensors the kernels write or index
+    through before any pointer reaches the library: out is a contiguous
+    float32 [B, H, D] on the query's device, the workspace is contiguous on
+    that device, the page table is [B, max_pages] and context_lens [B]."""
+    import torch
+    from vramancer_amd.paged_attention_cuda import check_outputs
+
+    q = torch.randn(2, 8, 64)
+    pt = torch.zeros(2, 3, dtype=torch.int32)
+    cl = torch.ones(2, dtype=torch.int32)
+    check_outputs(q, torch.empty(2, 8, 64), torch.empty(100, dtype=torch.uint8), pt, cl)
+    check_outputs(q, None, None, pt, cl)
+    bad = [
+        dict(out=torch.empty(2, 8, 64, dtype=torch.float16)),
+        dict(out=torch.empty(2, 8, 32)),
+        dict(out=torch.empty(2, 64, 8).transpose(1, 2)),
+        dict(out=torch.empty(2, 8, 64, device="meta")),
+        dict(workspace=torch.empty(64, dtype=torch.uint8)[::2]),
+        dict(workspace=torch.empty(64, dtype=torch.uint8, device="meta")),
+        dict(page_table=torch.zeros(1, 3, dtype=torch.int32)),
+        dict(page_table=torch.zeros(2, dtype=torch.int32)),
+        dict(page_table=torch.zeros(2, 0, dtype=torch.int32)),
+        dict(context_lens=torch.ones(3, dtype=torch.int32)),
+    ]
+    for kw in bad:
+        a = dict(out=None, workspace=None, page_table=pt, context_lens=cl)
+        a.update(kw)
+        with pytest.raises(RuntimeError):
+            check_outputs(q, a["out"], a["workspace"], a["page_table"], a["context_lens"])

@@ -60,12 +60,14 @@ def test_decode_matches_oracle_on_benchmark_shapes(name, kw):
     _assert_close(out, _oracle(inp, layer), name)
 
 
-def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pad=1):
+def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pad=1, v_mag=None):
     g = torch.Generator().manual_seed(seed)
     PS = 16
     npages = [(max(c, 0) + PS - 1) // PS for c in ctxs]
     P = sum(npages) + spare
     base = torch.randn(P, L, 2, KH, PS, D, generator=g)
+    if v_mag is not None:  # V magnitude: a number, or one factor per page [P]
+        base[:, :, 1] *= torch.as_tensor(v_mag, dtype=torch.float32).reshape(-1, 1, 1, 1, 1)
     scales = None
     if dtype == torch.int8:
         from oracle.kv_codecs import pool_from_logical, quantize_int8
@@ -382,3 +384,128 @@ def test_decode_full_size_fp8_sampled_parity():
         ref = PD.paged_attention_decode(q[b:b + 1].cpu(), pool[pages].cpu(), torch.arange(n, dtype=torch.int32)[None],
                                         lens[b:b + 1].cpu(), 0, kv_scales=sc[pages].cpu())
         _assert_close(out[b:b + 1], ref, f"fp8 seq {b} ctx {int(lens[b])}")
+
+
+def _dequant_pool(pool, sc, layer):
+    """Float32 copy of one layer of a quantized pool (V token-major), garbage included."""
+    f = torch.zeros(pool.shape, dtype=torch.float32)
+    ids = torch.arange(pool.shape[0])
+    for kv in (0, 1):
+        f[:, layer, kv] = PD._dequant_pages(pool, sc, ids, layer, kv)
+    return f
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+def test_decode_quantized_pool_ignores_garbage_past_context(dtype):
+    """Codes and scales of slots past the context, of a page the table marks
+    absent and of a page it never references may hold anything: NaN and inf
+    scales, and for fp8 the NaN code 0x7f (0x7f is int8's largest code).  The
+    output must equal the oracle's, which never reads them."""
+    from oracle.kv_codecs import pool_from_logical, pool_to_logical
+
+    _say(f"garbage past context {dtype}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, 128, [37, 160, 5], seed=31)
+    raw = pool_to_logical(pool.view(torch.uint8))
+    for b, c in enumerate(lens.tolist()):
+        last = int(table[b, (c - 1) // 16])
+        raw[last, 1, :, :, c % 16 or 16:, :] = 0x7F
+        if dtype == torch.int8:
+            sc[last, 1, 0, :, c % 16 or 16:] = float("inf")
+            sc[last, 1, 1, :, c % 16 or 16:] = float("nan")
+    spare = sorted(set(range(pool.shape[0])) - set(table[table >= 0].tolist()))[0]
+    raw[spare, 1] = 0x7F
+    sc[spare, 1] = float("nan")
+    table[1, 3] = -1  # an absent page in the middle of sequence 1
+    pool = pool_from_logical(raw).view(dtype)
+    out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), 1, kv_scales=sc.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    f = _dequant_pool(pool, sc, 1)
+    for b in range(3):
+        K, V = PD.gather_sequence(f, table[b], int(lens[b]), 1, skip_invalid=True)
+        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(128))
+        _assert_close(out[b].cpu(), ref, f"{dtype} seq {b}")
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+@pytest.mark.parametrize("v_mag", [1e-4, 1e5, 1e7, "per-page"])
+def test_decode_quantized_v_scale_independence(dtype, v_mag):
+    """V drawn at magnitudes from 1e-4 to 1e7 (and, "per-page", with each page
+    scaled by its own factor 10^u, u ~ U[-4, 4], so the V scales of one
+    partition span eight decades): the output keeps the relative precision
+    of V's codes.  Bar: |gpu - oracle| <= 1e-3 * max|oracle| over each
+    sequence's outputs, the oracle evaluated on the same codes and scales."""
+    ctxs = [37, 1600, 333]
+    if v_mag == "per-page":
+        g = torch.Generator().manual_seed(77)
+        n = sum((c + 15) // 16 for c in ctxs) + 3
+        v_mag = torch.pow(10.0, torch.rand(n, generator=g) * 8 - 4)
+    _say(f"V magnitude {dtype} {v_mag if not torch.is_tensor(v_mag) else 'per-page'}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 40, 8, 128, ctxs, seed=52, v_mag=v_mag)
+    out, ref = _run_both(q, pool, sc, table, lens, 1)
+    assert torch.isfinite(out).all()
+    for b in range(3):
+        err = (out[b] - ref[b]).abs().max().item()
+        bar = 1e-3 * ref[b].abs().max().item()
+        assert err <= bar, f"seq {b}: max abs err {err:.3e} > {bar:.3e}"
+
+
+def test_decode_full_size_int8_48_layer_bench_pool():
+    """The 14B int8 pool exactly as the benchmark times it: 48 layers of
+    16384 pages (29 GB of codes and scales, page stride 1.5 MB, offsets far
+    past 4 GiB), layers 0 / 12 / 24 / 36 filled.  Three sequences of each
+    filled layer match the oracle on their own pages, and relabelling the
+    physical pages of the whole pool leaves layer 36's output bit-identical."""
+    cfg = workloads.CONFIGS["14b-int8"]
+    layers = (0, 12, 24, 36)
+    _say("14b-int8 full 48-layer pool")
+    inp = workloads.make_decode_inputs(cfg, DEV, seed=0, layers=layers)
+    q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
+    assert pool.shape[:2] == (16384, 48)
+    for layer in layers:
+        out = paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc)
+        torch.cuda.synchronize()
+        for b in (1, 30, 62):
+            pages = table[b].long()
+            sub_pool = pool[pages, layer:layer + 1].cpu()
+            sub_sc = sc[pages, layer:layer + 1].cpu()
+            sub_table = torch.arange(pages.numel(), dtype=torch.int32)[None]
+            ref = PD.paged_attention_decode(q[b:b + 1].cpu(), sub_pool, sub_table, lens[b:b + 1].cpu(), 0,
+                                            kv_scales=sub_sc)
+            _assert_close(out[b:b + 1], ref, f"48-layer pool, layer {layer}, seq {b}")
+    P = pool.shape[0]
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(5)).to(DEV)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(P, device=DEV)
+    table2 = inv[table.long()].to(torch.int32)
+    pool2 = pool[perm]
+    sc2 = sc[perm]
+    del inp
+    out2 = paged_attention_decode(q, pool2, table2, lens, 36, kv_scales=sc2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_wrappers_reject_bad_out_workspace_and_tables():
+    """A wrong out (dtype, shape, device), a host workspace, or a page table /
+    context-length array of the wrong batch is refused before any launch."""
+    _say("wrapper argument checks")
+    q, pool, sc, table, lens = (t.to(DEV) for t in _pool_case(torch.int8, 2, 8, 2, 128, [40, 20], seed=1))
+    run = lambda **kw: paged_attention_decode(q, pool, kw.get("table", table), kw.get("lens", lens), 1,  # noqa: E731
+                                              kv_scales=sc, out=kw.get("out"), workspace=kw.get("ws"))
+    ref = run()
+    for kw in (dict(out=torch.empty(2, 8, 128, dtype=torch.float16, device=DEV)),
+               dict(out=torch.empty(2, 8, 64, device=DEV)),
+               dict(out=torch.empty(2, 8, 128)),
+               dict(ws=torch.empty(1 << 24, dtype=torch.uint8)),
+               dict(table=table[:1]),
+               dict(lens=lens[:1])):
+        with pytest.raises(RuntimeError):
+            run(**kw)
+    torch.testing.assert_close(run(out=torch.empty(2, 8, 128, device=DEV)), ref, rtol=0, atol=0)
+    packed = torch.zeros(pool.shape[:-1] + (64,), dtype=torch.uint8, device=DEV)
+    s4 = torch.ones(pool.shape[:-1] + (4,), dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        paged_attention_decode_q4(q, packed, s4, s4, table[:1], lens, 1)
+    with pytest.raises(RuntimeError):
+        paged_attention_decode_q4(q, packed, s4, s4, table, lens, 1, out=torch.empty(2, 8, 128, device=DEV)[:, :4])

@@ -166,6 +166,17 @@ def test_compressor_api_roundtrip_and_batch():
     assert torch.equal(torch.cat(refs[1]["angles"], -1), torch.cat(comp.compress(v, pack=False)["angles"], -1))
     single = comp.compress_batch([v])
     assert "angles_packed" in single[0]  # the reference's single-item quirk
+    # packed batch items equal the packed dicts of separate calls, field by field
+    for item, x in zip(comp.compress_batch([k, v, k[:1]], pack=True), (k, v, k[:1])):
+        alone = comp.compress(x)
+        assert item.keys() == alone.keys()
+        for key, val in alone.items():
+            if torch.is_tensor(val):
+                assert torch.equal(item[key], val), key
+            else:
+                assert item[key] == val, key
+        assert torch.equal(comp.decompress(item), comp.decompress(alone))
+    assert [r["shape"] for r in refs] == [tuple(k.shape), tuple(v.shape)]
     # sparse V attention against the oracle on the same codes
     q = torch.randn(1, 128)
     keys = torch.randn(40, 128)

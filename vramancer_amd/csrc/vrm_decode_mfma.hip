@@ -48,9 +48,15 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 constexpr float kInv254 = 1.0f / 254.0f;
 // The running maximum is raised only when a new score exceeds it by more than
 // this (log2 units), so the weights 2^(s - m) stay below 2^kLazyRescale and
-// the accumulators are rescaled rarely.  It also bounds the fp16 B operand:
-// weight * V scale < 2^kLazyRescale * V scale must stay below 65504.
+// the accumulators are rescaled rarely.
 constexpr float kLazyRescale = 3.0f;
+// The quantized kernel's PV weights are 2^(s - m - e) * vscale, with e a
+// power-of-two exponent of the V scales the stream has seen (vscale < 2^e
+// when e was chosen), so the fp16 B operand holds the same relative
+// precision whatever the absolute scale of V.  e is raised when a V scale
+// reaches 2^(e + kVScaleHeadroom): weights stay below 2^(kLazyRescale +
+// kVScaleHeadroom) = 32768 < 65504.
+constexpr int kVScaleHeadroom = 12;
 // Initial running maximum: finite so that 2^(-inf - m) is 0 for masked tokens.
 constexpr float kNoMax = -1.0e30f;
 
@@ -227,7 +233,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
 
   // ---------------- streaming state ----------------
   float m_run = kNoMax;  // running maximum of this lane's head (equal in its 4 lanes)
-  float l_run = 0.f;     // this lane's share of sum 2^(s - m_run)
+  int vexp = 0;          // V-scale exponent e (wave-uniform)
+  float vlimit = 0.f;    // 2^(e + kVScaleHeadroom), 0 until the first positive V scale sets e
+  float m_eff = kNoMax;  // m_run + e: the weights are 2^(s - m_eff) * vscale
+  float l_run = 0.f;     // this lane's share of sum 2^(s - m_eff)
   v4f acc[NB];           // O^T block blk: rows = dims 16 blk + 4 grp + r, column = head
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) acc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -306,18 +315,78 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
     }
+    // V scales of the pair's tokens (int8: token 4 grp + r % 4 of page
+    // pi + r / 4; fp8: vs[0] and vs[4] are the two pages' scales) and V codes.
+    float vs[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      vs[r] = KIND == K_I8 ? f4(s0.vs, r) : s0.vs.x;
+      vs[4 + r] = has1 ? (KIND == K_I8 ? f4(s1.vs, r) : s1.vs.x) : 0.f;
+    }
+    uint4 v0[NJ], v1[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      v0[j] = s0.v[j];
+      v1[j] = has1 ? s1.v[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // Only the sequence's last page holds tokens past the context (absent
+    // pages were zeroed when loaded).  When the pair reaches it, the scales
+    // of those tokens and, for fp8 (whose NaN codes would survive a zero
+    // weight), their codes are zeroed, so whatever the pool holds there
+    // cannot reach the output.  The test is wave-uniform.
+    if ((pi + 2) * kPS > tok_end) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int n_live = min(max(tok_end - (pi + u) * kPS - 4 * grp, 0), 4);  // this lane's live tokens
+        if constexpr (KIND == K_I8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (r >= n_live) vs[4 * u + r] = 0.f;
+        } else {
+          const uint32_t keep = n_live >= 4 ? 0xffffffffu : (1u << (8 * n_live)) - 1u;  // byte r = token 4 grp + r
+          uint4* v = u ? v1 : v0;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) v[j] = make_uint4(v[j].x & keep, v[j].y & keep, v[j].z & keep, v[j].w & keep);
+        }
+      }
+    }
+    // A V scale at or above 2^(e + kVScaleHeadroom) raises e (wave-uniform);
+    // the first positive scale sets it.
+    float vm = vs[0];
+    if constexpr (KIND == K_I8) {
+#pragma unroll
+      for (int r = 1; r < 8; ++r) vm = fmaxf(vm, vs[r]);
+    } else {
+      vm = fmaxf(vm, vs[4]);
+    }
+    int e_new = vexp;
+    if (__builtin_amdgcn_ballot_w64(vm > vlimit) != 0) {
+      float wm = fmaxf(vm, xor_shfl<16>(vm));
+      wm = fmaxf(wm, xor_shfl<32>(wm));
+      if (wm <= 3.0e38f) {  // finite: an inf scale keeps e (its tokens give inf / NaN as in the reference)
+        int ex;
+        (void)frexpf(wm, &ex);  // wm < 2^ex
+        e_new = max(ex, vlimit > 0.f ? vexp : ex);
+        vlimit = ldexpf(1.f, e_new + kVScaleHeadroom);
+      }
+    }
     float pm = sc[0];
 #pragma unroll
     for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
     pm = fmaxf(pm, xor_shfl<16>(pm));
     pm = fmaxf(pm, xor_shfl<32>(pm));
-    if (pm > m_run + kLazyRescale) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - pm);  // 0 while nothing has been accumulated
+    const bool up = pm > m_run + kLazyRescale;
+    if (up || e_new != vexp) {
+      const float m_new = up ? pm : m_run;
+      const float me_new = m_new + (float)e_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_eff - me_new);  // 0 while nothing has been accumulated
       l_run *= alpha;
 #pragma unroll
       for (int blk = 0; blk < NB; ++blk) acc[blk] *= alpha;
-      m_run = pm;
+      m_run = m_new;
+      m_eff = me_new;
     }
+    vexp = e_new;
     // B operand: k = 8 grp + e <-> token 4 grp + e % 4 of page pi + e / 4.
     uint32_t bh[4], bl[4];
 #pragma unroll
@@ -326,10 +395,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int r = 2 * e2 + u;
-        const float p = __builtin_amdgcn_exp2f(sc[r] - m_run);
+        const float p = __builtin_amdgcn_exp2f(sc[r] - m_eff);
         l_run += p;
-        const float vsc = KIND == K_I8 ? f4(r < 4 ? s0.vs : s1.vs, r & 3) : (r < 4 ? s0.vs.x : s1.vs.x);
-        w[u] = p * vsc;
+        w[u] = p * (KIND == K_I8 ? vs[r] : vs[r & 4]);
       }
       const v2h h = {(_Float16)w[0], (_Float16)w[1]};
       const v2h l = {(_Float16)(w[0] - (float)h[0]), (_Float16)(w[1] - (float)h[1])};
@@ -340,8 +408,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
     const v8h Bl = dwords_to_v8h(bl[0], bl[1], bl[2], bl[3]);
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
-      const uint32_t w0 = dword(s0.v[blk / 4], blk % 4);
-      const uint32_t w1 = has1 ? dword(s1.v[blk / 4], blk % 4) : 0u;
+      const uint32_t w0 = dword(v0[blk / 4], blk % 4);
+      const uint32_t w1 = dword(v1[blk / 4], blk % 4);
       v8h A;
       if constexpr (KIND == K_I8) {
         uint32_t a0, a1, a2, a3;
@@ -388,7 +456,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
       *reinterpret_cast<float4*>(out + blk * 16 + grp * 4) =
           make_float4(acc[blk][0], acc[blk][1], acc[blk][2], acc[blk][3]);
     if (grp == 0) {
-      ml_base[col * 2] = l_tot > 0.f ? m_run : -INFINITY;
+      ml_base[col * 2] = l_tot > 0.f ? m_eff : -INFINITY;  // l and acc are relative to 2^m_eff
       ml_base[col * 2 + 1] = l_tot;
     }
   }

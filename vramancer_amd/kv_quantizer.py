@@ -25,7 +25,7 @@ import torch.nn as nn
 from . import _lib
 from .turboquant_cuda import CUDATurboQuantOps, level_bins
 
-__all__ = ["KVCacheCompressor", "TurboQuantCompressor", "BatchedCompressedRef"]
+__all__ = ["KVCacheCompressor", "TurboQuantCompressor"]
 
 
 # Bit packing (MSB first): the byte layout of core/kv_quantizer.py:46-105.
@@ -78,61 +78,34 @@ def _unpack_angles(packed, N, level_dims, bits_per_angle):
     return list(torch.split(flat, list(level_dims), dim=-1))
 
 
-class BatchedCompressedRef(dict):
-    """Lazy view of rows [offset, offset + n) of a batched compress result
-    (core/kv_quantizer.py:115-177): slicing is deferred until first access."""
+def _split_rows(result: dict, rows: list, shapes: list) -> list:
+    """Per-item dicts over the rows of one batched result, as device views.
 
-    __slots__ = ("_backing", "_off", "_n", "_shape", "_resolved")
-    _KEYS = ("radius", "angles", "qjl_signs", "qjl_norms", "shape")
-
-    def __init__(self, backing: dict, offset: int, n_rows: int, shape: tuple):
-        super().__init__()
-        self._backing = backing
-        self._off = offset
-        self._n = n_rows
-        self._shape = shape
-        self._resolved = False
-
-    def _resolve(self):
-        if self._resolved:
-            return
-        o, n, b = self._off, self._n, self._backing
-        super().__setitem__("radius", b["radius"][o:o + n])
-        super().__setitem__("angles", [a[o:o + n] for a in b["angles"]])
-        super().__setitem__("qjl_signs", b["qjl_signs"][o:o + n])
-        super().__setitem__("qjl_norms", b["qjl_norms"][o:o + n])
-        super().__setitem__("shape", self._shape)
-        self._backing = None
-        self._resolved = True
-
-    def __getitem__(self, key):
-        self._resolve()
-        return super().__getitem__(key)
-
-    def __contains__(self, key):
-        if not self._resolved:
-            return key in self._KEYS
-        return super().__contains__(key)
-
-    def get(self, key, default=None):
-        if not self._resolved:
-            if key in self._KEYS:
-                self._resolve()
-                return super().__getitem__(key)
-            return default
-        return super().get(key, default)
-
-    def keys(self):
-        self._resolve()
-        return super().keys()
-
-    def values(self):
-        self._resolve()
-        return super().values()
-
-    def items(self):
-        self._resolve()
-        return super().items()
+    ``torch.split`` cuts every field in one call for all items, so the cost
+    does not grow with the number of fields times items in Python; each item
+    gets a plain dict of views (no copy) with its own input shape.  Works on
+    raw results (radius / angles / qjl_signs / qjl_norms) and on packed ones
+    (angles_packed / qjl_signs_packed), whose rows are packed independently.
+    """
+    columns = {}
+    for key, val in result.items():
+        if key == "shape" or key.startswith("_"):
+            continue
+        if isinstance(val, list):
+            columns[key] = list(zip(*(torch.split(level, rows) for level in val)))
+        else:
+            columns[key] = torch.split(val, rows)
+    items = []
+    for i, (shape, n) in enumerate(zip(shapes, rows)):
+        item = {key: (list(col[i]) if isinstance(result[key], list) else col[i]) for key, col in columns.items()}
+        item["shape"] = shape
+        for key in ("_qjl_dim", "_level_dims"):
+            if key in result:
+                item[key] = result[key]
+        if "_N" in result:
+            item["_N"] = n
+        items.append(item)
+    return items
 
 
 class KVCacheCompressor(nn.Module):
@@ -200,34 +173,24 @@ class KVCacheCompressor(nn.Module):
         return self._pack_compressed(result) if pack else result
 
     def compress_batch(self, kv_list: list, pack: bool = False) -> list:
-        """Compresses several tensors with one kernel launch; returns lazy raw
-        views (or packed dicts with pack=True).  A one-element list returns
+        """Compresses several tensors with one kernel launch and returns one
+        dict per tensor: raw codes (device views into the batch result), or,
+        with ``pack=True``, packed dicts (the whole batch is packed by one
+        launch per field, then split).  A one-element list returns
         ``[self.compress(kv)]`` (packed), as the reference does
         (core/kv_quantizer.py:443-444)."""
         if not kv_list:
             return []
         if len(kv_list) == 1:
             return [self.compress(kv_list[0])]
-        shapes = [kv.shape for kv in kv_list]
-        rows = [kv.reshape(-1, self.head_dim).shape[0] for kv in kv_list]
-        flat = torch.cat([kv.reshape(-1, self.head_dim) for kv in kv_list], dim=0)
-        result = CUDATurboQuantOps.compress_gpu(flat, *self._ops_args(), self._hadamard_signs, self.jl_matrix)
-        out = []
-        offset = 0
-        for shape, n in zip(shapes, rows):
-            if pack:
-                sliced = {
-                    "radius": result["radius"][offset:offset + n],
-                    "angles": [a[offset:offset + n] for a in result["angles"]],
-                    "qjl_signs": result["qjl_signs"][offset:offset + n],
-                    "qjl_norms": result["qjl_norms"][offset:offset + n],
-                    "shape": shape,
-                }
-                out.append(self._pack_compressed(sliced))
-            else:
-                out.append(BatchedCompressedRef(result, offset, n, shape))
-            offset += n
-        return out
+        shapes = [tuple(kv.shape) for kv in kv_list]
+        flat = [kv.reshape(-1, self.head_dim) for kv in kv_list]
+        rows = [f.shape[0] for f in flat]
+        result = CUDATurboQuantOps.compress_gpu(torch.cat(flat, dim=0), *self._ops_args(), self._hadamard_signs,
+                                                self.jl_matrix)
+        if pack:
+            result = self._pack_compressed(result)
+        return _split_rows(result, rows, shapes)
 
     def decompress(self, compressed):
         """Approximate K/V from polar codes only (no QJL), shaped like the input."""

@@ -55,6 +55,31 @@ def decode_workspace(batch: int, num_heads: int, num_kv_heads: int, head_dim: in
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
 
 
+def check_outputs(query, out, workspace, page_table, context_lens) -> None:
+    """Validates the caller-supplied tensors a decode writes or indexes through.
+
+    ``out`` must be a contiguous float32 [B, H, D] tensor and ``workspace`` a
+    contiguous tensor, both on the query's device: the kernels write through
+    their raw pointers.  ``page_table`` must be [B, max_pages] and
+    ``context_lens`` [B] (the kernels read B rows of max_pages entries)."""
+    import torch
+
+    B, H, D = query.shape
+    if page_table.dim() != 2 or page_table.shape[0] != B or page_table.shape[1] < 1:
+        raise RuntimeError(f"page_table must be [B={B}, max_pages >= 1], got {tuple(page_table.shape)}")
+    if tuple(context_lens.shape) != (B,):
+        raise RuntimeError(f"context_lens must be [B={B}], got {tuple(context_lens.shape)}")
+    if out is not None:
+        if (tuple(out.shape) != (B, H, D) or out.dtype != torch.float32 or not out.is_contiguous()
+                or out.device != query.device):
+            raise RuntimeError(f"out must be a contiguous float32 [{B}, {H}, {D}] tensor on {query.device}, got "
+                               f"{out.dtype} {tuple(out.shape)} on {out.device}")
+    if workspace is not None:
+        if workspace.device != query.device or not workspace.is_contiguous():
+            raise RuntimeError(f"workspace must be a contiguous tensor on {query.device}, got one on "
+                               f"{workspace.device}")
+
+
 def _prepare(query, page_table, context_lens, scale):
     import torch
 
@@ -98,8 +123,8 @@ def paged_attention_decode(
     P, L, two, KH, PS, Dp = kv_pool.shape
     if two != 2 or Dp != D:
         raise RuntimeError(f"kv_pool shape {tuple(kv_pool.shape)} does not match query head_dim {D}")
-    if page_table.dim() != 2 or page_table.shape[0] != B or context_lens.shape != (B,):
-        raise RuntimeError("page_table must be [B, max_pages] and context_lens [B]")
+    _lib.require_cuda(out, workspace)
+    check_outputs(query, out, workspace, page_table, context_lens)
     code = _lib.kv_dtype_code(kv_pool.dtype)
     if code in (_lib.VRM_KV_I8, _lib.VRM_KV_FP8E4M3):
         want = (P, L, 2, KH, PS) if code == _lib.VRM_KV_I8 else (P, L, 2, KH)
@@ -181,7 +206,8 @@ def paged_attention_decode_q4(
     import torch
 
     query, page_table, context_lens, scale = _prepare(query, page_table, context_lens, scale)
-    _lib.require_cuda(query, kv_pool_q4, kv_scales, kv_zeros, page_table, context_lens)
+    _lib.require_cuda(query, kv_pool_q4, kv_scales, kv_zeros, page_table, context_lens, out, workspace)
+    check_outputs(query, out, workspace, page_table, context_lens)
     B, H, D = query.shape
     P, L, two, KH, PS, Dh = kv_pool_q4.shape
     if two != 2 or Dh * 2 != D or kv_pool_q4.dtype != torch.uint8:

@@ -26,7 +26,7 @@ import math
 from typing import Any, Dict, Optional
 
 from . import _lib
-from .paged_attention_cuda import _check_lse, decode_workspace
+from .paged_attention_cuda import _check_lse, check_outputs, decode_workspace
 from .turboquant_cuda import angle_lut
 
 __all__ = [
@@ -213,6 +213,8 @@ def paged_attention_decode_turbo(query, tq_pool, page_table, context_lens, layer
     query = query.float().contiguous()
     page_table = page_table.to(torch.int32).contiguous()
     context_lens = context_lens.to(torch.int32).contiguous()
+    _lib.require_cuda(query, out, workspace, lse)
+    check_outputs(query, out, workspace, page_table, context_lens)
     max_pp = page_table.shape[1]
     if out is None:
         out = torch.empty((B, H, D), dtype=torch.float32, device=query.device)
