@@ -113,6 +113,25 @@ int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_sc
                      int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
 
 /*
+ * vrm_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  No counterpart in the reference; it
+ * allocates nothing and calls no allocating routine.  The split-K partials
+ * live in a fixed array of VRM_NOALLOC_SCRATCH_BYTES inside the library, one
+ * per GPU, held until the process ends; shapes whose workspace
+ * (vrm_paged_decode_workspace_bytes with vrm_paged_decode_num_splits) is
+ * larger are rejected with VRM_ERR_WORKSPACE.  All calls on one GPU share
+ * that array: calls that overlap on one GPU (concurrent streams or threads)
+ * race and must be serialised by the caller.  Same arguments, results and
+ * supported shapes as vrm_paged_decode otherwise.
+ */
+#define VRM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const float* kv_scales,
+                             const int32_t* page_table, const int32_t* context_lens, float* out,
+                             int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                             int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
+
+/*
  * The two passes of vrm_paged_decode, for callers that schedule them
  * separately (and for timing the dominant pass on its own):
  * vrm_paged_decode_partitions writes per-partition (max, sum, unnormalised

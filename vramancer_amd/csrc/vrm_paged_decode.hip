@@ -751,6 +751,85 @@ extern "C" int vrm_paged_decode(const float* query, const void* kv_pool, const f
                       D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth);
 }
 
+// ---------------------------------------------------------------------------
+// Decode without a caller workspace: the split-K partials live in a fixed
+// device array of this file, one copy per GPU, which the library looks up
+// once per device (hipGetSymbolAddress, with that device current) and then
+// addresses only through the returned pointer.  Nothing is allocated per
+// call.  Every call on one GPU uses that GPU's array and leaves it holding its
+// partials; nothing in it needs clearing (the partition pass writes the
+// header and every partial the merge reads), and calls that overlap on one
+// GPU race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = VRM_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace vrm {
+namespace dec {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the device of `st`.
+int scratch_of(hipStream_t st, void** ptr) {
+  int dev = 0, cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess) e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) {
+    set_error("vrm_paged_decode_noalloc: cannot identify the stream's device: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("vrm_paged_decode_noalloc: device %d outside [0, %d)", dev, kMaxDevices);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    if (dev != cur) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || !p) {
+      set_error("vrm_paged_decode_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
+                hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    }
+    g_scratch[dev] = p;
+  }
+  *ptr = g_scratch[dev];
+  return VRM_OK;
+}
+
+}  // namespace
+}  // namespace dec
+}  // namespace vrm
+
+extern "C" int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const float* kv_scales,
+                                        const int32_t* page_table, const int32_t* context_lens, float* out, int B,
+                                        int H, int KH, int D, int PS, int L, int P, int max_pp, int layer_idx,
+                                        float scale, int kv_dtype, vrm_stream_t stream) {
+  int rc = check_common(query, kv_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  const size_t need = header_bytes(B) + (size_t)items_capacity(B, KH) * H * (D + 2) * sizeof(float);
+  if (need > kNoAllocScratchBytes) {
+    set_error("vrm_paged_decode_noalloc: B=%d H=%d KH=%d D=%d needs %zu bytes of split-K scratch, above the "
+              "fixed %zu-byte array; use vrm_paged_decode with a workspace",
+              B, H, KH, D, need, kNoAllocScratchBytes);
+    return VRM_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  rc = scratch_of(reinterpret_cast<hipStream_t>(stream), &ws);
+  if (rc) return rc;
+  return decode_entry(query, kv_pool, kv_scales, page_table, context_lens, out, ws, kNoAllocScratchBytes, B, H, KH,
+                      D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth);
+}
+
 extern "C" int vrm_paged_decode_partitions(const float* query, const void* kv_pool, const float* kv_scales,
                                            const int32_t* page_table, const int32_t* context_lens, void* workspace,
                                            size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,
