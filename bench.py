@@ -42,7 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from vramancer_amd import _lib, kv_quant, tq_pages, workloads  # noqa: E402
-from vramancer_amd.paged_attention_cuda import decode_workspace  # noqa: E402
+from vramancer_amd.paged_attention_cuda import decode_workspace, prefer_balanced  # noqa: E402
 
 METRIC = "paged-attn decode µs/layer-step + HBM GB/s (% of peak), 14B-shape quantized KV"
 PEAK_HBM_GBPS = 8000.0
@@ -544,8 +544,21 @@ def main():
     ab = workloads.algorithmic_bytes(cfg, lens_list)
     log(f"pool {P} pages, {nsplit} partitions/sequence, algorithmic bytes/layer-step {ab['total'] / 1e6:.2f} MB")
 
+    # even batches over int8 / fp8 pools take the balanced decode (one
+    # workgroup per sequence and kv-head, no merge pass), as the manager does
+    balanced = (not turbo and not q4 and
+                prefer_balanced(lens_list, KH, pool.dtype))
+    log(f"decode mode: {'balanced' if balanced else 'work items + merge'}")
+
     def full(i):
         layer = layers[i % len(layers)]
+        if balanced:
+            rc = lib.vrm_paged_decode_balanced(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(),
+                                               lens.data_ptr(), out.data_ptr(), None, B, H, KH, D, PS, L, P, max_pp,
+                                               layer, scale, code, stream)
+            if rc:
+                _lib.check(rc, "balanced decode")
+            return
         if turbo:
             rc = lib.vrm_paged_decode_tq(q.data_ptr(), pool.data_ptr(), table.data_ptr(), lens.data_ptr(),
                                          out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp,
@@ -578,11 +591,14 @@ def main():
     for i in range(args.warmup):
         full(i)
     torch.cuda.synchronize()
-    pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
+    if balanced:
+        pps, n_items = None, None
+    else:
+        pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
     log(f"timing {args.steps} layer-steps")
     us_step = time_events(full, args.steps)
-    # TurboQuant and Q4: no separate partition entry; the kernel time is the whole decode
-    us_part = us_step if (turbo or q4) else time_events(partitions, args.steps)
+    # TurboQuant, Q4 and the balanced decode: one kernel, whose time is the whole decode
+    us_part = us_step if (turbo or q4 or balanced) else time_events(partitions, args.steps)
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
     # The drop-in Python call: the same decode through the module API, with the
@@ -597,7 +613,7 @@ def main():
         elif q4:
             paged_attention_decode_q4(q, pool, sc, zp, table, lens, layer, **kw)
         else:
-            paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc, **kw)
+            paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc, context_lens_host=lens_list, **kw)
 
     for i in range(5):
         api(i, False)
@@ -712,6 +728,7 @@ def main():
             "workload": desc,
             "batch": B, "num_heads": H, "num_kv_heads": KH, "head_dim": D, "context_tokens": int(sum(lens_list)),
             "page_size": PS, "num_layers": L, "num_pages": P, "pages_per_partition": pps, "work_items": n_items,
+            "decode_mode": "balanced" if balanced else "work-items",
             "layers_rotated": list(layers),
         },
         "hbm_gbps": round(overall, 1),
@@ -726,8 +743,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
-            "kernel": KERNEL[cfg.codec].format(D=D) + (f" (G={G}, whole decode)" if (turbo or q4)
-                                                       else f" (G={G}, partition pass)"),
+            "kernel": (KERNEL[cfg.codec].format(D=D) if not balanced else
+                       KERNEL[cfg.codec].format(D=D).replace(">", ",balanced>"))
+                      + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
             "kernel_us": round(us_part, 3),
         },
         "cpu_baseline": cpu,

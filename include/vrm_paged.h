@@ -132,6 +132,24 @@ int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const floa
                              int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
 
 /*
+ * vrm_paged_decode for batches whose sequences have about equal context
+ * lengths (the caller knows them on the host; the page manager does).  One
+ * workgroup per (sequence, kv-head or head chunk) splits the sequence's pages
+ * over its wavefronts and merges their partials in LDS, writing out directly:
+ * no workspace, no separate merge pass.  Correct for any lengths; its time
+ * follows the longest sequence, so ragged batches belong on vrm_paged_decode,
+ * which balances work items across sequences.  lse (nullable) receives
+ * ln sum_t exp(scale q.k_t) per (b, h) as in vrm_paged_decode_lse.  No
+ * counterpart in the reference (whose kernel is one warp per (head, sequence),
+ * csrc/paged_attention_kernel.cu:445-499, with no split).
+ * Supported: int8 and fp8 pools, D in {64, 128, 256}, PS == 16.
+ */
+int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const float* kv_scales,
+                              const int32_t* page_table, const int32_t* context_lens, float* out, float* lse,
+                              int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                              int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
+
+/*
  * The two passes of vrm_paged_decode, for callers that schedule them
  * separately (and for timing the dominant pass on its own):
  * vrm_paged_decode_partitions writes per-partition (max, sum, unnormalised

@@ -205,3 +205,36 @@ def test_decode_wrappers_validate_out_workspace_and_table():
         a.update(kw)
         with pytest.raises(RuntimeError):
             check_outputs(q, a["out"], a["workspace"], a["page_table"], a["context_lens"])
+
+
+def test_balanced_decode_selection_rule():
+    """The balanced decode is chosen only for int8 / fp8 pools, at least 128
+    (sequence, kv-head) pairs, and contexts within 10 % of their mean."""
+    import torch
+    from vramancer_amd.paged_attention_cuda import prefer_balanced
+
+    assert prefer_balanced([4096] * 64, 8, torch.int8)
+    assert prefer_balanced([4096] * 64, 8, torch.float8_e4m3fn)
+    assert not prefer_balanced([4096] * 64, 8, torch.bfloat16)
+    assert not prefer_balanced([4096] * 8, 8, torch.int8)          # 64 pairs: too few workgroups
+    assert not prefer_balanced([1024, 8192] * 32, 8, torch.int8)   # ragged
+    assert prefer_balanced([4000, 4400] * 32, 8, torch.int8)       # max 4400 <= 1.1 * mean 4200
+    assert not prefer_balanced([0] * 64, 8, torch.int8)
+    assert not prefer_balanced([], 8, torch.int8)
+    assert prefer_balanced(torch.full((64,), 4096, dtype=torch.int32), 8, torch.int8)
+
+
+def test_balanced_entry_rejects_bad_arguments(lib):
+    f = lib.vrm_paged_decode_balanced
+    args = [1, 1, 1, 1, 1, 1, None, 2, 8, 2, 128, 16, 1, 4, 2, 0, 0.1, _lib.VRM_KV_I8, None]
+
+    def call(i, v):
+        a = list(args)
+        a[i] = v
+        return f(*a)
+
+    assert call(0, None) == -1
+    assert call(2, None) == -1 and b"kv_scales" in lib.vrm_last_error()
+    assert call(17, _lib.VRM_KV_BF16) == -2
+    assert call(17, 99) == -1
+    assert call(10, 96) == -2 and b"head_dim" in lib.vrm_last_error()

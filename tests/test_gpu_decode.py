@@ -473,6 +473,15 @@ def test_decode_full_size_int8_48_layer_bench_pool():
             ref = PD.paged_attention_decode(q[b:b + 1].cpu(), sub_pool, sub_table, lens[b:b + 1].cpu(), 0,
                                             kv_scales=sub_sc)
             _assert_close(out[b:b + 1], ref, f"48-layer pool, layer {layer}, seq {b}")
+    # the balanced decode (what the manager picks for this even batch), layer 36
+    out_bal = paged_attention_decode(q, pool, table, lens, 36, kv_scales=sc, context_lens_host=lens.tolist())
+    torch.cuda.synchronize()
+    for b in (1, 30, 62):
+        pages = table[b].long()
+        ref = PD.paged_attention_decode(q[b:b + 1].cpu(), pool[pages, 36:37].cpu(),
+                                        torch.arange(pages.numel(), dtype=torch.int32)[None], lens[b:b + 1].cpu(), 0,
+                                        kv_scales=sc[pages, 36:37].cpu())
+        _assert_close(out_bal[b:b + 1], ref, f"48-layer pool, balanced, seq {b}")
     P = pool.shape[0]
     perm = torch.randperm(P, generator=torch.Generator().manual_seed(5)).to(DEV)
     inv = torch.empty_like(perm)
@@ -509,3 +518,86 @@ def test_wrappers_reject_bad_out_workspace_and_tables():
         paged_attention_decode_q4(q, packed, s4, s4, table[:1], lens, 1)
     with pytest.raises(RuntimeError):
         paged_attention_decode_q4(q, packed, s4, s4, table, lens, 1, out=torch.empty(2, 8, 128, device=DEV)[:, :4])
+
+
+def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
+    """vrm_paged_decode_balanced through the C ABI (device tensors)."""
+    lib = _lib.load()
+    B, H, D = q.shape
+    P, L, _, KH, PS, _ = pool.shape
+    out = torch.full((B, H, D), float("nan"), device=DEV)
+    scale = 1 / math.sqrt(D) if scale is None else scale
+    rc = lib.vrm_paged_decode_balanced(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(),
+                                       lens.data_ptr(), out.data_ptr(), _lib.ptr(lse), B, H, KH, D, PS, L, P,
+                                       table.shape[1], layer, scale, _lib.kv_dtype_code(pool.dtype),
+                                       _lib.stream_of(q))
+    _lib.check(rc, "vrm_paged_decode_balanced")
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+@pytest.mark.parametrize("H,KH,D,ctxs", [
+    (40, 8, 128, [37, 1600, 333, 0, 1, 4096]),   # ragged: correct for any lengths
+    (64, 8, 128, [512] * 20),                    # even
+    (16, 1, 128, [3000, 2999, 17]),              # one kv-head, 8 waves per workgroup
+    (8, 2, 256, [100, 260]),
+    (12, 12, 64, [64, 65, 700]),
+])
+def test_balanced_decode_matches_oracle(dtype, H, KH, D, ctxs):
+    """The balanced decode (one workgroup per sequence and kv-head, partitions
+    merged in LDS) against the oracle, at the decode bar."""
+    _say(f"balanced {dtype} H {H} KH {KH} D {D} B {len(ctxs)}")
+    q, pool, sc, table, lens = _pool_case(dtype, len(ctxs), H, KH, D, ctxs, seed=H + D + len(ctxs))
+    out = _balanced(*(t.to(DEV) for t in (q, pool, sc, table, lens)), 1)
+    ref = PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc)
+    assert torch.isfinite(out).all()
+    _assert_close(out, ref, f"balanced {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+def test_balanced_decode_garbage_absent_pages_and_lse(dtype):
+    """NaN / inf scales and 0x7f codes past the context, an absent page and an
+    unreferenced page are ignored; the lse output equals the work-item
+    decode's."""
+    from oracle.kv_codecs import pool_from_logical, pool_to_logical
+
+    _say(f"balanced garbage + lse {dtype}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, 128, [37, 160, 5], seed=31)
+    raw = pool_to_logical(pool.view(torch.uint8))
+    for b, c in enumerate(lens.tolist()):
+        last = int(table[b, (c - 1) // 16])
+        raw[last, 1, :, :, c % 16 or 16:, :] = 0x7F
+        if dtype == torch.int8:
+            sc[last, 1, :, :, c % 16 or 16:] = float("nan")
+    table[1, 3] = -1
+    pool = pool_from_logical(raw).view(dtype)
+    d = [t.to(DEV) for t in (q, pool, sc, table, lens)]
+    lse = torch.empty(3, 16, device=DEV)
+    out = _balanced(*d, 1, lse=lse)
+    lse_ref = torch.empty(3, 16, device=DEV)
+    ref_items = paged_attention_decode(d[0], d[1], d[3], d[4], 1, kv_scales=d[2], lse=lse_ref)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    f = _dequant_pool(pool, sc, 1)
+    for b in range(3):
+        K, V = PD.gather_sequence(f, table[b], int(lens[b]), 1, skip_invalid=True)
+        _assert_close(out[b].cpu(), PD.dense_attention(q[b], K, V, 1 / math.sqrt(128)), f"seq {b}")
+    torch.testing.assert_close(lse, lse_ref, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(out, ref_items, atol=1e-5, rtol=1e-5)
+
+
+def test_api_takes_the_balanced_decode_for_even_batches():
+    """paged_attention_decode with host lengths picks the balanced decode for an
+    even int8 batch (no workspace is allocated) and the work-item decode for a
+    ragged one; both match the oracle."""
+    from vramancer_amd import paged_attention_cuda as PAC
+
+    for ctxs, want in (([300] * 32, True), ([30, 3000] * 16, False)):
+        _say(f"api balanced choice {want}")
+        q, pool, sc, table, lens = _pool_case(torch.int8, len(ctxs), 40, 8, 128, ctxs, seed=len(set(ctxs)))
+        assert PAC.prefer_balanced(ctxs, 8, torch.int8) is want
+        out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), 1, kv_scales=sc.to(DEV),
+                                     context_lens_host=ctxs)
+        torch.cuda.synchronize()
+        _assert_close(out, PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc), f"api {want}")

@@ -34,6 +34,7 @@ struct DecodeArgs {
   float qscale;               // scale * log2(e): scores live in the log2 domain
   int target;                 // work items the partition size aims for
   float* lse;                 // optional [B][H] natural-log sum of exp(scale * q.k), written by the merge
+  float* out;                 // [B][H][D]: written directly by the balanced (one workgroup per sequence) mode
 };
 
 // ---------------------------------------------------------------------------
@@ -168,6 +169,14 @@ int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int 
 // Single-pass matrix-core (MFMA) split pass; kind is K_I8, K_FP8, K_BF16 or
 // K_F16, D the head dimension, G the query heads per wavefront (<= 16).
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
+
+// Balanced-batch decode: one workgroup per (sequence, kv-head / head chunk)
+// whose W wavefronts split the sequence's pages and merge their partials in
+// LDS, writing a.out (and a.lse) directly: no work items, no workspace, no
+// merge launch.  Correct for any context lengths; its time follows the
+// longest sequence, so it suits batches of about equal lengths.  kind is
+// K_I8 or K_FP8 (D 64, 128, 256) or K_BF16 / K_F16 (D 64, 128).
+hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
 // Paged decode over TurboQuant pages (vrm_decode_tq.hip).
 struct TqDecodeArgs {

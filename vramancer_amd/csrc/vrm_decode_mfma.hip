@@ -137,9 +137,69 @@ struct PageSlot {
 // contiguous run for a whole page-layer), which keeps DRAM accesses local.
 // The wavefronts share nothing and never synchronise.
 constexpr int kMaxWaves = 4;
+// Balanced mode: one workgroup of up to kMaxBalancedWaves wavefronts per
+// (sequence, unit); wavefront w streams the w-th of W equal page ranges.
+constexpr int kMaxBalancedWaves = 8;
 
-template <int KIND, int D>
-__global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArgs a, int G) {
+// Work of wavefront `wave` of a balanced-mode workgroup: the w-th of W
+// contiguous page ranges of sequence b (empty when the sequence is short).
+__device__ __forceinline__ WorkItem balanced_item(const DecodeArgs& a, int b, int wave, int W) {
+  WorkItem w;
+  w.b = b;
+  w.ctx = a.ctx_lens[b];
+  const int pages = seq_pages(w.ctx, a.max_pp);
+  const int per = (pages + W - 1) / W;
+  w.p_begin = min(wave * per, pages);
+  w.n_pages = min(per, pages - w.p_begin);
+  return w;
+}
+
+// Balanced-mode epilogue: the W wavefronts' partials (max m, sum l, unnormalised
+// accumulator; lane (col, grp) holds dims 16 blk + 4 grp + r of head col) are
+// merged through LDS with log-sum-exp weights 2^(m_w - max m) and written to
+// a.out[b][h0 .. h0 + G - 1] (and a.lse).  LDS: [W][G][D] accumulators, then
+// [W][G][2] (m, l).  Every wavefront of the workgroup must call it.
+template <int D, int NB>
+__device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b, int h0,
+                                               const v4f (&acc)[NB], float m, float l_tot) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  float* part = lds;
+  float* ml = lds + (size_t)W * G * D;
+  if (col < G) {
+    float* dst = part + ((size_t)wave * G + col) * D;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk)
+      *reinterpret_cast<float4*>(dst + blk * 16 + grp * 4) = make_float4(acc[blk][0], acc[blk][1], acc[blk][2], acc[blk][3]);
+    if (grp == 0) {
+      ml[((size_t)wave * G + col) * 2] = l_tot > 0.f ? m : -INFINITY;
+      ml[((size_t)wave * G + col) * 2 + 1] = l_tot;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+    const int g = i / D, d = i - g * D;
+    float M = -INFINITY;
+    for (int w = 0; w < W; ++w) M = fmaxf(M, ml[(w * G + g) * 2]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+      for (int w = 0; w < W; ++w) {
+        const float mw = ml[(w * G + g) * 2];
+        const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+        L = fmaf(f, ml[(w * G + g) * 2 + 1], L);
+        o = fmaf(f, part[((size_t)w * G + g) * D + d], o);
+      }
+    }
+    const size_t row = (size_t)b * a.H + h0 + g;
+    a.out[row * D + d] = L > 0.f ? o * (1.f / L) : 0.f;
+    // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
+    if (a.lse && d == 0) a.lse[row] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+  }
+}
+
+template <int KIND, int D, bool BALANCED>
+__global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
+    decode_stream_kernel(DecodeArgs a, int G) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
   constexpr int HEAD_BYTES = kPS * D;     // one (page, layer, K/V, head) slice
   constexpr int NJ = D / 64;              // 16-byte loads per lane and page, for K and for V
@@ -152,15 +212,22 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   const int grp = lane >> 4;
   const int group = a.H / a.KH;
   const int chunks = group / G;
-  const int unit = blockIdx.y * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // item mode: the workgroup's waves are W units of one work item; balanced
+  // mode: they are the W page ranges of one (sequence, unit)
+  const int unit = BALANCED ? (int)blockIdx.y : (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
   const int kvh = unit / chunks;
   const int h0 = kvh * group + (unit % chunks) * G;
 
-  // work item (sequence, partition) of this workgroup; the first wave of the
-  // launch also records the partition geometry for the merge pass
+  // work item (sequence, partition) of this wave; in item mode the first wave
+  // of the launch also records the partition geometry for the merge pass
   const int item = blockIdx.x;
   WorkItem wi;
-  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  if constexpr (BALANCED) {
+    wi = balanced_item(a, blockIdx.x, wave, blockDim.x >> 6);
+  } else {
+    if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  }
   const int b = wi.b;
   const int n_pages = wi.n_pages;
   const int last = n_pages - 1;
@@ -169,7 +236,6 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   // of page first + u (clamped to the last page)
   const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
   auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
-  float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
 
   const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
   const size_t page_stride = kv_stride * 2 * a.L;
@@ -428,7 +494,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   // Page q sits in slot q % RING.  The refill loads are unconditional (slots
   // past the last page reload it, an L2 hit), so each wait at the top of a
   // pair covers only the slots that pair consumes.
-  {
+  if (n_pages > 0) {
     PageSlot<D> ring[RING];
     const int ids0 = ids_at(0);
     int ids_next = ids_at(RING);
@@ -449,13 +515,17 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_kernel(DecodeArg
   // ---------------- partition result ----------------
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
-  if (col < G) {
+  if constexpr (BALANCED) {
+    extern __shared__ __align__(16) float balanced_lds[];
+    balanced_merge<D, NB>(a, balanced_lds, blockDim.x >> 6, wave, G, b, h0, acc, m_eff, l_tot);
+  } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk)
       *reinterpret_cast<float4*>(out + blk * 16 + grp * 4) =
           make_float4(acc[blk][0], acc[blk][1], acc[blk][2], acc[blk][3]);
     if (grp == 0) {
+      float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
       ml_base[col * 2] = l_tot > 0.f ? m_eff : -INFINITY;  // l and acc are relative to 2^m_eff
       ml_base[col * 2 + 1] = l_tot;
     }
@@ -1017,7 +1087,7 @@ template <int KIND, int D>
 void launch_kernel(const DecodeArgs& a0, int B, int units, int W, int G, hipStream_t st) {
   const void* fn;
   if constexpr (KIND == K_I8 || KIND == K_FP8)
-    fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D>);
+    fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, false>);
   else if constexpr (KIND == K_Q4)
     fn = reinterpret_cast<const void*>(&decode_stream_q4_kernel);
   else
@@ -1027,7 +1097,7 @@ void launch_kernel(const DecodeArgs& a0, int B, int units, int W, int G, hipStre
   dim3 grid(B + 2 * a.target, units / W, 1);  // at most B + 2 target work items
   dim3 block(64 * W);
   if constexpr (KIND == K_I8 || KIND == K_FP8)
-    hipLaunchKernelGGL((decode_stream_kernel<KIND, D>), grid, block, 0, st, a, G);
+    hipLaunchKernelGGL((decode_stream_kernel<KIND, D, false>), grid, block, 0, st, a, G);
   else if constexpr (KIND == K_Q4)
     hipLaunchKernelGGL(decode_stream_q4_kernel, grid, block, 0, st, a, G);
   else if constexpr (D <= 128)
@@ -1047,6 +1117,22 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Balanced mode: W wavefronts per (sequence, unit) workgroup, W the power of
+// two (<= kMaxBalancedWaves) that brings the launch closest to one resident
+// round of waves without exceeding it (at least 1).
+template <int KIND, int D>
+hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) {
+  const int units = a.KH * ((a.H / a.KH) / G);
+  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true>);
+  // resident waves for 4-wave workgroups (the LDS share of a workgroup is small)
+  const int resident = items_target(fn, 4, (size_t)4 * G * (D + 2) * sizeof(float), 1);
+  int W = 1;
+  while (W < kMaxBalancedWaves && (long)B * units * W * 2 <= resident) W *= 2;
+  const size_t lds = (size_t)W * G * (D + 2) * sizeof(float);
+  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true>), dim3(B, units, 1), dim3(64 * W), lds, st, a, G);
+  return hipGetLastError();
+}
+
 hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
   const int units = a.KH * ((a.H / a.KH) / G);
   int W = kMaxWaves;
@@ -1056,6 +1142,20 @@ hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
 }
 
 }  // namespace
+
+hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
+  if (G < 1 || G > 16) return hipErrorInvalidValue;
+  switch (kind) {
+    case K_I8:
+      return D == 64 ? launch_balanced_d<K_I8, 64>(a, B, G, st)
+                     : D == 128 ? launch_balanced_d<K_I8, 128>(a, B, G, st) : launch_balanced_d<K_I8, 256>(a, B, G, st);
+    case K_FP8:
+      return D == 64 ? launch_balanced_d<K_FP8, 64>(a, B, G, st)
+                     : D == 128 ? launch_balanced_d<K_FP8, 128>(a, B, G, st)
+                                : launch_balanced_d<K_FP8, 256>(a, B, G, st);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
   if (G < 1 || G > 16) return hipErrorInvalidValue;

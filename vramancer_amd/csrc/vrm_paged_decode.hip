@@ -830,6 +830,49 @@ extern "C" int vrm_paged_decode_noalloc(const float* query, const void* kv_pool,
                       D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth);
 }
 
+extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const float* kv_scales,
+                                         const int32_t* page_table, const int32_t* context_lens, float* out,
+                                         float* lse, int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                         int layer_idx, float scale, int kv_dtype, vrm_stream_t stream) {
+  const char* who = "vrm_paged_decode_balanced";
+  int rc = check_common(query, kv_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
+                        scale);
+  if (rc) return rc;
+  const int kind = kind_of(kv_dtype);
+  if (kind != K_I8 && kind != K_FP8) {
+    set_error("%s: kv_dtype %d unsupported (int8 and fp8 pools)", who, kv_dtype);
+    return kind < 0 ? VRM_ERR_ARG : VRM_ERR_UNSUPPORTED;
+  }
+  if (!kv_scales) {
+    set_error("%s: quantized pool needs kv_scales", who);
+    return VRM_ERR_ARG;
+  }
+  DecodeArgs a{};
+  a.query = query;
+  a.pool = static_cast<const uint8_t*>(kv_pool);
+  a.scales = kv_scales;
+  a.page_table = page_table;
+  a.ctx_lens = context_lens;
+  a.B = B;
+  a.H = H;
+  a.KH = KH;
+  a.L = L;
+  a.P = P;
+  a.max_pp = max_pp;
+  a.layer = layer_idx;
+  a.lse = lse;
+  a.out = out;
+  a.qscale = scale * kLog2e;
+  const hipError_t e = launch_stream_balanced(a, kind, B, D, pick_group_tile(H / KH, 16),
+                                              reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", who, hipGetErrorString(e));
+    return (int)e;
+  }
+  clear_error();
+  return VRM_OK;
+}
+
 extern "C" int vrm_paged_decode_partitions(const float* query, const void* kv_pool, const float* kv_scales,
                                            const int32_t* page_table, const int32_t* context_lens, void* workspace,
                                            size_t workspace_bytes, int B, int H, int KH, int D, int PS, int L, int P,

@@ -714,7 +714,7 @@ class PagedKVCacheManager:
             ctx.copy_(buf[:B])
             if n:
                 table.view(-1).index_copy_(0, buf[B:B + n], buf[B + n:].to(torch.int32))
-            c.update(epoch=epoch, counts=counts, buf=buf)
+            c.update(epoch=epoch, counts=counts, ntok=ntok, buf=buf)
             return c["result"]
         width = max_pp + max(16, max_pp // 8)
         host = np.empty(2 * B + 1 + total, dtype=np.int32)  # offsets, token counts, pages: one upload
@@ -729,8 +729,8 @@ class PagedKVCacheManager:
             _lib.ptr(buf[2 * B + 1:]) if total else None, total, _lib.ptr(buf), _lib.ptr(buf[B + 1:]), B, width,
             _lib.ptr(table), _lib.ptr(ctx), _lib.stream_of(table))
         _lib.check(rc, "build_block_table")
-        self._table_cache = dict(key=(rids, dev), epoch=epoch, entries=entries, counts=counts, width=width,
-                                 result=(table, ctx), buf=buf)
+        self._table_cache = dict(key=(rids, dev), epoch=epoch, entries=entries, counts=counts, ntok=ntok,
+                                 width=width, result=(table, ctx), buf=buf)
         return table, ctx
 
     def _workspace(self, B: int, H: int, max_pp: int, device):
@@ -760,8 +760,11 @@ class PagedKVCacheManager:
             return None
         table, ctx = got
         B, H = query.shape[0], query.shape[1]
+        # the host token counts pick the kernel (even batches: the balanced decode)
+        ntok = self._table_cache["ntok"] if self._table_cache is not None else None
         return paged_attention_decode(query, self._gpu_pool, table, ctx, layer_idx, scale, kv_scales=self._kv_scales,
-                                      workspace=self._workspace(B, H, table.shape[1], query.device))
+                                      workspace=self._workspace(B, H, table.shape[1], query.device),
+                                      context_lens_host=ntok)
 
     def _ensure_compressed(self, page_ids: Sequence[int], layer_idx: int) -> None:
         missing = [p for p in dict.fromkeys(page_ids) if self._tq_slots[p, layer_idx] == 0]

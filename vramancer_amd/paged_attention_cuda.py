@@ -26,8 +26,11 @@ from typing import Any, Optional
 
 from . import _lib
 
+_VRM_ERR_UNSUPPORTED = -2
+
 __all__ = [
     "paged_attention_decode",
+    "prefer_balanced",
     "combine_attention",
     "paged_attention_decode_q4",
     "has_cuda_paged_attention",
@@ -53,6 +56,29 @@ def decode_workspace(batch: int, num_heads: int, num_kv_heads: int, head_dim: in
     nsplit = lib.vrm_paged_decode_num_splits(batch, num_heads, num_kv_heads, max_pages_per_seq, page_size)
     nbytes = lib.vrm_paged_decode_workspace_bytes(batch, num_heads, head_dim, max(nsplit, 1))
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+# The balanced decode (one workgroup per sequence and kv-head, partitions
+# merged in LDS; vrm_paged_decode_balanced) replaces the work-item decode when
+# the caller knows the context lengths on the host and they are even: its time
+# follows the longest sequence, the work-item decode's the mean.
+BALANCED_MAX_SPREAD = 1.10   # longest context / mean context
+BALANCED_MIN_PAIRS = 128     # sequences x kv-heads: enough workgroups to fill the GPU
+
+
+def prefer_balanced(context_lens_host, num_kv_heads: int, kv_dtype) -> bool:
+    """True when the balanced decode suits this batch: an int8 or fp8 pool, at
+    least BALANCED_MIN_PAIRS (sequence, kv-head) pairs, and the longest context
+    within BALANCED_MAX_SPREAD of the mean (host-side lengths, no device sync)."""
+    import torch
+
+    if kv_dtype not in (torch.int8, torch.float8_e4m3fn):
+        return False
+    lens = [int(x) for x in context_lens_host]
+    if not lens or len(lens) * num_kv_heads < BALANCED_MIN_PAIRS:
+        return False
+    total = sum(max(x, 0) for x in lens)
+    return total > 0 and max(lens) * len(lens) <= BALANCED_MAX_SPREAD * total
 
 
 def check_outputs(query, out, workspace, page_table, context_lens) -> None:
@@ -106,12 +132,17 @@ def paged_attention_decode(
     out: Any = None,
     workspace: Any = None,
     lse: Any = None,        # optional [B, H] float32 output: ln sum_t exp(scale q.k_t)
+    context_lens_host: Any = None,  # optional host copy of context_lens (list / CPU tensor)
 ) -> Any:
     """Single-token attention straight from the paged KV pool.
 
     Mirrors core/paged_attention_cuda.py:129-184: ``scale`` defaults to
     1/sqrt(head_dim), query head h reads kv-head h // (H / KH), sequences with
     context length <= 0 produce zeros.  Returns [B, H, D] float32.
+
+    ``context_lens_host``, when given, must equal ``context_lens``; it only
+    selects the kernel (``prefer_balanced``): even batches over int8 / fp8
+    pools take the balanced decode, which needs no workspace.
     """
     import torch
 
@@ -138,6 +169,17 @@ def paged_attention_decode(
     if out is None:
         out = torch.empty((B, H, D), dtype=torch.float32, device=query.device)
     lib = _lib.load()
+    if context_lens_host is not None and prefer_balanced(context_lens_host, KH, kv_pool.dtype):
+        if lse is not None:
+            _check_lse(lse, B, H, query.device)
+        rc = lib.vrm_paged_decode_balanced(
+            _lib.ptr(query), _lib.ptr(kv_pool), _lib.ptr(kv_scales), _lib.ptr(page_table), _lib.ptr(context_lens),
+            _lib.ptr(out), _lib.ptr(lse), B, H, KH, D, PS, L, P, max_pp, int(layer_idx), scale, code,
+            _lib.stream_of(query),
+        )
+        if rc != _VRM_ERR_UNSUPPORTED:
+            _lib.check(rc, "paged_attention_decode (balanced)")
+            return out
     if workspace is None:
         workspace = decode_workspace(B, H, KH, D, max_pp, query.device, PS)
     ws_bytes = workspace.numel() * workspace.element_size()
