@@ -142,7 +142,9 @@ int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const floa
  * ln sum_t exp(scale q.k_t) per (b, h) as in vrm_paged_decode_lse.  No
  * counterpart in the reference (whose kernel is one warp per (head, sequence),
  * csrc/paged_attention_kernel.cu:445-499, with no split).
- * Supported: int8 and fp8 pools, D in {64, 128, 256}, PS == 16.
+ * Supported: int8 and fp8 pools, D in {64, 128}, PS == 16, and page tables
+ * narrow enough for a workgroup's LDS copy of one row (max_pp up to ~12000 at
+ * D = 128); other requests return VRM_ERR_UNSUPPORTED.
  */
 int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const float* kv_scales,
                               const int32_t* page_table, const int32_t* context_lens, float* out, float* lse,

@@ -541,8 +541,9 @@ def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
     (40, 8, 128, [37, 1600, 333, 0, 1, 4096]),   # ragged: correct for any lengths
     (64, 8, 128, [512] * 20),                    # even
     (16, 1, 128, [3000, 2999, 17]),              # one kv-head, 8 waves per workgroup
-    (8, 2, 256, [100, 260]),
+    (8, 2, 64, [100, 260]),
     (12, 12, 64, [64, 65, 700]),
+    (28, 4, 128, [8192, 8000, 1]),               # 512 pages in LDS
 ])
 def test_balanced_decode_matches_oracle(dtype, H, KH, D, ctxs):
     """The balanced decode (one workgroup per sequence and kv-head, partitions
@@ -585,6 +586,19 @@ def test_balanced_decode_garbage_absent_pages_and_lse(dtype):
         _assert_close(out[b].cpu(), PD.dense_attention(q[b], K, V, 1 / math.sqrt(128)), f"seq {b}")
     torch.testing.assert_close(lse, lse_ref, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(out, ref_items, atol=1e-5, rtol=1e-5)
+
+
+def test_balanced_decode_refuses_d256_and_the_api_falls_back():
+    """D = 256 is outside the balanced decode (VRM_ERR_UNSUPPORTED); the
+    Python API then runs the work-item decode for the same even batch."""
+    _say("balanced D=256 fallback")
+    q, pool, sc, table, lens = _pool_case(torch.int8, 64, 4, 2, 256, [80] * 64, seed=7)
+    d = [t.to(DEV) for t in (q, pool, sc, table, lens)]
+    with pytest.raises(RuntimeError, match="status -2"):
+        _balanced(*d, 1)
+    out = paged_attention_decode(d[0], d[1], d[3], d[4], 1, kv_scales=d[2], context_lens_host=[80] * 64)
+    torch.cuda.synchronize()
+    _assert_close(out, PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc), "D=256 fallback")
 
 
 def test_api_takes_the_balanced_decode_for_even_batches():

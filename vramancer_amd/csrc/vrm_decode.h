@@ -170,10 +170,24 @@ int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int 
 // K_F16, D the head dimension, G the query heads per wavefront (<= 16).
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
-// Balanced-batch decode: one workgroup per (sequence, kv-head / head chunk)
-// whose W wavefronts split the sequence's pages and merge their partials in
-// LDS, writing a.out (and a.lse) directly: no work items, no workspace, no
-// merge launch.  Correct for any context lengths; its time follows the
+// Balanced mode geometry: workgroups of kUnitsPerWg units x (1, 2 or 4)
+// wavefronts per unit.  LDS: the sequence's page ids [max_pp], the units'
+// page-pair counters [kUnitsPerWg], then (16-byte aligned) the merge area,
+// [W][G][D] accumulators and [W][G][2] (m, l); at most kMaxBalancedLds.
+constexpr int kMaxBalancedWaves = 8;
+constexpr int kUnitsPerWg = 2;
+constexpr size_t kMaxBalancedLds = 64 * 1024;
+__host__ __device__ inline size_t balanced_merge_offset(int max_pp) {
+  return ((size_t)max_pp * 4 + kUnitsPerWg * 4 + 15) / 16 * 16;
+}
+inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
+  return balanced_merge_offset(max_pp) + (size_t)W * G * (D + 2) * sizeof(float);
+}
+
+// Balanced-batch decode: one workgroup per (sequence, kUnitsPerWg units)
+// whose wavefronts take the sequence's page pairs from LDS counters and merge
+// their partials in LDS, writing a.out (and a.lse) directly: no work items,
+// no workspace, no merge launch.  Correct for any context lengths; its time follows the
 // longest sequence, so it suits batches of about equal lengths.  kind is
 // K_I8 or K_FP8 (D 64, 128, 256) or K_BF16 / K_F16 (D 64, 128).
 hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);

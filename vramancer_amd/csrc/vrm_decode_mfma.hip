@@ -137,31 +137,22 @@ struct PageSlot {
 // contiguous run for a whole page-layer), which keeps DRAM accesses local.
 // The wavefronts share nothing and never synchronise.
 constexpr int kMaxWaves = 4;
-// Balanced mode: one workgroup of up to kMaxBalancedWaves wavefronts per
-// (sequence, unit); wavefront w streams the w-th of W equal page ranges.
-constexpr int kMaxBalancedWaves = 8;
+// Balanced mode: one workgroup per (sequence, pair of units), kUnitsPerWg
+// units interleaved over its wavefronts (wave w serves unit w % 2), so that
+// each unit gets as many older as younger wavefronts: a SIMD issues for its
+// oldest wavefront first, and a unit served only by younger wavefronts
+// streams about a quarter slower.  The wavefronts of a unit take page pairs
+// from an LDS counter, so faster ones take more.
 
-// Work of wavefront `wave` of a balanced-mode workgroup: the w-th of W
-// contiguous page ranges of sequence b (empty when the sequence is short).
-__device__ __forceinline__ WorkItem balanced_item(const DecodeArgs& a, int b, int wave, int W) {
-  WorkItem w;
-  w.b = b;
-  w.ctx = a.ctx_lens[b];
-  const int pages = seq_pages(w.ctx, a.max_pp);
-  const int per = (pages + W - 1) / W;
-  w.p_begin = min(wave * per, pages);
-  w.n_pages = min(per, pages - w.p_begin);
-  return w;
-}
-
-// Balanced-mode epilogue: the W wavefronts' partials (max m, sum l, unnormalised
-// accumulator; lane (col, grp) holds dims 16 blk + 4 grp + r of head col) are
-// merged through LDS with log-sum-exp weights 2^(m_w - max m) and written to
-// a.out[b][h0 .. h0 + G - 1] (and a.lse).  LDS: [W][G][D] accumulators, then
-// [W][G][2] (m, l).  Every wavefront of the workgroup must call it.
+// Balanced-mode epilogue: the partials of the workgroup's wavefronts (max m,
+// sum l, unnormalised accumulator; lane (col, grp) holds dims 16 blk + 4 grp +
+// r of head col) are merged per unit through LDS with log-sum-exp weights
+// 2^(m_w - max m) and written to a.out[b][h0(u) .. h0(u) + G - 1] (and
+// a.lse).  Every wavefront of the workgroup must call it.
 template <int D, int NB>
-__device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b, int h0,
-                                               const v4f (&acc)[NB], float m, float l_tot) {
+__device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b,
+                                               int unit0, int units, int chunks, const v4f (&acc)[NB], float m,
+                                               float l_tot) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   float* part = lds;
@@ -177,19 +168,25 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
-    const int g = i / D, d = i - g * D;
+  const int group = a.H / a.KH;
+  for (int i = threadIdx.x; i < kUnitsPerWg * G * D; i += blockDim.x) {
+    const int ul = i / (G * D);
+    const int rem = i - ul * G * D;
+    const int g = rem / D, d = rem - g * D;
+    const int unit = unit0 + ul;
+    if (unit >= units) continue;
     float M = -INFINITY;
-    for (int w = 0; w < W; ++w) M = fmaxf(M, ml[(w * G + g) * 2]);
+    for (int w = ul; w < W; w += kUnitsPerWg) M = fmaxf(M, ml[(w * G + g) * 2]);
     float L = 0.f, o = 0.f;
     if (M != -INFINITY) {
-      for (int w = 0; w < W; ++w) {
+      for (int w = ul; w < W; w += kUnitsPerWg) {
         const float mw = ml[(w * G + g) * 2];
         const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
         L = fmaf(f, ml[(w * G + g) * 2 + 1], L);
         o = fmaf(f, part[((size_t)w * G + g) * D + d], o);
       }
     }
+    const int h0 = (unit / chunks) * group + (unit % chunks) * G;
     const size_t row = (size_t)b * a.H + h0 + g;
     a.out[row * D + d] = L > 0.f ? o * (1.f / L) : 0.f;
     // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
@@ -214,17 +211,37 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   const int chunks = group / G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // item mode: the workgroup's waves are W units of one work item; balanced
-  // mode: they are the W page ranges of one (sequence, unit)
-  const int unit = BALANCED ? (int)blockIdx.y : (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
-  const int kvh = unit / chunks;
-  const int h0 = kvh * group + (unit % chunks) * G;
+  // mode: wave w serves unit kUnitsPerWg * blockIdx.y + w % kUnitsPerWg of
+  // sequence blockIdx.x
+  const int units = a.KH * chunks;
+  const int unit = BALANCED ? (int)blockIdx.y * kUnitsPerWg + wave % kUnitsPerWg
+                            : (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
+  const bool unit_ok = !BALANCED || unit < units;
+  const int kvh = min(unit, units - 1) / chunks;
+  const int h0 = kvh * group + (min(unit, units - 1) % chunks) * G;
 
   // work item (sequence, partition) of this wave; in item mode the first wave
-  // of the launch also records the partition geometry for the merge pass
+  // of the launch also records the partition geometry for the merge pass;
+  // in balanced mode the item is the whole sequence and the wave takes page
+  // pairs of it as it goes
   const int item = blockIdx.x;
   WorkItem wi;
+  int* ids_lds = nullptr;  // balanced mode: the sequence's page ids
+  int* pair_ctr = nullptr;
+  float* merge_lds = nullptr;
   if constexpr (BALANCED) {
-    wi = balanced_item(a, blockIdx.x, wave, blockDim.x >> 6);
+    extern __shared__ __align__(16) int balanced_lds[];
+    wi.b = blockIdx.x;
+    wi.ctx = a.ctx_lens[wi.b];
+    wi.p_begin = 0;
+    wi.n_pages = seq_pages(wi.ctx, a.max_pp);
+    ids_lds = balanced_lds;
+    pair_ctr = balanced_lds + a.max_pp;
+    merge_lds = reinterpret_cast<float*>(reinterpret_cast<char*>(balanced_lds) + balanced_merge_offset(a.max_pp));
+    const int32_t* row = a.page_table + (size_t)wi.b * a.max_pp;
+    for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x) ids_lds[i] = row[i];
+    if (threadIdx.x < kUnitsPerWg) pair_ctr[threadIdx.x] = 0;
+    __syncthreads();
   } else {
     if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
   }
@@ -242,6 +259,62 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
   auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
   auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
+
+  // Loads are issued unconditionally from a clamped, always valid address and
+  // zeroed afterwards for an absent page, so every slot keeps the same loads
+  // in flight (a branch around a load makes the compiler wait for all of them).
+  auto load_page = [&](PageSlot<D>& s, int pid) {
+    const bool ok = page_ok(pid);
+    s.ok = ok;
+    const int pc = ok ? pid : 0;
+    const uint8_t* pb = layer_base + (size_t)pc * page_stride;
+    const uint8_t* kb = pb + col * D + grp * 16;
+    const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      s.k[j] = ld16(kb + j * 64);
+      s.v[j] = ld16(vb + j * 16);
+    }
+    if constexpr (KIND == K_I8) {
+      const size_t ts = head_index(pc, 0) * kPS + grp * 4;
+      s.ks = ldf4(a.scales + ts);
+      s.vs = ldf4(a.scales + ts + (size_t)a.KH * kPS);
+    } else {
+      s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
+      s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
+    }
+    if (!ok) {
+      s.vs = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) s.v[j] = make_uint4(0, 0, 0, 0);
+    }
+  };
+
+  // balanced mode: take the first two page pairs and issue their loads before
+  // the query set-up, so that the set-up runs under their latency
+  const int npairs = (n_pages + 1) / 2;
+  int* const pair_next = BALANCED ? pair_ctr + wave % kUnitsPerWg : nullptr;
+  auto grab = [&]() {
+    int v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(pair_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  auto load_pair = [&](PageSlot<D>& s0, PageSlot<D>& s1, int p) {
+    const int pg = 2 * min(p, npairs - 1);
+    load_page(s0, ids_lds[pg]);
+    load_page(s1, ids_lds[min(pg + 1, n_pages - 1)]);
+  };
+  PageSlot<D> bring[BALANCED ? 4 : 1];
+  int c0 = 0, c1 = 0;
+  const bool bstream = BALANCED && unit_ok && npairs > 0;
+  if constexpr (BALANCED) {
+    if (bstream) {
+      c0 = grab();
+      c1 = grab();
+      load_pair(bring[0], bring[1], c0);
+      load_pair(bring[2], bring[3], c1);
+    }
+  }
 
   // ---------------- query operand: this lane's head is min(col, G - 1) ----------------
   const float* qrow = a.query + ((size_t)b * a.H + h0 + min(col, G - 1)) * D;
@@ -306,36 +379,6 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   v4f acc[NB];           // O^T block blk: rows = dims 16 blk + 4 grp + r, column = head
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) acc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // Loads are issued unconditionally from a clamped, always valid address and
-  // zeroed afterwards for an absent page, so every slot keeps the same loads
-  // in flight (a branch around a load makes the compiler wait for all of them).
-  auto load_page = [&](PageSlot<D>& s, int pid) {
-    const bool ok = page_ok(pid);
-    s.ok = ok;
-    const int pc = ok ? pid : 0;
-    const uint8_t* pb = layer_base + (size_t)pc * page_stride;
-    const uint8_t* kb = pb + col * D + grp * 16;
-    const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      s.k[j] = ld16(kb + j * 64);
-      s.v[j] = ld16(vb + j * 16);
-    }
-    if constexpr (KIND == K_I8) {
-      const size_t ts = head_index(pc, 0) * kPS + grp * 4;
-      s.ks = ldf4(a.scales + ts);
-      s.vs = ldf4(a.scales + ts + (size_t)a.KH * kPS);
-    } else {
-      s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
-      s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
-    }
-    if (!ok) {
-      s.vs = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) s.v[j] = make_uint4(0, 0, 0, 0);
-    }
-  };
 
   // Scores (log2 domain) of this lane's 4 tokens 4 grp + r of page pi; -inf
   // for absent pages and tokens past the context.
@@ -491,10 +534,27 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   };
 
   // ---------------- stream the partition ----------------
-  // Page q sits in slot q % RING.  The refill loads are unconditional (slots
-  // past the last page reload it, an L2 hit), so each wait at the top of a
-  // pair covers only the slots that pair consumes.
-  if (n_pages > 0) {
+  if constexpr (BALANCED) {
+    // Page pairs taken from the unit's LDS counter (in increasing order per
+    // wave), two pairs in the ring: while one pair is consumed the other is
+    // in flight.  Loads past the last pair reload it (clamped, unconditional).
+    if (bstream) {
+      while (c0 < npairs) {
+        const int n0 = grab();
+        process_pair(bring[0], bring[1], 2 * c0, 2 * c0 + 1 < n_pages);
+        load_pair(bring[0], bring[1], n0);
+        c0 = n0;
+        if (c1 >= npairs) break;  // then c0 > c1 is past the end too
+        const int n1 = grab();
+        process_pair(bring[2], bring[3], 2 * c1, 2 * c1 + 1 < n_pages);
+        load_pair(bring[2], bring[3], n1);
+        c1 = n1;
+      }
+    }
+  } else if (n_pages > 0) {
+    // Page q sits in slot q % RING.  The refill loads are unconditional (slots
+    // past the last page reload it, an L2 hit), so each wait at the top of a
+    // pair covers only the slots that pair consumes.
     PageSlot<D> ring[RING];
     const int ids0 = ids_at(0);
     int ids_next = ids_at(RING);
@@ -516,8 +576,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   if constexpr (BALANCED) {
-    extern __shared__ __align__(16) float balanced_lds[];
-    balanced_merge<D, NB>(a, balanced_lds, blockDim.x >> 6, wave, G, b, h0, acc, m_eff, l_tot);
+    balanced_merge<D, NB>(a, merge_lds, blockDim.x >> 6, wave, G, b, blockIdx.y * kUnitsPerWg, units, chunks, acc,
+                          m_eff, l_tot);
   } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
@@ -1117,20 +1177,25 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Balanced mode: W wavefronts per (sequence, unit) workgroup, W the power of
-// two (<= kMaxBalancedWaves) that brings the launch closest to one resident
-// round of waves without exceeding it (at least 1).
+// Balanced mode: workgroups of kUnitsPerWg units x WPU wavefronts per unit,
+// WPU the largest of 4, 2, 1 whose launch fits one resident round of waves
+// and 64 KB of LDS.  Returns hipErrorInvalidValue when even WPU = 1 does not
+// fit (page tables too wide for the LDS copy of the ids).
 template <int KIND, int D>
 hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) {
   const int units = a.KH * ((a.H / a.KH) / G);
+  const int wgs_y = (units + kUnitsPerWg - 1) / kUnitsPerWg;
   const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true>);
-  // resident waves for 4-wave workgroups (the LDS share of a workgroup is small)
-  const int resident = items_target(fn, 4, (size_t)4 * G * (D + 2) * sizeof(float), 1);
-  int W = 1;
-  while (W < kMaxBalancedWaves && (long)B * units * W * 2 <= resident) W *= 2;
-  const size_t lds = (size_t)W * G * (D + 2) * sizeof(float);
-  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true>), dim3(B, units, 1), dim3(64 * W), lds, st, a, G);
-  return hipGetLastError();
+  const int resident = items_target(fn, kMaxBalancedWaves, 0, 1);  // resident waves (capped)
+  for (int wpu = 4; wpu >= 1; wpu /= 2) {
+    const int W = kUnitsPerWg * wpu;
+    const size_t lds = balanced_lds_bytes(a.max_pp, W, G, D);
+    if (lds > kMaxBalancedLds) continue;
+    if (wpu > 1 && (long)B * wgs_y * W > resident) continue;
+    hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true>), dim3(B, wgs_y, 1), dim3(64 * W), lds, st, a, G);
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
@@ -1148,11 +1213,10 @@ hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, i
   switch (kind) {
     case K_I8:
       return D == 64 ? launch_balanced_d<K_I8, 64>(a, B, G, st)
-                     : D == 128 ? launch_balanced_d<K_I8, 128>(a, B, G, st) : launch_balanced_d<K_I8, 256>(a, B, G, st);
+                     : D == 128 ? launch_balanced_d<K_I8, 128>(a, B, G, st) : hipErrorInvalidValue;
     case K_FP8:
       return D == 64 ? launch_balanced_d<K_FP8, 64>(a, B, G, st)
-                     : D == 128 ? launch_balanced_d<K_FP8, 128>(a, B, G, st)
-                                : launch_balanced_d<K_FP8, 256>(a, B, G, st);
+                     : D == 128 ? launch_balanced_d<K_FP8, 128>(a, B, G, st) : hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }

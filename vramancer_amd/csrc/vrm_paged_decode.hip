@@ -847,6 +847,16 @@ extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool
     set_error("%s: quantized pool needs kv_scales", who);
     return VRM_ERR_ARG;
   }
+  if (D != 64 && D != 128) {  // at D = 256 two page pairs per wave do not fit in registers
+    set_error("%s: head_dim %d unsupported (64, 128)", who, D);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  const int G = pick_group_tile(H / KH, 16);
+  if (balanced_lds_bytes(max_pp, kUnitsPerWg, G, D) > kMaxBalancedLds) {
+    set_error("%s: a page table of width %d does not fit the workgroup's LDS copy; use vrm_paged_decode", who,
+              max_pp);
+    return VRM_ERR_UNSUPPORTED;
+  }
   DecodeArgs a{};
   a.query = query;
   a.pool = static_cast<const uint8_t*>(kv_pool);
@@ -863,8 +873,7 @@ extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool
   a.lse = lse;
   a.out = out;
   a.qscale = scale * kLog2e;
-  const hipError_t e = launch_stream_balanced(a, kind, B, D, pick_group_tile(H / KH, 16),
-                                              reinterpret_cast<hipStream_t>(stream));
+  const hipError_t e = launch_stream_balanced(a, kind, B, D, G, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) {
     set_error("%s: kernel launch failed: %s", who, hipGetErrorString(e));
     return (int)e;
