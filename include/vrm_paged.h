@@ -13,7 +13,7 @@
  *
  * Pool layout (the reference's, core/paged_attention.py:321-330):
  *      kv_pool[P][L][2][KH][PS][D]    (index 2 selects K=0 / V=1)
- * with PS = 16 tokens per page.  A sequence's logical page i lives in physical
+ * with PS tokens per page (16 by default).  A sequence's logical page i lives in physical
  * page page_table[b][i]; tokens t < context_lens[b] are attended.
  * Float pools (f32, f16, bf16) keep each [PS][D] slice token-major, exactly as
  * the reference writes it.  The int8 and fp8 pools (this library's codecs,
@@ -104,7 +104,11 @@ size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit);
  *   workspace    >= vrm_paged_decode_workspace_bytes(B, H, D, nsplit) bytes,
  *                nsplit = vrm_paged_decode_num_splits(...); may be NULL when
  *                that size is 0
- * Supported: D in {64, 128, 256}, PS == 16, H % KH == 0.
+ * Supported: any D <= 256 and any page size PS >= 1 (the reference's range,
+ * csrc/paged_attention_kernel.cu:460-466), H % KH == 0; int8 / fp8 pools
+ * need D % 16 == 0 and PS % 4 == 0 (their tiled V), and other shapes return
+ * VRM_ERR_UNSUPPORTED.  Page 16 with D 64 / 128 / 256 runs the tuned
+ * matrix-core kernels; every other shape a generic kernel.
  */
 int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_scales,
                      const int32_t* page_table, const int32_t* context_lens,
@@ -201,6 +205,7 @@ int vrm_attn_combine(const float* out1, const float* lse1, const float* out2, co
  * csrc/paged_attention_kernel.cu:502-549 (wrapper core/paged_attention_cuda.py:238-288).
  *   kv_pool_q4  [P][L][2][KH][PS][D/2] uint8
  *   kv_scales, kv_zeros [P][L][2][KH][PS][D/32] float16 (passed as uint16 bits)
+ * Supported: D % 32 == 0 (D <= 256), any page size.
  */
 int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4,
                         const uint16_t* kv_scales, const uint16_t* kv_zeros,
@@ -228,7 +233,8 @@ int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4,
  *                   re-encoded as e4m3(fp32(e4m3 code) * s / s') when s' > s,
  *                   then the new row is e4m3(x / s') (round to nearest even).
  *                   Several tokens of one call must not share a page.
- * kv_pool/kv_scales as in vrm_paged_decode.
+ * kv_pool/kv_scales as in vrm_paged_decode.  Supported: D a multiple of 16 up
+ * to 256, PS a multiple of 4.
  */
 int vrm_kv_quant_append(const void* key, const void* value, int src_dtype,
                         const int32_t* page_ids, const int32_t* slots, int N,

@@ -12,7 +12,7 @@ fp8-e4m3fn, per (page, layer, K/V, kv-head) over the page's valid tokens:
     scale = amax(|x|) / 448
     code  = (x / scale).to(float8_e4m3fn)         (round to nearest even)
 pool layout: each (page, layer, K/V, kv-head) slice holds PS x D codes
-    (PS = 16, D a multiple of 16); K is token-major like the reference's pool,
+    (PS a multiple of 4, D a multiple of 16); K is token-major like the reference's pool,
     V is tiled: the code of token t, dim d sits at byte
         ((t // 4 * 16 + d % 16) * (D // 16) + d // 16) * 4 + t % 4
     (four consecutive tokens of one dim share a dword; the 16 dims d % 16 of a
@@ -85,20 +85,20 @@ def dequantize_fp8(codes_u8, scale):
 
 
 def v_token_major(v_slices):
-    """Physical V slices [..., 16, D] (tiled as the pool stores them) ->
-    logical [..., 16, D] (token t, dim d at [t, d])."""
+    """Physical V slices [..., PS, D] (tiled as the pool stores them) ->
+    logical [..., PS, D] (token t, dim d at [t, d]); PS % 4 == 0, D % 16 == 0."""
     *lead, PS, D = v_slices.shape
-    assert PS == 16 and D % 16 == 0, (PS, D)
+    assert PS % 4 == 0 and D % 16 == 0, (PS, D)
     # physical axes (t // 4, d % 16, d // 16, t % 4) -> logical (t // 4, t % 4, d // 16, d % 16)
-    tiles = v_slices.reshape(*lead, 4, 16, D // 16, 4)
+    tiles = v_slices.reshape(*lead, PS // 4, 16, D // 16, 4)
     return tiles.transpose(-1, -3).reshape(*lead, PS, D)
 
 
 def v_pool_order(v_logical):
-    """Logical V [..., 16, D] -> the pool's tiled physical [..., 16, D]."""
+    """Logical V [..., PS, D] -> the pool's tiled physical [..., PS, D]."""
     *lead, PS, D = v_logical.shape
-    assert PS == 16 and D % 16 == 0, (PS, D)
-    tiles = v_logical.reshape(*lead, 4, 4, D // 16, 16)
+    assert PS % 4 == 0 and D % 16 == 0, (PS, D)
+    tiles = v_logical.reshape(*lead, PS // 4, 4, D // 16, 16)
     return tiles.transpose(-1, -3).contiguous().reshape(*lead, PS, D)
 
 

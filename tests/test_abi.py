@@ -66,8 +66,9 @@ def test_decode_rejects_bad_arguments(lib):
     assert _decode(lib, q=None) == -1 and b"null" in lib.vrm_last_error()
     assert _decode(lib, H=7) == -1 and b"multiple" in lib.vrm_last_error()
     assert _decode(lib, layer=1) == -1 and b"layer_idx" in lib.vrm_last_error()
-    assert _decode(lib, D=96) == -2 and b"head_dim" in lib.vrm_last_error()
-    assert _decode(lib, PS=32) == -2 and b"page_size" in lib.vrm_last_error()
+    assert _decode(lib, D=257) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert _decode(lib, D=100, dt=_lib.VRM_KV_I8, sc=1) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert _decode(lib, PS=6, dt=_lib.VRM_KV_FP8E4M3, sc=1) == -2 and b"page_size" in lib.vrm_last_error()
     assert _decode(lib, dt=99) == -1 and b"kv_dtype" in lib.vrm_last_error()
     assert _decode(lib, dt=_lib.VRM_KV_I8) == -1 and b"kv_scales" in lib.vrm_last_error()
     assert _decode(lib, sc=1) == -1 and b"float pool" in lib.vrm_last_error()
@@ -91,6 +92,8 @@ def test_quant_rejects_bad_arguments(lib):
     assert call(src=7) == -1
     assert call(layer=2) == -1
     assert call(D=100) == -2
+    assert call(D=264) == -2
+    assert call(PS=6) == -2
     assert call(N=0) == 0  # nothing to do, nothing launched
 
 

@@ -60,9 +60,8 @@ def test_decode_matches_oracle_on_benchmark_shapes(name, kw):
     _assert_close(out, _oracle(inp, layer), name)
 
 
-def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pad=1, v_mag=None):
+def _pool_case(dtype, B, H, KH, D, ctxs, L=2, layer=1, seed=0, spare=3, table_pad=1, v_mag=None, PS=16):
     g = torch.Generator().manual_seed(seed)
-    PS = 16
     npages = [(max(c, 0) + PS - 1) // PS for c in ctxs]
     P = sum(npages) + spare
     base = torch.randn(P, L, 2, KH, PS, D, generator=g)
@@ -615,3 +614,71 @@ def test_api_takes_the_balanced_decode_for_even_batches():
                                      context_lens_host=ctxs)
         torch.cuda.synchronize()
         _assert_close(out, PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc), f"api {want}")
+
+
+# Head dims and page sizes outside the tuned kernels' (page 16, head_dim 64 /
+# 128 / 256): the reference kernel takes any head_dim <= 256 and the pool's
+# page size (csrc/paged_attention_kernel.cu:102-111, 460-466).  int8 / fp8
+# pools need D % 16 == 0 and PS % 4 == 0 (their tiled V).
+SHAPES_ALL = [(80, 16), (96, 16), (112, 16), (96, 8), (128, 8), (128, 32), (64, 32), (48, 4)]
+SHAPES_FLOAT = [(100, 16), (72, 7), (256, 5), (30, 32), (1, 16)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("D,PS", SHAPES_ALL, ids=[f"D{d}-PS{p}" for d, p in SHAPES_ALL])
+def test_decode_other_head_dims_and_page_sizes(dtype, D, PS):
+    _say(f"shape {dtype} D {D} PS {PS}")
+    ctxs = [5 * PS + 3, 1, 700, 0]
+    q, pool, sc, table, lens = _pool_case(dtype, 4, 12, 4, D, ctxs, seed=D * 7 + PS, PS=PS)
+    out, ref = _run_both(q, pool, sc, table, lens, 1)
+    _assert_close(out, ref, f"{dtype} D{D} PS{PS}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16], ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("D,PS", SHAPES_FLOAT, ids=[f"D{d}-PS{p}" for d, p in SHAPES_FLOAT])
+def test_decode_float_pools_any_head_dim_and_page_size(dtype, D, PS):
+    """Float pools at head_dims that are not multiples of 4 or 16 and odd
+    page sizes, including the reference's maximum head_dim 256 at page 5."""
+    _say(f"float shape {dtype} D {D} PS {PS}")
+    ctxs = [3 * PS + 1, 260, 17]
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 8, 2, D, ctxs, seed=D + PS, PS=PS)
+    out, ref = _run_both(q, pool, sc, table, lens, 1)
+    _assert_close(out, ref, f"{dtype} D{D} PS{PS}")
+
+
+@pytest.mark.parametrize("D,PS", [(96, 16), (64, 8), (128, 32), (160, 4)])
+def test_decode_q4_other_head_dims_and_page_sizes(D, PS):
+    _say(f"q4 D={D} PS={PS}")
+    g = torch.Generator().manual_seed(D + PS)
+    B, H, KH, L = 3, 8, 2, 2
+    ctxs = [70, 1, 400]
+    npages = [(c + PS - 1) // PS for c in ctxs]
+    P = sum(npages) + 2
+    packed = torch.randint(0, 256, (P, L, 2, KH, PS, D // 2), generator=g, dtype=torch.uint8)
+    sc = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 0.1 + 0.01).half()
+    zp = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 15).half()
+    perm = torch.randperm(P, generator=g)
+    table = torch.full((B, max(npages)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = torch.randn(B, H, D, generator=g)
+    lens = torch.tensor(ctxs, dtype=torch.int32)
+    out = paged_attention_decode_q4(q.to(DEV), packed.to(DEV), sc.to(DEV), zp.to(DEV), table.to(DEV), lens.to(DEV), 1)
+    torch.cuda.synchronize()
+    _assert_close(out.cpu(), PD.paged_attention_decode_q4(q, packed, sc, zp, table, lens, 1), f"q4 D{D} PS{PS}")
+
+
+def test_decode_other_shapes_absent_pages_and_many_partitions():
+    """D = 96, page 8: a long context split over many work items, an absent
+    page, and the int8 pool written through the quantizer."""
+    _say("D96 PS8 long + absent")
+    q, pool, sc, table, lens = _pool_case(torch.int8, 2, 16, 2, 96, [9001, 2000], L=1, layer=0, seed=13, PS=8)
+    table[0, 7] = -1
+    out = paged_attention_decode(q.to(DEV), pool.to(DEV), table.to(DEV), lens.to(DEV), 0, kv_scales=sc.to(DEV))
+    torch.cuda.synchronize()
+    f = _dequant_pool(pool, sc, 0)
+    for b in range(2):
+        K, V = PD.gather_sequence(f, table[b], int(lens[b]), 0, skip_invalid=True)
+        _assert_close(out[b].cpu(), PD.dense_attention(q[b], K, V, 1 / math.sqrt(96)), f"seq {b}")

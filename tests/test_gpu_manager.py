@@ -363,3 +363,42 @@ def test_turbo_batch_matches_single_requests():
     table, ctx = _host_table(m, rids)
     ref = PD.paged_attention_decode_turbo(_params(m._kv_compressor), qb, _codes(m, 0), table, ctx, head_map="mod")
     _assert_close(out, ref, "batch vs oracle")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32", "int8", "fp8"])
+@pytest.mark.parametrize("D,PS", [(96, 8), (80, 32)])
+def test_manager_decode_other_head_dims_and_page_sizes(dtype, D, PS):
+    """The manager's pool, writes, block table and decode at head_dim 96 with
+    pages of 8 tokens and head_dim 80 with pages of 32 (the reference's
+    PagedKVConfig takes any page_size and head_dim)."""
+    _say(f"manager {dtype} D{D} PS{PS}")
+    m = _mgr(dtype=dtype, num_kv_heads=4, max_pages=128, num_layers=2, head_dim=D, page_size=PS)
+    rids = ["a", "b", "c"]
+    _fill(m, rids, [3 * PS + 5, 1, 90], torch.bfloat16, seed=D + PS)
+    q = torch.randn(3, 8, D, generator=torch.Generator().manual_seed(9))
+    out = m.compute_attention_decode(q.to(DEV), rids, 1)
+    torch.cuda.synchronize()
+    table, ctx = _host_table(m, rids)
+    sc = None if m._kv_scales is None else m._kv_scales.cpu()
+    _assert_close(out, PD.paged_attention_decode(q, m._gpu_pool.cpu(), table, ctx, 1, kv_scales=sc),
+                  f"{dtype} D{D} PS{PS}")
+
+
+@pytest.mark.parametrize("dtype", ["int8", "fp8"])
+def test_manager_even_batch_takes_the_balanced_decode(dtype):
+    """32 requests of equal length over 4 kv-heads (128 pairs): the manager
+    hands its token counts to the decode, which takes the balanced kernel;
+    the output matches the oracle."""
+    from vramancer_amd.paged_attention_cuda import prefer_balanced
+
+    _say(f"manager balanced {dtype}")
+    m = _mgr(dtype=dtype, num_kv_heads=4, max_pages=160, num_layers=2, head_dim=128)
+    rids = [f"r{i}" for i in range(32)]
+    _fill(m, rids, [40] * 32, torch.bfloat16, seed=21, layers=[1])
+    q = torch.randn(32, 12, 128, generator=torch.Generator().manual_seed(2))
+    out = m.compute_attention_decode(q.to(DEV), rids, 1)
+    torch.cuda.synchronize()
+    assert prefer_balanced(m._table_cache["ntok"], 4, m._gpu_pool.dtype)
+    table, ctx = _host_table(m, rids)
+    _assert_close(out, PD.paged_attention_decode(q, m._gpu_pool.cpu(), table, ctx, 1, kv_scales=m._kv_scales.cpu()),
+                  f"balanced {dtype}")

@@ -127,3 +127,56 @@ def test_dequantize_pages_exact(codec):
         else:
             ref = KC.dequantize_fp8(pc[pid, 1].view(torch.uint8), sc[pid, 1][..., None, None])
         assert torch.equal(out[i], ref)
+
+
+@pytest.mark.parametrize("codec", ["int8", "fp8"])
+@pytest.mark.parametrize("D,PS", [(80, 16), (96, 8), (112, 32), (48, 4), (128, 32)])
+def test_quant_other_head_dims_and_page_sizes(codec, D, PS):
+    """Whole-page writes, appends and dequantization at head_dims and page
+    sizes beside 64 / 128 / 256 and 16 (any multiple of 16, and of 4): codes
+    and scales bit-identical to the codec definitions."""
+    _say(f"quant {codec} D{D} PS{PS}")
+    P, L, KH, NP = 9, 2, 3, 4
+    pool, scales = kv_quant.allocate_pool(P, L, KH, D, codec, PS, device=DEV)
+    kp = _src((NP, KH, PS, D), torch.bfloat16, D + PS)
+    vp = _src((NP, KH, PS, D), torch.bfloat16, D + PS + 1)
+    page_ids = torch.tensor([8, 0, 5, 2], dtype=torch.int32)
+    n_valid = torch.tensor([PS, 1, PS - 1, PS // 2], dtype=torch.int32)
+    kv_quant.quantize_pages(pool, scales, 1, page_ids.to(DEV), kp.to(DEV), vp.to(DEV), n_valid.to(DEV))
+    # one appended token into the half-full page (int8: slot PS // 2 of page 2)
+    kn = _src((1, KH, D), torch.float16, 3 * D)
+    vn = _src((1, KH, D), torch.float16, 3 * D + 1)
+    if codec == "int8":
+        kv_quant.quantize_append(pool, scales, 1, torch.tensor([2], dtype=torch.int32, device=DEV),
+                                 torch.tensor([PS // 2], dtype=torch.int32, device=DEV), kn.to(DEV), vn.to(DEV))
+    torch.cuda.synchronize()
+    pool_c = kv_quant.logical_view(pool).cpu().view(torch.uint8)
+    sc_c = scales.cpu()
+    for n in range(NP):
+        pid, nv = int(page_ids[n]), int(n_valid[n])
+        for kv, src in ((0, kp), (1, vp)):
+            for h in range(KH):
+                if codec == "int8":
+                    codes, s = KC.quantize_int8(src[n, h])
+                    codes = codes.view(torch.uint8).clone()
+                    s = s.clone()
+                    codes[nv:] = 0
+                    s[nv:] = 0
+                    if pid == 2:
+                        c1, s1 = KC.quantize_int8((kn if kv == 0 else vn)[0, h])
+                        codes[PS // 2] = c1.view(torch.uint8)
+                        s[PS // 2] = s1
+                    assert torch.equal(pool_c[pid, 1, kv, h], codes), (n, kv, h)
+                    assert torch.equal(sc_c[pid, 1, kv, h], s), (n, kv, h)
+                else:
+                    codes, s = KC.quantize_fp8_page(src[n, h], nv)
+                    assert torch.equal(pool_c[pid, 1, kv, h], codes), (n, kv, h)
+                    assert sc_c[pid, 1, kv, h].item() == s.item(), (n, kv, h)
+    out = kv_quant.dequantize_pages(pool, scales, 1, page_ids.to(DEV)).cpu()
+    pc = kv_quant.logical_view(pool).cpu()
+    for i, pid in enumerate(page_ids.tolist()):
+        if codec == "int8":
+            ref = KC.dequantize_int8(pc[pid, 1], sc_c[pid, 1])
+        else:
+            ref = KC.dequantize_fp8(pc[pid, 1].view(torch.uint8), sc_c[pid, 1][..., None, None])
+        assert torch.equal(out[i], ref)

@@ -5,7 +5,8 @@
 namespace vrm {
 namespace dec {
 
-constexpr int kPS = 16;               // tokens per page (the reference's default)
+constexpr int kPS = 16;               // tokens per page (the reference's default; the tuned kernels' page)
+constexpr int kMaxHeadDim = 256;      // the reference kernel's limit (csrc/paged_attention_kernel.cu:460)
 constexpr float kLog2e = 1.4426950408889634f;
 
 enum KvKind { K_F32 = 0, K_F16 = 1, K_BF16 = 2, K_I8 = 3, K_FP8 = 4, K_Q4 = 5 };
@@ -73,8 +74,9 @@ struct WorkItem {
   int ctx;      // context length of the sequence
 };
 
-__device__ __forceinline__ int seq_pages(int ctx, int max_pp) {
-  return ctx > 0 ? min((ctx + kPS - 1) / kPS, max_pp) : 0;
+// Pages of a sequence of ctx tokens (pages of ps tokens), capped by the table width.
+__device__ __forceinline__ int seq_pages(int ctx, int max_pp, int ps = kPS) {
+  return ctx > 0 ? min((ctx + ps - 1) / ps, max_pp) : 0;
 }
 
 __device__ __forceinline__ int wave_sum_int(int v) {
@@ -97,12 +99,13 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 // same geometry from the context lengths; when `writer` is set the wave also
 // stores it in the header.  Returns false when `item` lies past the last item.
 __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, int B, int max_pp, int target,
-                                          int item, bool writer, int32_t* __restrict__ header, WorkItem& w) {
+                                          int item, bool writer, int32_t* __restrict__ header, WorkItem& w,
+                                          int ps = kPS) {
   const int lane = __lane_id();
   int S = 0;
   for (int c = 0; c < B; c += 64) {
     const int b = c + lane;
-    S += b < B ? seq_pages(ctx_lens[b], max_pp) : 0;
+    S += b < B ? seq_pages(ctx_lens[b], max_pp, ps) : 0;
   }
   S = wave_sum_int(S);
   auto roundup4 = [](int v) { return max(4, (v + 3) / 4 * 4); };
@@ -110,14 +113,14 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
   int tails = 0;
   for (int c = 0; c < B; c += 64) {
     const int b = c + lane;
-    const int pages = b < B ? seq_pages(ctx_lens[b], max_pp) : 0;
+    const int pages = b < B ? seq_pages(ctx_lens[b], max_pp, ps) : 0;
     tails += (pages % pps) != 0 ? 1 : 0;
   }
   if (wave_sum_int(tails) * 8 > target) pps = roundup4((S + 2 * target - 1) / (2 * target));
   int n_full = 0;
   for (int c = 0; c < B; c += 64) {
     const int b = c + lane;
-    n_full += b < B ? seq_pages(ctx_lens[b], max_pp) / pps : 0;
+    n_full += b < B ? seq_pages(ctx_lens[b], max_pp, ps) / pps : 0;
   }
   n_full = wave_sum_int(n_full);
   bool found = false;
@@ -125,7 +128,7 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
   for (int c = 0; c < B; c += 64) {
     const int b = c + lane;
     const int ctx = b < B ? ctx_lens[b] : 0;
-    const int pages = seq_pages(ctx, max_pp);
+    const int pages = seq_pages(ctx, max_pp, ps);
     const int nf = pages / pps;
     const int nt = pages - nf * pps > 0 ? 1 : 0;
     const int incl_f = wave_inclusive_scan(nf) + carry_f;
@@ -165,6 +168,12 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
 
 // Work items one resident round of `kernel` holds (see work items above).
 int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int units);
+
+// Generic VALU partition pass for every pool kind at any head_dim <= 256 and
+// any page size (vrm_decode_generic.hip): the shapes the tuned kernels do
+// not compile for.  D and PS are runtime values; int8 / fp8 pools need
+// D % 16 == 0 and PS % 4 == 0 (their tiled V), Q4 pools D % 32 == 0.
+hipError_t launch_generic(const DecodeArgs& a, int kind, int B, int D, int PS, hipStream_t st);
 
 // Single-pass matrix-core (MFMA) split pass; kind is K_I8, K_FP8, K_BF16 or
 // K_F16, D the head dimension, G the query heads per wavefront (<= 16).

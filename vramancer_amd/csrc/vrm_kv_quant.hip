@@ -22,7 +22,6 @@
 namespace vrm {
 namespace {
 
-constexpr int kPS = 16;
 
 template <int SRC>
 __device__ __forceinline__ float load_src(const void* p, size_t i) {
@@ -55,6 +54,7 @@ struct QuantArgs {
   uint8_t* pool;
   float* scales;
   int KH, L, P, layer;
+  int D, PS;               // head_dim (multiple of 16, <= 256) and page size (multiple of 4)
 };
 
 __device__ __forceinline__ size_t head_index(const QuantArgs& a, int pid, int kv, int h) {
@@ -67,67 +67,66 @@ __device__ __forceinline__ int code_offset(int kv, int t, int d, int D) {
 }
 
 // int8, one wavefront per (token row, K/V, head).  src rows: [N][KH][D]
-// (append) or [NP][KH][PS][D] (pages).
-template <int SRC, int D, bool PAGES>
+// (append) or [NP][KH][PS][D] (pages).  DMAX = 64, 128 or 256 >= D.
+template <int SRC, int DMAX, bool PAGES>
 __global__ void __launch_bounds__(64) quant_i8_kernel(QuantArgs a) {
-  constexpr int PER = D / 64;
+  constexpr int PER = DMAX / 64;
+  const int D = a.D, PS = a.PS;
   const int lane = threadIdx.x;
   const int kv = blockIdx.x / a.KH, h = blockIdx.x % a.KH;
   const int n = blockIdx.y;
   const int t = PAGES ? blockIdx.z : 0;
   const int pid = a.page_ids[n];
   const int slot = PAGES ? t : a.slots[n];
-  if (pid < 0 || pid >= a.P || slot < 0 || slot >= kPS) return;
+  if (pid < 0 || pid >= a.P || slot < 0 || slot >= PS) return;
   const bool valid = PAGES ? (t < a.slots[n]) : true;
   const void* src = kv ? a.value : a.key;
-  const size_t row = PAGES ? (((size_t)n * a.KH + h) * kPS + t) * D : ((size_t)n * a.KH + h) * D;
+  const size_t row = PAGES ? (((size_t)n * a.KH + h) * PS + t) * D : ((size_t)n * a.KH + h) * D;
   float x[PER];
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    x[i] = valid ? load_src<SRC>(src, row + i * 64 + lane) : 0.f;
+    const int d = i * 64 + lane;
+    x[i] = (valid && d < D) ? load_src<SRC>(src, row + d) : 0.f;
     amax = fmaxf(amax, fabsf(x[i]));
   }
   amax = group_max<64>(amax);
   const float scale = __fdiv_rn(amax, 127.f);
-  int8_t* dst = reinterpret_cast<int8_t*>(a.pool) + head_index(a, pid, kv, h) * kPS * D;
+  int8_t* dst = reinterpret_cast<int8_t*>(a.pool) + head_index(a, pid, kv, h) * PS * D;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) dst[code_offset(kv, slot, i * 64 + lane, D)] = int8_code(x[i], scale);
-  if (lane == 0) a.scales[head_index(a, pid, kv, h) * kPS + slot] = scale;
+  for (int i = 0; i < PER; ++i) {
+    const int d = i * 64 + lane;
+    if (d < D) dst[code_offset(kv, slot, d, D)] = int8_code(x[i], scale);
+  }
+  if (lane == 0) a.scales[head_index(a, pid, kv, h) * PS + slot] = scale;
 }
 
-// fp8 whole pages, one 256-thread workgroup per (page, K/V, head).
-template <int SRC, int D>
+// fp8 whole pages, one 256-thread workgroup per (page, K/V, head): the page
+// maximum over its valid tokens, then the codes (the source is read twice).
+template <int SRC>
 __global__ void __launch_bounds__(256) quant_fp8_pages_kernel(QuantArgs a) {
-  constexpr int N = kPS * D;
-  constexpr int PER = N / 256;
+  const int D = a.D, PS = a.PS;
+  const int N = PS * D;
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int kv = blockIdx.x / a.KH, h = blockIdx.x % a.KH;
   const int n = blockIdx.y;
   const int pid = a.page_ids[n];
   if (pid < 0 || pid >= a.P) return;
-  const int n_valid = min(max(a.slots[n], 0), kPS);
+  const int n_valid = min(max(a.slots[n], 0), PS);
   const void* src = kv ? a.value : a.key;
   const size_t base = ((size_t)n * a.KH + h) * N;
-  float x[PER];
   float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int idx = i * 256 + tid;
-    x[i] = (idx / D < n_valid) ? load_src<SRC>(src, base + idx) : 0.f;
-    amax = fmaxf(amax, fabsf(x[i]));
-  }
+  for (int idx = tid; idx < n_valid * D; idx += 256) amax = fmaxf(amax, fabsf(load_src<SRC>(src, base + idx)));
   amax = group_max<64>(amax);
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float scale = __fdiv_rn(amax, 448.f);
   uint8_t* dst = a.pool + head_index(a, pid, kv, h) * N;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int idx = i * 256 + tid;
-    dst[code_offset(kv, idx / D, idx % D, D)] = (idx / D < n_valid) ? fp8_code(x[i], scale) : (uint8_t)0;
+  for (int idx = tid; idx < N; idx += 256) {
+    const int t = idx / D, d = idx - t * D;
+    dst[code_offset(kv, t, d, D)] = t < n_valid ? fp8_code(load_src<SRC>(src, base + idx), scale) : (uint8_t)0;
   }
   if (tid == 0) a.scales[head_index(a, pid, kv, h)] = scale;
 }
@@ -135,27 +134,20 @@ __global__ void __launch_bounds__(256) quant_fp8_pages_kernel(QuantArgs a) {
 // fp8 append, one 256-thread workgroup per (token, K/V, head).  The page
 // scale only grows; when it does, the codes already in the page are
 // re-encoded against the new scale.
-template <int SRC, int D>
+template <int SRC>
 __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
-  constexpr int PER = (D + 255) / 256;
+  const int D = a.D, PS = a.PS;  // D <= 256: one element per thread
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int kv = blockIdx.x / a.KH, h = blockIdx.x % a.KH;
   const int n = blockIdx.y;
   const int pid = a.page_ids[n];
   const int slot = a.slots[n];
-  if (pid < 0 || pid >= a.P || slot < 0 || slot >= kPS) return;
+  if (pid < 0 || pid >= a.P || slot < 0 || slot >= PS) return;
   const void* src = kv ? a.value : a.key;
   const size_t row = ((size_t)n * a.KH + h) * D;
-  float x[PER];
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = i * 256 + tid;
-    x[i] = d < D ? load_src<SRC>(src, row + d) : 0.f;
-    amax = fmaxf(amax, fabsf(x[i]));
-  }
-  amax = group_max<64>(amax);
+  const float x = tid < D ? load_src<SRC>(src, row + tid) : 0.f;
+  float amax = group_max<64>(fabsf(x));
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   const size_t hi = head_index(a, pid, kv, h);
   // Every thread reads the old scale before the barrier; thread 0 overwrites it after.
@@ -164,7 +156,7 @@ __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float want = __fdiv_rn(amax, 448.f);
   const float scale = fmaxf(old_scale, want);
-  uint8_t* page = a.pool + hi * (size_t)(kPS * D);
+  uint8_t* page = a.pool + hi * (size_t)(PS * D);
   if (slot > 0 && scale > old_scale) {
     for (int idx = tid; idx < slot * D; idx += 256) {
       const int off = code_offset(kv, idx / D, idx % D, D);
@@ -172,11 +164,7 @@ __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
       page[off] = fp8_code(y, scale);
     }
   }
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = i * 256 + tid;
-    if (d < D) page[code_offset(kv, slot, d, D)] = fp8_code(x[i], scale);
-  }
+  if (tid < D) page[code_offset(kv, slot, tid, D)] = fp8_code(x, scale);
   if (tid == 0) a.scales[hi] = scale;
 }
 
@@ -186,7 +174,7 @@ __global__ void __launch_bounds__(256) dequant_pages_kernel(QuantArgs a, float* 
   const int kv = blockIdx.x / a.KH, h = blockIdx.x % a.KH;
   const int n = blockIdx.y;
   const int pid = a.page_ids[n];
-  const size_t N = (size_t)kPS * D;
+  const size_t N = (size_t)a.PS * D;
   float* o = out + (((size_t)n * 2 + kv) * a.KH + h) * N;
   if (pid < 0 || pid >= a.P) {
     for (size_t i = threadIdx.x; i < N; i += 256) o[i] = 0.f;
@@ -200,7 +188,7 @@ __global__ void __launch_bounds__(256) dequant_pages_kernel(QuantArgs a, float* 
     if (FP8) {
       o[i] = e4m3fn_to_f32(c) * a.scales[hi];
     } else {
-      o[i] = (float)(int8_t)c * a.scales[hi * kPS + t];
+      o[i] = (float)(int8_t)c * a.scales[hi * a.PS + t];
     }
   }
 }
@@ -228,12 +216,12 @@ int check_quant(const void* key, const void* value, int src_dtype, const int32_t
     set_error("%s: kv_dtype %d is not a quantized pool", who, kv_dtype);
     return VRM_ERR_ARG;
   }
-  if (PS != kPS) {
-    set_error("%s: page_size %d unsupported (compiled for %d)", who, PS, kPS);
+  if (PS <= 0 || PS % 4 || PS > 65535) {
+    set_error("%s: page_size %d unsupported (a positive multiple of 4)", who, PS);
     return VRM_ERR_UNSUPPORTED;
   }
-  if (D != 64 && D != 128 && D != 256) {
-    set_error("%s: head_dim %d unsupported (64, 128, 256)", who, D);
+  if (D % 16 || D > 256) {
+    set_error("%s: head_dim %d unsupported (a multiple of 16 up to 256)", who, D);
     return VRM_ERR_UNSUPPORTED;
   }
   if (n > 65535 || 2 * KH > 65535) {
@@ -243,28 +231,29 @@ int check_quant(const void* key, const void* value, int src_dtype, const int32_t
   return VRM_OK;
 }
 
-template <int SRC, int D>
+template <int SRC, int DMAX>
 void launch_quant(const QuantArgs& a, int n, int kv_dtype, bool pages, hipStream_t st) {
   if (kv_dtype == VRM_KV_I8) {
     if (pages)
-      hipLaunchKernelGGL((quant_i8_kernel<SRC, D, true>), dim3(2 * a.KH, n, kPS), dim3(64), 0, st, a);
+      hipLaunchKernelGGL((quant_i8_kernel<SRC, DMAX, true>), dim3(2 * a.KH, n, a.PS), dim3(64), 0, st, a);
     else
-      hipLaunchKernelGGL((quant_i8_kernel<SRC, D, false>), dim3(2 * a.KH, n, 1), dim3(64), 0, st, a);
+      hipLaunchKernelGGL((quant_i8_kernel<SRC, DMAX, false>), dim3(2 * a.KH, n, 1), dim3(64), 0, st, a);
   } else {
     if (pages)
-      hipLaunchKernelGGL((quant_fp8_pages_kernel<SRC, D>), dim3(2 * a.KH, n), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((quant_fp8_pages_kernel<SRC>), dim3(2 * a.KH, n), dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((quant_fp8_append_kernel<SRC, D>), dim3(2 * a.KH, n), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((quant_fp8_append_kernel<SRC>), dim3(2 * a.KH, n), dim3(256), 0, st, a);
   }
 }
 
 template <int SRC>
 void launch_quant_d(const QuantArgs& a, int n, int kv_dtype, bool pages, int D, hipStream_t st) {
-  switch (D) {
-    case 64: launch_quant<SRC, 64>(a, n, kv_dtype, pages, st); break;
-    case 128: launch_quant<SRC, 128>(a, n, kv_dtype, pages, st); break;
-    default: launch_quant<SRC, 256>(a, n, kv_dtype, pages, st); break;
-  }
+  if (D <= 64)
+    launch_quant<SRC, 64>(a, n, kv_dtype, pages, st);
+  else if (D <= 128)
+    launch_quant<SRC, 128>(a, n, kv_dtype, pages, st);
+  else
+    launch_quant<SRC, 256>(a, n, kv_dtype, pages, st);
 }
 
 int run_quant(const void* key, const void* value, int src_dtype, const int32_t* page_ids, const int32_t* slots,
@@ -276,7 +265,7 @@ int run_quant(const void* key, const void* value, int src_dtype, const int32_t* 
     clear_error();
     return VRM_OK;
   }
-  QuantArgs a{key, value, page_ids, slots, static_cast<uint8_t*>(pool), scales, KH, L, P, layer};
+  QuantArgs a{key, value, page_ids, slots, static_cast<uint8_t*>(pool), scales, KH, L, P, layer, D, PS};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (src_dtype) {
     case VRM_SRC_F32: launch_quant_d<VRM_SRC_F32>(a, n, kv_dtype, pages, D, st); break;
@@ -318,8 +307,8 @@ extern "C" int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales,
     set_error("%s: bad sizes", who);
     return VRM_ERR_ARG;
   }
-  if (PS != kPS) {
-    set_error("%s: page_size %d unsupported", who, PS);
+  if (PS <= 0 || PS % 4 || D % 16 || D > 256) {
+    set_error("%s: page_size %d / head_dim %d unsupported (multiples of 4 / 16)", who, PS, D);
     return VRM_ERR_UNSUPPORTED;
   }
   if (kv_dtype != VRM_KV_I8 && kv_dtype != VRM_KV_FP8E4M3) {
@@ -328,7 +317,7 @@ extern "C" int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales,
   }
   if (NP == 0) return VRM_OK;
   QuantArgs a{nullptr, nullptr, page_ids, nullptr, const_cast<uint8_t*>(static_cast<const uint8_t*>(kv_pool)),
-              const_cast<float*>(kv_scales), KH, L, P, layer_idx};
+              const_cast<float*>(kv_scales), KH, L, P, layer_idx, D, PS};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (kv_dtype == VRM_KV_FP8E4M3)
     hipLaunchKernelGGL(dequant_pages_kernel<true>, dim3(2 * KH, NP), dim3(256), 0, st, a, out, D);

@@ -324,17 +324,17 @@ __global__ void __launch_bounds__(64) decode_split_kernel(DecodeArgs a) {
 // header by the partition pass.  Four wavefronts each fold every fourth
 // partial, BATCH at a time with all loads issued together (clamped,
 // unconditional), and the four results are combined through LDS.
-template <int D>
+template <int DMAX>
 __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restrict__ part_acc,
                                                             const float* __restrict__ part_ml,
                                                             const int32_t* __restrict__ header,
                                                             float* __restrict__ out, float* __restrict__ lse, int H,
-                                                            int B) {
-  constexpr int PER = D / 64;
+                                                            int B, int D) {
+  constexpr int PER = DMAX / 64;  // dims per lane; lanes past D idle
   constexpr int BATCH = 4;
   constexpr int WAVES = 4;
   __shared__ float sh_m[WAVES], sh_l[WAVES];
-  __shared__ float sh_res[WAVES][D];
+  __shared__ float sh_res[WAVES][DMAX];
   const int h = blockIdx.x, b = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int first = header[kHeaderInts + b];
@@ -357,7 +357,7 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
       m[buf][k] = part_ml[it * 2];
       l[buf][k] = part_ml[it * 2 + 1];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) x[buf][k][i] = part_acc[it * D + i * 64 + lane];
+      for (int i = 0; i < PER; ++i) x[buf][k][i] = i * 64 + lane < D ? part_acc[it * D + i * 64 + lane] : 0.f;
     }
   };
   auto fold_batch = [&](int buf, int s0) {
@@ -418,7 +418,8 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
     const float inv = L > 0.f ? 1.f / L : 0.f;
     float* dst = out + ((size_t)b * H + h) * D;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) dst[i * 64 + lane] = o[i] * inv;
+    for (int i = 0; i < PER; ++i)
+      if (i * 64 + lane < D) dst[i * 64 + lane] = o[i] * inv;
     // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
     if (lse && lane == 0) lse[(size_t)b * H + h] = L > 0.f ? (gm + log2f(L)) * 0.6931471805599453f : -INFINITY;
   }
@@ -494,20 +495,15 @@ hipError_t dispatch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) 
 hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStream_t st) {
   dim3 grid(a.H, B);
   const dim3 block(256);
-  switch (D) {
-    case 64:
-      hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
-                         a.H, B);
-      break;
-    case 128:
-      hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
-                         a.H, B);
-      break;
-    default:
-      hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
-                         a.H, B);
-      break;
-  }
+  if (D <= 64)
+    hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
+                       a.H, B, D);
+  else if (D <= 128)
+    hipLaunchKernelGGL(decode_reduce_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
+                       a.H, B, D);
+  else
+    hipLaunchKernelGGL(decode_reduce_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
+                       a.H, B, D);
   return hipGetLastError();
 }
 
@@ -538,12 +534,8 @@ int check_common(const float* query, const void* pool, const int32_t* page_table
     set_error("vrm_paged_decode: scale is NaN");
     return VRM_ERR_ARG;
   }
-  if (PS != kPS) {
-    set_error("vrm_paged_decode: page_size %d unsupported (compiled for %d)", PS, kPS);
-    return VRM_ERR_UNSUPPORTED;
-  }
-  if (D != 64 && D != 128 && D != 256) {
-    set_error("vrm_paged_decode: head_dim %d unsupported (64, 128, 256)", D);
+  if (D > kMaxHeadDim) {
+    set_error("vrm_paged_decode: head_dim %d above %d", D, kMaxHeadDim);
     return VRM_ERR_UNSUPPORTED;
   }
   if (B > 65535 || (long)B * H > 65535L * 65535L) {
@@ -556,7 +548,22 @@ int check_common(const float* query, const void* pool, const int32_t* page_table
 // Which passes run_decode enqueues.
 enum Passes { kBoth = 3, kPartitionsOnly = 1, kMergeOnly = 2 };
 
-int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D,
+// Shape limits of the pool kinds (VRM_ERR_UNSUPPORTED outside them): the
+// int8 / fp8 pools' tiled V needs D % 16 and PS % 4, the 4-bit pool's groups
+// D % 32.
+int check_kind_shape(int kind, int D, int PS, const char* who) {
+  if ((kind == K_I8 || kind == K_FP8) && (D % 16 || PS % 4)) {
+    set_error("%s: int8 / fp8 pools need head_dim %% 16 == 0 and page_size %% 4 == 0 (got %d, %d)", who, D, PS);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  if (kind == K_Q4 && D % 32) {
+    set_error("%s: head_dim %d is not a multiple of the group size 32", who, D);
+    return VRM_ERR_UNSUPPORTED;
+  }
+  return VRM_OK;
+}
+
+int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t workspace_bytes, int B, int D, int PS,
                float scale, hipStream_t st, int passes) {
   // The matrix-core stream kernels take the int8 / fp8 pools at every
   // head_dim, the 16-bit float pools at D <= 128 (at D = 256 their registers
@@ -565,8 +572,11 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   // the VALU kernel.
   const bool q4_aligned = ((reinterpret_cast<uintptr_t>(a.pool) & 3) | (reinterpret_cast<uintptr_t>(a.q4_scale) & 7) |
                            (reinterpret_cast<uintptr_t>(a.q4_zero) & 7)) == 0;
-  const bool mfma = kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128) ||
-                    (kind == K_Q4 && D == 128 && q4_aligned);
+  // The tuned kernels are compiled for page 16 and head_dim 64 / 128 / 256;
+  // every other shape runs on the generic kernel (vrm_decode_generic.hip).
+  const bool tuned = PS == kPS && (D == 64 || D == 128 || D == 256);
+  const bool mfma = tuned && (kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128) ||
+                              (kind == K_Q4 && D == 128 && q4_aligned));
   const int max_tile = mfma ? 16 : kind == K_Q4 ? 6 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
@@ -583,7 +593,13 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
   hipError_t e = hipSuccess;
-  if (passes & kPartitionsOnly) {
+  if ((passes & kPartitionsOnly) && !tuned) {
+    e = launch_generic(a, kind, B, D, PS, st);
+    if (e != hipSuccess) {
+      set_error("vrm_paged_decode: partition kernel launch failed: %s", hipGetErrorString(e));
+      return (int)e;
+    }
+  } else if (passes & kPartitionsOnly) {
     switch (kind) {
       case K_F32: e = dispatch_d<K_F32>(a, B, D, G, st); break;
       case K_F16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_F16>(a, B, D, G, st); break;
@@ -681,7 +697,9 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
   a.max_pp = max_pp;
   a.layer = layer_idx;
   a.lse = lse;
-  return run_decode(a, kind, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
+  rc = check_kind_shape(kind, D, PS, "vrm_paged_decode");
+  if (rc) return rc;
+  return run_decode(a, kind, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
                     passes);
 }
 
@@ -694,9 +712,9 @@ int tq_entry(const float* query, const uint8_t* tq_pool, const int32_t* page_tab
   int rc = check_common(query, tq_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
                         scale);
   if (rc) return rc;
-  if (D != 128 || qjl_dim != 64) {
-    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128 and qjl_dim 64 (got %d, %d)", D,
-              qjl_dim);
+  if (D != 128 || qjl_dim != 64 || PS != kPS) {
+    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128, qjl_dim 64 and page 16 (got %d, %d, "
+              "%d)", D, qjl_dim, PS);
     return VRM_ERR_UNSUPPORTED;
   }
   if (bits < 2 || bits > 4) {
@@ -847,8 +865,8 @@ extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool
     set_error("%s: quantized pool needs kv_scales", who);
     return VRM_ERR_ARG;
   }
-  if (D != 64 && D != 128) {  // at D = 256 two page pairs per wave do not fit in registers
-    set_error("%s: head_dim %d unsupported (64, 128)", who, D);
+  if ((D != 64 && D != 128) || PS != kPS) {  // at D = 256 two page pairs per wave do not fit in registers
+    set_error("%s: head_dim %d / page_size %d unsupported (64 or 128, page 16)", who, D, PS);
     return VRM_ERR_UNSUPPORTED;
   }
   const int G = pick_group_tile(H / KH, 16);
@@ -904,7 +922,7 @@ extern "C" int vrm_paged_decode_merge(const int32_t* context_lens, float* out, c
     set_error("vrm_paged_decode_merge: bad sizes");
     return VRM_ERR_ARG;
   }
-  if (PS != kPS || (D != 64 && D != 128 && D != 256)) {
+  if (PS <= 0 || D <= 0 || D > kMaxHeadDim) {
     set_error("vrm_paged_decode_merge: unsupported page_size %d / head_dim %d", PS, D);
     return VRM_ERR_UNSUPPORTED;
   }
@@ -918,7 +936,7 @@ extern "C" int vrm_paged_decode_merge(const int32_t* context_lens, float* out, c
   // The merge reads the partition geometry the partition pass left in the
   // workspace header; the dtype below only selects the workspace layout,
   // which is the same for every pool.
-  return run_decode(a, K_I8, out, const_cast<void*>(workspace), workspace_bytes, B, D, 1.f,
+  return run_decode(a, K_I8, out, const_cast<void*>(workspace), workspace_bytes, B, D, PS, 1.f,
                     reinterpret_cast<hipStream_t>(stream), kMergeOnly);
 }
 
@@ -951,7 +969,7 @@ extern "C" int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4
   a.P = P;
   a.max_pp = max_pp;
   a.layer = layer_idx;
-  return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, scale, reinterpret_cast<hipStream_t>(stream),
+  return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
                     kBoth);
 }
 
