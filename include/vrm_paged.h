@@ -358,15 +358,25 @@ int vrm_unpack_bits(const uint8_t* packed, long long rows, int M, int bits, uint
  * dicts per (page, layer, slot) (core/paged_attention.py:568-675, 1420-1496)
  * and attends them with compute_attention_turbo (:1259-1418).  Here the same
  * codes live in a device pool tq_pool[P][L][2][KH][slice] (bytes), one slice
- * of vrm_tq_slice_bytes() per (page, layer, K/V, kv-head) holding the page's
- * 16 tokens: angle bins (in a lane-friendly order of the reference's 127
- * bins), fp16 radius and, for K, the 64 QJL sign bits and the fp16 residual
- * norm.  Built for head_dim 128 (padded_dim 128), qjl_dim 64 and 2..4 bits
- * per angle; signs / jl / angle_lut are the compressor's buffers and the
+ * of vrm_tq_slice_bytes_ps() per (page, layer, K/V, kv-head) holding the
+ * page's tokens: angle bins, fp16 radius and, for K, the QJL sign bits and the
+ * fp16 residual norm.  Every compressor setting of the reference's
+ * KVCacheCompressor (core/kv_quantizer.py:205-240) with head_dim 33..256
+ * (padded_dim 64 / 128 / 256), 1..8 bits per angle and qjl_dim 1..256 is
+ * served, at any page size.  head_dim 128, qjl_dim 64, 2..4 bits and 16-token
+ * pages use a tuned slice (angle bins in a lane-friendly order of the
+ * reference's 127 bins) and decode kernel; every other setting a generic
+ * slice of per-token records (level-major angle bits, sign bits, radius,
+ * norm).  signs / jl / angle_lut are the compressor's buffers and the
  * {cos, sin} table of vrm_turboquant_compress.
  * -------------------------------------------------------------------------- */
 
-/* Bytes of one (page, layer, K/V, kv-head) slice; 0 for an unsupported shape. */
+/* Bytes of one (page, layer, K/V, kv-head) slice of page_size tokens; 0 for
+ * an unsupported setting.  No reference counterpart: the reference keeps
+ * per-slot dicts (core/paged_attention.py:568-675), the pool needs a size. */
+size_t vrm_tq_slice_bytes_ps(int head_dim, int bits, int qjl_dim, int page_size);
+
+/* vrm_tq_slice_bytes_ps at the default 16-token page. */
 size_t vrm_tq_slice_bytes(int head_dim, int bits, int qjl_dim);
 
 /*
@@ -376,7 +386,7 @@ size_t vrm_tq_slice_bytes(int head_dim, int bits, int qjl_dim);
  * path); V rows store angles and radius only (the attention never reads a
  * value's QJL fields).  Replaces write_kv's enqueue + flush_compression
  * (core/paged_attention.py:615-675).  Rows aimed at pages outside [0, P) or
- * slots outside [0, 16) are dropped.
+ * slots outside [0, PS) are dropped.
  */
 int vrm_tq_quant_append(const void* key, const void* value, int src_dtype,
                         const int32_t* page_ids, const int32_t* slots, int N,
@@ -385,7 +395,7 @@ int vrm_tq_quant_append(const void* key, const void* value, int src_dtype,
                         const float* angle_lut, vrm_stream_t stream);
 
 /*
- * Bulk write of whole pages (key/value [NP][KH][16][D]); page n holds
+ * Bulk write of whole pages (key/value [NP][KH][PS][D]); page n holds
  * n_valid[n] tokens, later slots get zero codes.  Replaces compress_page_bulk
  * (core/paged_attention.py:1420-1496).
  */
@@ -398,7 +408,7 @@ int vrm_tq_quant_pages(const void* key, const void* value, int src_dtype,
 /*
  * compress_page_bulk's device work (core/paged_attention.py:1420-1496): reads
  * pages page_ids[n] of layer layer_idx from a float pool kv_pool[P][L][2][KH]
- * [16][D] (kv_dtype f32, f16 or bf16, the manager's raw pool) and writes
+ * [PS][D] (kv_dtype f32, f16 or bf16, the manager's raw pool) and writes
  * their codes into the same (page, layer) of tq_pool; page n holds n_valid[n]
  * tokens, later slots get zero codes.  Codes as vrm_tq_quant_pages.
  */
@@ -409,8 +419,9 @@ int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int32_t* page_
 
 /*
  * Reads pages back in the reference's raw code format: row
- * ((n * 2 + kv) * KH + h) * 16 + t gets radius (fp16 bits), the 127
- * level-major bins, 64 sign bytes and the norm (V rows: zero signs / norm).
+ * ((n * 2 + kv) * KH + h) * PS + t gets radius (fp16 bits), the
+ * padded_dim - 1 level-major bins, qjl_dim sign bytes and the norm (V rows:
+ * zero signs / norm).
  * Inspection and offload helper.
  */
 int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids, int NP,

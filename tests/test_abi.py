@@ -130,7 +130,9 @@ def test_manager_and_attend_entries_reject_bad_arguments(lib):
 
     cp = lib.vrm_tq_compress_pool
     assert cp(1, _lib.VRM_KV_I8, 1, 1, 2, 1, 2, 128, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == -1
-    assert cp(1, _lib.VRM_KV_F16, 1, 1, 2, 1, 2, 64, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == -2
+    assert cp(1, _lib.VRM_KV_F16, 1, 1, 2, 1, 2, 300, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == -2
+    assert cp(1, _lib.VRM_KV_F16, 1, 1, 2, 1, 2, 96, 16, 1, 4, 0, 9, 64, 1, 1, 1, None) == -2
+    assert cp(1, _lib.VRM_KV_F16, 1, 1, 2, 1, 2, 96, 16, 1, 4, 0, 3, 257, 1, 1, 1, None) == -2
     assert cp(1, _lib.VRM_KV_F16, 1, 1, 0, 1, 2, 128, 16, 1, 4, 0, 3, 64, 1, 1, 1, None) == 0
 
     sb = lib.vrm_turboquant_score_workspace_bytes(5, 128, 64)
@@ -166,6 +168,28 @@ def test_manager_and_attend_entries_reject_bad_arguments(lib):
                                     _lib.VRM_KV_F32, None) == -1
     assert lib.vrm_paged_decode_tq_lse(1, 1, 1, 1, 1, None, 1, 1 << 30, 2, 8, 8, 128, 16, 1, 4, 4, 0, 0.1, 3, 64,
                                        1, 1, 1, 0, None) == -1
+
+
+def test_tq_slice_sizes():
+    """Slice sizes of the two TurboQuant page layouts, from their field
+    lists: the tuned one (head_dim 128, qjl_dim 64, 2..4 bits, 16 tokens:
+    16 * bits angle bytes, 8 sign bytes, 2 radius and 2 norm bytes a token)
+    and the generic one (a token record of ceil((padded_dim - 1) * bits / 32)
+    angle dwords, ceil(qjl_dim / 32) sign dwords and two fp16 fields)."""
+    lib = _lib.load()
+    for bits in (2, 3, 4):
+        assert lib.vrm_tq_slice_bytes(128, bits, 64) == 16 * (16 * bits + 8 + 4)
+        assert lib.vrm_tq_slice_bytes_ps(128, bits, 64, 16) == 16 * (16 * bits + 8 + 4)
+    cases = [  # head_dim, bits, qjl_dim, page_size, padded_dim
+        (96, 3, 64, 4, 128), (64, 1, 32, 16, 64), (64, 8, 33, 5, 64), (256, 5, 256, 16, 256),
+        (33, 2, 1, 1, 64), (128, 4, 64, 8, 128), (128, 1, 64, 16, 128), (200, 7, 100, 3, 256),
+    ]
+    for hd, bits, qjl, ps, pd in cases:
+        rec = 4 * (-(-(pd - 1) * bits // 32)) + 4 * (-(-qjl // 32)) + 4
+        assert lib.vrm_tq_slice_bytes_ps(hd, bits, qjl, ps) == ps * rec, (hd, bits, qjl, ps)
+    for bad in [(32, 3, 64, 16), (257, 3, 64, 16), (96, 0, 64, 16), (96, 9, 64, 16), (96, 3, 0, 16),
+                (96, 3, 257, 16), (96, 3, 64, 0)]:
+        assert lib.vrm_tq_slice_bytes_ps(*bad) == 0, bad
 
 
 def test_python_api_refuses_cpu_tensors():

@@ -53,6 +53,7 @@ SIGNATURES = {
     "vrm_turboquant_compress": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p]),
     "vrm_turboquant_decompress": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _i, _p]),
     "vrm_tq_slice_bytes": (_sz, [_i, _i, _i]),
+    "vrm_tq_slice_bytes_ps": (_sz, [_i, _i, _i, _i]),
     "vrm_tq_quant_append": (_i, [_p, _p, _i, _p, _p, _i, _p] + [_i] * 8 + [_p, _p, _p, _p]),
     "vrm_tq_quant_pages": (_i, [_p, _p, _i, _p, _p, _i, _p] + [_i] * 8 + [_p, _p, _p, _p]),
     "vrm_tq_read_pages": (_i, [_p, _p, _i] + [_i] * 8 + [_p, _p, _p, _p, _p]),

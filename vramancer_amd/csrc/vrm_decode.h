@@ -1,6 +1,7 @@
 // Types shared by the decode kernels of libvrm_paged.so.
 #pragma once
 #include "vrm_common.h"
+#include "vrm_tq_layout.h"
 
 namespace vrm {
 namespace dec {
@@ -203,12 +204,20 @@ hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, i
 
 // Paged decode over TurboQuant pages (vrm_decode_tq.hip).
 struct TqDecodeArgs {
-  const float* signs;  // [128] Hadamard signs
-  const float* jl;     // [64][128] JL matrix
+  const float* signs;  // [padded_dim] Hadamard signs
+  const float* jl;     // [qjl][padded_dim] JL matrix
   const float* lut;    // [cos level 0, sin level 0, cos levels >= 1, sin levels >= 1][2^bits]
-  float qjl_coef;      // sqrt(pi / 2) / 64
+  float qjl_coef;      // sqrt(pi / 2) / qjl, or 0 for scores without the QJL term
 };
 hipError_t launch_tq_decode(const DecodeArgs& a, const TqDecodeArgs& tq, int bits, int B, int G, hipStream_t st);
+
+// Paged decode over TurboQuant pages in the generic layout (vrm_decode_tq_generic.hip):
+// every compressor setting and page size the tuned kernel above does not
+// serve.  tq.lut holds 4 << bits floats, tq.signs padded_dim, tq.jl
+// [qjl][padded_dim]; D is the head_dim (<= padded_dim).
+hipError_t launch_tq_generic(const DecodeArgs& a, const TqDecodeArgs& tq, const tq::GenLayout& gl, int B, int D,
+                             hipStream_t st);
+size_t tq_generic_lds_bytes(const tq::GenLayout& gl);
 
 // Largest divisor of the GQA group size that is <= max_tile.
 inline int pick_group_tile(int group, int max_tile) {

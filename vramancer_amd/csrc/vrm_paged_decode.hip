@@ -624,9 +624,10 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   return VRM_OK;
 }
 
-// Partition pass over TurboQuant pages, then the shared merge.
-int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, float* out, void* workspace, size_t workspace_bytes,
-                  int B, int D, float scale, hipStream_t st) {
+// Partition pass over TurboQuant pages, then the shared merge.  gl is the
+// generic layout's geometry, or null for the tuned layout.
+int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, const tq::GenLayout* gl, float* out,
+                  void* workspace, size_t workspace_bytes, int B, int D, float scale, hipStream_t st) {
   const int G = pick_group_tile(a.H / a.KH, 16);
   a.B = B;
   const long cap = items_capacity(B, a.KH);
@@ -639,7 +640,7 @@ int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, float* out, vo
   a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
-  hipError_t e = launch_tq_decode(a, tq, bits, B, G, st);
+  hipError_t e = gl ? launch_tq_generic(a, tq, *gl, B, D, st) : launch_tq_decode(a, tq, bits, B, G, st);
   if (e != hipSuccess) {
     set_error("vrm_paged_decode_tq: partition kernel launch failed: %s", hipGetErrorString(e));
     return (int)e;
@@ -712,13 +713,15 @@ int tq_entry(const float* query, const uint8_t* tq_pool, const int32_t* page_tab
   int rc = check_common(query, tq_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
                         scale);
   if (rc) return rc;
-  if (D != 128 || qjl_dim != 64 || PS != kPS) {
-    set_error("vrm_paged_decode_tq: TurboQuant pages are built for head_dim 128, qjl_dim 64 and page 16 (got %d, %d, "
-              "%d)", D, qjl_dim, PS);
+  const bool tuned = tq::tuned_layout(D, bits, qjl_dim, PS);
+  if (!tuned && !tq::generic_ok(D, bits, qjl_dim, PS)) {
+    set_error("vrm_paged_decode_tq: TurboQuant pages take head_dim 33 .. 256, 1 .. 8 bits per angle, qjl_dim "
+              "1 .. 256 and a positive page size (got %d, %d, %d, %d)", D, bits, qjl_dim, PS);
     return VRM_ERR_UNSUPPORTED;
   }
-  if (bits < 2 || bits > 4) {
-    set_error("vrm_paged_decode_tq: bits_per_angle %d unsupported (2, 3, 4)", bits);
+  const tq::GenLayout gl = tq::gen_layout(D, bits, qjl_dim, PS);
+  if (!tuned && tq_generic_lds_bytes(gl) > 64 * 1024) {
+    set_error("vrm_paged_decode_tq: setting needs %zu bytes of LDS", tq_generic_lds_bytes(gl));
     return VRM_ERR_UNSUPPORTED;
   }
   if (!signs || !jl || !angle_lut) {
@@ -737,8 +740,9 @@ int tq_entry(const float* query, const uint8_t* tq_pool, const int32_t* page_tab
   a.max_pp = max_pp;
   a.layer = layer_idx;
   a.lse = lse;
-  TqDecodeArgs tq{signs, jl, angle_lut, qjl_coef};
-  return run_tq_decode(a, tq, bits, out, workspace, workspace_bytes, B, D, scale,
+  // the QJL coefficient sqrt(pi / 2) / qjl_dim, or 0 for scores without the term
+  TqDecodeArgs tq{signs, jl, angle_lut, qjl_coef != 0.f ? (float)(1.2533141373155003 / qjl_dim) : 0.f};
+  return run_tq_decode(a, tq, bits, tuned ? nullptr : &gl, out, workspace, workspace_bytes, B, D, scale,
                        reinterpret_cast<hipStream_t>(stream));
 }
 

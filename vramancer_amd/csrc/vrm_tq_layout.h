@@ -36,6 +36,7 @@
 // level-major bins (core/kv_quantizer.py:262-287): level l holds 64 >> l
 // angles and angle i of level l pairs elements 2 i, 2 i + 1 of level l - 1.
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 
 namespace vrm {
@@ -97,6 +98,62 @@ __host__ __device__ inline int bin_index_of(int g, int s, int bits) {
   }
   const int j = s / 3, r = s % 3;
   return r == 0 ? level_offset(1) + 8 * g + j : level_offset(0) + 16 * g + 2 * j + (r - 1);
+}
+
+// ---------------------------------------------------------------------------
+// Generic page layout: every other setting of the compressor (head_dim 33 ..
+// 256, i.e. padded_dim 64 / 128 / 256, 1 to 8 bits per angle, qjl_dim 1 ..
+// 256) and any page size.  A slice holds the page's PS tokens as records of
+// record_bytes(), in token order:
+//   angle bits   [angle_dw dwords]   level-major bin b at bits
+//                                    [b * bits, (b + 1) * bits), bit i of the
+//                                    record being bit i % 32 of dword i / 32
+//   sign bits    [sign_dw dwords]    QJL sign j at bit j (K only; V: zero)
+//   radius       fp16                final polar radius
+//   norm         fp16                residual norm (K only; V: zero)
+// ---------------------------------------------------------------------------
+struct GenLayout {
+  int pd;        // padded dim (64, 128, 256)
+  int levels;    // log2(pd)
+  int bits;      // bits per angle (1 .. 8)
+  int qjl;       // QJL rows
+  int ps;        // tokens per page
+  int angle_dw;  // dwords of angle bits per record
+  int sign_dw;   // dwords of sign bits per record
+  __host__ __device__ int record_bytes() const { return 4 * (angle_dw + sign_dw) + 4; }
+  __host__ __device__ int radius_offset() const { return 4 * (angle_dw + sign_dw); }
+  __host__ __device__ size_t slice_bytes() const { return (size_t)ps * record_bytes(); }
+};
+
+// Padded dim of a head_dim: the next power of two (the reference's
+// 2^ceil(log2 head_dim), core/kv_quantizer.py:225), or 0 outside 33 .. 256.
+__host__ __device__ inline int padded_dim_of(int head_dim) {
+  if (head_dim < 33 || head_dim > 256) return 0;
+  int pd = 64;
+  while (pd < head_dim) pd <<= 1;
+  return pd;
+}
+
+__host__ __device__ inline GenLayout gen_layout(int head_dim, int bits, int qjl, int ps) {
+  GenLayout g{};
+  g.pd = padded_dim_of(head_dim);
+  g.levels = g.pd == 64 ? 6 : g.pd == 128 ? 7 : 8;
+  g.bits = bits;
+  g.qjl = qjl;
+  g.ps = ps;
+  g.angle_dw = ((g.pd - 1) * bits + 31) / 32;
+  g.sign_dw = (qjl + 31) / 32;
+  return g;
+}
+
+// True for the settings the tuned layout above (and its decode kernel) serves.
+__host__ __device__ inline bool tuned_layout(int head_dim, int bits, int qjl, int ps) {
+  return head_dim == kPD && qjl == kQjl && ps == kTokens && bits >= 2 && bits <= 4;
+}
+
+// True for settings the generic layout serves.
+__host__ __device__ inline bool generic_ok(int head_dim, int bits, int qjl, int ps) {
+  return padded_dim_of(head_dim) != 0 && bits >= 1 && bits <= 8 && qjl >= 1 && qjl <= 256 && ps >= 1;
 }
 
 }  // namespace tq

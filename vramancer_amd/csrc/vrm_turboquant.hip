@@ -20,6 +20,7 @@
 // One 64-lane wavefront per row; the row lives in LDS between stages.
 #include "vrm_common.h"
 #include "vrm_fdlibm_atan2f.h"
+#include "vrm_tq_common.h"
 #include "vrm_tq_layout.h"
 
 #include <math.h>
@@ -28,66 +29,6 @@ namespace vrm {
 namespace {
 
 #pragma clang fp contract(off)
-
-// IEEE square root.  HIP's __fsqrt_rn is the approximate native v_sqrt_f32 in
-// this toolchain; sqrtf lowers to the correctly rounded sequence (hipcc's
-// default -fhip-fp32-correctly-rounded-divide-sqrt), as does '/'.
-__device__ __forceinline__ float sqrt_rn(float x) { return sqrtf(x); }
-
-template <int SRC>
-__device__ __forceinline__ float load_row(const void* p, size_t i) {
-  if constexpr (SRC == VRM_SRC_F32) {
-    return static_cast<const float*>(p)[i];
-  } else if constexpr (SRC == VRM_SRC_F16) {
-    return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-  } else {
-    return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
-  }
-}
-
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
-  return __builtin_bit_cast(unsigned short, (_Float16)x);  // round to nearest even
-}
-
-// Each row of the codec belongs to one wavefront, whose LDS working set no
-// other wavefront touches.  A wavefront's LDS operations complete in program
-// order, so a wavefront-scope fence is what orders one lane's LDS writes
-// before another lane's later reads: no s_barrier, and workgroups can carry
-// several rows whose wavefronts never wait for each other.
-__device__ __forceinline__ void row_sync() { __syncwarp(); }
-
-// In-register Walsh-Hadamard transform of a PD-element row spread as element
-// e -> (lane e % 64, register e / 64); same butterfly order as the reference.
-template <int PD>
-__device__ __forceinline__ void fwht(float (&v)[PD / 64], int lane) {
-  constexpr int PER = PD / 64;
-#pragma unroll
-  for (int h = 1; h < PD; h <<= 1) {
-    if (h < 64) {
-#pragma unroll
-      for (int k = 0; k < PER; ++k) {
-        float other;
-        switch (h) {
-          case 1: other = xor_shfl<1>(v[k]); break;
-          case 2: other = xor_shfl<2>(v[k]); break;
-          case 4: other = xor_shfl<4>(v[k]); break;
-          case 8: other = xor_shfl<8>(v[k]); break;
-          case 16: other = xor_shfl<16>(v[k]); break;
-          default: other = xor_shfl<32>(v[k]); break;
-        }
-        // lower element keeps a + b, upper keeps a - b with a = lower, b = upper
-        v[k] = (lane & h) ? __fsub_rn(other, v[k]) : __fadd_rn(v[k], other);
-      }
-    } else {
-      const int rh = h / 64;
-      float nv[PER];
-#pragma unroll
-      for (int k = 0; k < PER; ++k) nv[k] = (k & rh) ? __fsub_rn(v[k ^ rh], v[k]) : __fadd_rn(v[k], v[k ^ rh]);
-#pragma unroll
-      for (int k = 0; k < PER; ++k) v[k] = nv[k];
-    }
-  }
-}
 
 struct TqArgs {
   const void* kv;
@@ -384,6 +325,109 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
   row_sync();
   if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(BITS) + t * 8)[lane] = sign_bits[lane];
   if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = f32_to_f16_bits(norm);
+}
+
+// Writer of the generic page layout (vrm_tq_layout.h, GenLayout): every
+// compressor setting the tuned layout does not cover, any page size.  One
+// wavefront per (row, K/V), one row per workgroup; the codes are those of
+// tq_compress_kernel.
+template <int SRC, int PD>
+__global__ void __launch_bounds__(64) tq_pool_write_gen_kernel(TqPoolArgs a, tq::GenLayout g) {
+  __shared__ RowLds<PD> w;
+  __shared__ uint32_t sign_words[8];  // qjl <= 256
+  const int lane = threadIdx.x;
+  const int x = blockIdx.x;
+  const int kv = blockIdx.y;
+  // append: x = n * KH + h (token n); pages: x = (np * KH + h) * PS + t
+  int n, h, t;
+  bool live = true;
+  if (a.slots) {
+    n = x / a.KH;
+    h = x % a.KH;
+    t = a.slots[n];
+  } else {
+    t = x % g.ps;
+    h = (x / g.ps) % a.KH;
+    n = x / (g.ps * a.KH);
+    live = t < a.n_valid[n];
+  }
+  size_t src_first = (size_t)x * a.head_dim;
+  const int pid = a.page_ids[n];
+  if (pid < 0 || pid >= a.P || t < 0 || t >= g.ps) return;  // rows aimed outside the pool are dropped
+  if (a.from_pool) src_first = (((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * g.ps + t) * a.head_dim;
+  uint8_t* rec = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * g.slice_bytes() +
+                 (size_t)t * g.record_bytes();
+  uint32_t* rec32 = reinterpret_cast<uint32_t*>(rec);
+  uint16_t* rad16 = reinterpret_cast<uint16_t*>(rec + g.radius_offset());
+  if (!live) {  // slots past the page's valid tokens hold zero records
+    for (int i = lane; i < g.record_bytes() / 4; i += 64) rec32[i] = 0;
+    return;
+  }
+  float v[PD / 64];
+  const void* src = kv ? a.value : a.key;
+  const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, g.bits, v, w, lane);
+  // angle dword k covers record bits [32 k, 32 k + 32): bins from the one holding bit 32 k
+  for (int k = lane; k < g.angle_dw; k += 64) {
+    uint32_t word = 0;
+    for (int b = (32 * k) / g.bits; b < PD - 1 && b * g.bits < 32 * k + 32; ++b) {
+      const int shift = b * g.bits - 32 * k;  // negative for a bin straddling the dword start
+      const uint32_t val = w.bins[b];
+      word |= shift >= 0 ? (val << shift) : (val >> -shift);
+    }
+    rec32[k] = word;
+  }
+  if (lane == 0) rad16[0] = f32_to_f16_bits(radius);
+  if (kv == 1) {  // values carry no QJL fields
+    if (lane < g.sign_dw) rec32[g.angle_dw + lane] = 0;
+    if (lane == 0) rad16[1] = 0;
+    return;
+  }
+  if (lane < 8) sign_words[lane] = 0;
+  row_sync();
+  const float norm = qjl_row<PD>(v, radius, a.lut, g.bits, a.jl, g.qjl, w, lane, [&](int j, bool pos) {
+    if (pos) atomicOr(&sign_words[j >> 5], 1u << (j & 31));
+  });
+  row_sync();
+  if (lane < g.sign_dw) rec32[g.angle_dw + lane] = sign_words[lane];
+  if (lane == 0) rad16[1] = f32_to_f16_bits(norm);
+}
+
+// Reads a generic-layout pool back into the reference's raw code format:
+// row ((n * 2 + kv) * KH + h) * PS + t gets radius, level-major bins
+// [pd - 1], sign bytes [qjl] and norm.  V rows get zero signs and norms.
+__global__ void __launch_bounds__(64) tq_pool_read_gen_kernel(const uint8_t* pool, const int32_t* page_ids, int KH,
+                                                              int L_, int P, int layer, tq::GenLayout g,
+                                                              uint16_t* radius, uint8_t* angles, uint8_t* qjl_signs,
+                                                              uint16_t* norms) {
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
+  const int t = row % g.ps;
+  const int h = (row / g.ps) % KH;
+  const int kv = (row / (g.ps * KH)) % 2;
+  const int n = row / (g.ps * KH * 2);
+  const int pid = page_ids[n];
+  const int na = g.pd - 1;
+  if (pid < 0 || pid >= P) {  // absent page: zero codes
+    for (int i = lane; i < na; i += 64) angles[(size_t)row * na + i] = 0;
+    for (int j = lane; j < g.qjl; j += 64) qjl_signs[(size_t)row * g.qjl + j] = 0;
+    if (lane == 0) radius[row] = norms[row] = 0;
+    return;
+  }
+  const uint8_t* rec = pool + ((((size_t)pid * L_ + layer) * 2 + kv) * KH + h) * g.slice_bytes() +
+                       (size_t)t * g.record_bytes();
+  const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec);
+  const uint32_t mask = (1u << g.bits) - 1u;
+  for (int i = lane; i < na; i += 64) {
+    const int bit = i * g.bits, dw = bit >> 5, sh = bit & 31;
+    uint32_t x = rec32[dw] >> sh;
+    if (sh + g.bits > 32) x |= rec32[dw + 1] << (32 - sh);
+    angles[(size_t)row * na + i] = (uint8_t)(x & mask);
+  }
+  const uint16_t* rad16 = reinterpret_cast<const uint16_t*>(rec + g.radius_offset());
+  if (lane == 0) radius[row] = rad16[0];
+  for (int j = lane; j < g.qjl; j += 64)
+    qjl_signs[(size_t)row * g.qjl + j] = kv == 0 ? (uint8_t)((rec32[g.angle_dw + (j >> 5)] >> (j & 31)) & 1u) : 0;
+  if (lane == 0) norms[row] = kv == 0 ? rad16[1] : 0;
 }
 
 // Reads a TurboQuant pool back into the reference's raw code format, for
@@ -844,13 +888,9 @@ int check_tq_pool(int KH, int D, int PS, int L, int P, int layer_idx, int bits, 
     set_error("%s: bad sizes (KH=%d L=%d P=%d layer=%d)", who, KH, L, P, layer_idx);
     return VRM_ERR_ARG;
   }
-  if (D != tq::kPD || PS != tq::kTokens || qjl_dim != tq::kQjl) {
-    set_error("%s: TurboQuant pages are built for head_dim 128, page 16, qjl_dim 64 (got %d, %d, %d)", who, D, PS,
-              qjl_dim);
-    return VRM_ERR_UNSUPPORTED;
-  }
-  if (bits < 2 || bits > 4) {
-    set_error("%s: bits_per_angle %d unsupported (2, 3, 4)", who, bits);
+  if (!tq::tuned_layout(D, bits, qjl_dim, PS) && !tq::generic_ok(D, bits, qjl_dim, PS)) {
+    set_error("%s: TurboQuant pages take head_dim 33 .. 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256 and a "
+              "positive page size (got %d, %d, %d, %d)", who, D, bits, qjl_dim, PS);
     return VRM_ERR_UNSUPPORTED;
   }
   return VRM_OK;
@@ -898,6 +938,23 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.jl = jl;
   a.lut = angle_lut;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!tq::tuned_layout(D, bits, qjl_dim, PS)) {
+    const tq::GenLayout g = tq::gen_layout(D, bits, qjl_dim, PS);
+    const dim3 grid(rows, 2);
+#define VRM_TQ_WRITE_GEN(SRC)                                                                                  \
+  switch (g.pd) {                                                                                            \
+    case 64: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 64>), grid, dim3(64), 0, st, a, g); break;     \
+    case 128: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 128>), grid, dim3(64), 0, st, a, g); break;   \
+    default: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 256>), grid, dim3(64), 0, st, a, g); break;   \
+  }
+    switch (src_dtype) {
+      case VRM_SRC_F32: VRM_TQ_WRITE_GEN(VRM_SRC_F32); break;
+      case VRM_SRC_F16: VRM_TQ_WRITE_GEN(VRM_SRC_F16); break;
+      default: VRM_TQ_WRITE_GEN(VRM_SRC_BF16); break;
+    }
+#undef VRM_TQ_WRITE_GEN
+    return launch_status(who);
+  }
   // bulk writes pack kBulkRows rows (wavefronts) per workgroup, small ones one
   const bool bulk = rows >= kBulkMinRows;
   const dim3 grid(bulk ? (rows + kBulkRows - 1) / kBulkRows : rows, 2);
@@ -923,9 +980,15 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
 }
 }  // namespace
 
+extern "C" size_t vrm_tq_slice_bytes_ps(int head_dim, int bits, int qjl_dim, int page_size) {
+  if (tq::tuned_layout(head_dim, bits, qjl_dim, page_size)) return (size_t)tq::slice_bytes(bits);
+  if (tq::generic_ok(head_dim, bits, qjl_dim, page_size))
+    return tq::gen_layout(head_dim, bits, qjl_dim, page_size).slice_bytes();
+  return 0;
+}
+
 extern "C" size_t vrm_tq_slice_bytes(int head_dim, int bits, int qjl_dim) {
-  if (head_dim != tq::kPD || qjl_dim != tq::kQjl || bits < 2 || bits > 4) return 0;
-  return (size_t)tq::slice_bytes(bits);
+  return vrm_tq_slice_bytes_ps(head_dim, bits, qjl_dim, tq::kTokens);
 }
 
 extern "C" int vrm_tq_quant_append(const void* key, const void* value, int src_dtype, const int32_t* page_ids,
@@ -950,16 +1013,16 @@ extern "C" int vrm_tq_quant_pages(const void* key, const void* value, int src_dt
                                   int P, int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl,
                                   const float* angle_lut, vrm_stream_t stream) {
   const char* who = "vrm_tq_quant_pages";
-  if (NP < 0 || KH <= 0 || (long)NP * KH * tq::kTokens > 0x3fffffff) {
-    set_error("%s: bad sizes (NP=%d KH=%d)", who, NP, KH);
+  if (NP < 0 || KH <= 0 || PS <= 0 || (long)NP * KH * PS > 0x3fffffff) {
+    set_error("%s: bad sizes (NP=%d KH=%d PS=%d)", who, NP, KH, PS);
     return VRM_ERR_ARG;
   }
   if (NP > 0 && !n_valid) {
     set_error("%s: null n_valid", who);
     return VRM_ERR_ARG;
   }
-  return tq_pool_write(key, value, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D, PS,
-                       L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who);
+  return tq_pool_write(key, value, src_dtype, page_ids, nullptr, n_valid, NP * KH * PS, tq_pool, KH, D, PS, L, P,
+                       layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who);
 }
 
 extern "C" size_t vrm_turboquant_score_workspace_bytes(int M, int padded_dim, int qjl_dim) {
@@ -1037,8 +1100,8 @@ extern "C" int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int
                                     int P, int layer_idx, int bits, int qjl_dim, const float* signs, const float* jl,
                                     const float* angle_lut, vrm_stream_t stream) {
   const char* who = "vrm_tq_compress_pool";
-  if (NP < 0 || KH <= 0 || (long)NP * KH * tq::kTokens > 0x3fffffff) {
-    set_error("%s: bad sizes (NP=%d KH=%d)", who, NP, KH);
+  if (NP < 0 || KH <= 0 || PS <= 0 || (long)NP * KH * PS > 0x3fffffff) {
+    set_error("%s: bad sizes (NP=%d KH=%d PS=%d)", who, NP, KH, PS);
     return VRM_ERR_ARG;
   }
   int src_dtype;
@@ -1054,8 +1117,8 @@ extern "C" int vrm_tq_compress_pool(const void* kv_pool, int kv_dtype, const int
     set_error("%s: null n_valid", who);
     return VRM_ERR_ARG;
   }
-  return tq_pool_write(kv_pool, kv_pool, src_dtype, page_ids, nullptr, n_valid, NP * KH * tq::kTokens, tq_pool, KH, D,
-                       PS, L, P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who, true);
+  return tq_pool_write(kv_pool, kv_pool, src_dtype, page_ids, nullptr, n_valid, NP * KH * PS, tq_pool, KH, D, PS, L,
+                       P, layer_idx, bits, qjl_dim, signs, jl, angle_lut, stream, who, true);
 }
 
 extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids, int NP, int KH, int D, int PS,
@@ -1064,7 +1127,7 @@ extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids
   const char* who = "vrm_tq_read_pages";
   int rc = check_tq_pool(KH, D, PS, L, P, layer_idx, bits, qjl_dim, who);
   if (rc) return rc;
-  if (NP < 0 || (long)NP * 2 * KH * tq::kTokens > 0x7fffffff) {
+  if (NP < 0 || (long)NP * 2 * KH * PS > 0x7fffffff) {
     set_error("%s: bad count %d", who, NP);
     return VRM_ERR_ARG;
   }
@@ -1072,6 +1135,12 @@ extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids
   if (!tq_pool || !page_ids || !radius || !angles || !qjl_signs || !qjl_norms) {
     set_error("%s: null pointer argument", who);
     return VRM_ERR_ARG;
+  }
+  if (!tq::tuned_layout(D, bits, qjl_dim, PS)) {
+    hipLaunchKernelGGL(tq_pool_read_gen_kernel, dim3(NP * 2 * KH * PS), dim3(64), 0,
+                       reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx,
+                       tq::gen_layout(D, bits, qjl_dim, PS), radius, angles, qjl_signs, qjl_norms);
+    return launch_status(who);
   }
   hipLaunchKernelGGL(tq_pool_read_kernel, dim3(NP * 2 * KH * tq::kTokens), dim3(64), 0,
                      reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx, bits, radius,

@@ -192,9 +192,10 @@ class PagedKVCacheManager:
         self._kv_scales: Any = None
         self._tq_pool: Any = None
         self._tq_buffers: Optional[tuple] = None
-        # Bit s of _tq_slots[page, layer] is set once slot s of that page and
-        # layer holds TurboQuant codes (the reference's _compressed_pages
-        # entries, core/paged_attention.py:236-238).
+        # Bit min(s, 63) of _tq_slots[page, layer] is set once slot s of that
+        # page and layer holds TurboQuant codes (the reference's
+        # _compressed_pages entries, core/paged_attention.py:236-238); only
+        # "no bit set" is ever tested.
         self._tq_slots: Optional[np.ndarray] = None
         self._pending_compress: List[tuple] = []
         self._kv_compressor: Any = None
@@ -241,13 +242,11 @@ class PagedKVCacheManager:
             if kind not in ("float16", "bfloat16", "float32"):
                 raise RuntimeError("TurboQuant compression needs a float16, bfloat16 or float32 raw pool "
                                    f"(got {cfg.dtype})")
-            if cfg.page_size != tq_pages.PAGE_SIZE:
-                raise RuntimeError(f"TurboQuant pages hold {tq_pages.PAGE_SIZE} tokens (page_size {cfg.page_size})")
             self._kv_compressor = self._kv_compressor.to(dev)
             self._tq_pool = tq_pages.allocate_pool(cfg.max_pages, cfg.num_layers, cfg.num_kv_heads,
-                                                   self._kv_compressor, dev)
+                                                   self._kv_compressor, dev, cfg.page_size)
             self._tq_buffers = tq_pages._buffers(self._kv_compressor, dev)
-            self._tq_slots = np.zeros((cfg.max_pages, cfg.num_layers), dtype=np.uint32)
+            self._tq_slots = np.zeros((cfg.max_pages, cfg.num_layers), dtype=np.uint64)
 
     def _require_pool(self, what: str) -> None:
         if self._gpu_pool is None:
@@ -539,7 +538,7 @@ class PagedKVCacheManager:
             pairs = host if host is not None else list(zip(pids.tolist(), slots.tolist()))
             for pid, slot in pairs:
                 if 0 <= pid < cfg.max_pages and 0 <= slot < cfg.page_size:
-                    self._tq_slots[pid, layer_idx] |= np.uint32(1 << slot)
+                    self._tq_slots[pid, layer_idx] |= np.uint64(1 << min(slot, 63))
 
     def read_kv(self, request_id: str, layer_idx: int) -> Optional[Tuple[Any, Any]]:
         """(keys, values) of a request for one layer, [num_kv_heads, tokens,
@@ -816,7 +815,7 @@ class PagedKVCacheManager:
         comp = self._kv_compressor
         dev = self._tq_pool.device
         ids = torch.tensor(page_ids, dtype=torch.int32).to(dev)
-        codes = tq_pages.read_pages(self._tq_pool, layer_idx, ids, comp)  # [NP, K/V, KH, 16, ...]
+        codes = tq_pages.read_pages(self._tq_pool, layer_idx, ids, comp, cfg.page_size)  # [NP, K/V, KH, PS, ...]
         if scale is None:
             scale = 1.0 / math.sqrt(D)
         n = num_tokens
@@ -935,7 +934,7 @@ class PagedKVCacheManager:
             cfg.max_pages * L, 0, cfg.compression_bits, self._kv_compressor.qjl_dim, _lib.ptr(signs), _lib.ptr(jl),
             _lib.ptr(lut), _lib.stream_of(self._gpu_pool))
         _lib.check(rc, "compress_page_bulk")
-        self._tq_slots[page_id, layers] = np.uint32((1 << ps) - 1)
+        self._tq_slots[page_id, layers] = np.uint64((1 << min(ps, 64)) - 1)
         return True
 
     # ------------------------------------------------------------------

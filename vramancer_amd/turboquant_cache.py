@@ -33,9 +33,9 @@ Divergence from the reference, on purpose: a token's codes are written once.
 The reference re-compresses the decompressed older tokens at every spill
 (compress(decompress(old) ++ residual)), which quantises them again.
 
-Built for head_dim 128, 2-4 bits per angle and qjl_dim 64 (the TurboQuant
-page layout); a worker-GPU offloader (core/offloaded_compressor.py) is not
-supported.
+Takes every compressor setting the TurboQuant pages serve (head_dim 33 ..
+256, 1 .. 8 bits per angle, qjl_dim 1 .. 256); a worker-GPU offloader
+(core/offloaded_compressor.py) is not supported.
 """
 from __future__ import annotations
 
@@ -102,10 +102,9 @@ class TurboQuantLayer(CacheLayerMixin):
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         comp = self.compressor
         B, KH, _, D = key_states.shape
-        if D != 128 or comp.head_dim != 128 or comp.qjl_dim != 64 or comp.bits_per_angle not in (2, 3, 4):
-            raise RuntimeError("the TurboQuant cache is built for head_dim 128, qjl_dim 64 and 2-4 bits per angle "
-                               f"(got head_dim {D}, compressor {comp.head_dim}/{comp.qjl_dim}/"
-                               f"{comp.bits_per_angle})")
+        tq_pages._check_compressor(comp)
+        if D != comp.head_dim:
+            raise RuntimeError(f"key head_dim {D} does not match the compressor's {comp.head_dim}")
         if key_states.dtype not in (torch.float16, torch.bfloat16, torch.float32):
             raise RuntimeError(f"unsupported key dtype {key_states.dtype}")
         _lib.require_cuda(key_states, value_states)
@@ -189,7 +188,7 @@ class TurboQuantLayer(CacheLayerMixin):
         pool = self._tq_pool
         rc = _lib.load().vrm_tq_quant_append(
             _lib.ptr(k), _lib.ptr(v), _lib.src_dtype_code(k.dtype), _lib.ptr(pages), _lib.ptr(slots), B * n,
-            _lib.ptr(pool), KH, D, PAGE, 1, pool.shape[0], 0, self.compressor.bits_per_angle, 64, _lib.ptr(signs),
+            _lib.ptr(pool), KH, D, PAGE, 1, pool.shape[0], 0, self.compressor.bits_per_angle, self.compressor.qjl_dim, _lib.ptr(signs),
             _lib.ptr(jl), _lib.ptr(lut), _lib.stream_of(pool))
         _lib.check(rc, "TurboQuantLayer spill")
         self._n_comp += n
