@@ -40,6 +40,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 4;             // wavefronts per workgroup (at most)
+constexpr int kMaxHeads = 8;          // query heads per wave (hi / lo column halves)
 constexpr float kLazyRescale = 3.0f;  // as in vrm_decode_mfma.hip
 constexpr float kNoMax = -1.0e30f;
 
@@ -60,25 +61,92 @@ __device__ __forceinline__ uint32_t bit_field(const uint32_t* w, int pos) {
   return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh), 0, WIDTH);
 }
 
-// fp16 pair {fp16(a0 b0), fp16(a1 b1)}, each product rounded once to fp16
-// (v_fma_mix with float32 sources).
-__device__ __forceinline__ uint32_t mul_f16x2(float a0, float b0, float a1, float b1) {
-  uint32_t r;
-  asm("v_fma_mixlo_f16 %0, %1, %2, 0\n\tv_fma_mixhi_f16 %0, %3, %4, 0"
-      : "=&v"(r)
-      : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
-  return r;
+// Byte offset (field << LOG2) of the WIDTH-bit field at bit `pos` of the
+// little-endian bit stream w[], for a table of 2^LOG2-byte entries: one
+// right shift (or a funnel shift where the field straddles two dwords) and
+// one mask, the pair gfx950 issues fastest.
+template <int WIDTH, int LOG2>
+__device__ __forceinline__ uint32_t field_off(const uint32_t* w, int pos) {
+  const int dw = pos / 32, sh = pos % 32;
+  constexpr uint32_t mask = ((1u << WIDTH) - 1) << LOG2;
+  if (sh + WIDTH > 32) return __builtin_amdgcn_alignbit(w[dw + 1], w[dw], sh - LOG2) & mask;
+  if (sh >= LOG2) return (w[dw] >> (sh - LOG2)) & mask;
+  return (w[dw] << (LOG2 - sh)) & mask;
 }
 
-// fp16 pair {fp16(a0 b0 - h.lo), fp16(a1 b1 - h.hi)}: the residuals of the
-// products against their fp16 roundings h, each one fused multiply-add.
-__device__ __forceinline__ uint32_t residual_f16x2(float a0, float b0, float a1, float b1, uint32_t h) {
-  uint32_t r;
-  asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel_hi:[0,0,1]\n\t"
-      "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
-      : "=&v"(r)
-      : "v"(a0), "v"(b0), "v"(a1), "v"(b1), "v"(h));
-  return r;
+template <typename T>
+__device__ __forceinline__ T lds_at(const T* base, uint32_t off) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + off);
+}
+
+// Products of the last polar level rounded to fp16, eight per call: value
+// 4 j + k (j = 0, 1; k = 0..3) is y_j t_j.k.  hi gets fp16 of the float32
+// product; split8 also gives lo = fp16(y t - hi), the residual of the exact
+// product by one mixed-precision fused multiply-add against the fp16 hi.
+// (v_fma_mix{lo,hi}_f16 would round each product straight to fp16 in one
+// instruction, but on gfx950 each issues at half the rate of a multiply and
+// a packed conversion together; measured, this order is 10 % faster.)  The
+// results feed matrix-core instructions, which may read a VGPR only two wait
+// states after a VALU instruction wrote it.  The compiler pads its own code
+// for that but cannot see the writes inside an asm statement, so each block
+// ends with s_nop 1 (two wait states).
+__device__ __forceinline__ void round8(float y0, const float4& t0, float y1, const float4& t1, uint4& hi) {
+  float k[8];
+  asm("v_mul_f32 %4, %12, %14\n\t"
+      "v_mul_f32 %5, %12, %15\n\t"
+      "v_mul_f32 %6, %12, %16\n\t"
+      "v_mul_f32 %7, %12, %17\n\t"
+      "v_mul_f32 %8, %13, %18\n\t"
+      "v_mul_f32 %9, %13, %19\n\t"
+      "v_mul_f32 %10, %13, %20\n\t"
+      "v_mul_f32 %11, %13, %21\n\t"
+      "v_cvt_pk_f16_f32 %0, %4, %5\n\t"
+      "v_cvt_pk_f16_f32 %1, %6, %7\n\t"
+      "v_cvt_pk_f16_f32 %2, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %3, %10, %11\n\t"
+      "s_nop 1"
+      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]),
+        "=&v"(k[4]), "=&v"(k[5]), "=&v"(k[6]), "=&v"(k[7])
+      : "v"(y0), "v"(y1), "v"(t0.x), "v"(t0.y), "v"(t0.z), "v"(t0.w), "v"(t1.x), "v"(t1.y), "v"(t1.z),
+        "v"(t1.w));
+}
+
+__device__ __forceinline__ void split8(float y0, const float4& t0, float y1, const float4& t1, uint4& hi, uint4& lo) {
+  float k[8];
+  asm("v_mul_f32 %8, %16, %18\n\t"
+      "v_mul_f32 %9, %16, %19\n\t"
+      "v_mul_f32 %10, %16, %20\n\t"
+      "v_mul_f32 %11, %16, %21\n\t"
+      "v_mul_f32 %12, %17, %22\n\t"
+      "v_mul_f32 %13, %17, %23\n\t"
+      "v_mul_f32 %14, %17, %24\n\t"
+      "v_mul_f32 %15, %17, %25\n\t"
+      "v_cvt_pk_f16_f32 %0, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %1, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %2, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %3, %14, %15\n\t"
+      "v_fma_mix_f32 %8, %16, %18, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %9, %16, %19, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %10, %16, %20, -%1 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %11, %16, %21, -%1 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %12, %17, %22, -%2 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %13, %17, %23, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %14, %17, %24, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %15, %17, %25, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_cvt_pk_f16_f32 %4, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %5, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %6, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %7, %14, %15\n\t"
+      "s_nop 1"
+      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
+        "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]), "=&v"(k[6]), "=&v"(k[7])
+      : "v"(y0), "v"(y1), "v"(t0.x), "v"(t0.y), "v"(t0.z), "v"(t0.w), "v"(t1.x), "v"(t1.y), "v"(t1.z),
+        "v"(t1.w));
+}
+
+// Value of lane (lane + 8) % 16 of the same row of 16 lanes (DPP row_ror:8).
+__device__ __forceinline__ float row_swap8(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
 }
 
 // In-register Walsh-Hadamard transform of 128 values, element e in lane e % 64,
@@ -128,7 +196,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // (levels 3 and 2), for two sibling angles at once (index bin_a + NB bin_b)
   __shared__ float2 lut[NB];
   __shared__ float4 lut2[BITS <= 3 ? 1 : NB * NB];
-  __shared__ uint2 sign_lut[16];  // 4 sign bits -> 4 fp16 +-1 (bit i -> element i)
+  __shared__ uint2 sign_mask[16];  // 4 sign bits -> 4 fp16 sign masks (bit i clear: element i negated)
   // Two levels per lookup: for a node angle a and the angles b, c of its two
   // children (index a + NB (b + NB c)), the products (cos a cos b, cos a sin b,
   // sin a cos c, sin a sin c); t10 for levels 1/0 (level 0 has its own bin
@@ -148,6 +216,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int grp = lane >> 4;
+  // Matrix-core columns: column n < 8 carries the hi part of head n of the
+  // wave's G <= 8 heads, column n + 8 its lo part (columns of heads >= G
+  // repeat head G - 1).  A score or output is the sum of columns n and n + 8.
+  const int hcol = col & 7;
+  const bool lo_col = col >= 8;
   const int group = a.H / a.KH;
   const int chunks = group / G;
   const int unit = blockIdx.y * (blockDim.x >> 6) + wave;
@@ -163,8 +236,8 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   }
   if (threadIdx.x < 16) {
     uint32_t h[4];
-    for (int e = 0; e < 4; ++e) h[e] = ((threadIdx.x >> e) & 1) ? 0x3c00u : 0xbc00u;  // fp16 +1 / -1
-    sign_lut[threadIdx.x] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    for (int e = 0; e < 4; ++e) h[e] = ((threadIdx.x >> e) & 1) ? 0u : 0x8000u;
+    sign_mask[threadIdx.x] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
   __syncthreads();
 
@@ -182,7 +255,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // ---------------- q_rot of this wave's heads (row r: head min(r, G - 1)) ----------------
   const float root = (float)sqrt(128.0);
 #pragma unroll 1
-  for (int r = 0; r < 16; ++r) {
+  for (int r = 0; r < 8; ++r) {
     const float* qrow = a.query + ((size_t)b * a.H + h0 + min(r, G - 1)) * D;
     float v[2] = {qrow[lane] * tq.signs[lane], qrow[lane + 64] * tq.signs[lane + 64]};
     fwht128(v, lane);
@@ -190,21 +263,26 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     qb[r][lane + 64] = v[1] / root;
   }
   wave_sync();
-  // B operand of S^T: lane (col, grp) holds q_rot[col][32 grp + 8 c + e] * qscale
-  v8h QH[4][2];
+  // B operand of S^T: x = q_rot[hcol][32 grp + 8 c + e] * qscale as hi
+  // (columns < 8) + lo (columns >= 8); against K hi and K lo this sums
+  // (Kh + Kl)(qh + ql) over the two column halves.
+  v8h QB[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float x = qb[col][32 * grp + 8 * c + e] * a.qscale;
+      const float x = qb[hcol][32 * grp + 8 * c + e] * a.qscale;
       const _Float16 hi = (_Float16)x;
-      QH[c][0][e] = hi;
-      QH[c][1][e] = (_Float16)(x - (float)hi);
+      const _Float16 lo = (_Float16)(x - (float)hi);
+      QB[c][e] = lo_col ? lo : hi;
     }
   // q_proj^T = JL q_rot^T on the matrix cores: tile j (JL rows 16 j ..), result
   // in lane (col, grp) for rows 16 j + 4 grp + r.  The QJL product uses the
   // matching k order: chunk c, element e <-> JL row 16 (2 c + e / 4) + 4 grp + e % 4.
-  v8h PJ[2][2];
+  // PJ carries q_proj times the QJL scale, hi / lo by column half like QB.
+  const float qjl_scale = a.qscale * tq.qjl_coef;
+  const bool use_qjl = tq.qjl_coef != 0.f;
+  v8h PJ[2];
   {
     float pj[4][4];
 #pragma unroll
@@ -218,7 +296,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
           const float x = tq.jl[(size_t)(16 * j + col) * D + 32 * c + 8 * grp + e];
           ah[e] = (_Float16)x;
           al[e] = (_Float16)(x - (float)ah[e]);
-          const float y = qb[col][32 * c + 8 * grp + e];
+          const float y = qb[hcol][32 * c + 8 * grp + e];
           bh[e] = (_Float16)y;
           bl[e] = (_Float16)(y - (float)bh[e]);
         }
@@ -233,10 +311,9 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = pj[2 * c + e / 4][e % 4];
+        const float x = pj[2 * c + e / 4][e % 4] * qjl_scale;
         const _Float16 hi = (_Float16)x;
-        PJ[c][0][e] = hi;
-        PJ[c][1][e] = (_Float16)(x - (float)hi);
+        PJ[c][e] = lo_col ? (_Float16)(x - (float)hi) : hi;
       }
   }
   // one-hot operands of the V transpose: E_h[8 grp + e][col] = (8 grp + e == 16 h + col)
@@ -246,7 +323,6 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       onehot[h][e] = (grp == 2 * h + (col >> 3) && e == (col & 7)) ? (_Float16)1.f : (_Float16)0.f;
-  const float qjl_scale = a.qscale * tq.qjl_coef;
 
   // every wave of the workgroup is done with qbuf (all share the work item,
   // so all reach this point): its LDS now holds the two-level tables
@@ -307,18 +383,18 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // group is y[j] * t[j][k].
   auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&y)[8], float4 (&t)[8]) {
     constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
-    const float2 t6 = lut[(top0 >> sh31) & (NB - 1)];
-    const float2 t5 = lut[(topq >> sh31) & (NB - 1)];
+    const float2 t6 = lds_at(lut, field_off<BITS, 3>(&top0, sh31));
+    const float2 t5 = lds_at(lut, field_off<BITS, 3>(&topq, sh31));
     float p = radius;
     p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
     p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
-    const float2 c4 = lut[bit_field<BITS>(q, (kT32 ? 30 : 0) * BITS)];  // level 4
+    const float2 c4 = lds_at(lut, field_off<BITS, 3>(q, (kT32 ? 30 : 0) * BITS));  // level 4
     const float x3[2] = {p * c4.x, p * c4.y};
     if constexpr (kT32) {
       // levels 3 and 2: node j and its children in slots 24 + 3 j .. 26 + 3 j
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float4 t = t32[bit_field<3 * BITS>(q, (24 + 3 * j) * BITS)];
+        const float4 t = lds_at(t32, field_off<3 * BITS, 4>(q, (24 + 3 * j) * BITS));
         y[4 * j] = x3[j] * t.x;
         y[4 * j + 1] = x3[j] * t.y;
         y[4 * j + 2] = x3[j] * t.z;
@@ -326,11 +402,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       }
     } else {
       // level 3 (slots 1, 2), then level 2 (slots 3 .. 6), sibling angles together
-      const float4 a3 = lut2[bit_field<2 * BITS>(q, 1 * BITS)];
+      const float4 a3 = lds_at(lut2, field_off<2 * BITS, 4>(q, 1 * BITS));
       const float x2[4] = {x3[0] * a3.x, x3[0] * a3.y, x3[1] * a3.z, x3[1] * a3.w};
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
-        const float4 a2 = lut2[bit_field<2 * BITS>(q, (3 + i) * BITS)];
+        const float4 a2 = lds_at(lut2, field_off<2 * BITS, 4>(q, (3 + i) * BITS));
         y[2 * i] = x2[i] * a2.x;
         y[2 * i + 1] = x2[i] * a2.y;
         y[2 * i + 2] = x2[i + 1] * a2.z;
@@ -341,12 +417,12 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     // node slot 7 + j, children slots 15 + 2 j, 16 + 2 j)
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      t[j] = t10[kT32 ? bit_field<3 * BITS>(q, 3 * j * BITS)
-                      : bit_field<BITS>(q, (7 + j) * BITS) + NB * bit_field<2 * BITS>(q, (15 + 2 * j) * BITS)];
+      t[j] = lds_at(t10, kT32 ? field_off<3 * BITS, 4>(q, 3 * j * BITS)
+                              : field_off<BITS, 4>(q, (7 + j) * BITS) | field_off<2 * BITS, 4 + BITS>(q, (15 + 2 * j) * BITS));
   };
-  auto comp = [](const float4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; };
 
-  // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi.
+  // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi, for
+  // head hcol (both column halves hold the same sums).
   auto page_scores = [&](const TqSlot<BITS>& s, int pi, float* sc) {
     float y[8];
     float4 t[8];
@@ -355,36 +431,31 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       // k = y t as hi = fp16(k) and lo = fp16(k - hi)
-      uint32_t hw[4], lw[4];
+      uint4 hw, lw;
+      split8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], hw, lw);
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, hw), QB[c], c4, 0, 0, 0);
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lw), QB[c], c4, 0, 0, 0);
+    }
+    if (use_qjl) {
+      // The QJL term on the same accumulator: row operand +-norm of token col
+      // (the fp16 norm with its sign bit flipped where the sign bit is clear;
+      // exact), against PJ.
+      const uint32_t nn = s.knorm | (s.knorm << 16);
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const int j = (8 * c + e) >> 2, k = e & 3;
-        hw[e / 2] = mul_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1));
-        lw[e / 2] = residual_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1), hw[e / 2]);
+      for (int c = 0; c < 2; ++c) {
+        // elements e < 4: JL rows 32 c + 4 grp + e; e >= 4: rows 32 c + 16 + 4 grp + e - 4
+        const uint32_t word = c == 0 ? s.ksign.x : s.ksign.y;
+        const uint2 lo = sign_mask[__builtin_amdgcn_ubfe(word, 4 * grp, 4)];
+        const uint2 hi = sign_mask[__builtin_amdgcn_ubfe(word, 16 + 4 * grp, 4)];
+        const v8h sn = __builtin_bit_cast(v8h, make_uint4(nn ^ lo.x, nn ^ lo.y, nn ^ hi.x, nn ^ hi.y));
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(sn, PJ[c], c4, 0, 0, 0);
       }
-      const v8h kh = __builtin_bit_cast(v8h, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-      const v8h kl = __builtin_bit_cast(v8h, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][0], c4, 0, 0, 0);
-      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, QH[c][1], c4, 0, 0, 0);
-      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, QH[c][0], c4, 0, 0, 0);
     }
-    v4f cq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      // elements e < 4: JL rows 32 c + 4 grp + e; e >= 4: rows 32 c + 16 + 4 grp + e - 4
-      const uint32_t word = c == 0 ? s.ksign.x : s.ksign.y;
-      const uint2 lo = sign_lut[__builtin_amdgcn_ubfe(word, 4 * grp, 4)];
-      const uint2 hi = sign_lut[__builtin_amdgcn_ubfe(word, 16 + 4 * grp, 4)];
-      const v8h sg = __builtin_bit_cast(v8h, make_uint4(lo.x, lo.y, hi.x, hi.y));
-      cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][0], cq, 0, 0, 0);
-      cq = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg, PJ[c][1], cq, 0, 0, 0);
-    }
-    const float nrm = f16_to_f32(s.knorm);  // norm of token col; row r needs token 4 grp + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 4 * grp + r;
-      const float nt = __int_as_float(__builtin_amdgcn_ds_bpermute(t << 2, __float_as_int(nrm)));  // lane t holds token t
-      sc[r] = (s.ok && pi * kPS + t < tok_end) ? c4[r] + qjl_scale * nt * cq[r] : -INFINITY;
+      const float v = c4[r] + row_swap8(c4[r]);
+      sc[r] = (s.ok && pi * kPS + t < tok_end) ? v : -INFINITY;
     }
   };
 
@@ -404,13 +475,9 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, y, t);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const int j = (8 * c + e) >> 2, k = e & 3;
-        w[e / 2] = mul_f16x2(y[j], comp(t[j], k), y[j], comp(t[j], k + 1));
-      }
-      vop[c] = __builtin_bit_cast(v8h, make_uint4(w[0], w[1], w[2], w[3]));
+      uint4 w;
+      round8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], w);
+      vop[c] = __builtin_bit_cast(v8h, w);
     }
   };
 
@@ -435,14 +502,14 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       for (int i = 0; i < 8; ++i) acc[i] *= alpha;
       m_run = pm;
     }
-    v8h Bh, Bl;
+    // P^T as hi (columns < 8) and lo (columns >= 8)
+    v8h Bp;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p = __builtin_amdgcn_exp2f(sc[e] - m_run);
       l_run += p;
       const _Float16 hi = (_Float16)p;
-      Bh[e] = hi;
-      Bl[e] = (_Float16)(p - (float)hi);
+      Bp[e] = lo_col ? (_Float16)(p - (float)hi) : hi;
     }
     v8h vop0[4], vop1[4];
     v_operand(s0, pi, vop0);
@@ -457,8 +524,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
         v8h A;
 #pragma unroll
         for (int e = 0; e < 8; ++e) A[e] = (_Float16)t[e];  // exact: fp16 values
-        acc[2 * c + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bh, acc[2 * c + h], 0, 0, 0);
-        acc[2 * c + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bl, acc[2 * c + h], 0, 0, 0);
+        acc[2 * c + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bp, acc[2 * c + h], 0, 0, 0);
       }
   };
 
@@ -490,7 +556,8 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * grp + r;
-        qb[col][32 * (2 * h + (row >> 3)) + 8 * c + (row & 7)] = acc[2 * c + h][r];
+        // hi column + lo column of head hcol
+        qb[col][32 * (2 * h + (row >> 3)) + 8 * c + (row & 7)] = acc[2 * c + h][r] + row_swap8(acc[2 * c + h][r]);
       }
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
@@ -512,7 +579,8 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 
 }  // namespace
 
-hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int G, hipStream_t st) {
+hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, hipStream_t st) {
+  const int G = pick_group_tile(a0.H / a0.KH, kMaxHeads);
   const int units = a0.KH * ((a0.H / a0.KH) / G);
   int W = kWaves;
   while (units % W) --W;

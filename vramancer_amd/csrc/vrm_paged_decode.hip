@@ -628,7 +628,6 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
 // generic layout's geometry, or null for the tuned layout.
 int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, const tq::GenLayout* gl, float* out,
                   void* workspace, size_t workspace_bytes, int B, int D, float scale, hipStream_t st) {
-  const int G = pick_group_tile(a.H / a.KH, 16);
   a.B = B;
   const long cap = items_capacity(B, a.KH);
   const size_t need = header_bytes(B) + (size_t)cap * a.H * (D + 2) * sizeof(float);
@@ -640,7 +639,7 @@ int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, const tq::GenL
   a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
-  hipError_t e = gl ? launch_tq_generic(a, tq, *gl, B, D, st) : launch_tq_decode(a, tq, bits, B, G, st);
+  hipError_t e = gl ? launch_tq_generic(a, tq, *gl, B, D, st) : launch_tq_decode(a, tq, bits, B, st);
   if (e != hipSuccess) {
     set_error("vrm_paged_decode_tq: partition kernel launch failed: %s", hipGetErrorString(e));
     return (int)e;
