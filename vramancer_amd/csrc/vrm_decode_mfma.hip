@@ -296,7 +296,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   int* const pair_next = BALANCED ? pair_ctr + wave % kUnitsPerWg : nullptr;
   auto grab = [&]() {
     int v = 0;
-    if (lane == 0) v = __hip_atomic_fetch_add(pair_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if constexpr (BALANCED)
+      if (lane == 0) v = __hip_atomic_fetch_add(pair_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return __builtin_amdgcn_readfirstlane(v);
   };
   auto load_pair = [&](PageSlot<D>& s0, PageSlot<D>& s1, int p) {

@@ -144,6 +144,15 @@ __device__ __forceinline__ void split8(float y0, const float4& t0, float y1, con
         "v"(t1.w));
 }
 
+// Maximum over lanes lane % 16 + {0, 16, 32, 48} (the four rows of a
+// column), by the VALU lane swaps of gfx950 instead of LDS round trips.
+__device__ __forceinline__ float max_rows4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float m = __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), INFINITY);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return __builtin_amdgcn_fmed3f(__uint_as_float(b[0]), __uint_as_float(b[1]), INFINITY);
+}
+
 // Value of lane (lane + 8) % 16 of the same row of 16 lanes (DPP row_ror:8).
 __device__ __forceinline__ float row_swap8(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
@@ -481,20 +490,14 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     }
   };
 
-  auto process_pair = [&](const TqSlot<BITS>& s0, const TqSlot<BITS>& s1, int pi, bool has1) {
+  auto process_pair = [&](const TqSlot<BITS>& s0, const TqSlot<BITS>& s1, int pi) {
     float sc[8];
     page_scores(s0, pi, sc);
-    if (has1) {
-      page_scores(s1, pi + 1, sc + 4);
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
-    }
+    page_scores(s1, pi + 1, sc + 4);
     float pm = sc[0];
 #pragma unroll
     for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
-    pm = fmaxf(pm, xor_shfl<16>(pm));
-    pm = fmaxf(pm, xor_shfl<32>(pm));
+    pm = max_rows4(pm);
     if (pm > m_run + kLazyRescale) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
       l_run *= alpha;
@@ -539,7 +542,9 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       const int ids_ahead = ids_at(base + 2 * RING);
 #pragma unroll
       for (int u = 0; u < RING; u += 2) {
-        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
+        // pages past the partition repeat its last page id; their tokens are
+        // past tok_end, so they score -inf and carry radius 0
+        process_pair(ring[u], ring[u + 1], base + u);
         load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
         load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
       }
