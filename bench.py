@@ -48,6 +48,10 @@ METRIC = "paged-attn decode µs/layer-step + HBM GB/s (% of peak), 14B-shape qua
 PEAK_HBM_GBPS = 8000.0
 LAYERS_FILLED = (0, 12, 24, 36)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_14b_int8.json")
+# wave64 VALU instructions per launch of the VALU-bound kernels (rocprofv3 SQ counters)
+VALU_FILE = os.path.join(ROOT, "profiles", "valu_counts.json")
+# one wave64 VALU instruction per SIMD per 4 cycles: 256 CUs x 4 SIMDs at 2.4 GHz
+PEAK_VALU_GINST = 256 * 4 * 2.4 / 4
 KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_BF16, "int8": _lib.VRM_KV_I8,
            "fp8": _lib.VRM_KV_FP8E4M3}
 KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
@@ -711,6 +715,36 @@ def main():
                        "page 16, 4 bits per angle, Student-t(3) K/V"),
     }[cfg.name]
     G = next(g for g in range(16, 0, -1) if (H // KH) % g == 0)
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBPS, 4),
+        "traffic": traffic,
+        "kernel": (KERNEL[cfg.codec].format(D=D) if not balanced else
+                   KERNEL[cfg.codec].format(D=D).replace(">", ",balanced>"))
+                  + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
+        "kernel_us": round(us_part, 3),
+    }
+    valu = None
+    if (turbo or q4) and os.path.exists(VALU_FILE):
+        with open(VALU_FILE) as f:
+            valu = json.load(f)["workloads"].get(cfg.name)
+    if valu is not None:
+        # These kernels rebuild or unpack every code on the vector ALU: the
+        # binding roofline is VALU issue, the HBM figures stay as context.
+        ginst = valu["valu_insts_per_launch"] / (us_part * 1e-6) / 1e9
+        roofline.update({
+            "bound": "valu",
+            "achieved": round(ginst, 1),
+            "peak": PEAK_VALU_GINST,
+            "unit": "Ginst/s",
+            "frac": round(ginst / PEAK_VALU_GINST, 4),
+            "valu_insts_per_launch": valu["valu_insts_per_launch"],
+            "hbm_achieved_gbps": round(achieved, 1),
+            "hbm_frac": round(achieved / PEAK_HBM_GBPS, 4),
+        })
     result = {
         "metric": METRIC,
         "value": round(us_step, 3),
@@ -736,18 +770,7 @@ def main():
         "tokens_per_s": round(B / (us_step * 1e-6 * L), 1) if L > 1 else None,
         "append_us": round(us_append, 2) if us_append is not None else None,
         "algorithmic_bytes": int(ab["total"]),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": traffic,
-            "kernel": (KERNEL[cfg.codec].format(D=D) if not balanced else
-                       KERNEL[cfg.codec].format(D=D).replace(">", ",balanced>"))
-                      + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
-            "kernel_us": round(us_part, 3),
-        },
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "python_api": python_api,
     }
