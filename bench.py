@@ -30,6 +30,7 @@ materialised keys/values + SDPA the reference's cache hands a model.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -54,6 +55,7 @@ VALU_FILE = os.path.join(ROOT, "profiles", "valu_counts.json")
 PEAK_VALU_GINST = 256 * 4 * 2.4 / 4
 KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_BF16, "int8": _lib.VRM_KV_I8,
            "fp8": _lib.VRM_KV_FP8E4M3}
+KV_NAME = {"f32": "K_F32", "f16": "K_F16", "bf16": "K_BF16", "int8": "K_I8", "fp8": "K_FP8", "q4": "K_Q4"}
 KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
           "tq3": "decode_tq_kernel<3> + merge", "tq4": "decode_tq_kernel<4> + merge",
           "bf16": "decode_stream_float_kernel<K_BF16,{D}>", "f16": "decode_stream_float_kernel<K_F16,{D}>",
@@ -492,6 +494,11 @@ def main():
     ap.add_argument("--hf-cache", action="store_true",
                     help="time one layer of a decode step through the HF TurboQuant cache, paged attention vs "
                          "materialised K/V + SDPA")
+    ap.add_argument("--head-dim", type=int, default=None,
+                    help="override the workload's head_dim (any value <= 256; int8 / fp8 need a multiple of 16, "
+                         "4-bit a multiple of 32, TurboQuant 33..256)")
+    ap.add_argument("--page-size", type=int, default=None,
+                    help="override the workload's page size (int8 / fp8 need a multiple of 4)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 plain 1 GiB device-to-device copies (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -514,6 +521,10 @@ def main():
     lib = _lib.load()
     dev = torch.device("cuda:0")
     cfg = workloads.CONFIGS[args.workload]
+    shape_override = args.head_dim is not None or args.page_size is not None
+    if shape_override:
+        cfg = dataclasses.replace(cfg, head_dim=args.head_dim or cfg.head_dim,
+                                  page_size=args.page_size or cfg.page_size)
     if cfg.num_layers < 4:
         # steps rotate over 4 layers so that consecutive steps never hit in the Infinity Cache
         cfg = workloads.scaled(cfg, num_layers=4)
@@ -531,7 +542,7 @@ def main():
     B, H, D = q.shape
     if turbo:
         P, L, _, KH, _ = pool.shape
-        PS = 16
+        PS = cfg.page_size
         comp = inp["compressor"]
         tq_signs, tq_jl, tq_lut = tq_pages._buffers(comp, dev)
     else:
@@ -550,7 +561,7 @@ def main():
 
     # even batches over int8 / fp8 pools take the balanced decode (one
     # workgroup per sequence and kv-head, no merge pass), as the manager does
-    balanced = (not turbo and not q4 and
+    balanced = (not turbo and not q4 and D in (64, 128) and PS == 16 and
                 prefer_balanced(lens_list, KH, pool.dtype))
     log(f"decode mode: {'balanced' if balanced else 'work items + merge'}")
 
@@ -566,7 +577,7 @@ def main():
         if turbo:
             rc = lib.vrm_paged_decode_tq(q.data_ptr(), pool.data_ptr(), table.data_ptr(), lens.data_ptr(),
                                          out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P, max_pp,
-                                         layer, scale, comp.bits_per_angle, 64, tq_signs.data_ptr(),
+                                         layer, scale, comp.bits_per_angle, comp.qjl_dim, tq_signs.data_ptr(),
                                          tq_jl.data_ptr(), tq_lut.data_ptr(), stream)
             if rc:
                 _lib.check(rc, "turbo decode")
@@ -613,7 +624,7 @@ def main():
         layer = layers[i % len(layers)]
         kw = dict(out=out, workspace=ws) if prealloc else {}
         if turbo:
-            tq_pages.paged_attention_decode_turbo(q, pool, table, lens, layer, comp, **kw)
+            tq_pages.paged_attention_decode_turbo(q, pool, table, lens, layer, comp, page_size=PS, **kw)
         elif q4:
             paged_attention_decode_q4(q, pool, sc, zp, table, lens, layer, **kw)
         else:
@@ -642,7 +653,7 @@ def main():
         slot = (last % PS).to(torch.int32).contiguous()
 
         def append(i):
-            tq_pages.quantize_append(pool, layers[0], pid, slot, kn, vn, comp)
+            tq_pages.quantize_append(pool, layers[0], pid, slot, kn, vn, comp, page_size=PS)
 
         for i in range(5):
             append(i)
@@ -678,7 +689,7 @@ def main():
     achieved = ab["total"] / (us_part * 1e-6) / 1e9
     overall = ab["total"] / (us_step * 1e-6) / 1e9
     traffic = None
-    if cfg.name == "14b-int8" and os.path.exists(TRAFFIC_FILE):
+    if cfg.name == "14b-int8" and not shape_override and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     cpu = None
@@ -714,6 +725,18 @@ def main():
         "14b-turbo4": ("14b-turbo4 paged decode over TurboQuant pages: B=16, H=40, KH=8, D=128, context 32768, "
                        "page 16, 4 bits per angle, Student-t(3) K/V"),
     }[cfg.name]
+    if shape_override:
+        desc += f" (head_dim set to {D}, page size to {PS})"
+    if turbo:
+        tuned = 64 < D <= 128 and comp.qjl_dim == 64 and comp.bits_per_angle in (2, 3, 4) and PS == 16
+        pd = 1 << max(6, (D - 1).bit_length())
+        kname = KERNEL[cfg.codec] if tuned else f"decode_tq_gen_kernel<{pd}> + merge"
+    elif PS == 16 and D in (64, 128, 256):
+        kname = KERNEL[cfg.codec].format(D=D)
+        if balanced:
+            kname = kname.replace(">", ",balanced>")
+    else:
+        kname = f"decode_generic_kernel<{KV_NAME[cfg.codec]}>" + (" + merge" if q4 else "")
     G = next(g for g in range(16, 0, -1) if (H // KH) % g == 0)
     roofline = {
         "bound": "hbm",
@@ -722,13 +745,11 @@ def main():
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBPS, 4),
         "traffic": traffic,
-        "kernel": (KERNEL[cfg.codec].format(D=D) if not balanced else
-                   KERNEL[cfg.codec].format(D=D).replace(">", ",balanced>"))
-                  + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
+        "kernel": kname + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
         "kernel_us": round(us_part, 3),
     }
     valu = None
-    if (turbo or q4) and os.path.exists(VALU_FILE):
+    if (turbo or q4) and not shape_override and os.path.exists(VALU_FILE):
         with open(VALU_FILE) as f:
             valu = json.load(f)["workloads"].get(cfg.name)
     if valu is not None:

@@ -1,6 +1,7 @@
-"""TurboQuant pages of every other compressor setting (the generic page
-layout): head_dim 33 .. 256 (padded_dim 64 / 128 / 256), 1 .. 8 bits per
-angle, qjl_dim 1 .. 256, any page size.
+"""TurboQuant pages of every compressor setting: head_dim 33 .. 256
+(padded_dim 64 / 128 / 256), 1 .. 8 bits per angle, qjl_dim 1 .. 256, any
+page size.  head_dim 65 .. 128 with 64 QJL rows, 2 .. 4 bits and 16-token
+pages use the tuned slice and kernel; everything else the generic layout.
 
 * Codes written into pages equal, bit for bit, the standalone GPU
   compressor's codes (CUDATurboQuantOps.compress_gpu, itself checked against
@@ -35,6 +36,8 @@ ATOL, RTOL = 2e-3, 1e-2
 SETTINGS = [
     (64, 3, None, 16), (96, 3, None, 4), (256, 4, None, 16), (128, 1, None, 16), (128, 3, 32, 16),
     (128, 3, 64, 8), (80, 8, 100, 5), (200, 5, 256, 3), (33, 2, 7, 1), (128, 6, None, 32),
+    # head_dim 65 .. 128 at 64 QJL rows, 2-4 bits and 16-token pages share the tuned slice of head_dim 128
+    (96, 3, None, 16), (80, 4, None, 16), (65, 2, None, 16),
 ]
 
 
@@ -194,7 +197,7 @@ def _codes(pool, comp, layer, ps):
 DECODE = [  # head_dim, bits, qjl_dim, page size, H, KH
     (64, 3, None, 16, 8, 2), (96, 3, None, 4, 12, 4), (256, 4, None, 16, 16, 2), (96, 2, None, 16, 40, 8),
     (64, 1, None, 8, 8, 8), (256, 8, 100, 5, 4, 1), (128, 3, 64, 32, 40, 8), (80, 5, 33, 3, 6, 3),
-    (128, 3, 32, 16, 8, 2),
+    (128, 3, 32, 16, 8, 2), (96, 3, None, 16, 40, 8), (80, 4, None, 16, 12, 4), (65, 2, None, 16, 8, 1),
 ]
 
 

@@ -194,7 +194,7 @@ struct TqSlot {
 };
 
 template <int BITS>
-__global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G) {
+__global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G, int hd) {
   constexpr int NB = 1 << BITS;
   constexpr int RING = 4;
   constexpr int SLICE = T::slice_bytes(BITS);
@@ -265,8 +265,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   const float root = (float)sqrt(128.0);
 #pragma unroll 1
   for (int r = 0; r < 8; ++r) {
-    const float* qrow = a.query + ((size_t)b * a.H + h0 + min(r, G - 1)) * D;
-    float v[2] = {qrow[lane] * tq.signs[lane], qrow[lane + 64] * tq.signs[lane + 64]};
+    // the query padded with zeros to the padded dim, as the compressor pads keys
+    const float* qrow = a.query + ((size_t)b * a.H + h0 + min(r, G - 1)) * hd;
+    float v[2] = {lane < hd ? qrow[lane] * tq.signs[lane] : 0.f,
+                  lane + 64 < hd ? qrow[lane + 64] * tq.signs[lane + 64] : 0.f};
     fwht128(v, lane);
     qb[r][lane] = v[0] / root;
     qb[r][lane + 64] = v[1] / root;
@@ -571,9 +573,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   for (int hh = 0; hh < G; ++hh) {
     float v[2] = {qb[hh][lane], qb[hh][lane + 64]};
     fwht128(v, lane);
-    float* out = a.part_acc + ((size_t)item * a.H + h0 + hh) * D;
-    out[lane] = v[0] / root * s_lo;
-    out[lane + 64] = v[1] / root * s_hi;
+    // unrotated, then cut to the head_dim
+    float* out = a.part_acc + ((size_t)item * a.H + h0 + hh) * hd;
+    if (lane < hd) out[lane] = v[0] / root * s_lo;
+    if (lane + 64 < hd) out[lane + 64] = v[1] / root * s_hi;
   }
   if (col < G && grp == 0) {
     float* ml = a.part_ml + ((size_t)item * a.H + h0 + col) * 2;
@@ -584,7 +587,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 
 }  // namespace
 
-hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, hipStream_t st) {
+hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st) {
   const int G = pick_group_tile(a0.H / a0.KH, kMaxHeads);
   const int units = a0.KH * ((a0.H / a0.KH) / G);
   int W = kWaves;
@@ -597,9 +600,9 @@ hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bi
   dim3 grid(B + 2 * a.target, units / W, 1);
   dim3 block(64 * W);
   switch (bits) {
-    case 2: hipLaunchKernelGGL(decode_tq_kernel<2>, grid, block, 0, st, a, tq, G); break;
-    case 3: hipLaunchKernelGGL(decode_tq_kernel<3>, grid, block, 0, st, a, tq, G); break;
-    default: hipLaunchKernelGGL(decode_tq_kernel<4>, grid, block, 0, st, a, tq, G); break;
+    case 2: hipLaunchKernelGGL(decode_tq_kernel<2>, grid, block, 0, st, a, tq, G, hd); break;
+    case 3: hipLaunchKernelGGL(decode_tq_kernel<3>, grid, block, 0, st, a, tq, G, hd); break;
+    default: hipLaunchKernelGGL(decode_tq_kernel<4>, grid, block, 0, st, a, tq, G, hd); break;
   }
   return hipGetLastError();
 }

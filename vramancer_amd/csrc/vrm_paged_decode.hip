@@ -639,7 +639,7 @@ int run_tq_decode(DecodeArgs a, const TqDecodeArgs& tq, int bits, const tq::GenL
   a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
-  hipError_t e = gl ? launch_tq_generic(a, tq, *gl, B, D, st) : launch_tq_decode(a, tq, bits, B, st);
+  hipError_t e = gl ? launch_tq_generic(a, tq, *gl, B, D, st) : launch_tq_decode(a, tq, bits, B, D, st);
   if (e != hipSuccess) {
     set_error("vrm_paged_decode_tq: partition kernel launch failed: %s", hipGetErrorString(e));
     return (int)e;

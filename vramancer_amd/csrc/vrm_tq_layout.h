@@ -1,5 +1,5 @@
-// Layout of a TurboQuant KV page of this library (head_dim 128: padded_dim
-// 128, 7 polar levels, 127 angles, 64 QJL signs).
+// Layout of a TurboQuant KV page of this library (head_dim 65 .. 128:
+// padded_dim 128, 7 polar levels, 127 angles, 64 QJL signs).
 //
 // The pool keeps the reference's addressing, tq_pool[P][L][2][KH][slice],
 // one slice of kTqSliceBytes(bits) bytes per (page, layer, K/V, kv-head) with
@@ -146,9 +146,11 @@ __host__ __device__ inline GenLayout gen_layout(int head_dim, int bits, int qjl,
   return g;
 }
 
-// True for the settings the tuned layout above (and its decode kernel) serves.
+// True for the settings the tuned layout above (and its decode kernel) serves:
+// padded dim 128 (head_dim 65 .. 128, zero-padded before the rotation as the
+// compressor pads), 64 QJL rows, 16-token pages, 2 to 4 bits.
 __host__ __device__ inline bool tuned_layout(int head_dim, int bits, int qjl, int ps) {
-  return head_dim == kPD && qjl == kQjl && ps == kTokens && bits >= 2 && bits <= 4;
+  return head_dim > kPD / 2 && head_dim <= kPD && qjl == kQjl && ps == kTokens && bits >= 2 && bits <= 4;
 }
 
 // True for settings the generic layout serves.

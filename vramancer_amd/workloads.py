@@ -196,7 +196,7 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
 
         torch.manual_seed(seed)  # the rotation and JL matrix are fixed by the seed
         compressor = KVCacheCompressor(cfg.head_dim, int(cfg.codec[2]))
-        kv_pool = tq_pages.allocate_pool(P, L, KH, compressor, device)
+        kv_pool = tq_pages.allocate_pool(P, L, KH, compressor, device, PS)
         dtype = None
     elif cfg.codec in ("int8", "fp8"):
         dtype = _pool_dtype(cfg.codec)
@@ -218,7 +218,7 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
                     kv_zeros[s:e, layer, kv] = zp
             elif compressor is not None:
                 tq_pages.quantize_pages(kv_pool, layer, page_ids_all[s:e], k.to(torch.bfloat16),
-                                        v.to(torch.bfloat16), compressor)
+                                        v.to(torch.bfloat16), compressor, page_size=PS)
             elif kv_scales is not None:
                 # the quantized pools start from bf16 activations
                 kv_quant.quantize_pages(kv_pool, kv_scales, layer, page_ids_all[s:e], k.to(torch.bfloat16),
@@ -249,10 +249,16 @@ def algorithmic_bytes(cfg: DecodeConfig, lens: Sequence[int]) -> Dict[str, float
     tokens = sum(lens)
     pages = sum((n + PS - 1) // PS for n in lens)
     if cfg.codec in ("tq3", "tq4"):
-        # per token and kv-head: K angles + 64 sign bits + fp16 radius + fp16 norm, V angles + fp16 radius
+        # per token and kv-head: K angles + QJL sign bits + fp16 radius + fp16 norm, V angles + fp16
+        # radius; padded_dim - 1 angles of `bits` bits, padded_dim / 2 QJL rows (the compressor's
+        # defaults, core/kv_quantizer.py:225-229)
         bits = int(cfg.codec[2])
-        angles = (127 * bits + 7) // 8
-        kv = tokens * KH * ((angles + 8 + 2 + 2) + (angles + 2))
+        pd = 64
+        while pd < D:
+            pd *= 2
+        angles = ((pd - 1) * bits + 7) // 8
+        signs = (pd // 2 + 7) // 8
+        kv = tokens * KH * ((angles + signs + 2 + 2) + (angles + 2))
         scales = 0
         qo = 2 * len(lens) * H * D * 4
         table = pages * 4
