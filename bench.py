@@ -561,7 +561,7 @@ def main():
 
     # even batches over int8 / fp8 pools take the balanced decode (one
     # workgroup per sequence and kv-head, no merge pass), as the manager does
-    balanced = (not turbo and not q4 and D in (64, 128) and PS == 16 and
+    balanced = (not turbo and not q4 and D in (64, 80, 96, 112, 128) and PS == 16 and
                 prefer_balanced(lens_list, KH, pool.dtype))
     log(f"decode mode: {'balanced' if balanced else 'work items + merge'}")
 
@@ -731,7 +731,7 @@ def main():
         tuned = 64 < D <= 128 and comp.qjl_dim == 64 and comp.bits_per_angle in (2, 3, 4) and PS == 16
         pd = 1 << max(6, (D - 1).bit_length())
         kname = KERNEL[cfg.codec] if tuned else f"decode_tq_gen_kernel<{pd}> + merge"
-    elif PS == 16 and D in (64, 128, 256):
+    elif PS == 16 and (D in (64, 128, 256) or (D in (80, 96, 112) and cfg.codec in ("int8", "fp8", "bf16", "f16"))):
         kname = KERNEL[cfg.codec].format(D=D)
         if balanced:
             kname = kname.replace(">", ",balanced>")

@@ -146,7 +146,7 @@ int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const floa
  * ln sum_t exp(scale q.k_t) per (b, h) as in vrm_paged_decode_lse.  No
  * counterpart in the reference (whose kernel is one warp per (head, sequence),
  * csrc/paged_attention_kernel.cu:445-499, with no split).
- * Supported: int8 and fp8 pools, D in {64, 128}, PS == 16, and page tables
+ * Supported: int8 and fp8 pools, D in {64, 80, 96, 112, 128}, PS == 16, and page tables
  * narrow enough for a workgroup's LDS copy of one row (max_pp up to ~12000 at
  * D = 128); other requests return VRM_ERR_UNSUPPORTED.
  */

@@ -264,4 +264,6 @@ def test_balanced_entry_rejects_bad_arguments(lib):
     assert call(2, None) == -1 and b"kv_scales" in lib.vrm_last_error()
     assert call(17, _lib.VRM_KV_BF16) == -2
     assert call(17, 99) == -1
-    assert call(10, 96) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert call(10, 256) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert call(10, 48) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert call(11, 32) == -2 and b"page_size" in lib.vrm_last_error()

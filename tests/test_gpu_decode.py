@@ -325,12 +325,13 @@ def test_decode_q4_unaligned_scales_take_the_valu_kernel():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-def test_decode_float_pool_ignores_garbage_past_context(dtype):
+@pytest.mark.parametrize("D", [128, 80])
+def test_decode_float_pool_ignores_garbage_past_context(dtype, D):
     """Slots past the context in the last page, and pages the table marks
     absent, may hold anything (here NaN and inf); the output must equal the
     oracle's, which never reads them."""
-    _say(f"garbage past context {dtype}")
-    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, 128, [37, 160, 5], seed=31)
+    _say(f"garbage past context {dtype} D {D}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, D, [37, 160, 5], seed=31)
     for b, c in enumerate(lens.tolist()):
         last = int(table[b, (c - 1) // 16])
         pool[last, 1, :, :, c % 16 or 16:, :] = float("nan")
@@ -342,7 +343,7 @@ def test_decode_float_pool_ignores_garbage_past_context(dtype):
     assert torch.isfinite(out).all()
     for b in range(3):
         K, V = PD.gather_sequence(pool, table[b], int(lens[b]), 1, skip_invalid=True)
-        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(128))
+        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(D))
         _assert_close(out[b].cpu(), ref, f"seq {b}")
 
 
@@ -395,15 +396,16 @@ def _dequant_pool(pool, sc, layer):
 
 
 @pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
-def test_decode_quantized_pool_ignores_garbage_past_context(dtype):
+@pytest.mark.parametrize("D", [128, 96, 112])
+def test_decode_quantized_pool_ignores_garbage_past_context(dtype, D):
     """Codes and scales of slots past the context, of a page the table marks
     absent and of a page it never references may hold anything: NaN and inf
     scales, and for fp8 the NaN code 0x7f (0x7f is int8's largest code).  The
     output must equal the oracle's, which never reads them."""
     from oracle.kv_codecs import pool_from_logical, pool_to_logical
 
-    _say(f"garbage past context {dtype}")
-    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, 128, [37, 160, 5], seed=31)
+    _say(f"garbage past context {dtype} D {D}")
+    q, pool, sc, table, lens = _pool_case(dtype, 3, 16, 2, D, [37, 160, 5], seed=31)
     raw = pool_to_logical(pool.view(torch.uint8))
     for b, c in enumerate(lens.tolist()):
         last = int(table[b, (c - 1) // 16])
@@ -422,7 +424,7 @@ def test_decode_quantized_pool_ignores_garbage_past_context(dtype):
     f = _dequant_pool(pool, sc, 1)
     for b in range(3):
         K, V = PD.gather_sequence(f, table[b], int(lens[b]), 1, skip_invalid=True)
-        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(128))
+        ref = PD.dense_attention(q[b], K, V, 1 / math.sqrt(D))
         _assert_close(out[b].cpu(), ref, f"{dtype} seq {b}")
 
 
@@ -543,6 +545,9 @@ def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
     (8, 2, 64, [100, 260]),
     (12, 12, 64, [64, 65, 700]),
     (28, 4, 128, [8192, 8000, 1]),               # 512 pages in LDS
+    (40, 8, 96, [700, 333, 5]),                  # head_dims between 64 and 128
+    (16, 2, 80, [260, 17]),
+    (24, 4, 112, [1000, 999]),
 ])
 def test_balanced_decode_matches_oracle(dtype, H, KH, D, ctxs):
     """The balanced decode (one workgroup per sequence and kv-head, partitions

@@ -61,6 +61,12 @@ constexpr int kVScaleHeadroom = 12;
 constexpr float kNoMax = -1.0e30f;
 
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// 16 bytes at a 4-byte aligned address
+__device__ __forceinline__ uint4 ld16_a4(const uint8_t* p) {
+  uint4 r;
+  __builtin_memcpy(&r, __builtin_assume_aligned(p, 4), 16);
+  return r;
+}
 __device__ __forceinline__ float4 ldf4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 __device__ __forceinline__ v4i as_v4i(uint4 u) {
@@ -123,7 +129,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // One page of K and V for this lane, with the scales its tokens need.
 template <int D>
 struct PageSlot {
-  static constexpr int NJ = D / 64;
+  static constexpr int NJ = (D + 63) / 64;
   uint4 k[NJ];  // token col, dims 64 j + 16 grp .. + 15
   uint4 v[NJ];  // tokens 4 grp .. + 3 of dims col + 16 blk, blk = 4 j .. 4 j + 3
   float4 ks;    // int8: K scales of tokens 4 grp .. + 3; fp8: .x = the page's K scale
@@ -199,9 +205,13 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     decode_stream_kernel(DecodeArgs a, int G) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
   constexpr int HEAD_BYTES = kPS * D;     // one (page, layer, K/V, head) slice
-  constexpr int NJ = D / 64;              // 16-byte loads per lane and page, for K and for V
+  constexpr int NJ = (D + 63) / 64;       // 16-byte loads per lane and page, for K and for V
   constexpr int NB = D / 16;              // 16-dim blocks of the output column
-  static_assert(D % 64 == 0, "head_dim must be a multiple of 64");
+  // The last 64-dim chunk holds KPART dims (head_dim 80 / 96 / 112: 16 / 32 /
+  // 48): K lanes grp < KPART / 16 and the first KPART / 16 V dwords are real,
+  // the rest is zero (never loaded: past the row).
+  constexpr int KPART = D - 64 * (NJ - 1);
+  static_assert(D % 16 == 0 && D <= 256, "head_dim must be a multiple of 16, at most 256");
   static_assert(RING % 2 == 0, "pages are consumed in pairs");
 
   const int lane = threadIdx.x & 63;
@@ -272,8 +282,16 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      s.k[j] = ld16(kb + j * 64);
-      s.v[j] = ld16(vb + j * 16);
+      if (KPART == 64 || j < NJ - 1) {
+        s.k[j] = ld16(kb + j * 64);
+        s.v[j] = (D / 4) % 16 == 0 ? ld16(vb + j * 16) : ld16_a4(vb + j * 16);  // V rows of D / 4 bytes
+      } else {
+        const bool kin = grp < KPART / 16;
+        const uint4 kk = ld16(kin ? kb + j * 64 : kb);  // clamped into the row, then dropped
+        s.k[j] = kin ? kk : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t* vw = reinterpret_cast<const uint32_t*>(vb + j * 16);
+        s.v[j] = make_uint4(vw[0], KPART >= 32 ? vw[1] : 0u, KPART >= 48 ? vw[2] : 0u, 0u);
+      }
     }
     if constexpr (KIND == K_I8) {
       const size_t ts = head_index(pc, 0) * kPS + grp * 4;
@@ -324,7 +342,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int e4 = 0; e4 < 4; ++e4) {
-      const float4 f = ldf4(qrow + j * 64 + grp * 16 + e4 * 4);
+      const bool qin = 64 * j + 16 * grp < D;  // 16-dim groups past the head_dim are zero
+      const float4 f = qin ? ldf4(qrow + j * 64 + grp * 16 + e4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
       qv[j][4 * e4] = f.x;
       qv[j][4 * e4 + 1] = f.y;
       qv[j][4 * e4 + 2] = f.z;
@@ -628,7 +647,7 @@ template <> struct FloatOps<K_F16> {
 
 template <int D>
 struct FloatSlot {
-  static constexpr int NC = D / 32;
+  static constexpr int NC = (D + 31) / 32;
   uint4 k[NC];  // token col, dims 32 c + 8 grp .. + 7
   uint4 v[NC];  // same positions of V
   bool ok;      // page id inside the pool (wave-uniform)
@@ -642,9 +661,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   constexpr int RING = D <= 128 ? 4 : 2;
   constexpr int ROW = D * 2;              // bytes per token row
   constexpr int HEAD_BYTES = kPS * ROW;   // one (page, layer, K/V, head) slice
-  constexpr int NC = D / 32;              // 32-dim chunks: one 16-byte load per lane each
+  constexpr int NC = (D + 31) / 32;       // 32-dim chunks: one 16-byte load per lane each
   constexpr int NB = D / 16;              // 16-dim blocks of the output column
-  static_assert(D % 32 == 0, "head_dim must be a multiple of 32");
+  // head_dim 80 / 112: the last chunk holds 16 dims, lanes grp < 2 (the rest
+  // is zero, never loaded: past the row)
+  constexpr int CPART = D - 32 * (NC - 1);
+  static_assert(D % 16 == 0 && D <= 128, "head_dim must be a multiple of 16, at most 128");
 
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -680,8 +702,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   vec QH[NC][2];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const float4 f0 = ldf4(qrow + 32 * c + 8 * grp);
-    const float4 f1 = ldf4(qrow + 32 * c + 8 * grp + 4);
+    const bool qin = 32 * c + 8 * grp < D;
+    const float4 f0 = qin ? ldf4(qrow + 32 * c + 8 * grp) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 f1 = qin ? ldf4(qrow + 32 * c + 8 * grp + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float x[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -712,8 +735,16 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
     const uint8_t* kb = layer_base + (size_t)pc * page_stride + col * ROW + grp * 16;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      s.k[c] = ld16(kb + c * 64);
-      s.v[c] = ld16(kb + kv_stride + c * 64);
+      if (CPART == 32 || c < NC - 1) {
+        s.k[c] = ld16(kb + c * 64);
+        s.v[c] = ld16(kb + kv_stride + c * 64);
+      } else {
+        const bool in = grp < CPART / 8;
+        const int off = in ? c * 64 : 0;  // clamped into the row, then dropped
+        const uint4 kk = ld16(kb + off), vv = ld16(kb + kv_stride + off);
+        s.k[c] = in ? kk : make_uint4(0u, 0u, 0u, 0u);
+        s.v[c] = in ? vv : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
 
@@ -1172,6 +1203,9 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   while (units % W) --W;
   switch (D) {
     case 64: launch_kernel<KIND, 64>(a, B, units, W, G, st); break;
+    case 80: launch_kernel<KIND, 80>(a, B, units, W, G, st); break;
+    case 96: launch_kernel<KIND, 96>(a, B, units, W, G, st); break;
+    case 112: launch_kernel<KIND, 112>(a, B, units, W, G, st); break;
     case 128: launch_kernel<KIND, 128>(a, B, units, W, G, st); break;
     default: launch_kernel<KIND, 256>(a, B, units, W, G, st); break;
   }
@@ -1199,6 +1233,18 @@ hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) 
   return hipErrorInvalidValue;
 }
 
+template <int KIND>
+hipError_t launch_balanced_kind(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
+  switch (D) {
+    case 64: return launch_balanced_d<KIND, 64>(a, B, G, st);
+    case 80: return launch_balanced_d<KIND, 80>(a, B, G, st);
+    case 96: return launch_balanced_d<KIND, 96>(a, B, G, st);
+    case 112: return launch_balanced_d<KIND, 112>(a, B, G, st);
+    case 128: return launch_balanced_d<KIND, 128>(a, B, G, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
   const int units = a.KH * ((a.H / a.KH) / G);
   int W = kMaxWaves;
@@ -1212,12 +1258,8 @@ hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
 hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
   if (G < 1 || G > 16) return hipErrorInvalidValue;
   switch (kind) {
-    case K_I8:
-      return D == 64 ? launch_balanced_d<K_I8, 64>(a, B, G, st)
-                     : D == 128 ? launch_balanced_d<K_I8, 128>(a, B, G, st) : hipErrorInvalidValue;
-    case K_FP8:
-      return D == 64 ? launch_balanced_d<K_FP8, 64>(a, B, G, st)
-                     : D == 128 ? launch_balanced_d<K_FP8, 128>(a, B, G, st) : hipErrorInvalidValue;
+    case K_I8: return launch_balanced_kind<K_I8>(a, B, D, G, st);
+    case K_FP8: return launch_balanced_kind<K_FP8>(a, B, D, G, st);
     default: return hipErrorInvalidValue;
   }
 }

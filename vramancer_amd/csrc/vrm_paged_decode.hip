@@ -572,11 +572,16 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   // the VALU kernel.
   const bool q4_aligned = ((reinterpret_cast<uintptr_t>(a.pool) & 3) | (reinterpret_cast<uintptr_t>(a.q4_scale) & 7) |
                            (reinterpret_cast<uintptr_t>(a.q4_zero) & 7)) == 0;
-  // The tuned kernels are compiled for page 16 and head_dim 64 / 128 / 256;
-  // every other shape runs on the generic kernel (vrm_decode_generic.hip).
-  const bool tuned = PS == kPS && (D == 64 || D == 128 || D == 256);
-  const bool mfma = tuned && (kind == K_I8 || kind == K_FP8 || ((kind == K_BF16 || kind == K_F16) && D <= 128) ||
-                              (kind == K_Q4 && D == 128 && q4_aligned));
+  // The tuned kernels are compiled for page 16: the matrix-core stream at
+  // head_dim 64 / 80 / 96 / 112 / 128 (and 256 for int8 / fp8), the VALU split
+  // kernel at 64 / 128 / 256; every other shape runs on the generic kernel
+  // (vrm_decode_generic.hip).
+  const bool stream_d = D == 64 || D == 80 || D == 96 || D == 112 || D == 128 || D == 256;
+  const bool split_d = D == 64 || D == 128 || D == 256;
+  const bool mfma = PS == kPS && (((kind == K_I8 || kind == K_FP8) && stream_d) ||
+                                  ((kind == K_BF16 || kind == K_F16) && stream_d && D <= 128) ||
+                                  (kind == K_Q4 && D == 128 && q4_aligned));
+  const bool tuned = mfma || (PS == kPS && split_d);
   const int max_tile = mfma ? 16 : kind == K_Q4 ? 6 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
@@ -868,8 +873,9 @@ extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool
     set_error("%s: quantized pool needs kv_scales", who);
     return VRM_ERR_ARG;
   }
-  if ((D != 64 && D != 128) || PS != kPS) {  // at D = 256 two page pairs per wave do not fit in registers
-    set_error("%s: head_dim %d / page_size %d unsupported (64 or 128, page 16)", who, D, PS);
+  if ((D != 64 && D != 80 && D != 96 && D != 112 && D != 128) || PS != kPS) {
+    // at D = 256 two page pairs per wave do not fit in registers
+    set_error("%s: head_dim %d / page_size %d unsupported (64, 80, 96, 112 or 128, page 16)", who, D, PS);
     return VRM_ERR_UNSUPPORTED;
   }
   const int G = pick_group_tile(H / KH, 16);
