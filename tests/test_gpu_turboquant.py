@@ -60,6 +60,8 @@ def _compare_ieee(p, kv_cpu, gpu, tag):
                        ref["qjl_norms"].reshape(-1).view(torch.int16)), f"{tag}: qjl norms"
     flips = _signs_ok(gpu["qjl_signs"].cpu(), ref["qjl_signs"], proj, residual, p, tag)
     print(f"[{tag}] IEEE-exact; qjl sign tie flips: {flips} of {ref['qjl_signs'].numel()}", flush=True)
+    # ties of the float64 projection are rare: none seen on 2.3 M signs
+    assert flips <= max(1, ref["qjl_signs"].numel() // 10000), f"{tag}: {flips} QJL sign tie flips"
     return ref
 
 
@@ -78,6 +80,12 @@ def _compare_host_torch(p, kv_cpu, gpu, tag):
     n_bins = int((ga != ra).sum())
     n_rad = int((gr != rr).sum())
     print(f"[{tag}] vs host torch: {n_rad} radius ulp ties, {n_bins} edge-bin ties of {ra.numel()}", flush=True)
+    # Bounds on the host-dependent differences (torch's CPU sqrt is not correctly
+    # rounded; its error rate depends on the host's vector unit): at most 1 % of
+    # the radii one ulp apart (0.01-0.6 % seen), at most 0.1 % of the bins at an
+    # edge (none seen).
+    assert n_rad <= max(1, gr.numel() // 100), f"{tag}: {n_rad} of {gr.numel()} radii one ulp apart"
+    assert n_bins <= max(1, ra.numel() // 1000), f"{tag}: {n_bins} of {ra.numel()} edge bins differ"
 
 
 def test_compress_matches_reference_goldens():

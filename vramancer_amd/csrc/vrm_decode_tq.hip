@@ -292,7 +292,6 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // matching k order: chunk c, element e <-> JL row 16 (2 c + e / 4) + 4 grp + e % 4.
   // PJ carries q_proj times the QJL scale, hi / lo by column half like QB.
   const float qjl_scale = a.qscale * tq.qjl_coef;
-  const bool use_qjl = tq.qjl_coef != 0.f;
   v8h PJ[2];
   {
     float pj[4][4];
@@ -447,10 +446,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, hw), QB[c], c4, 0, 0, 0);
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lw), QB[c], c4, 0, 0, 0);
     }
-    if (use_qjl) {
+    {
       // The QJL term on the same accumulator: row operand +-norm of token col
       // (the fp16 norm with its sign bit flipped where the sign bit is clear;
-      // exact), against PJ.
+      // exact), against PJ (zero for scores without the term, whose norms are
+      // still finite; tokens past the context are masked below).
       const uint32_t nn = s.knorm | (s.knorm << 16);
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
