@@ -614,6 +614,21 @@ def main():
     us_step = time_events(full, args.steps)
     # TurboQuant, Q4 and the balanced decode: one kernel, whose time is the whole decode
     us_part = us_step if (turbo or q4 or balanced) else time_events(partitions, args.steps)
+    # The balanced decode's loads alone (same grid, addresses, order and ring,
+    # no computation): what its access pattern costs on this GPU.
+    us_loads = None
+    if balanced:
+        def loads(i):
+            rc = lib.vrm_paged_decode_balanced_loads(q.data_ptr(), pool.data_ptr(), sc_ptr, table.data_ptr(),
+                                                     lens.data_ptr(), out.data_ptr(), B, H, KH, D, PS, L, P, max_pp,
+                                                     layers[i % len(layers)], scale, code, stream)
+            if rc:
+                _lib.check(rc, "load-only pass")
+
+        for i in range(10):
+            loads(i)
+        us_loads = time_events(loads, args.steps)
+        log(f"load-only pass of the same pattern {us_loads:.2f} us")
     log(f"decode {us_step:.2f} us/layer-step, partition kernel {us_part:.2f} us")
 
     # The drop-in Python call: the same decode through the module API, with the
@@ -748,6 +763,10 @@ def main():
         "kernel": kname + (f" (G={G}, whole decode)" if (turbo or q4 or balanced) else f" (G={G}, partition pass)"),
         "kernel_us": round(us_part, 3),
     }
+    if us_loads is not None:
+        # the access pattern's own time and the kernel's speed as a fraction of it
+        roofline["pattern_loads_us"] = round(us_loads, 3)
+        roofline["frac_of_pattern"] = round(us_loads / us_part, 4)
     valu = None
     if (turbo or q4) and not shape_override and os.path.exists(VALU_FILE):
         with open(VALU_FILE) as f:

@@ -156,6 +156,19 @@ int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const flo
                               int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
 
 /*
+ * Measurement aid, no counterpart in the reference: the balanced decode's
+ * own loads (same grid, addresses, order, register ring and page hand-out)
+ * with the computation left out; a checksum of the loaded words lands in
+ * out (values meaningless).  Its time is what the decode's access pattern
+ * alone costs on this GPU, the ceiling against which the decode's own time
+ * is judged.  Same arguments and support as vrm_paged_decode_balanced.
+ */
+int vrm_paged_decode_balanced_loads(const float* query, const void* kv_pool, const float* kv_scales,
+                                    const int32_t* page_table, const int32_t* context_lens, float* out,
+                                    int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                    int layer_idx, float scale, int kv_dtype, vrm_stream_t stream);
+
+/*
  * The two passes of vrm_paged_decode, for callers that schedule them
  * separately (and for timing the dominant pass on its own):
  * vrm_paged_decode_partitions writes per-partition (max, sum, unnormalised

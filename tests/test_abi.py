@@ -267,3 +267,10 @@ def test_balanced_entry_rejects_bad_arguments(lib):
     assert call(10, 256) == -2 and b"head_dim" in lib.vrm_last_error()
     assert call(10, 48) == -2 and b"head_dim" in lib.vrm_last_error()
     assert call(11, 32) == -2 and b"page_size" in lib.vrm_last_error()
+    # the measuring build takes the same arguments (no lse) and the same checks
+    g = lib.vrm_paged_decode_balanced_loads
+    largs = args[:6] + args[7:]
+    assert g(*largs[:2], None, *largs[3:]) == -1 and b"kv_scales" in lib.vrm_last_error()
+    bad = list(largs)
+    bad[9] = 256
+    assert g(*bad) == -2 and b"head_dim" in lib.vrm_last_error()

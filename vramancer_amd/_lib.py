@@ -44,6 +44,7 @@ SIGNATURES = {
     "vrm_paged_decode": (_i, [_p, _p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _p]),
     "vrm_paged_decode_noalloc": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 9 + [_f, _i, _p]),
     "vrm_paged_decode_balanced": (_i, [_p] * 7 + [_i] * 9 + [_f, _i, _p]),
+    "vrm_paged_decode_balanced_loads": (_i, [_p] * 6 + [_i] * 9 + [_f, _i, _p]),
     "vrm_paged_decode_partitions": (_i, [_p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _p]),
     "vrm_paged_decode_merge": (_i, [_p, _p, _p, _sz] + [_i] * 6 + [_p]),
     "vrm_paged_decode_q4": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _p]),

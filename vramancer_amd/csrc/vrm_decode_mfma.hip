@@ -200,7 +200,10 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
   }
 }
 
-template <int KIND, int D, bool BALANCED>
+// LOADS: a measuring build that issues exactly the kernel's loads (same
+// addresses, order, ring and page hand-out) and folds the loaded words into
+// a checksum instead of computing: the time of its access pattern alone.
+template <int KIND, int D, bool BALANCED, bool LOADS = false>
 __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
     decode_stream_kernel(DecodeArgs a, int G) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
@@ -435,7 +438,19 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   };
 
   // Pages pi and pi + 1 (the second may lie past the partition).
+  uint32_t probe = 0;  // LOADS: checksum of the loaded words
   auto process_pair = [&](const PageSlot<D>& s0, const PageSlot<D>& s1, int pi, bool has1) {
+    if constexpr (LOADS) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        probe ^= s0.k[j].x ^ s0.k[j].y ^ s0.k[j].z ^ s0.k[j].w ^ s0.v[j].x ^ s0.v[j].y ^ s0.v[j].z ^ s0.v[j].w ^
+                 s1.k[j].x ^ s1.k[j].y ^ s1.k[j].z ^ s1.k[j].w ^ s1.v[j].x ^ s1.v[j].y ^ s1.v[j].z ^ s1.v[j].w;
+      probe ^= __float_as_uint(s0.ks.x + s0.ks.y + s0.ks.z + s0.ks.w + s0.vs.x + s0.vs.y + s0.vs.z + s0.vs.w +
+                               s1.ks.x + s1.ks.y + s1.ks.z + s1.ks.w + s1.vs.x + s1.vs.y + s1.vs.z + s1.vs.w);
+      (void)pi;
+      (void)has1;
+      return;
+    }
     float sc[8];
     page_scores(s0, pi, sc);
     if (has1) {
@@ -593,6 +608,10 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   }
 
   // ---------------- partition result ----------------
+  if constexpr (LOADS) {
+    a.out[((size_t)b * a.H + h0) * D + lane] = __uint_as_float(probe);  // lane < 64 <= D
+    return;
+  }
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   if constexpr (BALANCED) {
@@ -1216,31 +1235,33 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
 // WPU the largest of 4, 2, 1 whose launch fits one resident round of waves
 // and 64 KB of LDS.  Returns hipErrorInvalidValue when even WPU = 1 does not
 // fit (page tables too wide for the LDS copy of the ids).
-template <int KIND, int D>
+template <int KIND, int D, bool LOADS>
 hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) {
   const int units = a.KH * ((a.H / a.KH) / G);
   const int wgs_y = (units + kUnitsPerWg - 1) / kUnitsPerWg;
-  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true>);
+  // the launch shape of the decode itself, for both builds
+  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false>);
   const int resident = items_target(fn, kMaxBalancedWaves, 0, 1);  // resident waves (capped)
   for (int wpu = 4; wpu >= 1; wpu /= 2) {
     const int W = kUnitsPerWg * wpu;
     const size_t lds = balanced_lds_bytes(a.max_pp, W, G, D);
     if (lds > kMaxBalancedLds) continue;
     if (wpu > 1 && (long)B * wgs_y * W > resident) continue;
-    hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true>), dim3(B, wgs_y, 1), dim3(64 * W), lds, st, a, G);
+    hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, LOADS>), dim3(B, wgs_y, 1), dim3(64 * W), lds, st, a,
+                       G);
     return hipGetLastError();
   }
   return hipErrorInvalidValue;
 }
 
-template <int KIND>
+template <int KIND, bool LOADS>
 hipError_t launch_balanced_kind(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   switch (D) {
-    case 64: return launch_balanced_d<KIND, 64>(a, B, G, st);
-    case 80: return launch_balanced_d<KIND, 80>(a, B, G, st);
-    case 96: return launch_balanced_d<KIND, 96>(a, B, G, st);
-    case 112: return launch_balanced_d<KIND, 112>(a, B, G, st);
-    case 128: return launch_balanced_d<KIND, 128>(a, B, G, st);
+    case 64: return launch_balanced_d<KIND, 64, LOADS>(a, B, G, st);
+    case 80: return launch_balanced_d<KIND, 80, LOADS>(a, B, G, st);
+    case 96: return launch_balanced_d<KIND, 96, LOADS>(a, B, G, st);
+    case 112: return launch_balanced_d<KIND, 112, LOADS>(a, B, G, st);
+    case 128: return launch_balanced_d<KIND, 128, LOADS>(a, B, G, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1255,11 +1276,16 @@ hipError_t launch_q4(const DecodeArgs& a, int B, int G, hipStream_t st) {
 
 }  // namespace
 
-hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
+hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st,
+                                  bool loads_only) {
   if (G < 1 || G > 16) return hipErrorInvalidValue;
   switch (kind) {
-    case K_I8: return launch_balanced_kind<K_I8>(a, B, D, G, st);
-    case K_FP8: return launch_balanced_kind<K_FP8>(a, B, D, G, st);
+    case K_I8:
+      return loads_only ? launch_balanced_kind<K_I8, true>(a, B, D, G, st)
+                        : launch_balanced_kind<K_I8, false>(a, B, D, G, st);
+    case K_FP8:
+      return loads_only ? launch_balanced_kind<K_FP8, true>(a, B, D, G, st)
+                        : launch_balanced_kind<K_FP8, false>(a, B, D, G, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -856,11 +856,11 @@ extern "C" int vrm_paged_decode_noalloc(const float* query, const void* kv_pool,
                       D, PS, L, P, max_pp, layer_idx, scale, kv_dtype, stream, kBoth);
 }
 
-extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const float* kv_scales,
-                                         const int32_t* page_table, const int32_t* context_lens, float* out,
-                                         float* lse, int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
-                                         int layer_idx, float scale, int kv_dtype, vrm_stream_t stream) {
-  const char* who = "vrm_paged_decode_balanced";
+namespace {
+int balanced_entry(const float* query, const void* kv_pool, const float* kv_scales, const int32_t* page_table,
+                   const int32_t* context_lens, float* out, float* lse, int B, int H, int KH, int D, int PS, int L,
+                   int P, int max_pp, int layer_idx, float scale, int kv_dtype, vrm_stream_t stream, bool loads_only,
+                   const char* who) {
   int rc = check_common(query, kv_pool, page_table, context_lens, out, B, H, KH, D, PS, L, P, max_pp, layer_idx,
                         scale);
   if (rc) return rc;
@@ -900,13 +900,30 @@ extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool
   a.lse = lse;
   a.out = out;
   a.qscale = scale * kLog2e;
-  const hipError_t e = launch_stream_balanced(a, kind, B, D, G, reinterpret_cast<hipStream_t>(stream));
+  const hipError_t e = launch_stream_balanced(a, kind, B, D, G, reinterpret_cast<hipStream_t>(stream), loads_only);
   if (e != hipSuccess) {
     set_error("%s: kernel launch failed: %s", who, hipGetErrorString(e));
     return (int)e;
   }
   clear_error();
   return VRM_OK;
+}
+}  // namespace
+
+extern "C" int vrm_paged_decode_balanced(const float* query, const void* kv_pool, const float* kv_scales,
+                                         const int32_t* page_table, const int32_t* context_lens, float* out,
+                                         float* lse, int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                         int layer_idx, float scale, int kv_dtype, vrm_stream_t stream) {
+  return balanced_entry(query, kv_pool, kv_scales, page_table, context_lens, out, lse, B, H, KH, D, PS, L, P, max_pp,
+                        layer_idx, scale, kv_dtype, stream, false, "vrm_paged_decode_balanced");
+}
+
+extern "C" int vrm_paged_decode_balanced_loads(const float* query, const void* kv_pool, const float* kv_scales,
+                                               const int32_t* page_table, const int32_t* context_lens, float* out,
+                                               int B, int H, int KH, int D, int PS, int L, int P, int max_pp,
+                                               int layer_idx, float scale, int kv_dtype, vrm_stream_t stream) {
+  return balanced_entry(query, kv_pool, kv_scales, page_table, context_lens, out, nullptr, B, H, KH, D, PS, L, P,
+                        max_pp, layer_idx, scale, kv_dtype, stream, true, "vrm_paged_decode_balanced_loads");
 }
 
 extern "C" int vrm_paged_decode_partitions(const float* query, const void* kv_pool, const float* kv_scales,
