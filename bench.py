@@ -746,7 +746,9 @@ def main():
         tuned = 64 < D <= 128 and comp.qjl_dim == 64 and comp.bits_per_angle in (2, 3, 4) and PS == 16
         pd = 1 << max(6, (D - 1).bit_length())
         kname = KERNEL[cfg.codec] if tuned else f"decode_tq_gen_kernel<{pd}> + merge"
-    elif PS == 16 and (D in (64, 128, 256) or (D in (80, 96, 112) and cfg.codec in ("int8", "fp8", "bf16", "f16"))):
+    elif (PS == 16 and D in (64, 128, 256)) or (
+            PS in (16, 32, 64, 128, 256, 512, 1024) and D in (64, 80, 96, 112, 128, 256)
+            and (cfg.codec in ("int8", "fp8") or (cfg.codec in ("bf16", "f16") and D <= 128))):
         kname = KERNEL[cfg.codec].format(D=D)
         if balanced:
             kname = kname.replace(">", ",balanced>")

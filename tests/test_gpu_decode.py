@@ -625,7 +625,7 @@ def test_api_takes_the_balanced_decode_for_even_batches():
 # 128 / 256): the reference kernel takes any head_dim <= 256 and the pool's
 # page size (csrc/paged_attention_kernel.cu:102-111, 460-466).  int8 / fp8
 # pools need D % 16 == 0 and PS % 4 == 0 (their tiled V).
-SHAPES_ALL = [(80, 16), (96, 16), (112, 16), (96, 8), (128, 8), (128, 32), (64, 32), (48, 4)]
+SHAPES_ALL = [(80, 16), (96, 16), (112, 16), (96, 8), (128, 8), (128, 32), (64, 32), (48, 4), (96, 64), (112, 128)]
 SHAPES_FLOAT = [(100, 16), (72, 7), (256, 5), (30, 32), (1, 16)]
 
 

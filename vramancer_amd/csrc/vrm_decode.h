@@ -37,6 +37,7 @@ struct DecodeArgs {
   int target;                 // work items the partition size aims for
   float* lse;                 // optional [B][H] natural-log sum of exp(scale * q.k), written by the merge
   float* out;                 // [B][H][D]: written directly by the balanced (one workgroup per sequence) mode
+  int vshift;                 // stream kernels: pages hold 16 << vshift tokens (0: 16-token pages)
 };
 
 // ---------------------------------------------------------------------------

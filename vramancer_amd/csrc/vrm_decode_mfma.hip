@@ -207,7 +207,12 @@ template <int KIND, int D, bool BALANCED, bool LOADS = false>
 __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
     decode_stream_kernel(DecodeArgs a, int G) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
-  constexpr int HEAD_BYTES = kPS * D;     // one (page, layer, K/V, head) slice
+  // Pages of 16 << vshift tokens are streamed as 16-token sub-pages: work
+  // items, ids and masks count sub-pages, and sub-page v of a sequence is
+  // token block v & vmask of its table entry v >> vshift.
+  const int vshift = BALANCED ? 0 : a.vshift;  // the balanced mode takes 16-token pages only
+  const int vmask = (1 << vshift) - 1;
+  const int head_bytes = (kPS << vshift) * D;  // one (page, layer, K/V, head) slice
   constexpr int NJ = (D + 63) / 64;       // 16-byte loads per lane and page, for K and for V
   constexpr int NB = D / 16;              // 16-dim blocks of the output column
   // The last 64-dim chunk holds KPART dims (head_dim 80 / 96 / 112: 16 / 32 /
@@ -256,7 +261,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     if (threadIdx.x < kUnitsPerWg) pair_ctr[threadIdx.x] = 0;
     __syncthreads();
   } else {
-    if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+    if (!find_item(a.ctx_lens, a.B, a.max_pp << vshift, a.target, item, item == 0 && unit == 0, a.header, wi))
+      return;
   }
   const int b = wi.b;
   const int n_pages = wi.n_pages;
@@ -264,23 +270,30 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);  // valid tokens of the partition
   // page ids, fetched RING pages ahead of the data: lane u < RING reads the id
   // of page first + u (clamped to the last page)
-  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
-  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  const int32_t* prow = a.page_table + (size_t)b * a.max_pp;
+  // sub-page id (page << vshift | block), or -1 for an absent page
+  auto ids_at = [&](int first) {
+    const int v = wi.p_begin + min(first + (lane & (RING - 1)), last);
+    const int pid = prow[v >> vshift];
+    return pid >= 0 && pid < a.P ? (pid << vshift) | (v & vmask) : -1;
+  };
 
-  const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
+  const size_t kv_stride = (size_t)a.KH * head_bytes;
   const size_t page_stride = kv_stride * 2 * a.L;
-  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
-  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * head_bytes;
+  auto page_ok = [&](int vpid) { return vpid >= 0 && (vpid >> vshift) < a.P; };
   auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
 
   // Loads are issued unconditionally from a clamped, always valid address and
   // zeroed afterwards for an absent page, so every slot keeps the same loads
   // in flight (a branch around a load makes the compiler wait for all of them).
-  auto load_page = [&](PageSlot<D>& s, int pid) {
-    const bool ok = page_ok(pid);
+  auto load_page = [&](PageSlot<D>& s, int vpid) {
+    const bool ok = page_ok(vpid);
     s.ok = ok;
-    const int pc = ok ? pid : 0;
-    const uint8_t* pb = layer_base + (size_t)pc * page_stride;
+    const int pc = (ok ? vpid : 0) >> vshift;  // page
+    const int sub = (ok ? vpid : 0) & vmask;   // its 16-token block
+    // K rows and the 4-token V tiles of a block are 16 D bytes past the previous block's
+    const uint8_t* pb = layer_base + (size_t)pc * page_stride + sub * (kPS * D);
     const uint8_t* kb = pb + col * D + grp * 16;
     const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
 #pragma unroll
@@ -297,9 +310,9 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       }
     }
     if constexpr (KIND == K_I8) {
-      const size_t ts = head_index(pc, 0) * kPS + grp * 4;
+      const size_t ts = head_index(pc, 0) * (kPS << vshift) + sub * kPS + grp * 4;
       s.ks = ldf4(a.scales + ts);
-      s.vs = ldf4(a.scales + ts + (size_t)a.KH * kPS);
+      s.vs = ldf4(a.scales + ts + (size_t)a.KH * (kPS << vshift));
     } else {
       s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
       s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
@@ -679,7 +692,9 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   using el = typename Ops::el;
   constexpr int RING = D <= 128 ? 4 : 2;
   constexpr int ROW = D * 2;              // bytes per token row
-  constexpr int HEAD_BYTES = kPS * ROW;   // one (page, layer, K/V, head) slice
+  // pages of 16 << vshift tokens streamed as 16-token sub-pages (as in the quantized kernel)
+  const int vshift = a.vshift, vmask = (1 << a.vshift) - 1;
+  const int head_bytes = (kPS << vshift) * ROW;  // one (page, layer, K/V, head) slice
   constexpr int NC = (D + 31) / 32;       // 32-dim chunks: one 16-byte load per lane each
   constexpr int NB = D / 16;              // 16-dim blocks of the output column
   // head_dim 80 / 112: the last chunk holds 16 dims, lanes grp < 2 (the rest
@@ -700,21 +715,26 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   // launch also records the partition geometry for the merge pass
   const int item = blockIdx.x;
   WorkItem wi;
-  if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
+  if (!find_item(a.ctx_lens, a.B, a.max_pp << vshift, a.target, item, item == 0 && unit == 0, a.header, wi)) return;
   const int b = wi.b;
   const int n_pages = wi.n_pages;
   const int last = n_pages - 1;
   const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);  // valid tokens of the partition
   // page ids, fetched RING pages ahead of the data: lane u < RING reads the id
   // of page first + u (clamped to the last page)
-  const int32_t* trow = a.page_table + (size_t)b * a.max_pp + wi.p_begin;
-  auto ids_at = [&](int first) { return trow[min(first + (lane & (RING - 1)), last)]; };
+  const int32_t* prow = a.page_table + (size_t)b * a.max_pp;
+  // sub-page id (page << vshift | block), or -1 for an absent page
+  auto ids_at = [&](int first) {
+    const int v = wi.p_begin + min(first + (lane & (RING - 1)), last);
+    const int pid = prow[v >> vshift];
+    return pid >= 0 && pid < a.P ? (pid << vshift) | (v & vmask) : -1;
+  };
   float* ml_base = a.part_ml + ((size_t)item * a.H + h0) * 2;
 
-  const size_t kv_stride = (size_t)a.KH * HEAD_BYTES;
+  const size_t kv_stride = (size_t)a.KH * head_bytes;
   const size_t page_stride = kv_stride * 2 * a.L;
-  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
-  auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * head_bytes;
+  auto page_ok = [&](int vpid) { return vpid >= 0 && (vpid >> vshift) < a.P; };
 
   // query operand (B of S^T): lane (col, grp) holds q[32 c + 8 grp + e] * qscale, hi + lo
   const float* qrow = a.query + ((size_t)b * a.H + h0 + min(col, G - 1)) * D;
@@ -748,10 +768,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) acc[blk] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto load_page = [&](FloatSlot<D>& s, int pid) {
-    s.ok = page_ok(pid);
-    const int pc = s.ok ? pid : 0;
-    const uint8_t* kb = layer_base + (size_t)pc * page_stride + col * ROW + grp * 16;
+  auto load_page = [&](FloatSlot<D>& s, int vpid) {
+    s.ok = page_ok(vpid);
+    const int pc = (s.ok ? vpid : 0) >> vshift;
+    const int sub = (s.ok ? vpid : 0) & vmask;
+    const uint8_t* kb = layer_base + (size_t)pc * page_stride + (sub * kPS + col) * ROW + grp * 16;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       if (CPART == 32 || c < NC - 1) {

@@ -576,12 +576,18 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   // head_dim 64 / 80 / 96 / 112 / 128 (and 256 for int8 / fp8), the VALU split
   // kernel at 64 / 128 / 256; every other shape runs on the generic kernel
   // (vrm_decode_generic.hip).
+  // The int8 / fp8 / bf16 / f16 stream kernels also take pages of 32, 64, ...
+  // tokens (16 << vshift), which they stream as 16-token sub-pages.
   const bool stream_d = D == 64 || D == 80 || D == 96 || D == 112 || D == 128 || D == 256;
   const bool split_d = D == 64 || D == 128 || D == 256;
-  const bool mfma = PS == kPS && (((kind == K_I8 || kind == K_FP8) && stream_d) ||
-                                  ((kind == K_BF16 || kind == K_F16) && stream_d && D <= 128) ||
-                                  (kind == K_Q4 && D == 128 && q4_aligned));
+  int vshift = 0;
+  while ((kPS << vshift) < PS && vshift < 6) ++vshift;
+  const bool sub_pages = (kPS << vshift) == PS;  // PS = 16, 32, 64, ... 1024
+  const bool mfma = (PS == kPS && kind == K_Q4 && D == 128 && q4_aligned) ||
+                    (sub_pages && (((kind == K_I8 || kind == K_FP8) && stream_d) ||
+                                   ((kind == K_BF16 || kind == K_F16) && stream_d && D <= 128)));
   const bool tuned = mfma || (PS == kPS && split_d);
+  a.vshift = mfma ? vshift : 0;
   const int max_tile = mfma ? 16 : kind == K_Q4 ? 6 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
