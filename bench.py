@@ -57,7 +57,7 @@ KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_B
            "fp8": _lib.VRM_KV_FP8E4M3}
 KV_NAME = {"f32": "K_F32", "f16": "K_F16", "bf16": "K_BF16", "int8": "K_I8", "fp8": "K_FP8", "q4": "K_Q4"}
 KERNEL = {"int8": "decode_stream_kernel<K_I8,{D}>", "fp8": "decode_stream_kernel<K_FP8,{D}>",
-          "tq3": "decode_tq_kernel<3> + merge", "tq4": "decode_tq_kernel<4> + merge",
+          "tq3": "decode_tq_kernel<3,{PD}> + merge", "tq4": "decode_tq_kernel<4,{PD}> + merge",
           "bf16": "decode_stream_float_kernel<K_BF16,{D}>", "f16": "decode_stream_float_kernel<K_F16,{D}>",
           "f32": "decode_split_kernel<K_F32,{D},G>", "q4": "decode_stream_q4_kernel + merge"}
 
@@ -743,9 +743,9 @@ def main():
     if shape_override:
         desc += f" (head_dim set to {D}, page size to {PS})"
     if turbo:
-        tuned = 64 < D <= 128 and comp.qjl_dim == 64 and comp.bits_per_angle in (2, 3, 4) and PS == 16
         pd = 1 << max(6, (D - 1).bit_length())
-        kname = KERNEL[cfg.codec] if tuned else f"decode_tq_gen_kernel<{pd}> + merge"
+        tuned = pd in (64, 128) and comp.qjl_dim == pd // 2 and comp.bits_per_angle in (2, 3, 4) and PS == 16
+        kname = KERNEL[cfg.codec].format(PD=pd) if tuned else f"decode_tq_gen_kernel<{pd}> + merge"
     elif (PS == 16 and D in (64, 128, 256)) or (
             PS in (16, 32, 64, 128, 256, 512, 1024) and D in (64, 80, 96, 112, 128, 256)
             and (cfg.codec in ("int8", "fp8") or (cfg.codec in ("bf16", "f16") and D <= 128))):

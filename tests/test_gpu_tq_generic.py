@@ -1,7 +1,8 @@
 """TurboQuant pages of every compressor setting: head_dim 33 .. 256
 (padded_dim 64 / 128 / 256), 1 .. 8 bits per angle, qjl_dim 1 .. 256, any
-page size.  head_dim 65 .. 128 with 64 QJL rows, 2 .. 4 bits and 16-token
-pages use the tuned slice and kernel; everything else the generic layout.
+page size.  head_dim 33 .. 64 with 32 QJL rows and 65 .. 128 with 64 (the
+compressor's default qjl_dim), 2 .. 4 bits and 16-token pages use the tuned
+slices and kernel; everything else the generic layout.
 
 * Codes written into pages equal, bit for bit, the standalone GPU
   compressor's codes (CUDATurboQuantOps.compress_gpu, itself checked against
@@ -36,8 +37,10 @@ ATOL, RTOL = 2e-3, 1e-2
 SETTINGS = [
     (64, 3, None, 16), (96, 3, None, 4), (256, 4, None, 16), (128, 1, None, 16), (128, 3, 32, 16),
     (128, 3, 64, 8), (80, 8, 100, 5), (200, 5, 256, 3), (33, 2, 7, 1), (128, 6, None, 32),
-    # head_dim 65 .. 128 at 64 QJL rows, 2-4 bits and 16-token pages share the tuned slice of head_dim 128
-    (96, 3, None, 16), (80, 4, None, 16), (65, 2, None, 16),
+    # head_dim 65 .. 128 at 64 QJL rows, 2-4 bits and 16-token pages share the tuned slice of head_dim 128,
+    # head_dim 33 .. 64 at 32 QJL rows that of head_dim 64
+    (96, 3, None, 16), (80, 4, None, 16), (65, 2, None, 16), (64, 2, None, 16), (48, 4, None, 16),
+    (33, 3, None, 16),
 ]
 
 
@@ -198,6 +201,8 @@ DECODE = [  # head_dim, bits, qjl_dim, page size, H, KH
     (64, 3, None, 16, 8, 2), (96, 3, None, 4, 12, 4), (256, 4, None, 16, 16, 2), (96, 2, None, 16, 40, 8),
     (64, 1, None, 8, 8, 8), (256, 8, 100, 5, 4, 1), (128, 3, 64, 32, 40, 8), (80, 5, 33, 3, 6, 3),
     (128, 3, 32, 16, 8, 2), (96, 3, None, 16, 40, 8), (80, 4, None, 16, 12, 4), (65, 2, None, 16, 8, 1),
+    (64, 2, None, 16, 32, 4), (64, 4, None, 16, 16, 2), (48, 3, None, 16, 12, 3), (33, 4, None, 16, 8, 1),
+    (64, 3, None, 16, 40, 8), (64, 3, 16, 16, 28, 4),
 ]
 
 
@@ -213,7 +218,8 @@ def test_generic_decode_turbo_matches_oracle(case):
     _assert_close(out, ref, f"decode {case}")
 
 
-@pytest.mark.parametrize("setting", [(96, 3, None, 4), (64, 2, None, 16), (256, 4, None, 8)], ids=_sid)
+@pytest.mark.parametrize("setting", [(96, 3, None, 4), (64, 2, None, 16), (256, 4, None, 8), (64, 4, None, 16),
+                                     (56, 3, None, 16)], ids=_sid)
 def test_generic_decode_turbo_lse_and_no_qjl(setting):
     """The log-sum-exp output, with and without the QJL term: lse equals
     ln sum_t exp(scale score_t) of the oracle's scores, and without the QJL
@@ -280,6 +286,23 @@ def test_generic_decode_turbo_edge_cases_and_long_contexts():
     torch.cuda.synchronize()
     ref = PD.paged_attention_decode_turbo(_params(comp), q, _codes(pool, comp, 0, 16), table, lens)
     _assert_close(out, ref, "long contexts d256")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_tuned_d64_decode_edge_cases_and_long_contexts(bits):
+    """The tuned head_dim-64 slice: zero context, an absent page (-1), a
+    layer other than 0, a partial last page and contexts split over many
+    partitions, with 5 query heads per kv-head."""
+    _say(f"tuned d64 edges / long b{bits}")
+    comp = _compressor(64, bits, seed=21 + bits)
+    pool, q, table, lens = _turbo_case(comp, 5, 20, 4, [0, 64, 17, 4100, 1601], seed=9 + bits, ps=16, L=3, layer=1)
+    table[1, 2] = -1  # absent pages: their tokens are skipped
+    table[3, 5] = -1
+    out = tq_pages.paged_attention_decode_turbo(q.to(DEV), pool, table.to(DEV), lens.to(DEV), 1, comp, scale=0.2)
+    torch.cuda.synchronize()
+    assert (out[0] == 0).all()
+    ref = PD.paged_attention_decode_turbo(_params(comp), q, _codes(pool, comp, 1, 16), table, lens, scale=0.2)
+    _assert_close(out, ref, f"tuned d64 b{bits}")
 
 
 def _mgr_codes_match(m, rows, layer):

@@ -10,15 +10,18 @@
 // reconstructions (rotated domain, from the fp16 radius) of
 // KVCacheCompressor.attention_score / decompress (core/kv_quantizer.py:
 // 481-535).  The inverse rotation is linear, so it is applied once to the
-// weighted sum instead of to every value.
+// weighted sum instead of to every value.  (The formulas are written for
+// padded dim PD = 128 and 64 QJL rows; the kernel also serves PD = 64 with 32
+// rows, where each lane owns 16 dims instead of 32.)
 //
 // Work split as in the other stream kernels (work items of find_item, one
 // wavefront per (kv-head, head chunk), up to 16 query heads in the columns of
 // 16x16 MFMA tiles).  Lane (t, g) = (lane % 16, lane / 16) rebuilds dims
-// 32 g .. 32 g + 31 of token t of a page from quarter g of the token's angle
-// record (vrm_tq_layout.h), multiplying the radius by the {cos, sin} of the
-// bin centres level by level (6 down to 0) as the reference does, so the
-// reconstruction equals the reference's polar decode bit for bit.
+// Q g .. Q g + Q - 1 (Q = PD / 4) of token t of a page from quarter g of the
+// token's angle record (vrm_tq_layout.h), multiplying the radius by the
+// {cos, sin} of the bin centres level by level (top down to 0) as the
+// reference does, so the reconstruction equals the reference's polar decode
+// bit for bit.
 //   S^T   = K Q^T on v_mfma_f32_16x16x32_f16, K and q_rot as hi + lo fp16
 //           (k index (chunk c, group g, element e) <-> dim 32 g + 8 c + e);
 //   QJL   = S P^T: the sign bits as exact +-1 fp16 against q_rot JL^T
@@ -158,13 +161,14 @@ __device__ __forceinline__ float row_swap8(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
 }
 
-// In-register Walsh-Hadamard transform of 128 values, element e in lane e % 64,
-// register e / 64, in the reference's butterfly order.
-__device__ __forceinline__ void fwht128(float (&v)[2], int lane) {
+// In-register Walsh-Hadamard transform of PD = 64 or 128 values, element e in
+// lane e % 64, register e / 64, in the reference's butterfly order.
+template <int PD>
+__device__ __forceinline__ void fwht_pd(float (&v)[PD / 64], int lane) {
 #pragma unroll
   for (int h = 1; h < 64; h <<= 1) {
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
+    for (int k = 0; k < PD / 64; ++k) {
       float other;
       switch (h) {
         case 1: other = xor_shfl<1>(v[k]); break;
@@ -177,29 +181,48 @@ __device__ __forceinline__ void fwht128(float (&v)[2], int lane) {
       v[k] = (lane & h) ? other - v[k] : v[k] + other;
     }
   }
-  const float a = v[0], b = v[1];
-  v[0] = a + b;
-  v[1] = a - b;
+  if constexpr (PD == 128) {
+    const float a = v[0], b = v[1];
+    v[0] = a + b;
+    v[1] = a - b;
+  }
 }
 
-template <int BITS>
+// Dwords of a lane's angle quarter as loaded: quarter grp of a record starts
+// at bit grp * PD / 4 * BITS, a dword boundary except at PD 64 and 3 bits,
+// where odd quarters start at bit 16 of a dword and take two.
+template <int BITS, int PD>
+struct QuarterWords {
+  static constexpr bool kSplit = (PD / 4 * BITS) % 32 != 0;
+  static constexpr int kN = kSplit ? 2 : PD / 4 * BITS / 32;
+};
+
+template <int BITS, int PD>
 struct TqSlot {
-  uint32_t kq[BITS];  // K angle quarter grp of token col
-  uint32_t vq[BITS];  // V angle quarter grp of token col
-  uint32_t ktop[2];   // last dword of K quarters 0 and 1 + grp / 2 (level 6 / level 5 spares)
+  static constexpr int QW = QuarterWords<BITS, PD>::kN;
+  uint32_t kq[QW];    // K angle quarter grp of token col (as loaded)
+  uint32_t vq[QW];    // V angle quarter grp of token col
+  uint32_t ktop[2];   // dwords of K holding the spares of quarters 0 and 1 + grp / 2 (the top two levels)
   uint32_t vtop[2];
   uint32_t krad, vrad, knorm;  // fp16 bits
-  uint2 ksign;                 // 64 QJL sign bits of token col
+  uint32_t ksign[PD / 64];     // PD / 2 QJL sign bits of token col
   bool ok;                     // page id inside the pool (wave-uniform)
 };
 
-template <int BITS>
+template <int BITS, int PD>
 __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G, int hd) {
   constexpr int NB = 1 << BITS;
   constexpr int RING = 4;
-  constexpr int SLICE = T::slice_bytes(BITS);
-  constexpr int ABYTES = T::angle_bytes(BITS);
-  constexpr int D = T::kPD;
+  constexpr int SLICE = T::slice_bytes(PD, BITS);
+  constexpr int ABYTES = T::angle_bytes(PD, BITS);
+  constexpr int D = PD;
+  constexpr int QS = T::quarter_slots(PD);  // slots of a quarter = dims a lane rebuilds (32 or 16)
+  constexpr int NC = PD / 32;               // 8-dim chunks of a lane's dims
+  constexpr int NY = PD / 16;               // level-1 nodes of a lane's dims
+  constexpr int NQJ = PD / 64;              // dwords of QJL sign bits per token
+  constexpr int PER = PD / 64;              // Hadamard elements per lane
+  using QWords = QuarterWords<BITS, PD>;
+  using Slot = TqSlot<BITS, PD>;
 
   // {cos, sin} of the bin centres of levels >= 1, singly and, at 4 bits
   // (levels 3 and 2), for two sibling angles at once (index bin_a + NB bin_b)
@@ -262,27 +285,28 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   float(*qb)[D + 4] = qbuf[wave];
 
   // ---------------- q_rot of this wave's heads (row r: head min(r, G - 1)) ----------------
-  const float root = (float)sqrt(128.0);
+  const float root = (float)sqrt((double)PD);
 #pragma unroll 1
   for (int r = 0; r < 8; ++r) {
     // the query padded with zeros to the padded dim, as the compressor pads keys
     const float* qrow = a.query + ((size_t)b * a.H + h0 + min(r, G - 1)) * hd;
-    float v[2] = {lane < hd ? qrow[lane] * tq.signs[lane] : 0.f,
-                  lane + 64 < hd ? qrow[lane + 64] * tq.signs[lane + 64] : 0.f};
-    fwht128(v, lane);
-    qb[r][lane] = v[0] / root;
-    qb[r][lane + 64] = v[1] / root;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = lane + 64 * k < hd ? qrow[lane + 64 * k] * tq.signs[lane + 64 * k] : 0.f;
+    fwht_pd<PD>(v, lane);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) qb[r][lane + 64 * k] = v[k] / root;
   }
   wave_sync();
-  // B operand of S^T: x = q_rot[hcol][32 grp + 8 c + e] * qscale as hi
+  // B operand of S^T: x = q_rot[hcol][Q grp + 8 c + e] * qscale as hi
   // (columns < 8) + lo (columns >= 8); against K hi and K lo this sums
   // (Kh + Kl)(qh + ql) over the two column halves.
-  v8h QB[4];
+  v8h QB[NC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float x = qb[hcol][32 * grp + 8 * c + e] * a.qscale;
+      const float x = qb[hcol][QS * grp + 8 * c + e] * a.qscale;
       const _Float16 hi = (_Float16)x;
       const _Float16 lo = (_Float16)(x - (float)hi);
       QB[c][e] = lo_col ? lo : hi;
@@ -292,14 +316,14 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // matching k order: chunk c, element e <-> JL row 16 (2 c + e / 4) + 4 grp + e % 4.
   // PJ carries q_proj times the QJL scale, hi / lo by column half like QB.
   const float qjl_scale = a.qscale * tq.qjl_coef;
-  v8h PJ[2];
+  v8h PJ[NQJ];
   {
-    float pj[4][4];
+    float pj[2 * NQJ][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2 * NQJ; ++j) {
       v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < NC; ++c) {
         v8h ah, al, bh, bl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -318,7 +342,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       for (int r = 0; r < 4; ++r) pj[j][r] = acc[r];
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < NQJ; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = pj[2 * c + e / 4][e % 4] * qjl_scale;
@@ -353,51 +377,97 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 
   // ---------------- streaming state ----------------
   float m_run = kNoMax, l_run = 0.f;
-  // O^T block 2 c + h: row 4 grp + r <-> dim 32 (2 h + (4 grp + r) / 8) + 8 c + (4 grp + r) % 8
-  v4f acc[8];
+  // O^T block 2 c + h: row 4 grp + r <-> dim Q (2 h + (4 grp + r) / 8) + 8 c + (4 grp + r) % 8
+  v4f acc[2 * NC];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 2 * NC; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const size_t kv_stride = (size_t)a.KH * SLICE;
   const size_t page_stride = kv_stride * 2 * a.L;
   const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * SLICE;
   auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
-  const int top1 = (1 + (grp >> 1)) * BITS + BITS - 1;  // dword of slot 31 of quarter 1 + grp / 2
+  // quarter grp: first dword and bit offset in it (0, or 16 for odd quarters at PD 64 and 3 bits)
+  const int q_dw = grp * QS * BITS / 32;
+  const uint32_t q_sh = (grp * QS * BITS) % 32;
+  // the spare slot QS - 1 of quarter 0 (the root angle) and of quarter
+  // 1 + grp / 2 (the next level): dwords, and the spare's bit in them, which
+  // is top_sh for every quarter except the odd one at PD 64 and 3 bits (16
+  // bits higher, shifted down before use by top1_sh)
+  constexpr int top_bit = (QS - 1) * BITS;
+  constexpr int top0_dw = top_bit / 32;
+  constexpr int top_sh = top_bit % 32;  // a spare never straddles a dword
+  const int top1_bit = (1 + (grp >> 1)) * QS * BITS + top_bit;
+  const int top1_dw = top1_bit / 32;
+  const uint32_t top1_sh = top1_bit % 32 - top_sh;
 
-  auto load_page = [&](TqSlot<BITS>& s, int pid) {
+  auto load_page = [&](Slot& s, int pid) {
     s.ok = page_ok(pid);
     const uint8_t* ks = layer_base + (size_t)(s.ok ? pid : 0) * page_stride;
     const uint8_t* vs = ks + kv_stride;
     const uint32_t* krec = reinterpret_cast<const uint32_t*>(ks + col * ABYTES);
     const uint32_t* vrec = reinterpret_cast<const uint32_t*>(vs + col * ABYTES);
 #pragma unroll
-    for (int i = 0; i < BITS; ++i) {
-      s.kq[i] = krec[grp * BITS + i];
-      s.vq[i] = vrec[grp * BITS + i];
+    for (int i = 0; i < QWords::kN; ++i) {
+      s.kq[i] = krec[q_dw + i];
+      s.vq[i] = vrec[q_dw + i];
     }
-    s.ktop[0] = krec[BITS - 1];
-    s.ktop[1] = krec[top1];
-    s.vtop[0] = vrec[BITS - 1];
-    s.vtop[1] = vrec[top1];
-    s.krad = reinterpret_cast<const uint16_t*>(ks + T::radius_offset(BITS))[col];
-    s.vrad = reinterpret_cast<const uint16_t*>(vs + T::radius_offset(BITS))[col];
-    s.knorm = reinterpret_cast<const uint16_t*>(ks + T::norms_offset(BITS))[col];
-    s.ksign = reinterpret_cast<const uint2*>(ks + T::signs_offset(BITS))[col];
+    s.ktop[0] = krec[top0_dw];
+    s.ktop[1] = krec[top1_dw];
+    s.vtop[0] = vrec[top0_dw];
+    s.vtop[1] = vrec[top1_dw];
+    s.krad = reinterpret_cast<const uint16_t*>(ks + T::radius_offset(PD, BITS))[col];
+    s.vrad = reinterpret_cast<const uint16_t*>(vs + T::radius_offset(PD, BITS))[col];
+    s.knorm = reinterpret_cast<const uint16_t*>(ks + T::norms_offset(PD, BITS))[col];
+    if constexpr (NQJ == 2) {
+      const uint2 w = reinterpret_cast<const uint2*>(ks + T::signs_offset(PD, BITS))[col];
+      s.ksign[0] = w.x;
+      s.ksign[NQJ - 1] = w.y;
+    } else {
+      s.ksign[0] = reinterpret_cast<const uint32_t*>(ks + T::signs_offset(PD, BITS))[col];
+    }
   };
 
-  // dims 32 grp .. 32 grp + 31 of one token: the reference's tree of
+  // dims Q grp .. Q grp + Q - 1 of one token: the reference's tree of
   // products, two levels per lookup from the product tables below level 4
   // (4 bits: levels 3 and 2 one at a time with sibling angles together), so
   // each value is the reference's within a float32 rounding or two.
   // Leaves the last level's products to the caller: value 4 j + k of the
-  // group is y[j] * t[j][k].
-  auto rebuild = [&](const uint32_t* q, uint32_t top0, uint32_t topq, float radius, float (&y)[8], float4 (&t)[8]) {
-    constexpr int sh31 = (31 * BITS) % 32;  // slot 31 never straddles a dword
-    const float2 t6 = lds_at(lut, field_off<BITS, 3>(&top0, sh31));
-    const float2 t5 = lds_at(lut, field_off<BITS, 3>(&topq, sh31));
+  // group is y[j] * t[j][k].  The quarter's words are aligned here, at the
+  // point of use, so that the ring's loads stay in flight until then.
+  auto rebuild = [&](const uint32_t* qw, uint32_t top0, uint32_t topq, float radius, float (&y)[NY],
+                     float4 (&t)[NY]) {
+    uint32_t q[QWords::kN];
+    if constexpr (QWords::kSplit) {
+      q[0] = __builtin_amdgcn_alignbit(qw[1], qw[0], q_sh);
+      q[1] = qw[1] >> q_sh;
+      topq >>= top1_sh;
+    } else {
+#pragma unroll
+      for (int i = 0; i < QWords::kN; ++i) q[i] = qw[i];
+    }
+    const float2 t6 = lds_at(lut, field_off<BITS, 3>(&top0, top_sh));
+    const float2 t5 = lds_at(lut, field_off<BITS, 3>(&topq, top_sh));
     float p = radius;
-    p = p * ((grp >> 1) ? t6.y : t6.x);  // bit 6 of the dims
-    p = p * ((grp & 1) ? t5.y : t5.x);   // bit 5
+    p = p * ((grp >> 1) ? t6.y : t6.x);  // top bit of the dims (bit 6 at PD 128)
+    p = p * ((grp & 1) ? t5.y : t5.x);   // the next one
+    if constexpr (PD == 64) {
+      // levels 3 and 2: the quarter's root and its children
+      if constexpr (kT32) {
+        const float4 t3 = lds_at(t32, field_off<3 * BITS, 4>(q, 12 * BITS));
+        y[0] = p * t3.x;
+        y[1] = p * t3.y;
+        y[2] = p * t3.z;
+        y[3] = p * t3.w;
+      } else {
+        const float2 c3 = lds_at(lut, field_off<BITS, 3>(q, 0));
+        const float x2[2] = {p * c3.x, p * c3.y};
+        const float4 a2 = lds_at(lut2, field_off<2 * BITS, 4>(q, 1 * BITS));
+        y[0] = x2[0] * a2.x;
+        y[1] = x2[0] * a2.y;
+        y[2] = x2[1] * a2.z;
+        y[3] = x2[1] * a2.w;
+      }
+    } else {
     const float2 c4 = lds_at(lut, field_off<BITS, 3>(q, (kT32 ? 30 : 0) * BITS));  // level 4
     const float x3[2] = {p * c4.x, p * c4.y};
     if constexpr (kT32) {
@@ -423,23 +493,25 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
         y[2 * i + 3] = x2[i + 1] * a2.w;
       }
     }
+    }
     // levels 1 and 0: node j and its children in slots 3 j .. 3 j + 2 (4 bits:
-    // node slot 7 + j, children slots 15 + 2 j, 16 + 2 j)
+    // node slot NY - 1 + j, children slots 2 NY - 1 + 2 j, 2 NY + 2 j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NY; ++j)
       t[j] = lds_at(t10, kT32 ? field_off<3 * BITS, 4>(q, 3 * j * BITS)
-                              : field_off<BITS, 4>(q, (7 + j) * BITS) | field_off<2 * BITS, 4 + BITS>(q, (15 + 2 * j) * BITS));
+                              : field_off<BITS, 4>(q, (NY - 1 + j) * BITS) |
+                                    field_off<2 * BITS, 4 + BITS>(q, (2 * NY - 1 + 2 * j) * BITS));
   };
 
   // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi, for
   // head hcol (both column halves hold the same sums).
-  auto page_scores = [&](const TqSlot<BITS>& s, int pi, float* sc) {
-    float y[8];
-    float4 t[8];
+  auto page_scores = [&](const Slot& s, int pi, float* sc) {
+    float y[NY];
+    float4 t[NY];
     rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), y, t);
     v4f c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
       // k = y t as hi = fp16(k) and lo = fp16(k - hi)
       uint4 hw, lw;
       split8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], hw, lw);
@@ -453,9 +525,9 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       // still finite; tokens past the context are masked below).
       const uint32_t nn = s.knorm | (s.knorm << 16);
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < NQJ; ++c) {
         // elements e < 4: JL rows 32 c + 4 grp + e; e >= 4: rows 32 c + 16 + 4 grp + e - 4
-        const uint32_t word = c == 0 ? s.ksign.x : s.ksign.y;
+        const uint32_t word = s.ksign[c];
         const uint2 lo = sign_mask[__builtin_amdgcn_ubfe(word, 4 * grp, 4)];
         const uint2 hi = sign_mask[__builtin_amdgcn_ubfe(word, 16 + 4 * grp, 4)];
         const v8h sn = __builtin_bit_cast(v8h, make_uint4(nn ^ lo.x, nn ^ lo.y, nn ^ hi.x, nn ^ hi.y));
@@ -479,20 +551,20 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   };
   // Values of this lane's token; absent pages and tokens past the context get
   // radius 0 (whatever the page holds), so they contribute exact zeros.
-  auto v_operand = [&](const TqSlot<BITS>& s, int pi, v8h (&vop)[4]) {
-    float y[8];
-    float4 t[8];
+  auto v_operand = [&](const Slot& s, int pi, v8h (&vop)[NC]) {
+    float y[NY];
+    float4 t[NY];
     const bool live = s.ok && pi * kPS + col < tok_end;
     rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, y, t);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
       uint4 w;
       round8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], w);
       vop[c] = __builtin_bit_cast(v8h, w);
     }
   };
 
-  auto process_pair = [&](const TqSlot<BITS>& s0, const TqSlot<BITS>& s1, int pi) {
+  auto process_pair = [&](const Slot& s0, const Slot& s1, int pi) {
     float sc[8];
     page_scores(s0, pi, sc);
     page_scores(s1, pi + 1, sc + 4);
@@ -504,7 +576,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
       l_run *= alpha;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+      for (int i = 0; i < 2 * NC; ++i) acc[i] *= alpha;
       m_run = pm;
     }
     // P^T as hi (columns < 8) and lo (columns >= 8)
@@ -516,11 +588,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       const _Float16 hi = (_Float16)p;
       Bp[e] = lo_col ? (_Float16)(p - (float)hi) : hi;
     }
-    v8h vop0[4], vop1[4];
+    v8h vop0[NC], vop1[NC];
     v_operand(s0, pi, vop0);
     v_operand(s1, pi + 1, vop1);  // past the partition: radius 0
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float t[8];
@@ -535,7 +607,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 
   // ---------------- stream the partition ----------------
   {
-    TqSlot<BITS> ring[RING];
+    Slot ring[RING];
     const int ids0 = ids_at(0);
     int ids_next = ids_at(RING);
 #pragma unroll
@@ -557,26 +629,31 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // ---------------- partition result: columns to natural dims, unrotate ----------------
   __syncthreads();  // the tables are dead once every wave has streamed its pages
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * grp + r;
         // hi column + lo column of head hcol
-        qb[col][32 * (2 * h + (row >> 3)) + 8 * c + (row & 7)] = acc[2 * c + h][r] + row_swap8(acc[2 * c + h][r]);
+        qb[col][QS * (2 * h + (row >> 3)) + 8 * c + (row & 7)] = acc[2 * c + h][r] + row_swap8(acc[2 * c + h][r]);
       }
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   wave_sync();
-  const float s_lo = tq.signs[lane], s_hi = tq.signs[lane + 64];
+  float sg[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) sg[k] = tq.signs[lane + 64 * k];
   for (int hh = 0; hh < G; ++hh) {
-    float v[2] = {qb[hh][lane], qb[hh][lane + 64]};
-    fwht128(v, lane);
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) v[k] = qb[hh][lane + 64 * k];
+    fwht_pd<PD>(v, lane);
     // unrotated, then cut to the head_dim
     float* out = a.part_acc + ((size_t)item * a.H + h0 + hh) * hd;
-    if (lane < hd) out[lane] = v[0] / root * s_lo;
-    if (lane + 64 < hd) out[lane + 64] = v[1] / root * s_hi;
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (lane + 64 * k < hd) out[lane + 64 * k] = v[k] / root * sg[k];
   }
   if (col < G && grp == 0) {
     float* ml = a.part_ml + ((size_t)item * a.H + h0 + col) * 2;
@@ -587,24 +664,29 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 
 }  // namespace
 
-hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st) {
+template <int PD>
+hipError_t launch_tq_pd(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st) {
   const int G = pick_group_tile(a0.H / a0.KH, kMaxHeads);
   const int units = a0.KH * ((a0.H / a0.KH) / G);
   int W = kWaves;
   while (units % W) --W;
   DecodeArgs a = a0;
-  const void* fn = bits == 2   ? reinterpret_cast<const void*>(&decode_tq_kernel<2>)
-                   : bits == 3 ? reinterpret_cast<const void*>(&decode_tq_kernel<3>)
-                               : reinterpret_cast<const void*>(&decode_tq_kernel<4>);
+  const void* fn = bits == 2   ? reinterpret_cast<const void*>(&decode_tq_kernel<2, PD>)
+                   : bits == 3 ? reinterpret_cast<const void*>(&decode_tq_kernel<3, PD>)
+                               : reinterpret_cast<const void*>(&decode_tq_kernel<4, PD>);
   a.target = items_target(fn, W, 0, units);
   dim3 grid(B + 2 * a.target, units / W, 1);
   dim3 block(64 * W);
   switch (bits) {
-    case 2: hipLaunchKernelGGL(decode_tq_kernel<2>, grid, block, 0, st, a, tq, G, hd); break;
-    case 3: hipLaunchKernelGGL(decode_tq_kernel<3>, grid, block, 0, st, a, tq, G, hd); break;
-    default: hipLaunchKernelGGL(decode_tq_kernel<4>, grid, block, 0, st, a, tq, G, hd); break;
+    case 2: hipLaunchKernelGGL((decode_tq_kernel<2, PD>), grid, block, 0, st, a, tq, G, hd); break;
+    case 3: hipLaunchKernelGGL((decode_tq_kernel<3, PD>), grid, block, 0, st, a, tq, G, hd); break;
+    default: hipLaunchKernelGGL((decode_tq_kernel<4, PD>), grid, block, 0, st, a, tq, G, hd); break;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_tq_decode(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st) {
+  return hd <= 64 ? launch_tq_pd<64>(a0, tq, bits, B, hd, st) : launch_tq_pd<128>(a0, tq, bits, B, hd, st);
 }
 
 }  // namespace dec

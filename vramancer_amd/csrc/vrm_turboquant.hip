@@ -247,12 +247,13 @@ struct TqPoolArgs {
   const float* lut;
 };
 
-template <int SRC, int BITS, int ROWS>
+template <int SRC, int BITS, int ROWS, int PD>
 __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) {
   namespace L = vrm::tq;
-  constexpr int PD = L::kPD;
+  constexpr int QJL = L::tuned_qjl(PD);
+  constexpr int SLICE = L::slice_bytes(PD, BITS);
   __shared__ RowLds<PD> rows_lds[ROWS];
-  __shared__ uint32_t rows_signs[ROWS][L::kQjl / 32];
+  __shared__ uint32_t rows_signs[ROWS][QJL / 32];
   __shared__ float lut_lds[4 << BITS];  // the angle table ({level 0, levels >= 1} x {cos, sin} x 2^BITS)
   const int lane = threadIdx.x & 63;
   if (threadIdx.x < (4 << BITS)) lut_lds[threadIdx.x] = a.lut[threadIdx.x];
@@ -281,34 +282,37 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
   const int pid = a.page_ids[n];
   if (pid < 0 || pid >= a.P || t < 0 || t >= L::kTokens) return;  // rows aimed outside the pool are dropped
   if (a.from_pool) src_first = (((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::kTokens + t) * a.head_dim;
-  uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * L::slice_bytes(BITS);
-  const int abytes = L::angle_bytes(BITS);
+  uint8_t* slice = a.pool + ((((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h) * SLICE;
+  constexpr int abytes = L::angle_bytes(PD, BITS);
+  constexpr int sbytes = L::sign_bytes(PD);
   uint8_t* rec = slice + (size_t)t * abytes;
-  uint16_t* radius_out = reinterpret_cast<uint16_t*>(slice + L::radius_offset(BITS)) + t;
+  uint16_t* radius_out = reinterpret_cast<uint16_t*>(slice + L::radius_offset(PD, BITS)) + t;
   if (!live) {  // slots past the page's valid tokens hold zero records
     for (int i = lane; i < abytes; i += 64) rec[i] = 0;
     if (lane == 0) *radius_out = 0;
     if (kv == 0) {
-      if (lane < 8) slice[L::signs_offset(BITS) + t * 8 + lane] = 0;
-      if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = 0;
+      if (lane < sbytes) slice[L::signs_offset(PD, BITS) + t * sbytes + lane] = 0;
+      if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(PD, BITS))[t] = 0;
     }
     return;
   }
   float v[PD / 64];
   const void* src = kv ? a.value : a.key;
   const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, BITS, v, w, lane);
-  // angle record: dword k of quarter g covers quarter bits [32 k, 32 k + 32),
-  // i.e. at most 32 / BITS + 2 slots from the one holding bit 32 k
-  if (lane < 4 * BITS) {  // BITS dwords per quarter
-    const int g = lane / BITS, k = lane % BITS;
+  // angle record: the PD slots (4 quarters of PD / 4) as one bit stream, so
+  // dword k covers slots from the one holding bit 32 k, at most 32 / BITS + 2
+  if (lane < abytes / 4) {
+    const int k = lane;
     const int s0 = (32 * k) / BITS;
     uint32_t word = 0;
 #pragma unroll
     for (int m = 0; m < 32 / BITS + 2; ++m) {
-      const int slot = s0 + m;
-      const int bi = slot < 32 && slot * BITS < 32 * k + 32 ? L::bin_index_of(g, slot, BITS) : -1;
+      const int gs = s0 + m;  // slot gs % (PD / 4) of quarter gs / (PD / 4)
+      const int bi = gs < PD && gs * BITS < 32 * k + 32
+                         ? L::bin_index_of(PD, gs / L::quarter_slots(PD), gs % L::quarter_slots(PD), BITS)
+                         : -1;
       if (bi >= 0) {
-        const int shift = slot * BITS - 32 * k;  // negative for a slot straddling the dword start
+        const int shift = gs * BITS - 32 * k;  // negative for a slot straddling the dword start
         const uint32_t val = w.bins[bi];
         word |= shift >= 0 ? (val << shift) : (val >> -shift);
       }
@@ -317,14 +321,15 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
   }
   if (lane == 0) *radius_out = f32_to_f16_bits(radius);
   if (kv == 1) return;
-  if (lane < L::kQjl / 32) sign_bits[lane] = 0;
+  if (lane < QJL / 32) sign_bits[lane] = 0;
   row_sync();
-  const float norm = qjl_row<PD>(v, radius, lut_lds, BITS, a.jl, L::kQjl, w, lane, [&](int j, bool pos) {
+  const float norm = qjl_row<PD>(v, radius, lut_lds, BITS, a.jl, QJL, w, lane, [&](int j, bool pos) {
     if (pos) atomicOr(&sign_bits[j >> 5], 1u << (j & 31));
   });
   row_sync();
-  if (lane < L::kQjl / 32) reinterpret_cast<uint32_t*>(slice + L::signs_offset(BITS) + t * 8)[lane] = sign_bits[lane];
-  if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(BITS))[t] = f32_to_f16_bits(norm);
+  if (lane < QJL / 32)
+    reinterpret_cast<uint32_t*>(slice + L::signs_offset(PD, BITS) + t * sbytes)[lane] = sign_bits[lane];
+  if (lane == 0) reinterpret_cast<uint16_t*>(slice + L::norms_offset(PD, BITS))[t] = f32_to_f16_bits(norm);
 }
 
 // Writer of the generic page layout (vrm_tq_layout.h, GenLayout): every
@@ -435,8 +440,9 @@ __global__ void __launch_bounds__(64) tq_pool_read_gen_kernel(const uint8_t* poo
 // ((n * 2 + kv) * KH + h) * 16 + t), radius, level-major bins, sign bytes and
 // norm.  V rows get zero signs and norms.
 __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, const int32_t* page_ids, int KH,
-                                                          int L_, int P, int layer, int bits, uint16_t* radius,
-                                                          uint8_t* angles, uint8_t* qjl_signs, uint16_t* norms) {
+                                                          int L_, int P, int layer, int pd, int bits,
+                                                          uint16_t* radius, uint8_t* angles, uint8_t* qjl_signs,
+                                                          uint16_t* norms) {
   namespace L = vrm::tq;
   const int lane = threadIdx.x;
   const int row = blockIdx.x;
@@ -445,30 +451,32 @@ __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, c
   const int kv = (row / (L::kTokens * KH)) % 2;
   const int n = row / (L::kTokens * KH * 2);
   const int pid = page_ids[n];
+  const int na = pd - 1, qjl = L::tuned_qjl(pd);
   if (pid < 0 || pid >= P) {  // absent page: zero codes
-    for (int i = lane; i < L::kAngles; i += 64) angles[(size_t)row * L::kAngles + i] = 0;
-    if (lane < L::kQjl) qjl_signs[(size_t)row * L::kQjl + lane] = 0;
+    for (int i = lane; i < na; i += 64) angles[(size_t)row * na + i] = 0;
+    if (lane < qjl) qjl_signs[(size_t)row * qjl + lane] = 0;
     if (lane == 0) radius[row] = norms[row] = 0;
     return;
   }
-  const uint8_t* slice = pool + ((((size_t)pid * L_ + layer) * 2 + kv) * KH + h) * L::slice_bytes(bits);
-  const uint8_t* rec = slice + (size_t)t * L::angle_bytes(bits);
-  for (int i = lane; i < L::kAngles; i += 64) {
+  const uint8_t* slice = pool + ((((size_t)pid * L_ + layer) * 2 + kv) * KH + h) * L::slice_bytes(pd, bits);
+  const int abytes = L::angle_bytes(pd, bits);
+  const uint8_t* rec = slice + (size_t)t * abytes;
+  for (int i = lane; i < na; i += 64) {
     // find (quarter, slot) of level-major bin i
     int l = 0;
-    while (i >= L::level_offset(l + 1)) ++l;
+    while (i >= L::level_offset(pd, l + 1)) ++l;
     int g, s;
-    L::slot_of(l, i - L::level_offset(l), bits, g, s);
-    const int bit = g * 32 * bits + s * bits;
-    uint32_t x = rec[bit / 8] | ((bit / 8 + 1 < L::angle_bytes(bits)) ? (uint32_t)rec[bit / 8 + 1] << 8 : 0u);
-    angles[(size_t)row * L::kAngles + i] = (uint8_t)((x >> (bit % 8)) & ((1u << bits) - 1));
+    L::slot_of(pd, l, i - L::level_offset(pd, l), bits, g, s);
+    const int bit = (g * L::quarter_slots(pd) + s) * bits;
+    uint32_t x = rec[bit / 8] | ((bit / 8 + 1 < abytes) ? (uint32_t)rec[bit / 8 + 1] << 8 : 0u);
+    angles[(size_t)row * na + i] = (uint8_t)((x >> (bit % 8)) & ((1u << bits) - 1));
   }
-  if (lane == 0) radius[row] = reinterpret_cast<const uint16_t*>(slice + L::radius_offset(bits))[t];
-  if (lane < L::kQjl) {
-    const uint8_t byte = kv == 0 ? slice[L::signs_offset(bits) + t * 8 + lane / 8] : 0;
-    qjl_signs[(size_t)row * L::kQjl + lane] = (byte >> (lane % 8)) & 1;
+  if (lane == 0) radius[row] = reinterpret_cast<const uint16_t*>(slice + L::radius_offset(pd, bits))[t];
+  if (lane < qjl) {
+    const uint8_t byte = kv == 0 ? slice[L::signs_offset(pd, bits) + t * L::sign_bytes(pd) + lane / 8] : 0;
+    qjl_signs[(size_t)row * qjl + lane] = (byte >> (lane % 8)) & 1;
   }
-  if (lane == 0) norms[row] = kv == 0 ? reinterpret_cast<const uint16_t*>(slice + L::norms_offset(bits))[t] : 0;
+  if (lane == 0) norms[row] = kv == 0 ? reinterpret_cast<const uint16_t*>(slice + L::norms_offset(pd, bits))[t] : 0;
 }
 
 template <int PD, int ROWS>
@@ -938,7 +946,8 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   a.jl = jl;
   a.lut = angle_lut;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (!tq::tuned_layout(D, bits, qjl_dim, PS)) {
+  const int pd = tq::tuned_pd(D, bits, qjl_dim, PS);
+  if (!pd) {
     const tq::GenLayout g = tq::gen_layout(D, bits, qjl_dim, PS);
     const dim3 grid(rows, 2);
 #define VRM_TQ_WRITE_GEN(SRC)                                                                                  \
@@ -958,11 +967,16 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   // bulk writes pack kBulkRows rows (wavefronts) per workgroup, small ones one
   const bool bulk = rows >= kBulkMinRows;
   const dim3 grid(bulk ? (rows + kBulkRows - 1) / kBulkRows : rows, 2);
-#define VRM_TQ_WRITE_R(SRC, B)                                                                               \
+#define VRM_TQ_WRITE_RP(SRC, B, PDV)                                                                         \
   if (bulk)                                                                                                  \
-    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, kBulkRows>), grid, dim3(64 * kBulkRows), 0, st, a);     \
+    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, kBulkRows, PDV>), grid, dim3(64 * kBulkRows), 0, st, a); \
   else                                                                                                       \
-    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, 1>), grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((tq_pool_write_kernel<SRC, B, 1, PDV>), grid, dim3(64), 0, st, a);
+#define VRM_TQ_WRITE_R(SRC, B)          \
+  if (pd == 64)                         \
+    VRM_TQ_WRITE_RP(SRC, B, 64)         \
+  else                                  \
+    VRM_TQ_WRITE_RP(SRC, B, 128)
 #define VRM_TQ_WRITE(SRC)                          \
   switch (bits) {                                  \
     case 2: VRM_TQ_WRITE_R(SRC, 2); break;         \
@@ -976,12 +990,13 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   }
 #undef VRM_TQ_WRITE
 #undef VRM_TQ_WRITE_R
+#undef VRM_TQ_WRITE_RP
   return launch_status(who);
 }
 }  // namespace
 
 extern "C" size_t vrm_tq_slice_bytes_ps(int head_dim, int bits, int qjl_dim, int page_size) {
-  if (tq::tuned_layout(head_dim, bits, qjl_dim, page_size)) return (size_t)tq::slice_bytes(bits);
+  if (const int pd = tq::tuned_pd(head_dim, bits, qjl_dim, page_size)) return (size_t)tq::slice_bytes(pd, bits);
   if (tq::generic_ok(head_dim, bits, qjl_dim, page_size))
     return tq::gen_layout(head_dim, bits, qjl_dim, page_size).slice_bytes();
   return 0;
@@ -1136,14 +1151,15 @@ extern "C" int vrm_tq_read_pages(const uint8_t* tq_pool, const int32_t* page_ids
     set_error("%s: null pointer argument", who);
     return VRM_ERR_ARG;
   }
-  if (!tq::tuned_layout(D, bits, qjl_dim, PS)) {
+  const int pd = tq::tuned_pd(D, bits, qjl_dim, PS);
+  if (!pd) {
     hipLaunchKernelGGL(tq_pool_read_gen_kernel, dim3(NP * 2 * KH * PS), dim3(64), 0,
                        reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx,
                        tq::gen_layout(D, bits, qjl_dim, PS), radius, angles, qjl_signs, qjl_norms);
     return launch_status(who);
   }
   hipLaunchKernelGGL(tq_pool_read_kernel, dim3(NP * 2 * KH * tq::kTokens), dim3(64), 0,
-                     reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx, bits, radius,
+                     reinterpret_cast<hipStream_t>(stream), tq_pool, page_ids, KH, L, P, layer_idx, pd, bits, radius,
                      angles, qjl_signs, qjl_norms);
   return launch_status(who);
 }
