@@ -147,6 +147,38 @@ __device__ __forceinline__ void split8(float y0, const float4& t0, float y1, con
         "v"(t1.w));
 }
 
+// The P^T operand of eight weights p (float32): fp16(p) where neg_sel is -0
+// (hi columns), fp16(p - fp16(p)) where it is -1 (lo columns), as one packed
+// conversion per two values, one mixed fused multiply-add per value
+// (p + neg_sel * fp16(p), exact) and one packed conversion per two.  The
+// result feeds a matrix-core instruction: the block ends with s_nop 1.
+__device__ __forceinline__ uint4 weights8(const float (&p)[8], float neg_sel) {
+  uint4 out;
+  uint32_t h[4];
+  float d[8];
+  asm("v_cvt_pk_f16_f32 %4, %16, %17\n\t"
+      "v_cvt_pk_f16_f32 %5, %18, %19\n\t"
+      "v_cvt_pk_f16_f32 %6, %20, %21\n\t"
+      "v_cvt_pk_f16_f32 %7, %22, %23\n\t"
+      "v_fma_mix_f32 %8, %4, %24, %16 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %9, %4, %24, %17 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %10, %5, %24, %18 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %11, %5, %24, %19 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %12, %6, %24, %20 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %13, %6, %24, %21 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %14, %7, %24, %22 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %15, %7, %24, %23 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_cvt_pk_f16_f32 %0, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %1, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %2, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %3, %14, %15\n\t"
+      "s_nop 1"
+      : "=&v"(out.x), "=&v"(out.y), "=&v"(out.z), "=&v"(out.w), "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]),
+        "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
+      : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7]), "v"(neg_sel));
+  return out;
+}
+
 // Maximum over lanes lane % 16 + {0, 16, 32, 48} (the four rows of a
 // column), by the VALU lane swaps of gfx950 instead of LDS round trips.
 __device__ __forceinline__ float max_rows4(float x) {
@@ -253,6 +285,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // repeat head G - 1).  A score or output is the sum of columns n and n + 8.
   const int hcol = col & 7;
   const bool lo_col = col >= 8;
+  const float neg_sel = lo_col ? -1.f : -0.f;  // P^T: hi columns fp16(p), lo columns fp16(p - fp16(p))
+  // byte offset of the cos (+0) or sin (+4) half of a {cos, sin} entry for
+  // the top two levels of this lane's dims
+  const uint32_t sel6 = (uint32_t)(grp >> 1) << 2, sel5 = (uint32_t)(grp & 1) << 2;
   const int group = a.H / a.KH;
   const int chunks = group / G;
   const int unit = blockIdx.y * (blockDim.x >> 6) + wave;
@@ -260,6 +296,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   const int h0 = kvh * group + (unit % chunks) * G;
 
   for (int i = threadIdx.x; i < NB; i += blockDim.x) lut[i] = make_float2(tq.lut[2 * NB + i], tq.lut[3 * NB + i]);
+  const float* lutf = reinterpret_cast<const float*>(lut);
   if constexpr (BITS > 3) {
     for (int i = threadIdx.x; i < NB * NB; i += blockDim.x) {
       const int ba = i % NB, bb = i / NB;
@@ -445,11 +482,14 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
 #pragma unroll
       for (int i = 0; i < QWords::kN; ++i) q[i] = qw[i];
     }
-    const float2 t6 = lds_at(lut, field_off<BITS, 3>(&top0, top_sh));
-    const float2 t5 = lds_at(lut, field_off<BITS, 3>(&topq, top_sh));
+    // the {cos, sin} entry's component this lane's dims take: cos where the
+    // top bit of the dims (bit 6 at PD 128) is clear, sin where set; then
+    // the same for the next bit
+    const float t6 = lds_at(lutf, field_off<BITS, 3>(&top0, top_sh) | sel6);
+    const float t5 = lds_at(lutf, field_off<BITS, 3>(&topq, top_sh) | sel5);
     float p = radius;
-    p = p * ((grp >> 1) ? t6.y : t6.x);  // top bit of the dims (bit 6 at PD 128)
-    p = p * ((grp & 1) ? t5.y : t5.x);   // the next one
+    p = p * t6;
+    p = p * t5;
     if constexpr (PD == 64) {
       // levels 3 and 2: the quarter's root and its children
       if constexpr (kT32) {
@@ -504,8 +544,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   };
 
   // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi, for
-  // head hcol (both column halves hold the same sums).
-  auto page_scores = [&](const Slot& s, int pi, float* sc) {
+  // head hcol (both column halves hold the same sums).  Unless the pair is
+  // full (a present page, every token inside the context), tokens of absent
+  // pages and past the context score -inf.
+  auto page_scores = [&](const Slot& s, int pi, bool full, float* sc) {
     float y[NY];
     float4 t[NY];
     rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), y, t);
@@ -535,10 +577,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 4 * grp + r;
-      const float v = c4[r] + row_swap8(c4[r]);
-      sc[r] = (s.ok && pi * kPS + t < tok_end) ? v : -INFINITY;
+    for (int r = 0; r < 4; ++r) sc[r] = c4[r] + row_swap8(c4[r]);
+    if (!full) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (!(s.ok && pi * kPS + 4 * grp + r < tok_end)) sc[r] = -INFINITY;
     }
   };
 
@@ -551,11 +594,12 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   };
   // Values of this lane's token; absent pages and tokens past the context get
   // radius 0 (whatever the page holds), so they contribute exact zeros.
-  auto v_operand = [&](const Slot& s, int pi, v8h (&vop)[NC]) {
+  auto v_operand = [&](const Slot& s, int pi, bool full, v8h (&vop)[NC]) {
     float y[NY];
     float4 t[NY];
-    const bool live = s.ok && pi * kPS + col < tok_end;
-    rebuild(s.vq, s.vtop[0], s.vtop[1], live ? f16_to_f32(s.vrad) : 0.f, y, t);
+    float radius = f16_to_f32(s.vrad);
+    if (!full && !(s.ok && pi * kPS + col < tok_end)) radius = 0.f;
+    rebuild(s.vq, s.vtop[0], s.vtop[1], radius, y, t);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       uint4 w;
@@ -565,9 +609,11 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   };
 
   auto process_pair = [&](const Slot& s0, const Slot& s1, int pi) {
+    // wave-uniform: both pages present and every token inside the context
+    const bool full = s0.ok && s1.ok && (pi + 2) * kPS <= tok_end;
     float sc[8];
-    page_scores(s0, pi, sc);
-    page_scores(s1, pi + 1, sc + 4);
+    page_scores(s0, pi, full, sc);
+    page_scores(s1, pi + 1, full, sc + 4);
     float pm = sc[0];
 #pragma unroll
     for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
@@ -580,17 +626,16 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
       m_run = pm;
     }
     // P^T as hi (columns < 8) and lo (columns >= 8)
-    v8h Bp;
+    float pw[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = __builtin_amdgcn_exp2f(sc[e] - m_run);
-      l_run += p;
-      const _Float16 hi = (_Float16)p;
-      Bp[e] = lo_col ? (_Float16)(p - (float)hi) : hi;
+      pw[e] = __builtin_amdgcn_exp2f(sc[e] - m_run);
+      l_run += pw[e];
     }
+    const v8h Bp = __builtin_bit_cast(v8h, weights8(pw, neg_sel));
     v8h vop0[NC], vop1[NC];
-    v_operand(s0, pi, vop0);
-    v_operand(s1, pi + 1, vop1);  // past the partition: radius 0
+    v_operand(s0, pi, full, vop0);
+    v_operand(s1, pi + 1, full, vop1);  // past the partition: radius 0
 #pragma unroll
     for (int c = 0; c < NC; ++c)
 #pragma unroll
