@@ -90,7 +90,7 @@ def host_us(fn, n):
     return (t1 - t0) * 1e6 / n
 
 
-def cpu_baseline(inp, layer, n_seq, reps):
+def cpu_baseline(inp, layer, n_seq, reps, page_size=16):
     """The reference's PyTorch decode path (restated in oracle/) on the host
     cores, over the first n_seq sequences of the same workload.  Returns
     microseconds per context token and the thread count."""
@@ -111,8 +111,9 @@ def cpu_baseline(inp, layer, n_seq, reps):
         from oracle import turboquant as TQ
 
         codes = {k: v.cpu() for k, v in tq_pages.read_pages(inp["kv_pool"], layer, pages.to(torch.int32),
-                                                               comp).items()}
-        p = TQ.TQParams(128, comp.bits_per_angle, 128, 7, 64, comp._hadamard_signs.cpu(), comp.jl_matrix.cpu())
+                                                               comp, page_size).items()}
+        p = TQ.TQParams(comp.head_dim, comp.bits_per_angle, comp._padded_dim, comp._n_levels, comp.qjl_dim,
+                        comp._hadamard_signs.cpu(), comp.jl_matrix.cpu())
         PD.paged_attention_decode_turbo(p, q, codes, tbl, lens)  # warm-up
         times = []
         for _ in range(reps):
@@ -710,7 +711,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         log(f"CPU baseline on {args.cpu_seqs} sequences")
-        per_token_us, threads = cpu_baseline(inp, layers[0], min(args.cpu_seqs, B), args.cpu_reps)
+        per_token_us, threads = cpu_baseline(inp, layers[0], min(args.cpu_seqs, B), args.cpu_reps, PS)
         cpu = {
             "value": round(per_token_us * sum(lens_list), 1),
             "unit": "us/layer-step",
@@ -770,9 +771,11 @@ def main():
         roofline["pattern_loads_us"] = round(us_loads, 3)
         roofline["frac_of_pattern"] = round(us_loads / us_part, 4)
     valu = None
-    if (turbo or q4) and not shape_override and os.path.exists(VALU_FILE):
+    if (turbo or q4) and os.path.exists(VALU_FILE):
+        # counts per workload at its own shape ("<workload>") or another ("<workload>@d<D>-ps<PS>")
+        key = cfg.name if not shape_override else f"{cfg.name}@d{D}-ps{PS}"
         with open(VALU_FILE) as f:
-            valu = json.load(f)["workloads"].get(cfg.name)
+            valu = json.load(f)["workloads"].get(key)
     if valu is not None:
         # These kernels rebuild or unpack every code on the vector ALU: the
         # binding roofline is VALU issue, the HBM figures stay as context.

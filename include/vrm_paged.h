@@ -376,9 +376,10 @@ int vrm_unpack_bits(const uint8_t* packed, long long rows, int M, int bits, uint
  * fp16 residual norm.  Every compressor setting of the reference's
  * KVCacheCompressor (core/kv_quantizer.py:205-240) with head_dim 33..256
  * (padded_dim 64 / 128 / 256), 1..8 bits per angle and qjl_dim 1..256 is
- * served, at any page size.  head_dim 128, qjl_dim 64, 2..4 bits and 16-token
- * pages use a tuned slice (angle bins in a lane-friendly order of the
- * reference's 127 bins) and decode kernel; every other setting a generic
+ * served, at any page size.  head_dim 33..128 with the compressor's default
+ * qjl_dim (padded_dim / 2: 32 or 64), 2..4 bits and 16-token pages use tuned
+ * slices (angle bins in a lane-friendly order of the reference's
+ * padded_dim - 1 bins) and decode kernel; every other setting a generic
  * slice of per-token records (level-major angle bits, sign bits, radius,
  * norm).  signs / jl / angle_lut are the compressor's buffers and the
  * {cos, sin} table of vrm_turboquant_compress.

@@ -213,7 +213,7 @@ struct TqDecodeArgs {
   const float* lut;    // [cos level 0, sin level 0, cos levels >= 1, sin levels >= 1][2^bits]
   float qjl_coef;      // sqrt(pi / 2) / qjl, or 0 for scores without the QJL term
 };
-// hd: the head_dim (65 .. 128: the tuned layout's padded dim is 128).
+// hd: the head_dim (33 .. 64 or 65 .. 128: the tuned layouts' padded dims 64 and 128).
 hipError_t launch_tq_decode(const DecodeArgs& a, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st);
 
 // Paged decode over TurboQuant pages in the generic layout (vrm_decode_tq_generic.hip):

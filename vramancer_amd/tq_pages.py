@@ -9,15 +9,16 @@ the host side per call.  Here the same codes live in a device pool
 
     tq_pool[P, L, 2, KH, slice]   (uint8, slice = slice_bytes(bits) bytes)
 
-one slice per (page, layer, K/V, kv-head) with the page's 16 tokens: the 127
-angle bins, the fp16 radius and, for K, the 64 QJL sign bits and the fp16
-residual norm.  The codes are those of ``KVCacheCompressor.compress``; the
+one slice per (page, layer, K/V, kv-head) with the page's tokens: the
+padded_dim - 1 angle bins, the fp16 radius and, for K, the QJL sign bits and
+the fp16 residual norm.  The codes are those of ``KVCacheCompressor.compress``; the
 decode computes compute_attention_turbo's attention (QJL-corrected scores on
 the rotated query, dense decompressed values) with query head h reading
 kv-head h // (H / KH), the mapping of the paged decode path.
 
-Head_dim 128 with 64 QJL rows, 2 to 4 bits per angle and pages of 16 tokens
-use the tuned layout and decode kernel; every other compressor setting
+Head_dim 33 .. 128 with the compressor's default QJL rows (padded_dim / 2:
+32 at head_dim <= 64, 64 above), 2 to 4 bits per angle and pages of 16 tokens
+use the tuned layouts and decode kernel; every other compressor setting
 (head_dim 33 .. 256, 1 to 8 bits, QJL rows up to 256) and page size uses the
 generic layout and kernels of the same library.
 """
