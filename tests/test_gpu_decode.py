@@ -123,6 +123,19 @@ def test_decode_zero_and_single_token_contexts():
         torch.testing.assert_close(out[1, h], pool[pid, 1, 1, h // 4, 0].float(), atol=1e-6, rtol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn], ids=lambda d: str(d).split(".")[-1])
+def test_decode_merge_starts_the_longest_sequence_first(dtype):
+    """The merge runs the sequence with the most partials in its first
+    workgroup row (swapped with sequence 0): the longest sequence in the
+    middle of the batch, a tie for the longest, sequence 0 empty and a
+    one-token one, all against the oracle."""
+    _say(f"merge order {dtype}")
+    for ctxs in ([0, 300, 12000, 40, 1, 12000, 900], [5000, 17, 0, 4999, 64]):
+        q, pool, sc, table, lens = _pool_case(dtype, len(ctxs), 16, 4, 128, ctxs, L=1, layer=0, seed=len(ctxs))
+        out, ref = _run_both(q, pool, sc, table, lens, 0)
+        _assert_close(out, ref, f"{dtype} {ctxs}")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.int8, torch.float8_e4m3fn],
                          ids=lambda d: str(d).split(".")[-1])
 def test_decode_long_context_many_partitions(dtype):

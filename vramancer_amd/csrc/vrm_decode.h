@@ -60,6 +60,7 @@ struct DecodeArgs {
 //
 // Workspace header (int32), written by the partition pass for the merge:
 //   [0] pps   [1] number of items   [2] number of full items
+//   [3] the sequence with the most partitions (the merge starts it first)
 //   [kHeaderInts + b],         b = 0 .. B : first full item of sequence b
 //                                           (entry B = number of full items)
 //   [kHeaderInts + B + 1 + b], b < B      : tail item of sequence b, or -1
@@ -84,6 +85,12 @@ __device__ __forceinline__ int seq_pages(int ctx, int max_pp, int ps = kPS) {
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) v += __builtin_amdgcn_ds_bpermute((__lane_id() ^ m) << 2, v);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max_int(int v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v = max(v, __builtin_amdgcn_ds_bpermute((__lane_id() ^ m) << 2, v));
   return v;
 }
 
@@ -159,11 +166,27 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
     carry_f = __builtin_amdgcn_readlane(incl_f, 63);
     carry_t = __builtin_amdgcn_readlane(incl_t, 63);
   }
-  if (writer && lane == 0) {
-    header[0] = pps;
-    header[1] = carry_t;
-    header[2] = n_full;
-    header[kHeaderInts + B] = n_full;
+  if (writer) {
+    // the sequence with the most partitions (first of equals), in a pass of
+    // its own so that the other waves' path stays as it is
+    int most = -1, most_b = 0;
+    for (int c = 0; c < B; c += 64) {
+      const int b = c + lane;
+      const int pages = b < B ? seq_pages(ctx_lens[b], max_pp, ps) : 0;
+      const int cnt = b < B ? pages / pps + (pages % pps != 0 ? 1 : 0) : -1;
+      const int cmax = wave_max_int(cnt);
+      if (cmax > most) {
+        most = cmax;
+        most_b = c + __builtin_ffsll(__ballot(cnt == cmax)) - 1;
+      }
+    }
+    if (lane == 0) {
+      header[0] = pps;
+      header[1] = carry_t;
+      header[2] = n_full;
+      header[3] = most_b;
+      header[kHeaderInts + B] = n_full;
+    }
   }
   return found;
 }

@@ -335,7 +335,10 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
   constexpr int WAVES = 4;
   __shared__ float sh_m[WAVES], sh_l[WAVES];
   __shared__ float sh_res[WAVES][DMAX];
-  const int h = blockIdx.x, b = blockIdx.y;
+  // Workgroups start in blockIdx order: the sequence with the most partials
+  // (the longest fold) takes row 0, so that its merge overlaps the others'.
+  const int big = min(max(header[3], 0), B - 1);
+  const int h = blockIdx.x, b = blockIdx.y == 0 ? big : ((int)blockIdx.y == big ? 0 : (int)blockIdx.y);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int first = header[kHeaderInts + b];
   const int nf = header[kHeaderInts + b + 1] - first;
