@@ -33,6 +33,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace vrm {
 namespace dec {
 namespace {
@@ -41,6 +43,7 @@ namespace T = vrm::tq;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;             // wavefronts per workgroup (at most)
 constexpr int kMaxHeads = 8;          // query heads per wave (hi / lo column halves)
@@ -145,6 +148,41 @@ __device__ __forceinline__ void split8(float y0, const float4& t0, float y1, con
         "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]), "=&v"(k[6]), "=&v"(k[7])
       : "v"(y0), "v"(y1), "v"(t0.x), "v"(t0.y), "v"(t0.z), "v"(t0.w), "v"(t1.x), "v"(t1.y), "v"(t1.z),
         "v"(t1.w));
+}
+
+// split8 for tables that also carry fp16 copies of their entries (h0, h1:
+// the fp16 t_j.k as two packed pairs each).  hi is the fp16 product of the
+// fp16 factors, fp16(y_j) * fp16(t_j.k) by one packed multiply per two values
+// (within two units in the last place of fp16(y t)), and lo = fp16(y t - hi)
+// is the residual of the exact product as in split8, so hi + lo carries y t
+// to the same 22 bits.  Ends with s_nop 1 (its results are MFMA operands).
+__device__ __forceinline__ void split8p(float y0, const float4& t0, uint2 h0, float y1, const float4& t1, uint2 h1,
+                                        uint4& hi, uint4& lo) {
+  float k[8];
+  uint32_t yh;
+  asm("v_cvt_pk_f16_f32 %16, %17, %18\n\t"
+      "v_pk_mul_f16 %0, %27, %16 op_sel_hi:[1,0]\n\t"
+      "v_pk_mul_f16 %1, %28, %16 op_sel_hi:[1,0]\n\t"
+      "v_pk_mul_f16 %2, %29, %16 op_sel:[0,1] op_sel_hi:[1,1]\n\t"
+      "v_pk_mul_f16 %3, %30, %16 op_sel:[0,1] op_sel_hi:[1,1]\n\t"
+      "v_fma_mix_f32 %8, %17, %19, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %9, %17, %20, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %10, %17, %21, -%1 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %11, %17, %22, -%1 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %12, %18, %23, -%2 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %13, %18, %24, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %14, %18, %25, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mix_f32 %15, %18, %26, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]\n\t"
+      "v_cvt_pk_f16_f32 %4, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %5, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %6, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %7, %14, %15\n\t"
+      "s_nop 1"
+      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
+        "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]), "=&v"(k[6]), "=&v"(k[7]),
+        "=&v"(yh)
+      : "v"(y0), "v"(y1), "v"(t0.x), "v"(t0.y), "v"(t0.z), "v"(t0.w), "v"(t1.x), "v"(t1.y), "v"(t1.z),
+        "v"(t1.w), "v"(h0.x), "v"(h0.y), "v"(h1.x), "v"(h1.y));
 }
 
 // The P^T operand of eight weights p (float32): fp16(p) where neg_sel is -0
@@ -266,15 +304,21 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // sin a cos c, sin a sin c); t10 for levels 1/0 (level 0 has its own bin
   // centres) and, at 2 and 3 bits, t32 for levels 3/2.  They share LDS with
   // qbuf (per wave: q_rot rows before the stream, the output columns after
-  // it), which is dead while the tables are read.
+  // it), which is dead while the tables are read.  At 2 and 3 bits t10 is
+  // followed by t10h, the same products as fp16 pairs (the factors of K's
+  // packed hi parts, split8p) at the same 16-byte stride, so one address
+  // serves both lookups.
   constexpr bool kT32 = BITS <= 3;
+  // K's hi parts by split8p (at padded dim 64 its extra registers cost the
+  // third wavefront per SIMD, measured slower)
+  constexpr bool kPackedHi = kT32 && PD == 128;
   constexpr int NT = NB * NB * NB;
   constexpr int QBUF_BYTES = kWaves * 16 * (D + 4) * 4;
-  constexpr int TAB_BYTES = (kT32 ? 2 : 1) * NT * 16;
+  constexpr int TAB_BYTES = (kT32 ? 3 : 1) * NT * 16;
   __shared__ __attribute__((aligned(16))) unsigned char shbuf[QBUF_BYTES > TAB_BYTES ? QBUF_BYTES : TAB_BYTES];
   float(*qbuf)[16][D + 4] = reinterpret_cast<float(*)[16][D + 4]>(shbuf);
   float4* t10 = reinterpret_cast<float4*>(shbuf);
-  float4* t32 = t10 + NT;
+  float4* t32 = t10 + (kT32 ? 2 : 1) * NT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -405,7 +449,13 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     const float* sin0 = tq.lut + NB;
     for (int i = threadIdx.x; i < NT; i += blockDim.x) {
       const int ia = i % NB, ib = (i / NB) % NB, ic = i / (NB * NB);
-      t10[i] = make_float4(cos1[ia] * cos0[ib], cos1[ia] * sin0[ib], sin1[ia] * cos0[ic], sin1[ia] * sin0[ic]);
+      const float4 e = make_float4(cos1[ia] * cos0[ib], cos1[ia] * sin0[ib], sin1[ia] * cos0[ic], sin1[ia] * sin0[ic]);
+      t10[i] = e;
+      if constexpr (kPackedHi) {
+        const uint32_t h01 = __builtin_bit_cast(uint32_t, v2h{(_Float16)e.x, (_Float16)e.y});
+        const uint32_t h23 = __builtin_bit_cast(uint32_t, v2h{(_Float16)e.z, (_Float16)e.w});
+        t10[NT + i] = make_float4(__uint_as_float(h01), __uint_as_float(h23), 0.f, 0.f);
+      }
       if constexpr (kT32)
         t32[i] = make_float4(cos1[ia] * cos1[ib], cos1[ia] * sin1[ib], sin1[ia] * cos1[ic], sin1[ia] * sin1[ic]);
     }
@@ -471,8 +521,10 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // Leaves the last level's products to the caller: value 4 j + k of the
   // group is y[j] * t[j][k].  The quarter's words are aligned here, at the
   // point of use, so that the ring's loads stay in flight until then.
-  auto rebuild = [&](const uint32_t* qw, uint32_t top0, uint32_t topq, float radius, float (&y)[NY],
-                     float4 (&t)[NY]) {
+  // with_fp16 (std::true_type, tables of 2 and 3 bits): also th[j], the fp16
+  // copy of t[j] (split8p's factors).
+  auto rebuild = [&](auto with_fp16, const uint32_t* qw, uint32_t top0, uint32_t topq, float radius,
+                     float (&y)[NY], float4 (&t)[NY], uint2 (&th)[NY]) {
     uint32_t q[QWords::kN];
     if constexpr (QWords::kSplit) {
       q[0] = __builtin_amdgcn_alignbit(qw[1], qw[0], q_sh);
@@ -537,10 +589,13 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     // levels 1 and 0: node j and its children in slots 3 j .. 3 j + 2 (4 bits:
     // node slot NY - 1 + j, children slots 2 NY - 1 + 2 j, 2 NY + 2 j)
 #pragma unroll
-    for (int j = 0; j < NY; ++j)
-      t[j] = lds_at(t10, kT32 ? field_off<3 * BITS, 4>(q, 3 * j * BITS)
-                              : field_off<BITS, 4>(q, (NY - 1 + j) * BITS) |
-                                    field_off<2 * BITS, 4 + BITS>(q, (2 * NY - 1 + 2 * j) * BITS));
+    for (int j = 0; j < NY; ++j) {
+      const uint32_t off = kT32 ? field_off<3 * BITS, 4>(q, 3 * j * BITS)
+                                : field_off<BITS, 4>(q, (NY - 1 + j) * BITS) |
+                                      field_off<2 * BITS, 4 + BITS>(q, (2 * NY - 1 + 2 * j) * BITS);
+      t[j] = lds_at(t10, off);
+      if constexpr (decltype(with_fp16)::value) th[j] = lds_at(reinterpret_cast<const uint2*>(t10 + NT), off);
+    }
   };
 
   // Scores (log2 domain) of this lane's tokens 4 grp + r of page pi, for
@@ -550,13 +605,17 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   auto page_scores = [&](const Slot& s, int pi, bool full, float* sc) {
     float y[NY];
     float4 t[NY];
-    rebuild(s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), y, t);
+    uint2 th[NY];
+    rebuild(std::integral_constant<bool, kPackedHi>{}, s.kq, s.ktop[0], s.ktop[1], f16_to_f32(s.krad), y, t, th);
     v4f c4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      // k = y t as hi = fp16(k) and lo = fp16(k - hi)
+      // k = y t as hi (fp16 near k) and lo = fp16(k - hi)
       uint4 hw, lw;
-      split8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], hw, lw);
+      if constexpr (kPackedHi)
+        split8p(y[2 * c], t[2 * c], th[2 * c], y[2 * c + 1], t[2 * c + 1], th[2 * c + 1], hw, lw);
+      else
+        split8(y[2 * c], t[2 * c], y[2 * c + 1], t[2 * c + 1], hw, lw);
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, hw), QB[c], c4, 0, 0, 0);
       c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lw), QB[c], c4, 0, 0, 0);
     }
@@ -599,7 +658,8 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
     float4 t[NY];
     float radius = f16_to_f32(s.vrad);
     if (!full && !(s.ok && pi * kPS + col < tok_end)) radius = 0.f;
-    rebuild(s.vq, s.vtop[0], s.vtop[1], radius, y, t);
+    uint2 th[NY];
+    rebuild(std::false_type{}, s.vq, s.vtop[0], s.vtop[1], radius, y, t, th);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       uint4 w;
