@@ -154,19 +154,24 @@ def require_cuda(*tensors) -> None:
             raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
 
 
-def kv_dtype_code(dtype) -> int:
-    import torch
+_KV_CODES: dict = {}
 
-    table = {
-        torch.float32: VRM_KV_F32,
-        torch.float16: VRM_KV_F16,
-        torch.bfloat16: VRM_KV_BF16,
-        torch.int8: VRM_KV_I8,
-        torch.float8_e4m3fn: VRM_KV_FP8E4M3,
-    }
-    if dtype not in table:
+
+def kv_dtype_code(dtype) -> int:
+    if not _KV_CODES:
+        import torch
+
+        _KV_CODES.update({
+            torch.float32: VRM_KV_F32,
+            torch.float16: VRM_KV_F16,
+            torch.bfloat16: VRM_KV_BF16,
+            torch.int8: VRM_KV_I8,
+            torch.float8_e4m3fn: VRM_KV_FP8E4M3,
+        })
+    code = _KV_CODES.get(dtype)
+    if code is None:
         raise RuntimeError(f"unsupported KV pool dtype {dtype}")
-    return table[dtype]
+    return code
 
 
 def src_dtype_code(dtype) -> int:

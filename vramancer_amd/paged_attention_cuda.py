@@ -74,11 +74,16 @@ def prefer_balanced(context_lens_host, num_kv_heads: int, kv_dtype) -> bool:
 
     if kv_dtype not in (torch.int8, torch.float8_e4m3fn):
         return False
-    lens = [int(x) for x in context_lens_host]
-    if not lens or len(lens) * num_kv_heads < BALANCED_MIN_PAIRS:
+    # built-in reductions over a list of ints (this runs once per layer call,
+    # so it avoids a per-element Python loop)
+    lens = context_lens_host.tolist() if hasattr(context_lens_host, "tolist") else context_lens_host
+    n = len(lens)
+    if not n or n * num_kv_heads < BALANCED_MIN_PAIRS:
         return False
-    total = sum(max(x, 0) for x in lens)
-    return total > 0 and max(lens) * len(lens) <= BALANCED_MAX_SPREAD * total
+    total = sum(lens)
+    if min(lens) < 0:
+        total = sum(x for x in lens if x > 0)
+    return total > 0 and max(lens) * n <= BALANCED_MAX_SPREAD * total
 
 
 def check_outputs(query, out, workspace, page_table, context_lens) -> None:
