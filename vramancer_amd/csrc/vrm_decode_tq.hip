@@ -46,6 +46,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;             // wavefronts per workgroup (at most)
+constexpr int kWideWaves = 8;         // the wide build: one workgroup per CU sharing a 128 KB table
 constexpr int kMaxHeads = 8;          // query heads per wave (hi / lo column halves)
 constexpr float kLazyRescale = 3.0f;  // as in vrm_decode_mfma.hip
 constexpr float kNoMax = -1.0e30f;
@@ -279,8 +280,13 @@ struct TqSlot {
   bool ok;                     // page id inside the pool (wave-uniform)
 };
 
-template <int BITS, int PD>
-__global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G, int hd) {
+// WIDE (4 bits at padded dim 128): workgroups of up to kWideWaves
+// wavefronts, one per CU, so that its t10 fits in LDS with the fp16 copy
+// K's packed hi parts read (128 KB).
+template <int BITS, int PD, bool WIDE>
+__global__ void __launch_bounds__(64 * (WIDE ? kWideWaves : kWaves), WIDE ? 1 : 2)
+    decode_tq_kernel(DecodeArgs a, TqDecodeArgs tq, int G, int hd) {
+  constexpr int WAVES = WIDE ? kWideWaves : kWaves;
   constexpr int NB = 1 << BITS;
   constexpr int RING = 4;
   constexpr int SLICE = T::slice_bytes(PD, BITS);
@@ -307,18 +313,18 @@ __global__ void __launch_bounds__(64 * kWaves, 2) decode_tq_kernel(DecodeArgs a,
   // it), which is dead while the tables are read.  At 2 and 3 bits t10 is
   // followed by t10h, the same products as fp16 pairs (the factors of K's
   // packed hi parts, split8p) at the same 16-byte stride, so one address
-  // serves both lookups.
+  // serves both lookups (at 4 bits in the wide build only: 64 KB each).
   constexpr bool kT32 = BITS <= 3;
   // K's hi parts by split8p (at padded dim 64 its extra registers cost the
   // third wavefront per SIMD, measured slower)
-  constexpr bool kPackedHi = kT32 && PD == 128;
+  constexpr bool kPackedHi = PD == 128 && (kT32 || WIDE);
   constexpr int NT = NB * NB * NB;
-  constexpr int QBUF_BYTES = kWaves * 16 * (D + 4) * 4;
-  constexpr int TAB_BYTES = (kT32 ? 3 : 1) * NT * 16;
+  constexpr int QBUF_BYTES = WAVES * 16 * (D + 4) * 4;
+  constexpr int TAB_BYTES = ((kPackedHi ? 2 : 1) + (kT32 ? 1 : 0)) * NT * 16;
   __shared__ __attribute__((aligned(16))) unsigned char shbuf[QBUF_BYTES > TAB_BYTES ? QBUF_BYTES : TAB_BYTES];
   float(*qbuf)[16][D + 4] = reinterpret_cast<float(*)[16][D + 4]>(shbuf);
   float4* t10 = reinterpret_cast<float4*>(shbuf);
-  float4* t32 = t10 + (kT32 ? 2 : 1) * NT;
+  float4* t32 = t10 + (kPackedHi ? 2 : 1) * NT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -773,19 +779,28 @@ template <int PD>
 hipError_t launch_tq_pd(const DecodeArgs& a0, const TqDecodeArgs& tq, int bits, int B, int hd, hipStream_t st) {
   const int G = pick_group_tile(a0.H / a0.KH, kMaxHeads);
   const int units = a0.KH * ((a0.H / a0.KH) / G);
-  int W = kWaves;
+  // 4 bits at padded dim 128 take the wide build when its workgroups are full
+  const bool wide = bits == 4 && PD == 128 && units % kWideWaves == 0;
+  int W = wide ? kWideWaves : kWaves;
   while (units % W) --W;
   DecodeArgs a = a0;
-  const void* fn = bits == 2   ? reinterpret_cast<const void*>(&decode_tq_kernel<2, PD>)
-                   : bits == 3 ? reinterpret_cast<const void*>(&decode_tq_kernel<3, PD>)
-                               : reinterpret_cast<const void*>(&decode_tq_kernel<4, PD>);
+  constexpr bool kHasWide = PD == 128;
+  const void* fn = bits == 2   ? reinterpret_cast<const void*>(&decode_tq_kernel<2, PD, false>)
+                   : bits == 3 ? reinterpret_cast<const void*>(&decode_tq_kernel<3, PD, false>)
+                   : wide      ? reinterpret_cast<const void*>(&decode_tq_kernel<4, PD, kHasWide>)
+                               : reinterpret_cast<const void*>(&decode_tq_kernel<4, PD, false>);
   a.target = items_target(fn, W, 0, units);
   dim3 grid(B + 2 * a.target, units / W, 1);
   dim3 block(64 * W);
   switch (bits) {
-    case 2: hipLaunchKernelGGL((decode_tq_kernel<2, PD>), grid, block, 0, st, a, tq, G, hd); break;
-    case 3: hipLaunchKernelGGL((decode_tq_kernel<3, PD>), grid, block, 0, st, a, tq, G, hd); break;
-    default: hipLaunchKernelGGL((decode_tq_kernel<4, PD>), grid, block, 0, st, a, tq, G, hd); break;
+    case 2: hipLaunchKernelGGL((decode_tq_kernel<2, PD, false>), grid, block, 0, st, a, tq, G, hd); break;
+    case 3: hipLaunchKernelGGL((decode_tq_kernel<3, PD, false>), grid, block, 0, st, a, tq, G, hd); break;
+    default:
+      if (wide)
+        hipLaunchKernelGGL((decode_tq_kernel<4, PD, kHasWide>), grid, block, 0, st, a, tq, G, hd);
+      else
+        hipLaunchKernelGGL((decode_tq_kernel<4, PD, false>), grid, block, 0, st, a, tq, G, hd);
+      break;
   }
   return hipGetLastError();
 }
