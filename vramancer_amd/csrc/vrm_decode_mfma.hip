@@ -174,29 +174,38 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
     }
   }
   __syncthreads();
+  // One (unit, head) output row per wavefront at a time: its log-sum-exp
+  // weights are computed once (wave-uniform), each lane folds its dims
+  // lane + 64 i in the same order as the partials were written.
   const int group = a.H / a.KH;
-  for (int i = threadIdx.x; i < kUnitsPerWg * G * D; i += blockDim.x) {
-    const int ul = i / (G * D);
-    const int rem = i - ul * G * D;
-    const int g = rem / D, d = rem - g * D;
+  constexpr int PER = (D + 63) / 64;
+  for (int pr = wave; pr < kUnitsPerWg * G; pr += W) {
+    const int ul = pr / G, g = pr - ul * G;
     const int unit = unit0 + ul;
     if (unit >= units) continue;
     float M = -INFINITY;
     for (int w = ul; w < W; w += kUnitsPerWg) M = fmaxf(M, ml[(w * G + g) * 2]);
-    float L = 0.f, o = 0.f;
+    float L = 0.f, o[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[i] = 0.f;
     if (M != -INFINITY) {
       for (int w = ul; w < W; w += kUnitsPerWg) {
         const float mw = ml[(w * G + g) * 2];
         const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
         L = fmaf(f, ml[(w * G + g) * 2 + 1], L);
-        o = fmaf(f, part[((size_t)w * G + g) * D + d], o);
+        const float* src = part + ((size_t)w * G + g) * D + lane;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+          if (lane + 64 * i < D) o[i] = fmaf(f, src[64 * i], o[i]);
       }
     }
     const int h0 = (unit / chunks) * group + (unit % chunks) * G;
     const size_t row = (size_t)b * a.H + h0 + g;
-    a.out[row * D + d] = L > 0.f ? o * (1.f / L) : 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (lane + 64 * i < D) a.out[row * D + lane + 64 * i] = L > 0.f ? o[i] * (1.f / L) : 0.f;
     // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
-    if (a.lse && d == 0) a.lse[row] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+    if (a.lse && lane == 0) a.lse[row] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
   }
 }
 
