@@ -223,7 +223,7 @@ inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
 // their partials in LDS, writing a.out (and a.lse) directly: no work items,
 // no workspace, no merge launch.  Correct for any context lengths; its time follows the
 // longest sequence, so it suits batches of about equal lengths.  kind is
-// K_I8 or K_FP8 (D 64, 128, 256) or K_BF16 / K_F16 (D 64, 128).
+// K_I8 or K_FP8, D a multiple of 16 from 64 to 128.
 // loads_only: the measuring build that issues the same loads and computes
 // nothing (a checksum of the words goes to out).
 hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st,

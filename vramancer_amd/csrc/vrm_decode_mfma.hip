@@ -230,6 +230,9 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   constexpr int KPART = D - 64 * (NJ - 1);
   static_assert(D % 16 == 0 && D <= 256, "head_dim must be a multiple of 16, at most 256");
   static_assert(RING % 2 == 0, "pages are consumed in pairs");
+  // the measuring build leaves its checksum in out, which only the balanced
+  // entry sets (item mode writes partials to the workspace)
+  static_assert(!LOADS || BALANCED, "the load-only build exists for the balanced mode only");
 
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -699,7 +702,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
   using Ops = FloatOps<KIND>;
   using vec = typename Ops::vec;
   using el = typename Ops::el;
-  constexpr int RING = D <= 128 ? 4 : 2;
+  // One page pair in registers: its refill is issued when the pair has been
+  // consumed.  A float page is twice an int8 one, and four slots per wave put
+  // so many bytes in flight that the pool's reads slowed down (bf16, 32
+  // sequences of 1k-8k tokens, 28 / 4 heads, D = 128: partition pass 74.5 us
+  // with four slots, 72.0 with two).
+  constexpr int RING = 2;
   constexpr int ROW = D * 2;              // bytes per token row
   // pages of 16 << vshift tokens streamed as 16-token sub-pages (as in the quantized kernel)
   const int vshift = a.vshift, vmask = (1 << a.vshift) - 1;
