@@ -957,6 +957,41 @@ __device__ __forceinline__ constexpr int q4_elem_of(int o) { return (o & 1) ? 4 
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
+// Eight floats w as the float16 pair hi = fp16(w), lo = fp16(w - hi) (the
+// residual exact, one rounding): a packed conversion per two values, one
+// mixed fused multiply-add per value, a packed conversion per two.  The
+// results are matrix-core operands, which may read a VGPR only two wait states
+// after a VALU write; the compiler cannot see the writes of an asm statement,
+// so the block ends with s_nop 1.
+__device__ __forceinline__ void split_hilo8(const float (&w)[8], uint4& hi, uint4& lo) {
+  float d[8];
+  asm("v_cvt_pk_f16_f32 %0, %16, %17\n\t"
+      "v_cvt_pk_f16_f32 %1, %18, %19\n\t"
+      "v_cvt_pk_f16_f32 %2, %20, %21\n\t"
+      "v_cvt_pk_f16_f32 %3, %22, %23\n\t"
+      "v_fma_mix_f32 %8, %0, -1.0, %16 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %9, %0, -1.0, %17 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %10, %1, -1.0, %18 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %11, %1, -1.0, %19 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %12, %2, -1.0, %20 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %13, %2, -1.0, %21 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %14, %3, -1.0, %22 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %15, %3, -1.0, %23 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_cvt_pk_f16_f32 %4, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %5, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %6, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %7, %14, %15\n\t"
+      "s_nop 1"
+      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
+        "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
+      : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));
+}
+
+// Low halves of two int32 (x, y) as one dword (x in bits 0-15).
+__device__ __forceinline__ uint32_t low_halves(int x, int y) {
+  return __builtin_amdgcn_perm((uint32_t)y, (uint32_t)x, 0x05040100u);
+}
+
 __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(DecodeArgs a, int G) {
   constexpr int D = 128;
   constexpr int RING = 4;
@@ -994,8 +1029,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * HEAD_BYTES;
   auto page_ok = [&](int pid) { return pid >= 0 && pid < a.P; };
   // lane (col, grp) fetches token col of array grp: K scales, K zeros, V scales, V zeros
-  const uint8_t* sz_base = reinterpret_cast<const uint8_t*>((grp & 1) ? a.q4_zero : a.q4_scale) + col * 8;
-  const int sz_kv = grp >> 1;
+  // (slice index ((page L + layer) 2 + K/V) KH + kv-head: the page's part is
+  // wave-uniform, the K/V part a per-lane offset)
+  const uint8_t* sz_base = reinterpret_cast<const uint8_t*>((grp & 1) ? a.q4_zero : a.q4_scale) + col * 8 +
+                           (size_t)((grp >> 1) * a.KH + kvh) * SZH;
+  const int code_off = col * ROW + grp * 4;  // this lane's bytes in a (page, layer, K/V, head) slice
 
   // ---------------- query: digits per group, group sums ----------------
   const float* qrow = a.query + ((size_t)b * a.H + h0 + min(col, G - 1)) * D;
@@ -1025,9 +1063,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   qmax = fmaxf(qmax, xor_shfl<32>(qmax));
   const float inv = qmax > 0.f ? 127.f / qmax : 0.f;
   const float qunit = qmax * (1.f / 127.f) * a.qscale * kInv254;  // per unit of 254 d1 + d2 + d3 / 254
+  // the zero points' share in the same units: -sum_{d in g} q_d / qunit
   float nqsum[NG];
 #pragma unroll
-  for (int c = 0; c < NG; ++c) nqsum[c] = -qsum[c];
+  for (int c = 0; c < NG; ++c) nqsum[c] = qunit > 0.f ? -qsum[c] / qunit : 0.f;
   long QA[NG][3];
 #pragma unroll
   for (int c = 0; c < NG; ++c) {
@@ -1065,14 +1104,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
   auto load_page = [&](Q4Slot& s, int pid) {
     s.ok = page_ok(pid);
     const int pc = s.ok ? pid : 0;
-    const uint8_t* kb = layer_base + (size_t)pc * page_stride + col * ROW + grp * 4;
+    const uint8_t* kb = layer_base + (size_t)pc * page_stride;  // wave-uniform
 #pragma unroll
     for (int c = 0; c < NG; ++c) {
-      s.k[c] = *reinterpret_cast<const uint32_t*>(kb + c * 16);
-      s.v[c] = *reinterpret_cast<const uint32_t*>(kb + kv_stride + c * 16);
+      s.k[c] = *reinterpret_cast<const uint32_t*>(kb + code_off + c * 16);
+      s.v[c] = *reinterpret_cast<const uint32_t*>(kb + kv_stride + code_off + c * 16);
     }
-    const size_t head = (((size_t)pc * a.L + a.layer) * 2 + sz_kv) * a.KH + kvh;
-    s.sz = *reinterpret_cast<const uint2*>(sz_base + head * SZH);
+    const uint8_t* sb = sz_base + ((size_t)pc * a.L + a.layer) * 2 * a.KH * SZH;  // the page's slices
+    s.sz = *reinterpret_cast<const uint2*>(sb);
   };
 
   // scales / zeros of this lane's tokens 4 grp .. + 3 of one staged page:
@@ -1090,6 +1129,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     v4h ks[4], kz[4];
     staged(u, 0, ks);
     staged(u, 1, kz);
+    // in units of qunit: sum_g s_g (q.n_g / qunit - z_g sum_{d in g} q_d / qunit)
     float tot[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NG; ++c) {
@@ -1100,22 +1140,27 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
       c3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(kop, QA[c][2], c3, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        // |254 c1 + c2| <= 255 * 127 * 15 * 32 < 2^24: exact as a float
-        const float d12 = (float)(c1[r] * 254 + c2[r]);
-        const float dot = fmaf((float)c3[r], kInv254, d12) * qunit;
+        // |c1| <= 15 * 127 * 32 fits 24 bits, and |254 c1 + c2| < 2^24 is
+        // exact as a float
+        const float d12 = (float)(__mul24(c1[r], 254) + c2[r]);
+        const float dot = fmaf((float)c3[r], kInv254, d12);
         tot[r] = fmaf((float)ks[r][c], fmaf((float)kz[r][c], nqsum[c], dot), tot[r]);
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = (s.ok && pi * kPS + grp * 4 + r < tok_end) ? tot[r] : -INFINITY;
+    for (int r = 0; r < 4; ++r) sc[r] = (s.ok && pi * kPS + grp * 4 + r < tok_end) ? tot[r] * qunit : -INFINITY;
   };
 
-  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page, exact.
-  auto v_block = [&](const Q4Slot& s, int blk, float* out4) {
-    v4i t = {0, 0, 0, 0};
-    t = __builtin_amdgcn_mfma_i32_16x16x32_i8(q4_operand(s.v[blk >> 1]), onehot[blk & 1], t, 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) out4[r] = (float)t[r];
+  // V^T of 16 dims (block blk) for this lane's 4 tokens of one page, as two
+  // dwords of fp16 pairs, exact: the product starts from 0x6400 (fp16 1024),
+  // so each 32-bit result holds 0x6400 + nibble, whose low half is the fp16
+  // value 1024 + nibble; 1024 is then subtracted (exact).
+  const v4i kF16Bias = {0x6400, 0x6400, 0x6400, 0x6400};
+  auto v_block = [&](const Q4Slot& s, int blk, uint32_t& d0, uint32_t& d1) {
+    const v4i t = __builtin_amdgcn_mfma_i32_16x16x32_i8(q4_operand(s.v[blk >> 1]), onehot[blk & 1], kF16Bias, 0, 0, 0);
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    d0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, low_halves(t[0], t[1])) - k1024);
+    d1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, low_halves(t[2], t[3])) - k1024);
   };
 
   auto process_pair = [&](const Q4Slot& s0, const Q4Slot& s1, int pi, bool has1) {
@@ -1166,23 +1211,24 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     }
     v8h Bh[NG], Bl[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g)
+    for (int g = 0; g < NG; ++g) {
+      float w[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float w = p[e] * (float)vs[e >> 2][e & 3][g];  // 0 for dead tokens (staged zero scale)
-        corr[g] = fmaf(w, (float)vz[e >> 2][e & 3][g], corr[g]);
-        const _Float16 hi = (_Float16)w;
-        Bh[g][e] = hi;
-        Bl[g][e] = (_Float16)(w - (float)hi);
+        w[e] = p[e] * (float)vs[e >> 2][e & 3][g];  // 0 for dead tokens (staged zero scale)
+        corr[g] = fmaf(w[e], (float)vz[e >> 2][e & 3][g], corr[g]);
       }
+      uint4 hw, lw;
+      split_hilo8(w, hw, lw);
+      Bh[g] = __builtin_bit_cast(v8h, hw);
+      Bl[g] = __builtin_bit_cast(v8h, lw);
+    }
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
-      float t[8];
-      v_block(s0, blk, t);
-      v_block(s1, blk, t + 4);
-      v8h A;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) A[e] = (_Float16)t[e];  // nibbles: exact
+      uint32_t a0, a1, a2, a3;
+      v_block(s0, blk, a0, a1);
+      v_block(s1, blk, a2, a3);
+      const v8h A = dwords_to_v8h(a0, a1, a2, a3);  // nibbles: exact
       acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bh[blk >> 1], acc[blk], 0, 0, 0);
       acc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bl[blk >> 1], acc[blk], 0, 0, 0);
     }
