@@ -217,6 +217,48 @@ def test_decode_q4_matches_oracle(H, KH, D):
     _assert_close(out.cpu(), ref, "q4")
 
 
+@pytest.mark.parametrize("v_mag", [1e-4, 1e5, "per-page"])
+def test_decode_q4_v_scale_independence(v_mag):
+    """Q4 V scales (fp16) at magnitudes from about 1e-6 to 1e4, and, "per-page",
+    with each page's V scales multiplied by its own 10^u, u ~ U[-4, 4]: the
+    output keeps the relative precision of V's codes, and scales above the
+    fp16 range of a plain weight (p * s up to 8 * 65504) do not overflow.
+    Bar: |gpu - oracle| <= 1e-3 * max|oracle| per sequence."""
+    _say(f"q4 V magnitude {v_mag}")
+    g = torch.Generator().manual_seed(31)
+    B, H, KH, D, PS, L = 3, 40, 8, 128, 16, 2
+    ctxs = [37, 1600, 333]
+    npages = [(c + PS - 1) // PS for c in ctxs]
+    P = sum(npages) + 2
+    packed = torch.randint(0, 256, (P, L, 2, KH, PS, D // 2), generator=g, dtype=torch.uint8)
+    sc = torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 0.1 + 0.01
+    zp = (torch.rand(P, L, 2, KH, PS, D // 32, generator=g) * 15).half()
+    if v_mag == "per-page":
+        mag = torch.pow(10.0, torch.rand(P, generator=g) * 8 - 4).reshape(P, 1, 1, 1, 1)
+    else:
+        mag = torch.tensor(float(v_mag))
+    sc[:, :, 1] = sc[:, :, 1] * mag
+    sc = sc.half()
+    assert torch.isfinite(sc).all()
+    perm = torch.randperm(P, generator=g)
+    table = torch.full((B, max(npages)), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    q = torch.randn(B, H, D, generator=g)
+    lens = torch.tensor(ctxs, dtype=torch.int32)
+    out = paged_attention_decode_q4(q.to(DEV), packed.to(DEV), sc.to(DEV), zp.to(DEV), table.to(DEV), lens.to(DEV), 1)
+    torch.cuda.synchronize()
+    ref = PD.paged_attention_decode_q4(q, packed, sc, zp, table, lens, 1)
+    out = out.cpu()
+    assert torch.isfinite(out).all()
+    for b in range(B):
+        err = (out[b] - ref[b]).abs().max().item()
+        bar = 1e-3 * ref[b].abs().max().item()
+        assert err <= bar, f"seq {b}: max abs err {err:.3e} > {bar:.3e}"
+
+
 def test_decode_full_size_int8_sampled_parity_and_relabel_invariance():
     """14B int8 at its full size (B=64, context 4096, 16384 pages): the output of
     a sample of sequences matches the oracle, and relabelling the physical pages

@@ -928,9 +928,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_float_kernel(Dec
 //                   cores: token col's nibbles move to lane (col, grp) as
 //                   tokens 4 grp .. + 3 of one dim, exactly.
 //   O^T += V^T P^T  v_mfma_f32_16x16x32_f16 per 16-dim block, the B operand of
-//                   the block's group g holding p s_g (hi + lo float16); the
-//                   zero points' share, sum_t p s_g z_g per (group, head), is
-//                   accumulated beside it and subtracted at the end.
+//                   the block's group g holding p s_g (hi + lo float16, with
+//                   the V-scale exponent of the int8 kernel, so that any fp16
+//                   V scale keeps its precision); the zero points' share,
+//                   sum_t p s_g z_g per (group, head), is accumulated beside it
+//                   and subtracted at the end.
 // Scales and zeros (4 x 128 bytes per page and head: K s, K z, V s, V z)
 // arrive as one 8-byte load per lane and pass through 1 KB of LDS per wave,
 // from which each lane reads the 4 tokens x 4 groups its rows need.
@@ -985,6 +987,16 @@ __device__ __forceinline__ void split_hilo8(const float (&w)[8], uint4& hi, uint
       : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
         "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
       : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));
+}
+
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+// fp16 bit pattern of 2^k, saturated to infinity above the fp16 range and
+// to 0 below its subnormals.
+__device__ __forceinline__ uint32_t f16_bits_of_pow2(int k) {
+  if (k > 15) return 0x7c00u;
+  if (k >= -14) return (uint32_t)(k + 15) << 10;
+  return k >= -24 ? 1u << (k + 24) : 0u;
 }
 
 // Low halves of two int32 (x, y) as one dword (x in bits 0-15).
@@ -1092,7 +1104,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     onehot[h] = (long)bits;
   }
 
-  float m_run = kNoMax;
+  float m_run = kNoMax;  // running maximum of this lane's head
+  int vexp = 0;              // V-scale exponent e (wave-uniform)
+  uint32_t vlimit_bits = 0;  // fp16 bits of 2^(e + kVScaleHeadroom), 0 until the first positive V scale sets e
+  float m_eff = kNoMax;      // m_run + e: the weights are 2^(s - m_eff) * vscale
   float l_run = 0.f;
   float corr[NG];  // this lane's share of sum_t p s_g z_g for its head, per group
   v4f acc[NB];
@@ -1170,11 +1185,48 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     // and the previous pair's reads came before these writes
     const bool live0 = s0.ok && pi * kPS + col < tok_end;
     const bool live1 = has1 && s1.ok && (pi + 1) * kPS + col < tok_end;
-    sz_lds[wave][0][lane] = live0 ? s0.sz : make_uint2(0u, 0u);
-    sz_lds[wave][1][lane] = live1 ? s1.sz : make_uint2(0u, 0u);
+    const uint2 z0 = live0 ? s0.sz : make_uint2(0u, 0u), z1 = live1 ? s1.sz : make_uint2(0u, 0u);
+    sz_lds[wave][0][lane] = z0;
+    sz_lds[wave][1][lane] = z1;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // The V scales of the pair (lanes grp 2 hold token col's four group
+    // scales of V): one at or above 2^(e + kVScaleHeadroom) raises e
+    // (wave-uniform), the first positive one sets it.  The test compares raw
+    // fp16 bits (ordered as the values for non-negative scales; a negative
+    // scale's sign bit only sends the pair to the exact path below).
+    uint32_t vb;
+    {
+      const v2u16 a = __builtin_elementwise_max(__builtin_bit_cast(v2u16, z0.x), __builtin_bit_cast(v2u16, z0.y));
+      const v2u16 c = __builtin_elementwise_max(__builtin_bit_cast(v2u16, z1.x), __builtin_bit_cast(v2u16, z1.y));
+      const v2u16 m = __builtin_elementwise_max(a, c);
+      vb = grp == 2 ? max((uint32_t)m[0], (uint32_t)m[1]) : 0u;
+    }
+    int e_new = vexp;
+    if (__builtin_amdgcn_ballot_w64(vb > vlimit_bits) != 0) {
+      float vm = 0.f;  // the largest magnitude, exactly
+      if (grp == 2) {
+        const uint32_t w[4] = {z0.x, z0.y, z1.x, z1.y};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v2h h = __builtin_bit_cast(v2h, w[i] & 0x7fff7fffu);
+          vm = fmaxf(vm, fmaxf((float)h[0], (float)h[1]));
+        }
+      }
+      float wm = fmaxf(vm, xor_shfl<1>(vm));
+      wm = fmaxf(wm, xor_shfl<2>(wm));
+      wm = fmaxf(wm, xor_shfl<4>(wm));
+      wm = fmaxf(wm, xor_shfl<8>(wm));
+      wm = fmaxf(wm, xor_shfl<16>(wm));
+      wm = fmaxf(wm, xor_shfl<32>(wm));
+      if (wm <= 65504.f) {  // finite: an inf scale keeps e (its tokens give inf / NaN as in the reference)
+        int ex;
+        (void)frexpf(wm, &ex);  // wm < 2^ex
+        e_new = max(ex, vlimit_bits > 0u ? vexp : ex);
+        vlimit_bits = f16_bits_of_pow2(e_new + kVScaleHeadroom);
+      }
+    }
     float sc[8];
     page_scores(s0, 0, pi, sc);
     if (has1) {
@@ -1188,15 +1240,20 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     for (int r = 1; r < 8; ++r) pm = fmaxf(pm, sc[r]);
     pm = fmaxf(pm, xor_shfl<16>(pm));
     pm = fmaxf(pm, xor_shfl<32>(pm));
-    if (pm > m_run + kLazyRescale) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - pm);
+    const bool up = pm > m_run + kLazyRescale;
+    if (up || e_new != vexp) {
+      const float m_new = up ? pm : m_run;
+      const float me_new = m_new + (float)e_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_eff - me_new);  // 0 while nothing has been accumulated
       l_run *= alpha;
 #pragma unroll
       for (int g = 0; g < NG; ++g) corr[g] *= alpha;
 #pragma unroll
       for (int blk = 0; blk < NB; ++blk) acc[blk] *= alpha;
-      m_run = pm;
+      m_run = m_new;
+      m_eff = me_new;
     }
+    vexp = e_new;
     v4h vs[2][4], vz[2][4];
     staged(0, 2, vs[0]);
     staged(0, 3, vz[0]);
@@ -1206,7 +1263,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
     float p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      p[e] = __builtin_amdgcn_exp2f(sc[e] - m_run);
+      p[e] = __builtin_amdgcn_exp2f(sc[e] - m_eff);
       l_run += p[e];
     }
     v8h Bh[NG], Bl[NG];
@@ -1272,7 +1329,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) decode_stream_q4_kernel(Decode
           make_float4(acc[blk][0] - z, acc[blk][1] - z, acc[blk][2] - z, acc[blk][3] - z);
     }
     if (grp == 0) {
-      ml_base[col * 2] = l_tot > 0.f ? m_run : -INFINITY;
+      ml_base[col * 2] = l_tot > 0.f ? m_eff : -INFINITY;  // l and acc are relative to 2^m_eff
       ml_base[col * 2 + 1] = l_tot;
     }
   }
