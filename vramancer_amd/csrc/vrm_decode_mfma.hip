@@ -109,6 +109,36 @@ __device__ __forceinline__ v8h dwords_to_v8h(uint32_t a, uint32_t b, uint32_t c,
   return __builtin_bit_cast(v8h, make_uint4(a, b, c, d));
 }
 
+// Eight floats w as the float16 pair hi = fp16(w), lo = fp16(w - hi) (the
+// residual exact, one rounding): a packed conversion per two values, one
+// mixed fused multiply-add per value, a packed conversion per two.  The
+// results are matrix-core operands, which may read a VGPR only two wait states
+// after a VALU write; the compiler cannot see the writes of an asm statement,
+// so the block ends with s_nop 1.
+__device__ __forceinline__ void split_hilo8(const float (&w)[8], uint4& hi, uint4& lo) {
+  float d[8];
+  asm("v_cvt_pk_f16_f32 %0, %16, %17\n\t"
+      "v_cvt_pk_f16_f32 %1, %18, %19\n\t"
+      "v_cvt_pk_f16_f32 %2, %20, %21\n\t"
+      "v_cvt_pk_f16_f32 %3, %22, %23\n\t"
+      "v_fma_mix_f32 %8, %0, -1.0, %16 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %9, %0, -1.0, %17 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %10, %1, -1.0, %18 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %11, %1, -1.0, %19 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %12, %2, -1.0, %20 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %13, %2, -1.0, %21 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %14, %3, -1.0, %22 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mix_f32 %15, %3, -1.0, %23 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_cvt_pk_f16_f32 %4, %8, %9\n\t"
+      "v_cvt_pk_f16_f32 %5, %10, %11\n\t"
+      "v_cvt_pk_f16_f32 %6, %12, %13\n\t"
+      "v_cvt_pk_f16_f32 %7, %14, %15\n\t"
+      "s_nop 1"
+      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
+        "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
+      : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));
+}
+
 // Three signed 8-bit digits of u in [-127, 127]: u ~= d1 + d2/254 + d3/254^2.
 __device__ __forceinline__ void digits3(float u, int& d1, int& d2, int& d3) {
   const float f1 = rintf(u);
@@ -557,24 +587,17 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     }
     vexp = e_new;
     // B operand: k = 8 grp + e <-> token 4 grp + e % 4 of page pi + e / 4.
-    uint32_t bh[4], bl[4];
+    float w[8];
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      float w[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int r = 2 * e2 + u;
-        const float p = __builtin_amdgcn_exp2f(sc[r] - m_eff);
-        l_run += p;
-        w[u] = p * (KIND == K_I8 ? vs[r] : vs[r & 4]);
-      }
-      const v2h h = {(_Float16)w[0], (_Float16)w[1]};
-      const v2h l = {(_Float16)(w[0] - (float)h[0]), (_Float16)(w[1] - (float)h[1])};
-      bh[e2] = __builtin_bit_cast(uint32_t, h);
-      bl[e2] = __builtin_bit_cast(uint32_t, l);
+    for (int r = 0; r < 8; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[r] - m_eff);
+      l_run += p;
+      w[r] = p * (KIND == K_I8 ? vs[r] : vs[r & 4]);
     }
-    const v8h Bh = dwords_to_v8h(bh[0], bh[1], bh[2], bh[3]);
-    const v8h Bl = dwords_to_v8h(bl[0], bl[1], bl[2], bl[3]);
+    uint4 bh, bl;
+    split_hilo8(w, bh, bl);
+    const v8h Bh = __builtin_bit_cast(v8h, bh);
+    const v8h Bl = __builtin_bit_cast(v8h, bl);
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       const uint32_t w0 = dword(v0[blk / 4], blk % 4);
@@ -958,36 +981,6 @@ __device__ __forceinline__ constexpr int q4_dim_of(int e) { return e < 4 ? 2 * e
 __device__ __forceinline__ constexpr int q4_elem_of(int o) { return (o & 1) ? 4 + (o >> 1) : (o >> 1); }
 
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-
-// Eight floats w as the float16 pair hi = fp16(w), lo = fp16(w - hi) (the
-// residual exact, one rounding): a packed conversion per two values, one
-// mixed fused multiply-add per value, a packed conversion per two.  The
-// results are matrix-core operands, which may read a VGPR only two wait states
-// after a VALU write; the compiler cannot see the writes of an asm statement,
-// so the block ends with s_nop 1.
-__device__ __forceinline__ void split_hilo8(const float (&w)[8], uint4& hi, uint4& lo) {
-  float d[8];
-  asm("v_cvt_pk_f16_f32 %0, %16, %17\n\t"
-      "v_cvt_pk_f16_f32 %1, %18, %19\n\t"
-      "v_cvt_pk_f16_f32 %2, %20, %21\n\t"
-      "v_cvt_pk_f16_f32 %3, %22, %23\n\t"
-      "v_fma_mix_f32 %8, %0, -1.0, %16 op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %9, %0, -1.0, %17 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %10, %1, -1.0, %18 op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %11, %1, -1.0, %19 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %12, %2, -1.0, %20 op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %13, %2, -1.0, %21 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %14, %3, -1.0, %22 op_sel_hi:[1,0,0]\n\t"
-      "v_fma_mix_f32 %15, %3, -1.0, %23 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-      "v_cvt_pk_f16_f32 %4, %8, %9\n\t"
-      "v_cvt_pk_f16_f32 %5, %10, %11\n\t"
-      "v_cvt_pk_f16_f32 %6, %12, %13\n\t"
-      "v_cvt_pk_f16_f32 %7, %14, %15\n\t"
-      "s_nop 1"
-      : "=&v"(hi.x), "=&v"(hi.y), "=&v"(hi.z), "=&v"(hi.w), "=&v"(lo.x), "=&v"(lo.y), "=&v"(lo.z), "=&v"(lo.w),
-        "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]), "=&v"(d[6]), "=&v"(d[7])
-      : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]));
-}
 
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
