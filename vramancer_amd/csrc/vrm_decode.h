@@ -204,11 +204,11 @@ hipError_t launch_generic(const DecodeArgs& a, int kind, int B, int D, int PS, h
 // K_F16, D the head dimension, G the query heads per wavefront (<= 16).
 hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
-// Balanced mode geometry: workgroups of kUnitsPerWg units x (1, 2 or 4)
+// Balanced mode geometry: workgroups of kUnitsPerWg units x (1, 2, 4 or 6)
 // wavefronts per unit.  LDS: the sequence's page ids [max_pp], the units'
 // page-pair counters [kUnitsPerWg], then (16-byte aligned) the merge area,
 // [W][G][D] accumulators and [W][G][2] (m, l); at most kMaxBalancedLds.
-constexpr int kMaxBalancedWaves = 8;
+constexpr int kMaxBalancedWaves = 12;
 constexpr int kUnitsPerWg = 2;
 constexpr size_t kMaxBalancedLds = 64 * 1024;
 __host__ __device__ inline size_t balanced_merge_offset(int max_pp) {

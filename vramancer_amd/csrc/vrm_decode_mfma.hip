@@ -366,8 +366,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     }
   };
 
-  // balanced mode: take the first two page pairs and issue their loads before
-  // the query set-up, so that the set-up runs under their latency
+  // balanced mode: take the first page pair and issue its loads before the
+  // query set-up, so that the set-up runs under their latency
   const int npairs = (n_pages + 1) / 2;
   int* const pair_next = BALANCED ? pair_ctr + wave % kUnitsPerWg : nullptr;
   auto grab = [&]() {
@@ -381,15 +381,13 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     load_page(s0, ids_lds[pg]);
     load_page(s1, ids_lds[min(pg + 1, n_pages - 1)]);
   };
-  PageSlot<D> bring[BALANCED ? 4 : 1];
-  int c0 = 0, c1 = 0;
+  PageSlot<D> bring[BALANCED ? 2 : 1];
+  int c0 = 0;
   const bool bstream = BALANCED && unit_ok && npairs > 0;
   if constexpr (BALANCED) {
     if (bstream) {
       c0 = grab();
-      c1 = grab();
       load_pair(bring[0], bring[1], c0);
-      load_pair(bring[2], bring[3], c1);
     }
   }
 
@@ -619,19 +617,17 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // ---------------- stream the partition ----------------
   if constexpr (BALANCED) {
     // Page pairs taken from the unit's LDS counter (in increasing order per
-    // wave), two pairs in the ring: while one pair is consumed the other is
-    // in flight.  Loads past the last pair reload it (clamped, unconditional).
+    // wave), one pair in registers: its refill is issued once it has been
+    // consumed, and the other wavefronts of the SIMD (three per SIMD) keep
+    // the memory busy meanwhile.  Fewer bytes in flight than two pairs per
+    // wavefront at two per SIMD, and the pool's reads run faster for it.
+    // Loads past the last pair reload it (clamped, unconditional).
     if (bstream) {
       while (c0 < npairs) {
         const int n0 = grab();
         process_pair(bring[0], bring[1], 2 * c0, 2 * c0 + 1 < n_pages);
         load_pair(bring[0], bring[1], n0);
         c0 = n0;
-        if (c1 >= npairs) break;  // then c0 > c1 is past the end too
-        const int n1 = grab();
-        process_pair(bring[2], bring[3], 2 * c1, 2 * c1 + 1 < n_pages);
-        load_pair(bring[2], bring[3], n1);
-        c1 = n1;
       }
     }
   } else if (n_pages > 0) {
@@ -1366,7 +1362,7 @@ hipError_t launch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
 }
 
 // Balanced mode: workgroups of kUnitsPerWg units x WPU wavefronts per unit,
-// WPU the largest of 4, 2, 1 whose launch fits one resident round of waves
+// WPU the largest of 6, 4, 2, 1 whose launch fits one resident round of waves
 // and 64 KB of LDS.  Returns hipErrorInvalidValue when even WPU = 1 does not
 // fit (page tables too wide for the LDS copy of the ids).
 template <int KIND, int D, bool LOADS>
@@ -1376,7 +1372,7 @@ hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) 
   // the launch shape of the decode itself, for both builds
   const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false>);
   const int resident = items_target(fn, kMaxBalancedWaves, 0, 1);  // resident waves (capped)
-  for (int wpu = 4; wpu >= 1; wpu /= 2) {
+  for (int wpu = 6; wpu >= 1; wpu = wpu == 6 ? 4 : wpu / 2) {
     const int W = kUnitsPerWg * wpu;
     const size_t lds = balanced_lds_bytes(a.max_pp, W, G, D);
     if (lds > kMaxBalancedLds) continue;
