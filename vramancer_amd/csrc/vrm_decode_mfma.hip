@@ -329,42 +329,50 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // Loads are issued unconditionally from a clamped, always valid address and
   // zeroed afterwards for an absent page, so every slot keeps the same loads
   // in flight (a branch around a load makes the compiler wait for all of them).
-  auto load_page = [&](PageSlot<D>& s, int vpid) {
+  // A slot's K half (codes, scales and the page's ok flag) and V half load
+  // separately: the balanced mode refills K as soon as a pair's scores are
+  // taken and V once its PV product is done.
+  auto load_page_part = [&](PageSlot<D>& s, int vpid, bool kpart, bool vpart) {
     const bool ok = page_ok(vpid);
-    s.ok = ok;
     const int pc = (ok ? vpid : 0) >> vshift;  // page
     const int sub = (ok ? vpid : 0) & vmask;   // its 16-token block
     // K rows and the 4-token V tiles of a block are 16 D bytes past the previous block's
     const uint8_t* pb = layer_base + (size_t)pc * page_stride + sub * (kPS * D);
     const uint8_t* kb = pb + col * D + grp * 16;
     const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
+    if (kpart) s.ok = ok;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       if (KPART == 64 || j < NJ - 1) {
-        s.k[j] = ld16(kb + j * 64);
-        s.v[j] = (D / 4) % 16 == 0 ? ld16(vb + j * 16) : ld16_a4(vb + j * 16);  // V rows of D / 4 bytes
+        if (kpart) s.k[j] = ld16(kb + j * 64);
+        if (vpart) s.v[j] = (D / 4) % 16 == 0 ? ld16(vb + j * 16) : ld16_a4(vb + j * 16);  // V rows of D / 4 bytes
       } else {
-        const bool kin = grp < KPART / 16;
-        const uint4 kk = ld16(kin ? kb + j * 64 : kb);  // clamped into the row, then dropped
-        s.k[j] = kin ? kk : make_uint4(0u, 0u, 0u, 0u);
-        const uint32_t* vw = reinterpret_cast<const uint32_t*>(vb + j * 16);
-        s.v[j] = make_uint4(vw[0], KPART >= 32 ? vw[1] : 0u, KPART >= 48 ? vw[2] : 0u, 0u);
+        if (kpart) {
+          const bool kin = grp < KPART / 16;
+          const uint4 kk = ld16(kin ? kb + j * 64 : kb);  // clamped into the row, then dropped
+          s.k[j] = kin ? kk : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (vpart) {
+          const uint32_t* vw = reinterpret_cast<const uint32_t*>(vb + j * 16);
+          s.v[j] = make_uint4(vw[0], KPART >= 32 ? vw[1] : 0u, KPART >= 48 ? vw[2] : 0u, 0u);
+        }
       }
     }
     if constexpr (KIND == K_I8) {
       const size_t ts = head_index(pc, 0) * (kPS << vshift) + sub * kPS + grp * 4;
-      s.ks = ldf4(a.scales + ts);
-      s.vs = ldf4(a.scales + ts + (size_t)a.KH * (kPS << vshift));
+      if (kpart) s.ks = ldf4(a.scales + ts);
+      if (vpart) s.vs = ldf4(a.scales + ts + (size_t)a.KH * (kPS << vshift));
     } else {
-      s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
-      s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
+      if (kpart) s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
+      if (vpart) s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
     }
-    if (!ok) {
+    if (vpart && !ok) {
       s.vs = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) s.v[j] = make_uint4(0, 0, 0, 0);
     }
   };
+  auto load_page = [&](PageSlot<D>& s, int vpid) { load_page_part(s, vpid, true, true); };
 
   // balanced mode: take the first page pair and issue its loads before the
   // query set-up, so that the set-up runs under their latency
@@ -376,10 +384,10 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       if (lane == 0) v = __hip_atomic_fetch_add(pair_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  auto load_pair = [&](PageSlot<D>& s0, PageSlot<D>& s1, int p) {
+  auto load_pair = [&](PageSlot<D>& s0, PageSlot<D>& s1, int p, bool kpart = true, bool vpart = true) {
     const int pg = 2 * min(p, npairs - 1);
-    load_page(s0, ids_lds[pg]);
-    load_page(s1, ids_lds[min(pg + 1, n_pages - 1)]);
+    load_page_part(s0, ids_lds[pg], kpart, vpart);
+    load_page_part(s1, ids_lds[min(pg + 1, n_pages - 1)], kpart, vpart);
   };
   PageSlot<D> bring[BALANCED ? 2 : 1];
   int c0 = 0;
@@ -492,14 +500,19 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
 
   // Pages pi and pi + 1 (the second may lie past the partition).
   uint32_t probe = 0;  // LOADS: checksum of the loaded words
-  auto process_pair = [&](const PageSlot<D>& s0, const PageSlot<D>& s1, int pi, bool has1) {
+  // after_scores runs once the pair's K half is dead (the balanced mode
+  // refills it there).
+  auto process_pair = [&](const PageSlot<D>& s0, const PageSlot<D>& s1, int pi, bool has1, auto&& after_scores) {
     if constexpr (LOADS) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-        probe ^= s0.k[j].x ^ s0.k[j].y ^ s0.k[j].z ^ s0.k[j].w ^ s0.v[j].x ^ s0.v[j].y ^ s0.v[j].z ^ s0.v[j].w ^
-                 s1.k[j].x ^ s1.k[j].y ^ s1.k[j].z ^ s1.k[j].w ^ s1.v[j].x ^ s1.v[j].y ^ s1.v[j].z ^ s1.v[j].w;
-      probe ^= __float_as_uint(s0.ks.x + s0.ks.y + s0.ks.z + s0.ks.w + s0.vs.x + s0.vs.y + s0.vs.z + s0.vs.w +
-                               s1.ks.x + s1.ks.y + s1.ks.z + s1.ks.w + s1.vs.x + s1.vs.y + s1.vs.z + s1.vs.w);
+        probe ^= s0.k[j].x ^ s0.k[j].y ^ s0.k[j].z ^ s0.k[j].w ^ s1.k[j].x ^ s1.k[j].y ^ s1.k[j].z ^ s1.k[j].w;
+      probe ^= __float_as_uint(s0.ks.x + s0.ks.y + s0.ks.z + s0.ks.w + s1.ks.x + s1.ks.y + s1.ks.z + s1.ks.w);
+      after_scores();
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        probe ^= s0.v[j].x ^ s0.v[j].y ^ s0.v[j].z ^ s0.v[j].w ^ s1.v[j].x ^ s1.v[j].y ^ s1.v[j].z ^ s1.v[j].w;
+      probe ^= __float_as_uint(s0.vs.x + s0.vs.y + s0.vs.z + s0.vs.w + s1.vs.x + s1.vs.y + s1.vs.z + s1.vs.w);
       (void)pi;
       (void)has1;
       return;
@@ -512,6 +525,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[4 + r] = -INFINITY;
     }
+    after_scores();
     // V scales of the pair's tokens (int8: token 4 grp + r % 4 of page
     // pi + r / 4; fp8: vs[0] and vs[4] are the two pages' scales) and V codes.
     float vs[8];
@@ -625,8 +639,9 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     if (bstream) {
       while (c0 < npairs) {
         const int n0 = grab();
-        process_pair(bring[0], bring[1], 2 * c0, 2 * c0 + 1 < n_pages);
-        load_pair(bring[0], bring[1], n0);
+        process_pair(bring[0], bring[1], 2 * c0, 2 * c0 + 1 < n_pages,
+                     [&] { load_pair(bring[0], bring[1], n0, true, false); });
+        load_pair(bring[0], bring[1], n0, false, true);
         c0 = n0;
       }
     }
@@ -643,7 +658,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       const int ids_ahead = ids_at(base + 2 * RING);
 #pragma unroll
       for (int u = 0; u < RING; u += 2) {
-        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages);
+        if (base + u < n_pages) process_pair(ring[u], ring[u + 1], base + u, base + u + 1 < n_pages, [] {});
         load_page(ring[u], __builtin_amdgcn_readlane(ids_next, u));
         load_page(ring[u + 1], __builtin_amdgcn_readlane(ids_next, u + 1));
       }
