@@ -596,7 +596,7 @@ def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
 @pytest.mark.parametrize("H,KH,D,ctxs", [
     (40, 8, 128, [37, 1600, 333, 0, 1, 4096]),   # ragged: correct for any lengths
     (64, 8, 128, [512] * 20),                    # even
-    (16, 1, 128, [3000, 2999, 17]),              # one kv-head, 8 waves per workgroup
+    (16, 1, 128, [3000, 2999, 17]),              # one kv-head, 16 heads per wave: 4-wave workgroups fit the LDS
     (8, 2, 64, [100, 260]),
     (12, 12, 64, [64, 65, 700]),
     (28, 4, 128, [8192, 8000, 1]),               # 512 pages in LDS
