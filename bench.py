@@ -3,11 +3,14 @@
 Workload (the configuration the headline metric is quoted on): Qwen2.5-14B-
 shaped decode attention, 64 sequences x 4096 tokens of context, 40 query heads
 over 8 KV heads, head_dim 128, page 16, in a 48-layer pool of 16384 pages
-(25.8 GB of int8 codes + per-token fp32 scales).  K/V are bf16 N(0, 1) with 2
+(25.8 GB of int8 codes + per-token fp32 scales, kept side by side per kv-head
+in 33 KB (page, layer) slabs: the library's inline layout).  K/V are bf16 N(0, 1) with 2
 of 128 channels per head scaled by 20, quantized to int8 with one scale per
 (token, head).  One step = one layer-step: every sequence attends once for one
 new query token over one layer.  Steps rotate over 4 filled layers so that the
-working set (4 x 556 MB) does not fit the 256 MB Infinity Cache.
+working set (4 x 556 MB) does not fit the 256 MB Infinity Cache.  After the
+warm-up the decode keeps running untimed for --settle seconds, so that the
+timed region starts on quiet HBM (see settle()).
 
 Prints one JSON line.  value = microseconds per layer-step (lower is better);
 the line also carries the achieved HBM bandwidth on algorithmic bytes, the
@@ -76,6 +79,23 @@ def time_events(fn, steps):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) * 1e3 / steps  # microseconds per call
+
+
+def settle(fn, seconds):
+    """Runs fn untimed for about `seconds` (synchronising every 50 calls) and
+    returns (calls, elapsed seconds).  The timed region starts once the HBM is
+    quiet: the kernel driver clears the memory an earlier process freed in the
+    background, which on MI355X slows this decode's reads by about 4 % for
+    about a second after a 30 GB pool is freed (the driver's round runs the
+    GPU tests, each with such pools, just before the benchmark)."""
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            fn(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n, time.perf_counter() - t0
 
 
 def host_us(fn, n):
@@ -482,6 +502,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--settle", type=float, default=2.0,
+                    help="seconds of further untimed decode steps after the warm-up, so that the timed region "
+                         "starts on quiet HBM (0: none)")
     ap.add_argument("--cpu-seqs", type=int, default=32, help="sequences in the CPU-baseline sample")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
@@ -555,6 +578,8 @@ def main():
     nsplit = lib.vrm_paged_decode_num_splits(B, H, KH, max_pp, PS)
     stream = _lib.stream_of(q)
     code = KV_CODE.get(cfg.codec)
+    if cfg.codec in ("int8", "fp8"):
+        code = kv_quant.abi_dtype_code(pool, sc)  # the pool's layout (inline, as allocate_pool makes it)
     sc_ptr = sc.data_ptr() if sc is not None else None
     lens_list = lens.tolist()
     ab = workloads.algorithmic_bytes(cfg, lens_list)
@@ -607,6 +632,8 @@ def main():
     for i in range(args.warmup):
         full(i)
     torch.cuda.synchronize()
+    settled = settle(full, args.settle)
+    log(f"settle: {settled[0]} more untimed layer-steps over {settled[1]:.2f} s")
     if balanced:
         pps, n_items = None, None
     else:
@@ -729,12 +756,13 @@ def main():
             "tq4": "tq4-polar", "q4": "u4-asym"}[cfg.codec]
     desc = {
         "14b-int8": ("14b-int8 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, "
-                     "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales"),
+                     "48-layer pool of 16384 pages, int8 codes + per-token fp32 scales in the inline slab layout"),
         "14b-q4": ("14b-q4 paged decode: B=64, H=40, KH=8, D=128, context 4096, page 16, 48-layer pool of "
                    "16384 pages, 4-bit asymmetric codes + per-32-dim-group fp16 scale and zero"),
         "7b-bf16": "7b-bf16 paged decode: B=32, H=28, KH=4, D=128, context ~U[1024, 8192], page 16, bf16 pool",
         "mixed-fp8": ("mixed-fp8 paged decode: 128 sequences lognormal(median 2048, sigma 1) + one of 131072, "
-                      "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales"),
+                      "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales in the inline slab "
+                      "layout"),
         "fp32-plumbing": "fp32-plumbing paged decode: B=4, H=KH=12, D=64, context 512, page 16, fp32 pool",
         "14b-turbo3": ("14b-turbo3 paged decode over TurboQuant pages: B=16, H=40, KH=8, D=128, context 32768, "
                        "page 16, 3 bits per angle, Student-t(3) K/V"),
@@ -797,6 +825,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"steps": settled[0], "seconds": round(settled[1], 2)},
         "ms_per_step": round(us_step / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define VRM_ABI_VERSION 1
+#define VRM_ABI_VERSION 2
 
 /* Status codes (negative: rejected on the host, nothing was launched). */
 #define VRM_OK 0
@@ -47,8 +47,35 @@ typedef enum vrm_kv_dtype {
   VRM_KV_F16 = 1,      /* float16 pool                                        */
   VRM_KV_BF16 = 2,     /* bfloat16 pool                                       */
   VRM_KV_I8 = 3,       /* int8 codes, float32 scale per (page,layer,kv,head,token) */
-  VRM_KV_FP8E4M3 = 4   /* OCP e4m3fn codes, float32 scale per (page,layer,kv,head) */
+  VRM_KV_FP8E4M3 = 4,  /* OCP e4m3fn codes, float32 scale per (page,layer,kv,head) */
+  VRM_KV_I8_INLINE = 5,      /* VRM_KV_I8 codes and scales in the inline slab layout */
+  VRM_KV_FP8E4M3_INLINE = 6  /* VRM_KV_FP8E4M3 codes and scales in the inline slab layout */
 } vrm_kv_dtype;
+
+/*
+ * Inline slab layout of the int8 / fp8 pools (VRM_KV_*_INLINE).  The codes
+ * and scales of one (page, layer) share one slab of vrm_kv_slab_bytes() bytes,
+ * and the slab holds, for each kv-head h in turn, a record of
+ *      K codes [PS][D] | V codes [PS][D] (tiled as above)
+ *      | int8: K scales [PS], V scales [PS] float32
+ *      | fp8:  K scale, V scale float32, 8 zero bytes
+ * (PS (2 D + 8) bytes for int8, 2 PS D + 16 for fp8).  Element (p, l, kv, h,
+ * t, d) of the logical kv_pool[P][L][2][KH][PS][D] is then at byte
+ * (p L + l) slab + h record + kv PS D + (its place in the slice), and the
+ * logical kv_scales[P][L][2][KH]([PS]) are float32s at the same slab and
+ * record offsets from kv_scales = (char *)kv_pool + 2 PS D.  Every entry
+ * that takes a pool takes these dtypes with kv_scales at exactly that
+ * address (anything else is VRM_ERR_ARG).  No counterpart in the reference
+ * (whose pools are float only): a page of one layer is then one contiguous
+ * run per kv-head, and the slab is not a power-of-two multiple of 32 KB at
+ * the shapes of the tuned kernels, which HBM reads faster when pages are
+ * scattered over the pool.
+ */
+
+/* Bytes of one (page, layer) slab of a pool of kv_dtype: 2 KH PS D times the
+ * element size for the plain layouts (codes only: their scales live in
+ * kv_scales), KH records for the inline layouts; 0 for a bad argument. */
+size_t vrm_kv_slab_bytes(int kv_dtype, int KH, int PS, int D);
 
 /* Element type of new K/V rows handed to the quantizers. */
 typedef enum vrm_src_dtype {

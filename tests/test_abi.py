@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.vrm_abi_version() == _lib.VRM_ABI_VERSION == 1
+    assert lib.vrm_abi_version() == _lib.VRM_ABI_VERSION == 2
 
 
 def _header_bytes(B):
@@ -53,6 +53,11 @@ def test_split_geometry_is_host_only(lib):
     assert lib.vrm_paged_decode_num_splits(1, 3, 2, 4, 16) == 0  # H % KH != 0
 
 
+# a fake scale pointer far from the fake pool pointers (a plain pool's scales
+# must not start inside its codes)
+SC = 1 << 40
+
+
 def _decode(lib, **kw):
     a = dict(q=1, pool=1, sc=None, pt=1, cl=1, out=1, ws=1, wsb=1 << 30, B=2, H=8, KH=2, D=128, PS=16, L=1, P=4,
              max_pp=2, layer=0, scale=0.1, dt=_lib.VRM_KV_BF16)
@@ -67,8 +72,8 @@ def test_decode_rejects_bad_arguments(lib):
     assert _decode(lib, H=7) == -1 and b"multiple" in lib.vrm_last_error()
     assert _decode(lib, layer=1) == -1 and b"layer_idx" in lib.vrm_last_error()
     assert _decode(lib, D=257) == -2 and b"head_dim" in lib.vrm_last_error()
-    assert _decode(lib, D=100, dt=_lib.VRM_KV_I8, sc=1) == -2 and b"head_dim" in lib.vrm_last_error()
-    assert _decode(lib, PS=6, dt=_lib.VRM_KV_FP8E4M3, sc=1) == -2 and b"page_size" in lib.vrm_last_error()
+    assert _decode(lib, D=100, dt=_lib.VRM_KV_I8, sc=SC) == -2 and b"head_dim" in lib.vrm_last_error()
+    assert _decode(lib, PS=6, dt=_lib.VRM_KV_FP8E4M3, sc=SC) == -2 and b"page_size" in lib.vrm_last_error()
     assert _decode(lib, dt=99) == -1 and b"kv_dtype" in lib.vrm_last_error()
     assert _decode(lib, dt=_lib.VRM_KV_I8) == -1 and b"kv_scales" in lib.vrm_last_error()
     assert _decode(lib, sc=1) == -1 and b"float pool" in lib.vrm_last_error()
@@ -76,9 +81,53 @@ def test_decode_rejects_bad_arguments(lib):
     assert _decode(lib, scale=float("nan")) == -1
 
 
+def test_kv_slab_bytes(lib):
+    """Bytes per (page, layer): plain layouts 2 KH PS D elements (codes only),
+    inline records of PS (2 D + 8) bytes (int8) or 2 PS D + 16 (fp8) per kv-head."""
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8, 8, 16, 128) == 32768
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_FP8E4M3, 8, 16, 128) == 32768
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 8, 16, 128) == 8 * (16 * 256 + 128) == 33792
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_FP8E4M3_INLINE, 8, 16, 128) == 8 * (4096 + 16)
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 3, 8, 48) == 3 * 8 * (96 + 8)
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_BF16, 4, 16, 128) == 2 * 4 * 16 * 128 * 2
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_F32, 12, 16, 64) == 2 * 12 * 16 * 64 * 4
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 8, 6, 128) == 0   # page size not a multiple of 4
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 8, 16, 100) == 0  # head_dim not a multiple of 16
+    assert lib.vrm_kv_slab_bytes(99, 8, 16, 128) == 0
+
+
+def test_inline_pool_scale_pointer_checks(lib):
+    """An inline pool's kv_scales must be kv_pool + 2 PS D; a plain pool's may
+    not start inside its codes (an inline buffer passed with the plain dtype).
+    Both are refused on the host by the decode, balanced, quantizer and
+    dequantizer entries."""
+    pool = 1 << 20
+    inl = pool + 2 * 16 * 128
+    # accepted pointers: the call goes on to the workspace check
+    assert _decode(lib, pool=pool, sc=inl, dt=_lib.VRM_KV_I8_INLINE, wsb=16) == -3
+    assert _decode(lib, pool=pool, sc=inl, dt=_lib.VRM_KV_FP8E4M3_INLINE, wsb=16) == -3
+    assert _decode(lib, pool=pool, sc=inl + 4, dt=_lib.VRM_KV_I8_INLINE) == -1 and b"inline" in lib.vrm_last_error()
+    assert _decode(lib, pool=pool, sc=inl, dt=_lib.VRM_KV_I8) == -1 and b"inside" in lib.vrm_last_error()
+    assert _decode(lib, pool=pool, sc=inl, dt=_lib.VRM_KV_FP8E4M3) == -1 and b"inside" in lib.vrm_last_error()
+    bal = lib.vrm_paged_decode_balanced
+    args = [1, pool, inl, 1, 1, 1, None, 2, 8, 2, 128, 16, 1, 4, 2, 0, 0.1, _lib.VRM_KV_I8, None]
+    assert bal(*args) == -1 and b"inside" in lib.vrm_last_error()
+    args[2] = inl + 16
+    args[17] = _lib.VRM_KV_I8_INLINE
+    assert bal(*args) == -1 and b"inline" in lib.vrm_last_error()
+    q = lib.vrm_kv_quant_append
+    assert q(1, 1, _lib.VRM_SRC_BF16, 1, 1, 4, pool, inl, _lib.VRM_KV_I8, 2, 128, 16, 1, 4, 0, None) == -1
+    assert b"inside" in lib.vrm_last_error()
+    assert q(1, 1, _lib.VRM_SRC_BF16, 1, 1, 0, pool, inl, _lib.VRM_KV_I8_INLINE, 2, 128, 16, 1, 4, 0, None) == 0
+    assert q(1, 1, _lib.VRM_SRC_BF16, 1, 1, 0, pool, SC, _lib.VRM_KV_I8_INLINE, 2, 128, 16, 1, 4, 0, None) == -1
+    dq = lib.vrm_kv_dequant_pages
+    assert dq(pool, inl, _lib.VRM_KV_FP8E4M3, 1, 0, 1, 2, 128, 16, 1, 4, 0, None) == -1
+    assert dq(pool, inl, _lib.VRM_KV_FP8E4M3_INLINE, 1, 0, 1, 2, 128, 16, 1, 4, 0, None) == 0
+
+
 def test_quant_rejects_bad_arguments(lib):
     f = lib.vrm_kv_quant_append
-    ok = dict(k=1, v=1, src=_lib.VRM_SRC_BF16, pid=1, sl=1, N=4, pool=1, sc=1, dt=_lib.VRM_KV_I8, KH=8, D=128, PS=16,
+    ok = dict(k=1, v=1, src=_lib.VRM_SRC_BF16, pid=1, sl=1, N=4, pool=1, sc=SC, dt=_lib.VRM_KV_I8, KH=8, D=128, PS=16,
               L=2, P=10, layer=0)
 
     def call(**kw):
@@ -253,7 +302,7 @@ def test_balanced_decode_selection_rule():
 
 def test_balanced_entry_rejects_bad_arguments(lib):
     f = lib.vrm_paged_decode_balanced
-    args = [1, 1, 1, 1, 1, 1, None, 2, 8, 2, 128, 16, 1, 4, 2, 0, 0.1, _lib.VRM_KV_I8, None]
+    args = [1, 1, SC, 1, 1, 1, None, 2, 8, 2, 128, 16, 1, 4, 2, 0, 0.1, _lib.VRM_KV_I8, None]
 
     def call(i, v):
         a = list(args)

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import paged_decode as PD
-from vramancer_amd import _lib, workloads
+from vramancer_amd import _lib, kv_quant, workloads
 from vramancer_amd.paged_attention_cuda import paged_attention_decode, paged_attention_decode_q4
 
 pytestmark = pytest.mark.gpu
@@ -585,7 +585,7 @@ def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
     scale = 1 / math.sqrt(D) if scale is None else scale
     rc = lib.vrm_paged_decode_balanced(q.data_ptr(), pool.data_ptr(), sc.data_ptr(), table.data_ptr(),
                                        lens.data_ptr(), out.data_ptr(), _lib.ptr(lse), B, H, KH, D, PS, L, P,
-                                       table.shape[1], layer, scale, _lib.kv_dtype_code(pool.dtype),
+                                       table.shape[1], layer, scale, kv_quant.abi_dtype_code(pool, sc),
                                        _lib.stream_of(q))
     _lib.check(rc, "vrm_paged_decode_balanced")
     torch.cuda.synchronize()
@@ -645,6 +645,58 @@ def test_balanced_decode_garbage_absent_pages_and_lse(dtype):
         _assert_close(out[b].cpu(), PD.dense_attention(q[b], K, V, 1 / math.sqrt(128)), f"seq {b}")
     torch.testing.assert_close(lse, lse_ref, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(out, ref_items, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+@pytest.mark.parametrize("D,PS", [(128, 16), (64, 16), (96, 16), (128, 32), (256, 16), (48, 8), (80, 4)])
+def test_inline_layout_decodes_like_the_plain_layout(dtype, D, PS):
+    """The same codes and scales copied into the inline layout give
+    bit-identical outputs and lse through the decode paths that read the
+    pool: the work-item stream kernels (pages of 16 and 32 tokens), the
+    generic kernel (other head_dims and pages) and the no-allocation entry;
+    the balanced decode (head_dim <= 128, page 16) within 1e-5; and they
+    match the oracle."""
+    _say(f"inline vs plain {dtype} D{D} PS{PS}")
+    codec = "int8" if dtype == torch.int8 else "fp8"
+    ctxs = [300, 17, 1000, 0, 129, 64]
+    B, H, KH = len(ctxs), 16, 2
+    q, pool, sc, table, lens = _pool_case(dtype, B, H, KH, D, ctxs, seed=D + PS, PS=PS)
+    P, L = pool.shape[:2]
+    ip, isc = kv_quant.allocate_pool(P, L, KH, D, codec, PS, DEV)
+    ip.copy_(pool.to(DEV))
+    isc.copy_(sc.to(DEV))
+    assert kv_quant.pool_layout(ip, isc) == "inline"
+    d = [t.to(DEV) for t in (q, pool, sc, table, lens)]
+    lib = _lib.load()
+    scale = 1 / math.sqrt(D)
+    outs = {}
+    for name, (pp, ss) in (("plain", (d[1], d[2])), ("inline", (ip, isc))):
+        lse = torch.empty(B, H, device=DEV)
+        got = [paged_attention_decode(d[0], pp, d[3], d[4], 1, kv_scales=ss, lse=lse), lse]
+        na = torch.full((B, H, D), float("nan"), device=DEV)
+        ns = lib.vrm_paged_decode_num_splits(B, H, KH, d[3].shape[1], PS)
+        if lib.vrm_paged_decode_workspace_bytes(B, H, D, ns) <= _lib.NOALLOC_SCRATCH_BYTES:
+            rc = lib.vrm_paged_decode_noalloc(d[0].data_ptr(), pp.data_ptr(), ss.data_ptr(), d[3].data_ptr(),
+                                              d[4].data_ptr(), na.data_ptr(), B, H, KH, D, PS, L, P, d[3].shape[1],
+                                              1, scale, kv_quant.abi_dtype_code(pp, ss), _lib.stream_of(d[0]))
+            _lib.check(rc, "vrm_paged_decode_noalloc")
+        else:  # the fixed scratch array is too small for this shape
+            na.zero_()
+        got.append(na)
+        if PS == 16 and D <= 128:
+            lse_b = torch.empty(B, H, device=DEV)
+            got += [_balanced(d[0], pp, ss, d[3], d[4], 1, lse=lse_b), lse_b]
+        outs[name] = got
+    torch.cuda.synchronize()
+    # the work-item paths are deterministic: bit-identical; the balanced
+    # decode hands page pairs out as its wavefronts free up, so its summation
+    # order (and last bits) vary from run to run whatever the layout
+    for i, (a, b) in enumerate(zip(outs["plain"], outs["inline"])):
+        if i < 3:
+            assert torch.equal(a, b), f"output {i} differs between the layouts"
+        else:
+            torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
+    _assert_close(outs["inline"][0], PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc), "oracle")
 
 
 def test_balanced_decode_refuses_d256_and_the_api_falls_back():

@@ -24,13 +24,18 @@ def _src(shape, dtype, seed, outliers=True):
     return x.to(dtype)
 
 
+# the two memory layouts of the quantized pools (kv_quant.allocate_pool)
+LAYOUTS = ["inline", "plain"]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float16, torch.float32],
                          ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("D", [64, 128, 256])
-def test_int8_append_bit_exact(src_dtype, D):
-    _say(f"int8 append {src_dtype} D{D}")
+def test_int8_append_bit_exact(src_dtype, D, layout):
+    _say(f"int8 append {src_dtype} D{D} {layout}")
     P, L, KH, PS, N = 12, 3, 4, 16, 9
-    pool, scales = kv_quant.allocate_pool(P, L, KH, D, "int8", device=DEV)
+    pool, scales = kv_quant.allocate_pool(P, L, KH, D, "int8", device=DEV, layout=layout)
     k = _src((N, KH, D), src_dtype, 1)
     v = _src((N, KH, D), src_dtype, 2)
     page_ids = torch.tensor([3, 3, 7, 0, 11, 5, 5, 9, 1], dtype=torch.int32)
@@ -47,13 +52,15 @@ def test_int8_append_bit_exact(src_dtype, D):
     mask = torch.zeros(P, L, 2, KH, PS, dtype=torch.bool)
     mask[page_ids.long(), 2, :, :, slots.long()] = True
     assert (sc_c[~mask] == 0).all()
+    assert (pool_c.view(torch.uint8)[~mask] == 0).all()
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("codec", ["int8", "fp8"])
-def test_quantize_pages_bit_exact(codec):
-    _say(f"pages {codec}")
+def test_quantize_pages_bit_exact(codec, layout):
+    _say(f"pages {codec} {layout}")
     P, L, KH, PS, D, NP = 20, 2, 8, 16, 128, 7
-    pool, scales = kv_quant.allocate_pool(P, L, KH, D, codec, device=DEV)
+    pool, scales = kv_quant.allocate_pool(P, L, KH, D, codec, device=DEV, layout=layout)
     kp = _src((NP, KH, PS, D), torch.bfloat16, 3)
     vp = _src((NP, KH, PS, D), torch.bfloat16, 4)
     page_ids = torch.tensor([19, 0, 4, 8, 15, 2, 11], dtype=torch.int32)
@@ -80,12 +87,13 @@ def test_quantize_pages_bit_exact(codec):
                     assert sc_c[pid, 1, kv, h].item() == s.item(), (n, kv, h)
 
 
-def test_fp8_append_sequence_bit_exact():
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_fp8_append_sequence_bit_exact(layout):
     """Token-by-token appends into fp8 pages, with the scale growing on some
     appends, match the oracle's append policy code for code."""
-    _say("fp8 append sequence")
+    _say(f"fp8 append sequence {layout}")
     P, L, KH, PS, D = 4, 1, 2, 16, 128
-    pool, scales = kv_quant.allocate_pool(P, L, KH, D, "fp8", device=DEV)
+    pool, scales = kv_quant.allocate_pool(P, L, KH, D, "fp8", device=DEV, layout=layout)
     g = torch.Generator().manual_seed(5)
     ref_codes = torch.zeros(P, 2, KH, PS, D, dtype=torch.uint8)
     ref_scale = torch.zeros(P, 2, KH)
@@ -110,11 +118,12 @@ def test_fp8_append_sequence_bit_exact():
     assert torch.equal(scales.cpu()[:, 0], ref_scale)
 
 
+@pytest.mark.parametrize("layout", LAYOUTS)
 @pytest.mark.parametrize("codec", ["int8", "fp8"])
-def test_dequantize_pages_exact(codec):
-    _say(f"dequant {codec}")
+def test_dequantize_pages_exact(codec, layout):
+    _say(f"dequant {codec} {layout}")
     P, L, KH, PS, D = 6, 2, 4, 16, 64
-    pool, scales = kv_quant.allocate_pool(P, L, KH, D, codec, device=DEV)
+    pool, scales = kv_quant.allocate_pool(P, L, KH, D, codec, device=DEV, layout=layout)
     kp = _src((P, KH, PS, D), torch.float32, 6)
     vp = _src((P, KH, PS, D), torch.float32, 7)
     ids = torch.arange(P, dtype=torch.int32, device=DEV)

@@ -12,7 +12,7 @@ import math
 import pytest
 import torch
 
-from vramancer_amd import _lib, workloads
+from vramancer_amd import _lib, kv_quant, workloads
 from vramancer_amd.paged_attention_cuda import decode_workspace
 
 DEV = "cuda:0"
@@ -35,7 +35,7 @@ def _both(layer, inp):
     B, H, D = q.shape
     P, L, _, KH, PS, _ = pool.shape
     max_pp = table.shape[1]
-    code = _lib.kv_dtype_code(pool.dtype)
+    code = kv_quant.abi_dtype_code(pool, sc)
     scale = 1.0 / math.sqrt(D)
     s = _lib.stream_of(q)
     ws = decode_workspace(B, H, KH, D, max_pp, q.device, PS)

@@ -14,13 +14,18 @@ from typing import Optional
 
 from .build import LIB_PATH
 
-VRM_ABI_VERSION = 1
+VRM_ABI_VERSION = 2
 
 VRM_KV_F32 = 0
 VRM_KV_F16 = 1
 VRM_KV_BF16 = 2
 VRM_KV_I8 = 3
 VRM_KV_FP8E4M3 = 4
+VRM_KV_I8_INLINE = 5
+VRM_KV_FP8E4M3_INLINE = 6
+
+# size of the fixed split-K array of vrm_paged_decode_noalloc (VRM_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 VRM_SRC_F32 = 0
 VRM_SRC_F16 = 1
@@ -39,6 +44,7 @@ _ll = ctypes.c_longlong
 SIGNATURES = {
     "vrm_abi_version": (_i, []),
     "vrm_last_error": (ctypes.c_char_p, []),
+    "vrm_kv_slab_bytes": (_sz, [_i, _i, _i, _i]),
     "vrm_paged_decode_num_splits": (_i, [_i, _i, _i, _i, _i]),
     "vrm_paged_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "vrm_paged_decode": (_i, [_p, _p, _p, _p, _p, _p, _p, _sz] + [_i] * 9 + [_f, _i, _p]),

@@ -80,4 +80,75 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // OCP e4m3fn byte -> float32 (exact); shared with the host tests.
 __device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) { return vrm_e4m3::decode(b); }
 
+// Where a pool keeps the codes and scales of (page, layer, K/V, kv-head):
+// the codes of that slice start at pool + (page * L + layer) * slab + kvh *
+// head + kv * this->kv bytes, its scales at scales + (page * L + layer) *
+// s_slab + kvh * s_head + kv * s_kv floats (then one per token for int8).
+// Plain pools are the dense [P][L][2][KH][PS][row] arrays (and, for int8 /
+// fp8, a separate dense scale array); the inline int8 / fp8 layout keeps a
+// kv-head's K codes, V codes, K scales and V scales side by side in the
+// (page, layer) slab, the scale pointer then being pool + 2 PS D.
+struct PoolGeom {
+  long long slab;    // pool bytes per (page, layer)
+  long long head;    // bytes from one kv-head's code slices to the next one's
+  long long kv;      // bytes from a kv-head's K codes to its V codes
+  long long s_slab;  // scale floats per (page, layer)
+  long long s_head;  // scale floats from one kv-head to the next
+  long long s_kv;    // scale floats from a kv-head's K scales to its V scales
+};
+
+inline bool inline_pool(int kv_dtype) { return kv_dtype == VRM_KV_I8_INLINE || kv_dtype == VRM_KV_FP8E4M3_INLINE; }
+
+// Bytes of one kv-head's record in an inline slab: K and V codes, then the
+// int8 per-token scales of K and V (PS each), or the fp8 page scales of K and
+// V padded to 16 bytes (so every record starts 16-byte aligned).
+inline long long inline_head_bytes(bool fp8, int PS, int D) {
+  return fp8 ? 2LL * PS * D + 16 : (long long)PS * (2LL * D + 8);
+}
+
+// Geometry of a pool of kv_dtype whose token rows hold row_bytes bytes (D
+// codes, D / 2 for the 4-bit pool, D elements of a float pool).
+inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_bytes) {
+  PoolGeom g{};
+  const bool fp8 = kv_dtype == VRM_KV_FP8E4M3 || kv_dtype == VRM_KV_FP8E4M3_INLINE;
+  const long long slice = (long long)PS * row_bytes;
+  if (inline_pool(kv_dtype)) {
+    g.head = inline_head_bytes(fp8, PS, D);
+    g.kv = slice;
+    g.slab = KH * g.head;
+    g.s_slab = g.slab / 4;
+    g.s_head = g.head / 4;
+    g.s_kv = fp8 ? 1 : PS;
+  } else {
+    g.head = slice;
+    g.kv = KH * slice;
+    g.slab = 2 * g.kv;
+    const long long per_head = fp8 ? 1 : PS;  // int8: one scale per token; fp8: one per page
+    g.s_head = per_head;
+    g.s_kv = KH * per_head;
+    g.s_slab = 2 * g.s_kv;
+  }
+  return g;
+}
+
+// An inline pool's scales sit 2 PS D bytes past its codes; a plain pool's
+// are a separate array (one that starts inside the codes is an inline buffer
+// passed with the plain dtype, refused rather than misread or overwritten).
+inline int check_pool_scales(int kv_dtype, const void* kv_pool, const void* kv_scales, int KH, int PS, int D, int L,
+                             int P, const char* who) {
+  const char* pool = static_cast<const char*>(kv_pool);
+  const char* sc = static_cast<const char*>(kv_scales);
+  if (inline_pool(kv_dtype)) {
+    if (sc != pool + 2LL * PS * D) {
+      set_error("%s: an inline pool's kv_scales must point %lld bytes past kv_pool", who, 2LL * PS * D);
+      return VRM_ERR_ARG;
+    }
+  } else if (sc && sc >= pool && sc < pool + (long long)P * L * 2 * KH * PS * D) {
+    set_error("%s: kv_scales points inside the codes of a plain pool (an inline pool needs the inline kv_dtype)",
+              who);
+    return VRM_ERR_ARG;
+  }
+  return VRM_OK;
+}
+
 }  // namespace vrm

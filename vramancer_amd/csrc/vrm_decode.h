@@ -38,6 +38,7 @@ struct DecodeArgs {
   float* lse;                 // optional [B][H] natural-log sum of exp(scale * q.k), written by the merge
   float* out;                 // [B][H][D]: written directly by the balanced (one workgroup per sequence) mode
   int vshift;                 // stream kernels: pages hold 16 << vshift tokens (0: 16-token pages)
+  PoolGeom g;                 // where the pool keeps each (page, layer, K/V, kv-head) slice and its scales
 };
 
 // ---------------------------------------------------------------------------

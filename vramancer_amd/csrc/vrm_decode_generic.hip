@@ -105,14 +105,15 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
   const int b = wi.b;
 
   const int RB = row_bytes<KIND>(D);
-  const size_t slice = (size_t)PS * RB;              // one (page, layer, K/V, head) slice
-  const size_t kv_stride = (size_t)a.KH * slice;
-  const size_t page_stride = kv_stride * 2 * a.L;
   const int ngrp = D / 32;                           // 4-bit groups per row
+  // 4-bit pools: (page, layer, K/V, head) index of the dense scale / zero arrays
   auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
+  // codes of a (page, layer, K/V, kv-head) slice and, for int8 / fp8, its scales
   auto slice_of = [&](int pid, int kv) {
-    return a.pool + (size_t)pid * page_stride + (size_t)a.layer * 2 * kv_stride + (size_t)kv * kv_stride +
-           (size_t)kvh * slice;
+    return a.pool + ((size_t)pid * a.L + a.layer) * a.g.slab + (size_t)kvh * a.g.head + (size_t)kv * a.g.kv;
+  };
+  auto scales_of = [&](int pid, int kv) {
+    return a.scales + ((size_t)pid * a.L + a.layer) * a.g.s_slab + (size_t)kvh * a.g.s_head + (size_t)kv * a.g.s_kv;
   };
   const bool vec4 = (D & 3) == 0;
 
@@ -149,9 +150,8 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
         pid = trow[pg];
         if (pid >= 0 && pid < a.P) {
           const uint8_t* row = slice_of(pid, 0) + (size_t)slot * RB;
-          const size_t hi = head_index(pid, 0);
           if constexpr (KIND == K_Q4) {
-            const size_t gi = (hi * PS + slot) * ngrp;
+            const size_t gi = (head_index(pid, 0) * PS + slot) * ngrp;
             for (int c = 0; c < ngrp; ++c) {
               const float sc = f16_bits_to_f32(a.q4_scale[gi + c]);
               const float zp = f16_bits_to_f32(a.q4_zero[gi + c]);
@@ -184,8 +184,8 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
               }
             }
             float ks = 1.f;
-            if constexpr (KIND == K_I8) ks = a.scales[hi * PS + slot];
-            if constexpr (KIND == K_FP8) ks = a.scales[hi];
+            if constexpr (KIND == K_I8) ks = scales_of(pid, 0)[slot];
+            if constexpr (KIND == K_FP8) ks = scales_of(pid, 0)[0];
             if constexpr (KIND == K_I8 || KIND == K_FP8) {
 #pragma unroll
               for (int g = 0; g < G; ++g) s[g] *= ks;
@@ -230,12 +230,11 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
       const int tok = tok0 + c0 + tl;
       const int slot = tok % PS;
       const uint8_t* vs = slice_of(pid, 1);
-      const size_t hi = head_index(pid, 1);
       float w[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) w[g] = s_lds[g * kGenChunk + tl];
       if constexpr (KIND == K_I8 || KIND == K_FP8) {
-        const float vscale = KIND == K_I8 ? a.scales[hi * PS + slot] : a.scales[hi];
+        const float vscale = scales_of(pid, 1)[KIND == K_I8 ? slot : 0];
 #pragma unroll
         for (int g = 0; g < G; ++g) w[g] *= vscale;
       }
@@ -248,7 +247,7 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
             const uint8_t c = vs[(((slot >> 2) * 16 + (d & 15)) * (D >> 4) + (d >> 4)) * 4 + (slot & 3)];
             v = KIND == K_I8 ? (float)(int8_t)c : e4m3fn_to_f32(c);
           } else if constexpr (KIND == K_Q4) {
-            const size_t gi = (hi * PS + slot) * ngrp + (d >> 5);
+            const size_t gi = (head_index(pid, 1) * PS + slot) * ngrp + (d >> 5);
             v = (elem<KIND>(vs + (size_t)slot * RB, d) - f16_bits_to_f32(a.q4_zero[gi])) *
                 f16_bits_to_f32(a.q4_scale[gi]);
           } else {

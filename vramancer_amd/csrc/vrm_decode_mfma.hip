@@ -251,7 +251,6 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // token block v & vmask of its table entry v >> vshift.
   const int vshift = BALANCED ? 0 : a.vshift;  // the balanced mode takes 16-token pages only
   const int vmask = (1 << vshift) - 1;
-  const int head_bytes = (kPS << vshift) * D;  // one (page, layer, K/V, head) slice
   constexpr int NJ = (D + 63) / 64;       // 16-byte loads per lane and page, for K and for V
   constexpr int NB = D / 16;              // 16-dim blocks of the output column
   // The last 64-dim chunk holds KPART dims (head_dim 80 / 96 / 112: 16 / 32 /
@@ -320,11 +319,13 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     return pid >= 0 && pid < a.P ? (pid << vshift) | (v & vmask) : -1;
   };
 
-  const size_t kv_stride = (size_t)a.KH * head_bytes;
-  const size_t page_stride = kv_stride * 2 * a.L;
-  const uint8_t* layer_base = a.pool + (size_t)a.layer * 2 * kv_stride + (size_t)kvh * head_bytes;
+  // (page, layer) slabs and the kv-head's place in them, for codes and scales
+  // (the plain and the inline pool layouts differ only in these strides)
+  const size_t page_stride = (size_t)a.g.slab * a.L;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * a.g.slab + (size_t)kvh * a.g.head;
+  const size_t s_page_stride = (size_t)a.g.s_slab * a.L;
+  const float* s_layer_base = a.scales + (size_t)a.layer * a.g.s_slab + (size_t)kvh * a.g.s_head;
   auto page_ok = [&](int vpid) { return vpid >= 0 && (vpid >> vshift) < a.P; };
-  auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
 
   // Loads are issued unconditionally from a clamped, always valid address and
   // zeroed afterwards for an absent page, so every slot keeps the same loads
@@ -339,7 +340,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     // K rows and the 4-token V tiles of a block are 16 D bytes past the previous block's
     const uint8_t* pb = layer_base + (size_t)pc * page_stride + sub * (kPS * D);
     const uint8_t* kb = pb + col * D + grp * 16;
-    const uint8_t* vb = pb + kv_stride + (grp * 16 + col) * (D / 4);
+    const uint8_t* vb = pb + a.g.kv + (grp * 16 + col) * (D / 4);
     if (kpart) s.ok = ok;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -358,13 +359,14 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
         }
       }
     }
+    const float* sb = s_layer_base + (size_t)pc * s_page_stride;
     if constexpr (KIND == K_I8) {
-      const size_t ts = head_index(pc, 0) * (kPS << vshift) + sub * kPS + grp * 4;
-      if (kpart) s.ks = ldf4(a.scales + ts);
-      if (vpart) s.vs = ldf4(a.scales + ts + (size_t)a.KH * (kPS << vshift));
+      const float* ts = sb + sub * kPS + grp * 4;
+      if (kpart) s.ks = ldf4(ts);
+      if (vpart) s.vs = ldf4(ts + a.g.s_kv);
     } else {
-      if (kpart) s.ks = make_float4(a.scales[head_index(pc, 0)], 0.f, 0.f, 0.f);
-      if (vpart) s.vs = make_float4(a.scales[head_index(pc, 1)], 0.f, 0.f, 0.f);
+      if (kpart) s.ks = make_float4(sb[0], 0.f, 0.f, 0.f);
+      if (vpart) s.vs = make_float4(sb[a.g.s_kv], 0.f, 0.f, 0.f);
     }
     if (vpart && !ok) {
       s.vs = make_float4(0.f, 0.f, 0.f, 0.f);

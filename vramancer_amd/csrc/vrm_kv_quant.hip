@@ -22,6 +22,11 @@
 namespace vrm {
 namespace {
 
+bool quant_pool(int kv_dtype) {
+  return kv_dtype == VRM_KV_I8 || kv_dtype == VRM_KV_FP8E4M3 || inline_pool(kv_dtype);
+}
+bool fp8_pool(int kv_dtype) { return kv_dtype == VRM_KV_FP8E4M3 || kv_dtype == VRM_KV_FP8E4M3_INLINE; }
+
 
 template <int SRC>
 __device__ __forceinline__ float load_src(const void* p, size_t i) {
@@ -55,10 +60,16 @@ struct QuantArgs {
   float* scales;
   int KH, L, P, layer;
   int D, PS;               // head_dim (multiple of 16, <= 256) and page size (multiple of 4)
+  PoolGeom g;              // plain or inline layout of codes and scales
 };
 
-__device__ __forceinline__ size_t head_index(const QuantArgs& a, int pid, int kv, int h) {
-  return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + h;
+// Codes of the (page, layer, K/V, kv-head) slice and its scales (int8: PS of
+// them, one per token; fp8: one).
+__device__ __forceinline__ uint8_t* slice_of(const QuantArgs& a, int pid, int kv, int h) {
+  return a.pool + ((size_t)pid * a.L + a.layer) * a.g.slab + (size_t)h * a.g.head + (size_t)kv * a.g.kv;
+}
+__device__ __forceinline__ float* scales_of(const QuantArgs& a, int pid, int kv, int h) {
+  return a.scales + ((size_t)pid * a.L + a.layer) * a.g.s_slab + (size_t)h * a.g.s_head + (size_t)kv * a.g.s_kv;
 }
 
 // Offset of (token t, dim d) inside a slice: K token-major, V tiled.
@@ -92,13 +103,13 @@ __global__ void __launch_bounds__(64) quant_i8_kernel(QuantArgs a) {
   }
   amax = group_max<64>(amax);
   const float scale = __fdiv_rn(amax, 127.f);
-  int8_t* dst = reinterpret_cast<int8_t*>(a.pool) + head_index(a, pid, kv, h) * PS * D;
+  int8_t* dst = reinterpret_cast<int8_t*>(slice_of(a, pid, kv, h));
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int d = i * 64 + lane;
     if (d < D) dst[code_offset(kv, slot, d, D)] = int8_code(x[i], scale);
   }
-  if (lane == 0) a.scales[head_index(a, pid, kv, h) * PS + slot] = scale;
+  if (lane == 0) scales_of(a, pid, kv, h)[slot] = scale;
 }
 
 // fp8 whole pages, one 256-thread workgroup per (page, K/V, head): the page
@@ -123,12 +134,12 @@ __global__ void __launch_bounds__(256) quant_fp8_pages_kernel(QuantArgs a) {
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float scale = __fdiv_rn(amax, 448.f);
-  uint8_t* dst = a.pool + head_index(a, pid, kv, h) * N;
+  uint8_t* dst = slice_of(a, pid, kv, h);
   for (int idx = tid; idx < N; idx += 256) {
     const int t = idx / D, d = idx - t * D;
     dst[code_offset(kv, t, d, D)] = t < n_valid ? fp8_code(load_src<SRC>(src, base + idx), scale) : (uint8_t)0;
   }
-  if (tid == 0) a.scales[head_index(a, pid, kv, h)] = scale;
+  if (tid == 0) *scales_of(a, pid, kv, h) = scale;
 }
 
 // fp8 append, one 256-thread workgroup per (token, K/V, head).  The page
@@ -149,14 +160,14 @@ __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
   const float x = tid < D ? load_src<SRC>(src, row + tid) : 0.f;
   float amax = group_max<64>(fabsf(x));
   if ((tid & 63) == 0) red[tid >> 6] = amax;
-  const size_t hi = head_index(a, pid, kv, h);
+  float* const sp = scales_of(a, pid, kv, h);
   // Every thread reads the old scale before the barrier; thread 0 overwrites it after.
-  const float old_scale = slot > 0 ? a.scales[hi] : 0.f;
+  const float old_scale = slot > 0 ? *sp : 0.f;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float want = __fdiv_rn(amax, 448.f);
   const float scale = fmaxf(old_scale, want);
-  uint8_t* page = a.pool + hi * (size_t)(PS * D);
+  uint8_t* page = slice_of(a, pid, kv, h);
   if (slot > 0 && scale > old_scale) {
     for (int idx = tid; idx < slot * D; idx += 256) {
       const int off = code_offset(kv, idx / D, idx % D, D);
@@ -165,7 +176,7 @@ __global__ void __launch_bounds__(256) quant_fp8_append_kernel(QuantArgs a) {
     }
   }
   if (tid < D) page[code_offset(kv, slot, tid, D)] = fp8_code(x, scale);
-  if (tid == 0) a.scales[hi] = scale;
+  if (tid == 0) *sp = scale;
 }
 
 // Dequantize pages: out[n][2][KH][PS][D] float32.
@@ -180,15 +191,15 @@ __global__ void __launch_bounds__(256) dequant_pages_kernel(QuantArgs a, float* 
     for (size_t i = threadIdx.x; i < N; i += 256) o[i] = 0.f;
     return;
   }
-  const size_t hi = head_index(a, pid, kv, h);
-  const uint8_t* codes = a.pool + hi * N;
+  const uint8_t* codes = slice_of(a, pid, kv, h);
+  const float* sc = scales_of(a, pid, kv, h);
   for (size_t i = threadIdx.x; i < N; i += 256) {
     const int t = (int)(i / D), d = (int)(i % D);
     const uint8_t c = codes[code_offset(kv, t, d, D)];
     if (FP8) {
-      o[i] = e4m3fn_to_f32(c) * a.scales[hi];
+      o[i] = e4m3fn_to_f32(c) * sc[0];
     } else {
-      o[i] = (float)(int8_t)c * a.scales[hi * a.PS + t];
+      o[i] = (float)(int8_t)c * sc[t];
     }
   }
 }
@@ -212,7 +223,7 @@ int check_quant(const void* key, const void* value, int src_dtype, const int32_t
     set_error("%s: unknown source dtype %d", who, src_dtype);
     return VRM_ERR_ARG;
   }
-  if (kv_dtype != VRM_KV_I8 && kv_dtype != VRM_KV_FP8E4M3) {
+  if (!quant_pool(kv_dtype)) {
     set_error("%s: kv_dtype %d is not a quantized pool", who, kv_dtype);
     return VRM_ERR_ARG;
   }
@@ -228,12 +239,12 @@ int check_quant(const void* key, const void* value, int src_dtype, const int32_t
     set_error("%s: too many rows in one call (%d)", who, n);
     return VRM_ERR_UNSUPPORTED;
   }
-  return VRM_OK;
+  return check_pool_scales(kv_dtype, pool, scales, KH, PS, D, L, P, who);
 }
 
 template <int SRC, int DMAX>
 void launch_quant(const QuantArgs& a, int n, int kv_dtype, bool pages, hipStream_t st) {
-  if (kv_dtype == VRM_KV_I8) {
+  if (!fp8_pool(kv_dtype)) {
     if (pages)
       hipLaunchKernelGGL((quant_i8_kernel<SRC, DMAX, true>), dim3(2 * a.KH, n, a.PS), dim3(64), 0, st, a);
     else
@@ -265,7 +276,8 @@ int run_quant(const void* key, const void* value, int src_dtype, const int32_t* 
     clear_error();
     return VRM_OK;
   }
-  QuantArgs a{key, value, page_ids, slots, static_cast<uint8_t*>(pool), scales, KH, L, P, layer, D, PS};
+  QuantArgs a{key, value, page_ids, slots, static_cast<uint8_t*>(pool), scales, KH, L, P, layer, D, PS,
+              pool_geom(kv_dtype, KH, PS, D, D)};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (src_dtype) {
     case VRM_SRC_F32: launch_quant_d<VRM_SRC_F32>(a, n, kv_dtype, pages, D, st); break;
@@ -311,15 +323,17 @@ extern "C" int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales,
     set_error("%s: page_size %d / head_dim %d unsupported (multiples of 4 / 16)", who, PS, D);
     return VRM_ERR_UNSUPPORTED;
   }
-  if (kv_dtype != VRM_KV_I8 && kv_dtype != VRM_KV_FP8E4M3) {
+  if (!quant_pool(kv_dtype)) {
     set_error("%s: kv_dtype %d is not a quantized pool", who, kv_dtype);
     return VRM_ERR_ARG;
   }
+  const int rc = check_pool_scales(kv_dtype, kv_pool, kv_scales, KH, PS, D, L, P, who);
+  if (rc) return rc;
   if (NP == 0) return VRM_OK;
   QuantArgs a{nullptr, nullptr, page_ids, nullptr, const_cast<uint8_t*>(static_cast<const uint8_t*>(kv_pool)),
-              const_cast<float*>(kv_scales), KH, L, P, layer_idx, D, PS};
+              const_cast<float*>(kv_scales), KH, L, P, layer_idx, D, PS, pool_geom(kv_dtype, KH, PS, D, D)};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (kv_dtype == VRM_KV_FP8E4M3)
+  if (fp8_pool(kv_dtype))
     hipLaunchKernelGGL(dequant_pages_kernel<true>, dim3(2 * KH, NP), dim3(256), 0, st, a, out, D);
   else
     hipLaunchKernelGGL(dequant_pages_kernel<false>, dim3(2 * KH, NP), dim3(256), 0, st, a, out, D);

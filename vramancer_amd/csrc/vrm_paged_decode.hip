@@ -672,11 +672,20 @@ int kind_of(int kv_dtype) {
     case VRM_KV_F32: return K_F32;
     case VRM_KV_F16: return K_F16;
     case VRM_KV_BF16: return K_BF16;
-    case VRM_KV_I8: return K_I8;
-    case VRM_KV_FP8E4M3: return K_FP8;
+    case VRM_KV_I8:
+    case VRM_KV_I8_INLINE: return K_I8;
+    case VRM_KV_FP8E4M3:
+    case VRM_KV_FP8E4M3_INLINE: return K_FP8;
     default: return -1;
   }
 }
+
+// Pool geometry of a decode call (kv_dtype selects the plain or inline layout).
+PoolGeom geom_of(int kv_dtype, int kind, int KH, int PS, int D) {
+  const long long row = kind == K_F32 ? 4LL * D : (kind == K_F16 || kind == K_BF16) ? 2LL * D : kind == K_Q4 ? D / 2 : D;
+  return pool_geom(kv_dtype, KH, PS, D, row);
+}
+
 
 int decode_entry(const float* query, const void* kv_pool, const float* kv_scales, const int32_t* page_table,
                  const int32_t* context_lens, float* out, void* workspace, size_t workspace_bytes, int B, int H,
@@ -698,6 +707,8 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
     set_error("vrm_paged_decode: kv_scales given for a float pool");
     return VRM_ERR_ARG;
   }
+  rc = check_pool_scales(kv_dtype, kv_pool, kv_scales, KH, PS, D, L, P, "vrm_paged_decode");
+  if (rc) return rc;
   DecodeArgs a{};
   a.query = query;
   a.pool = static_cast<const uint8_t*>(kv_pool);
@@ -711,6 +722,7 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
   a.max_pp = max_pp;
   a.layer = layer_idx;
   a.lse = lse;
+  a.g = geom_of(kv_dtype, kind, KH, PS, D);
   rc = check_kind_shape(kind, D, PS, "vrm_paged_decode");
   if (rc) return rc;
   return run_decode(a, kind, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
@@ -882,6 +894,8 @@ int balanced_entry(const float* query, const void* kv_pool, const float* kv_scal
     set_error("%s: quantized pool needs kv_scales", who);
     return VRM_ERR_ARG;
   }
+  rc = check_pool_scales(kv_dtype, kv_pool, kv_scales, KH, PS, D, L, P, who);
+  if (rc) return rc;
   if ((D != 64 && D != 80 && D != 96 && D != 112 && D != 128) || PS != kPS) {
     // at D = 256 two page pairs per wave do not fit in registers
     set_error("%s: head_dim %d / page_size %d unsupported (64, 80, 96, 112 or 128, page 16)", who, D, PS);
@@ -909,6 +923,7 @@ int balanced_entry(const float* query, const void* kv_pool, const float* kv_scal
   a.lse = lse;
   a.out = out;
   a.qscale = scale * kLog2e;
+  a.g = geom_of(kv_dtype, kind, KH, PS, D);
   const hipError_t e = launch_stream_balanced(a, kind, B, D, G, reinterpret_cast<hipStream_t>(stream), loads_only);
   if (e != hipSuccess) {
     set_error("%s: kernel launch failed: %s", who, hipGetErrorString(e));
@@ -1004,6 +1019,7 @@ extern "C" int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4
   a.P = P;
   a.max_pp = max_pp;
   a.layer = layer_idx;
+  a.g = geom_of(VRM_KV_I8, K_Q4, KH, PS, D);  // plain layout of D / 2 bytes per row
   return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
                     kBoth);
 }

@@ -22,6 +22,21 @@ defines them in the style of the reference's pool API:
   token-major for inspection;
 * the write itself replaces the raw index-put of
   ``PagedKVCacheManager.write_kv`` (core/paged_attention.py:611-612).
+
+Two memory layouts hold the same logical tensors:
+
+* ``plain``: ``kv_pool`` a dense ``[P, L, 2, KH, PS, D]`` array and
+  ``kv_scales`` a separate dense array;
+* ``inline`` (what ``allocate_pool`` returns by default): one byte buffer of
+  ``P * L`` slabs, each holding per kv-head its K codes, V codes and K / V
+  scales side by side (int8: ``PS * (2 D + 8)`` bytes per kv-head; fp8:
+  ``2 PS D + 16``).  ``kv_pool`` and ``kv_scales`` are strided views of that
+  buffer with the usual shapes, so indexing them reads the same values as in
+  the plain layout.  A layer's page is one contiguous run per kv-head, and
+  at the tuned shapes the slab (33 KB at KH=8, PS=16, D=128) keeps the
+  pages of a layer off the power-of-two strides that HBM reads slower when
+  pages are scattered.  ``pool_dtype_code`` tells the kernels which layout a
+  pair of tensors has.
 """
 from __future__ import annotations
 
@@ -32,6 +47,9 @@ from . import _lib
 __all__ = [
     "logical_view",
     "allocate_pool",
+    "abi_dtype_code",
+    "pool_dtype_code",
+    "pool_layout",
     "quantize_append",
     "quantize_pages",
     "dequantize_pages",
@@ -50,19 +68,89 @@ def _codec_dtype(codec: str):
     raise ValueError(f"unknown codec {codec!r}; expected one of {CODECS}")
 
 
+LAYOUTS = ("inline", "plain")
+
+
+def _inline_geometry(num_layers: int, num_kv_heads: int, page_size: int, head_dim: int, fp8: bool):
+    """(slab bytes, kv-head record bytes, code strides, scale strides) of the
+    inline layout; strides in elements of the code / float32 views."""
+    L, KH, PS, D = num_layers, num_kv_heads, page_size, head_dim
+    head = 2 * PS * D + 16 if fp8 else PS * (2 * D + 8)
+    slab = KH * head
+    codes = (L * slab, slab, PS * D, head, D, 1)
+    if fp8:
+        scales = (L * slab // 4, slab // 4, 1, head // 4)
+    else:
+        scales = (L * slab // 4, slab // 4, PS, head // 4, 1)
+    return slab, head, codes, scales
+
+
 def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, head_dim: int, codec: str,
-                  page_size: int = 16, device: Any = "cuda") -> Tuple[Any, Any]:
-    """Zero-initialised (codes, scales) for a quantized pool."""
+                  page_size: int = 16, device: Any = "cuda", layout: str = "inline") -> Tuple[Any, Any]:
+    """Zero-initialised (codes, scales) for a quantized pool, in the inline
+    layout (the default) or the plain one."""
     import torch
 
     dtype = _codec_dtype(codec)
-    pool = torch.zeros((num_pages, num_layers, 2, num_kv_heads, page_size, head_dim), dtype=torch.uint8,
-                       device=device).view(dtype)
-    if codec == "int8":
-        scales = torch.zeros((num_pages, num_layers, 2, num_kv_heads, page_size), dtype=torch.float32, device=device)
-    else:
-        scales = torch.zeros((num_pages, num_layers, 2, num_kv_heads), dtype=torch.float32, device=device)
+    P, L, KH, PS, D = num_pages, num_layers, num_kv_heads, page_size, head_dim
+    scale_shape = (P, L, 2, KH, PS) if codec == "int8" else (P, L, 2, KH)
+    if layout == "plain":
+        pool = torch.zeros((P, L, 2, KH, PS, D), dtype=torch.uint8, device=device).view(dtype)
+        return pool, torch.zeros(scale_shape, dtype=torch.float32, device=device)
+    if layout != "inline":
+        raise ValueError(f"unknown layout {layout!r}; expected one of {LAYOUTS}")
+    if D % 16 or PS % 4:
+        raise ValueError(f"quantized pools need head_dim % 16 == 0 and page_size % 4 == 0 (got {D}, {PS})")
+    slab, _, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, codec == "fp8")
+    buf = torch.zeros(P * L * slab, dtype=torch.uint8, device=device)
+    pool = buf.view(dtype).as_strided((P, L, 2, KH, PS, D), code_strides)
+    scales = buf.view(torch.float32).as_strided(scale_shape, scale_strides, storage_offset=2 * PS * D // 4)
     return pool, scales
+
+
+def _same_strides(t, strides) -> bool:
+    return all(n <= 1 or st == want for n, st, want in zip(t.shape, t.stride(), strides))
+
+
+def pool_layout(kv_pool, kv_scales) -> Optional[str]:
+    """``"plain"`` when both tensors are dense, ``"inline"`` when they are the
+    two views of one inline buffer, ``None`` otherwise."""
+    if kv_pool.is_contiguous() and kv_scales.is_contiguous():
+        return "plain"
+    if kv_pool.dim() != 6:
+        return None
+    P, L, two, KH, PS, D = kv_pool.shape
+    fp8 = _lib.kv_dtype_code(kv_pool.dtype) == _lib.VRM_KV_FP8E4M3
+    _, _, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, fp8)
+    if (_same_strides(kv_pool, code_strides) and _same_strides(kv_scales, scale_strides)
+            and kv_scales.data_ptr() == kv_pool.data_ptr() + 2 * PS * D):
+        return "inline"
+    return None
+
+
+def abi_dtype_code(kv_pool, kv_scales=None) -> int:
+    """kv_dtype code of the C ABI for any pool: the float pools by element
+    type, the quantized ones by element type and layout (``RuntimeError`` for
+    a quantized pair in neither layout)."""
+    if kv_scales is None:
+        return _lib.kv_dtype_code(kv_pool.dtype)
+    code = pool_dtype_code(kv_pool, kv_scales)
+    if code is None:
+        raise RuntimeError("kv_pool / kv_scales are neither dense arrays nor the views allocate_pool returns")
+    return code
+
+
+def pool_dtype_code(kv_pool, kv_scales) -> Optional[int]:
+    """The kv_dtype code of the C ABI for a quantized pool and its scales
+    (VRM_KV_I8 / VRM_KV_FP8E4M3 plain, VRM_KV_*_INLINE inline), ``None``
+    when they are in neither layout."""
+    code = _lib.kv_dtype_code(kv_pool.dtype)
+    layout = pool_layout(kv_pool, kv_scales)
+    if layout is None or code not in (_lib.VRM_KV_I8, _lib.VRM_KV_FP8E4M3):
+        return None
+    if layout == "plain":
+        return code
+    return _lib.VRM_KV_I8_INLINE if code == _lib.VRM_KV_I8 else _lib.VRM_KV_FP8E4M3_INLINE
 
 
 def logical_view(kv_pool):
@@ -92,9 +180,11 @@ def _check_pool(kv_pool, kv_scales):
     want = (P, L, 2, KH, PS) if code == _lib.VRM_KV_I8 else (P, L, 2, KH)
     if tuple(kv_scales.shape) != want or kv_scales.dtype != torch.float32:
         raise RuntimeError(f"kv_scales must be float32 of shape {want}")
-    if not (kv_pool.is_contiguous() and kv_scales.is_contiguous()):
-        raise RuntimeError("kv_pool and kv_scales must be contiguous (they are written in place)")
-    return code, P, L, KH, PS, D
+    layout_code = pool_dtype_code(kv_pool, kv_scales)
+    if layout_code is None:
+        raise RuntimeError("kv_pool and kv_scales must be dense arrays or the two views allocate_pool returns "
+                           "(they are written in place)")
+    return layout_code, P, L, KH, PS, D
 
 
 def quantize_append(kv_pool: Any, kv_scales: Any, layer_idx: int, page_ids: Any, slots: Any,

@@ -10,7 +10,8 @@ extension.  Differences a caller can observe:
 * bfloat16, int8 and float8_e4m3fn pools are supported; the quantized pools
   take their scales through the extra keyword ``kv_scales`` (int8: one
   float32 per (page, layer, K/V, kv-head, token); fp8: one per
-  (page, layer, K/V, kv-head));
+  (page, layer, K/V, kv-head)), either as dense arrays or as the two views of
+  one inline buffer that ``kv_quant.allocate_pool`` returns;
 * there is no silent PyTorch fallback: CPU tensors or a missing library raise
   ``RuntimeError`` (the reference logs and falls back,
   core/paged_attention_cuda.py:178-183);
@@ -163,13 +164,22 @@ def paged_attention_decode(
     check_outputs(query, out, workspace, page_table, context_lens)
     code = _lib.kv_dtype_code(kv_pool.dtype)
     if code in (_lib.VRM_KV_I8, _lib.VRM_KV_FP8E4M3):
+        from . import kv_quant
+
         want = (P, L, 2, KH, PS) if code == _lib.VRM_KV_I8 else (P, L, 2, KH)
         if kv_scales is None or tuple(kv_scales.shape) != want or kv_scales.dtype != torch.float32:
             raise RuntimeError(f"{kv_pool.dtype} pool needs float32 kv_scales of shape {want}")
-        kv_scales = kv_scales.contiguous()
+        # plain (dense) or inline (the two views of kv_quant.allocate_pool) as
+        # they are; any other strides are copied to the plain layout
+        layout_code = kv_quant.pool_dtype_code(kv_pool, kv_scales)
+        if layout_code is None:
+            kv_pool, kv_scales = kv_pool.contiguous(), kv_scales.contiguous()
+        else:
+            code = layout_code
     elif kv_scales is not None:
         raise RuntimeError("kv_scales is only meaningful for int8 / float8_e4m3fn pools")
-    kv_pool = kv_pool.contiguous()
+    else:
+        kv_pool = kv_pool.contiguous()
     max_pp = page_table.shape[1]
     if out is None:
         out = torch.empty((B, H, D), dtype=torch.float32, device=query.device)
