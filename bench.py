@@ -502,6 +502,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--pool-layout", default=None, choices=("inline", "plain"),
+                    help="memory layout of the int8 / fp8 pools (default: kv_quant.default_layout of the codec)")
     ap.add_argument("--settle", type=float, default=2.0,
                     help="seconds of further untimed decode steps after the warm-up, so that the timed region "
                          "starts on quiet HBM (0: none)")
@@ -559,7 +561,7 @@ def main():
     # the set-up); the zero codes of the other layers cost the decode the same.
     fill = (layers[0],) if turbo else layers
     log(f"building {cfg.name} pool ({cfg.num_layers} layers, filling {fill}, rotating {layers})")
-    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=fill)
+    inp = workloads.make_decode_inputs(cfg, dev, seed=0, layers=fill, layout=args.pool_layout)
     torch.cuda.synchronize()
     q, pool, sc, table, lens = inp["query"], inp["kv_pool"], inp["kv_scales"], inp["page_table"], inp["context_lens"]
     zp = inp["kv_zeros"]
@@ -761,8 +763,7 @@ def main():
                    "16384 pages, 4-bit asymmetric codes + per-32-dim-group fp16 scale and zero"),
         "7b-bf16": "7b-bf16 paged decode: B=32, H=28, KH=4, D=128, context ~U[1024, 8192], page 16, bf16 pool",
         "mixed-fp8": ("mixed-fp8 paged decode: 128 sequences lognormal(median 2048, sigma 1) + one of 131072, "
-                      "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales in the inline slab "
-                      "layout"),
+                      "H=64, KH=8, D=128, page 16, fp8 e4m3fn codes + per-page fp32 scales"),
         "fp32-plumbing": "fp32-plumbing paged decode: B=4, H=KH=12, D=64, context 512, page 16, fp32 pool",
         "14b-turbo3": ("14b-turbo3 paged decode over TurboQuant pages: B=16, H=40, KH=8, D=128, context 32768, "
                        "page 16, 3 bits per angle, Student-t(3) K/V"),
@@ -771,6 +772,10 @@ def main():
     }[cfg.name]
     if shape_override:
         desc += f" (head_dim set to {D}, page size to {PS})"
+    if cfg.codec in ("int8", "fp8") and (args.pool_layout or kv_quant.default_layout(cfg.codec)) != "inline":
+        desc = desc.replace("in the inline slab layout", "in the plain layout (separate scale array)")
+    elif cfg.codec in ("int8", "fp8") and "inline" not in desc:
+        desc += " in the inline slab layout"
     if turbo:
         pd = 1 << max(6, (D - 1).bit_length())
         tuned = pd in (64, 128) and comp.qjl_dim == pd // 2 and comp.bits_per_angle in (2, 3, 4) and PS == 16

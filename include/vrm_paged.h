@@ -54,27 +54,30 @@ typedef enum vrm_kv_dtype {
 
 /*
  * Inline slab layout of the int8 / fp8 pools (VRM_KV_*_INLINE).  The codes
- * and scales of one (page, layer) share one slab of vrm_kv_slab_bytes() bytes,
- * and the slab holds, for each kv-head h in turn, a record of
+ * and scales of one (page, layer) share one slab of vrm_kv_slab_bytes()
+ * bytes at (p L + l) slab, holding for each kv-head h in turn a record of
  *      K codes [PS][D] | V codes [PS][D] (tiled as above)
- *      | int8: K scales [PS], V scales [PS] float32
- *      | fp8:  K scale, V scale float32, 8 zero bytes
- * (PS (2 D + 8) bytes for int8, 2 PS D + 16 for fp8).  Element (p, l, kv, h,
- * t, d) of the logical kv_pool[P][L][2][KH][PS][D] is then at byte
- * (p L + l) slab + h record + kv PS D + (its place in the slice), and the
- * logical kv_scales[P][L][2][KH]([PS]) are float32s at the same slab and
- * record offsets from kv_scales = (char *)kv_pool + 2 PS D.  Every entry
- * that takes a pool takes these dtypes with kv_scales at exactly that
- * address (anything else is VRM_ERR_ARG).  No counterpart in the reference
- * (whose pools are float only): a page of one layer is then one contiguous
- * run per kv-head, and the slab is not a power-of-two multiple of 32 KB at
- * the shapes of the tuned kernels, which HBM reads faster when pages are
- * scattered over the pool.
+ *      | int8: K scales [PS], V scales [PS] float32 (PS (2 D + 8) bytes)
+ *      | fp8:  K scale, V scale float32, zero bytes up to 2 PS D + 128
+ * Code (p, l, kv, h, t, d) of the logical kv_pool[P][L][2][KH][PS][D] is at
+ * byte (p L + l) slab + h record + kv PS D + (its place in the slice), and
+ * the logical kv_scales[P][L][2][KH]([PS]) are float32s at the same slab and
+ * record offsets plus kv PS (+ t) (int8) or kv (fp8) from
+ * kv_scales = (char *)kv_pool + 2 PS D.  Every entry that takes a pool takes
+ * these dtypes with kv_scales at exactly that address (anything else is
+ * VRM_ERR_ARG).  No counterpart in the reference (whose pools are float
+ * only): a page of one layer is one contiguous run per kv-head, and the slab
+ * is not a power-of-two multiple of 32 KB, which HBM reads faster when the
+ * pages of a pool of many layers are scattered over it (int8 14B shape, 48
+ * layers: 4 % faster).  The int8 pools of the Python layer use it by default;
+ * the fp8 pools do not (their few page scales read faster as a separate
+ * array in the ragged work-item decode).
  */
 
 /* Bytes of one (page, layer) slab of a pool of kv_dtype: 2 KH PS D times the
  * element size for the plain layouts (codes only: their scales live in
- * kv_scales), KH records for the inline layouts; 0 for a bad argument. */
+ * kv_scales), codes and scales for the inline layouts; 0 for a bad
+ * argument. */
 size_t vrm_kv_slab_bytes(int kv_dtype, int KH, int PS, int D);
 
 /* Element type of new K/V rows handed to the quantizers. */

@@ -83,11 +83,12 @@ def test_decode_rejects_bad_arguments(lib):
 
 def test_kv_slab_bytes(lib):
     """Bytes per (page, layer): plain layouts 2 KH PS D elements (codes only),
-    inline records of PS (2 D + 8) bytes (int8) or 2 PS D + 16 (fp8) per kv-head."""
+    inline records of PS (2 D + 8) bytes (int8) or 2 PS D + 128 (fp8) per
+    kv-head."""
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8, 8, 16, 128) == 32768
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_FP8E4M3, 8, 16, 128) == 32768
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 8, 16, 128) == 8 * (16 * 256 + 128) == 33792
-    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_FP8E4M3_INLINE, 8, 16, 128) == 8 * (4096 + 16)
+    assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_FP8E4M3_INLINE, 8, 16, 128) == 8 * (4096 + 128)
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_I8_INLINE, 3, 8, 48) == 3 * 8 * (96 + 8)
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_BF16, 4, 16, 128) == 2 * 4 * 16 * 128 * 2
     assert lib.vrm_kv_slab_bytes(_lib.VRM_KV_F32, 12, 16, 64) == 2 * 12 * 16 * 64 * 4

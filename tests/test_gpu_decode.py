@@ -662,7 +662,7 @@ def test_inline_layout_decodes_like_the_plain_layout(dtype, D, PS):
     B, H, KH = len(ctxs), 16, 2
     q, pool, sc, table, lens = _pool_case(dtype, B, H, KH, D, ctxs, seed=D + PS, PS=PS)
     P, L = pool.shape[:2]
-    ip, isc = kv_quant.allocate_pool(P, L, KH, D, codec, PS, DEV)
+    ip, isc = kv_quant.allocate_pool(P, L, KH, D, codec, PS, DEV, layout="inline")
     ip.copy_(pool.to(DEV))
     isc.copy_(sc.to(DEV))
     assert kv_quant.pool_layout(ip, isc) == "inline"

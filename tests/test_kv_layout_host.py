@@ -1,7 +1,7 @@
 """Host tests of the quantized pools' two memory layouts (no GPU): the inline
 layout's views put every code and scale at the byte the C ABI documents
-(include/vrm_paged.h: per (page, layer) slab, per kv-head record of K codes,
-V codes, K scales, V scales), the sizes agree with the library's
+(include/vrm_paged.h: per (page, layer) slab, per kv-head a record of K
+codes, V codes, K scales, V scales), the sizes agree with the library's
 vrm_kv_slab_bytes, and the layout detection tells inline, plain and other
 strides apart."""
 import pytest
@@ -18,9 +18,9 @@ def _buffer(t):
 @pytest.mark.parametrize("codec", ["int8", "fp8"])
 @pytest.mark.parametrize("P,L,KH,PS,D", [(3, 2, 2, 8, 32), (2, 3, 3, 4, 48), (2, 1, 8, 16, 128)])
 def test_inline_views_hit_the_documented_bytes(codec, P, L, KH, PS, D):
-    pool, sc = kv_quant.allocate_pool(P, L, KH, D, codec, PS, device="cpu")
+    pool, sc = kv_quant.allocate_pool(P, L, KH, D, codec, PS, device="cpu", layout="inline")
     fp8 = codec == "fp8"
-    head = 2 * PS * D + 16 if fp8 else PS * (2 * D + 8)
+    head = 2 * PS * D + 128 if fp8 else PS * (2 * D + 8)
     slab = KH * head
     buf = _buffer(pool)
     assert buf.numel() == P * L * slab
@@ -50,8 +50,16 @@ def test_inline_slab_matches_the_library():
     lib = _lib.load()
     for codec, code in (("int8", _lib.VRM_KV_I8_INLINE), ("fp8", _lib.VRM_KV_FP8E4M3_INLINE)):
         for KH, PS, D in ((8, 16, 128), (3, 4, 48), (1, 32, 256)):
-            pool, _ = kv_quant.allocate_pool(2, 3, KH, D, codec, PS, device="cpu")
+            pool, _ = kv_quant.allocate_pool(2, 3, KH, D, codec, PS, device="cpu", layout="inline")
             assert _buffer(pool).numel() == 2 * 3 * lib.vrm_kv_slab_bytes(code, KH, PS, D)
+
+
+def test_default_layouts():
+    """int8 pools are inline by default, fp8 pools plain."""
+    assert kv_quant.default_layout("int8") == "inline" and kv_quant.default_layout("fp8") == "plain"
+    p8, s8 = kv_quant.allocate_pool(2, 2, 2, 32, "int8", 8, device="cpu")
+    pf, sf = kv_quant.allocate_pool(2, 2, 2, 32, "fp8", 8, device="cpu")
+    assert kv_quant.pool_layout(p8, s8) == "inline" and kv_quant.pool_layout(pf, sf) == "plain"
 
 
 def test_layout_detection():

@@ -86,8 +86,8 @@ __device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) { return vrm_e4m3::de
 // s_slab + kvh * s_head + kv * s_kv floats (then one per token for int8).
 // Plain pools are the dense [P][L][2][KH][PS][row] arrays (and, for int8 /
 // fp8, a separate dense scale array); the inline int8 / fp8 layout keeps a
-// kv-head's K codes, V codes, K scales and V scales side by side in the
-// (page, layer) slab, the scale pointer then being pool + 2 PS D.
+// kv-head's codes and scales in the (page, layer) slab (inline_scale_offset
+// below), the scale pointer then pointing into the first slab.
 struct PoolGeom {
   long long slab;    // pool bytes per (page, layer)
   long long head;    // bytes from one kv-head's code slices to the next one's
@@ -99,12 +99,12 @@ struct PoolGeom {
 
 inline bool inline_pool(int kv_dtype) { return kv_dtype == VRM_KV_I8_INLINE || kv_dtype == VRM_KV_FP8E4M3_INLINE; }
 
-// Bytes of one kv-head's record in an inline slab: K and V codes, then the
-// int8 per-token scales of K and V (PS each), or the fp8 page scales of K and
-// V padded to 16 bytes (so every record starts 16-byte aligned).
-inline long long inline_head_bytes(bool fp8, int PS, int D) {
-  return fp8 ? 2LL * PS * D + 16 : (long long)PS * (2LL * D + 8);
-}
+// Inline slabs hold per kv-head a record of its K and V codes followed by
+// its K and V scales: int8 PS each (PS (2 D + 8) bytes in all), fp8 one each,
+// the record padded to 2 PS D + 128 bytes so that every kv-head's codes start
+// on a 128-byte line.  The first record's scales are 2 PS D bytes into the
+// pool.
+inline long long inline_scale_offset(int PS, int D) { return 2LL * PS * D; }
 
 // Geometry of a pool of kv_dtype whose token rows hold row_bytes bytes (D
 // codes, D / 2 for the 4-bit pool, D elements of a float pool).
@@ -113,12 +113,19 @@ inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_byt
   const bool fp8 = kv_dtype == VRM_KV_FP8E4M3 || kv_dtype == VRM_KV_FP8E4M3_INLINE;
   const long long slice = (long long)PS * row_bytes;
   if (inline_pool(kv_dtype)) {
-    g.head = inline_head_bytes(fp8, PS, D);
     g.kv = slice;
-    g.slab = KH * g.head;
+    if (fp8) {
+      g.head = 2 * slice + 128;
+      g.slab = KH * g.head;
+      g.s_head = g.head / 4;
+      g.s_kv = 1;
+    } else {
+      g.head = 2 * slice + 8LL * PS;
+      g.slab = KH * g.head;
+      g.s_head = g.head / 4;
+      g.s_kv = PS;
+    }
     g.s_slab = g.slab / 4;
-    g.s_head = g.head / 4;
-    g.s_kv = fp8 ? 1 : PS;
   } else {
     g.head = slice;
     g.kv = KH * slice;
@@ -131,16 +138,18 @@ inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_byt
   return g;
 }
 
-// An inline pool's scales sit 2 PS D bytes past its codes; a plain pool's
-// are a separate array (one that starts inside the codes is an inline buffer
-// passed with the plain dtype, refused rather than misread or overwritten).
+// An inline pool's scales sit inline_scale_offset() bytes past its codes; a
+// plain pool's are a separate array (one that starts inside the codes is an
+// inline buffer passed with the plain dtype, refused rather than misread or
+// overwritten).
 inline int check_pool_scales(int kv_dtype, const void* kv_pool, const void* kv_scales, int KH, int PS, int D, int L,
                              int P, const char* who) {
   const char* pool = static_cast<const char*>(kv_pool);
   const char* sc = static_cast<const char*>(kv_scales);
   if (inline_pool(kv_dtype)) {
-    if (sc != pool + 2LL * PS * D) {
-      set_error("%s: an inline pool's kv_scales must point %lld bytes past kv_pool", who, 2LL * PS * D);
+    const long long off = inline_scale_offset(PS, D);
+    if (sc != pool + off) {
+      set_error("%s: an inline pool's kv_scales must point %lld bytes past kv_pool", who, off);
       return VRM_ERR_ARG;
     }
   } else if (sc && sc >= pool && sc < pool + (long long)P * L * 2 * KH * PS * D) {

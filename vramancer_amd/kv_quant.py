@@ -27,16 +27,20 @@ Two memory layouts hold the same logical tensors:
 
 * ``plain``: ``kv_pool`` a dense ``[P, L, 2, KH, PS, D]`` array and
   ``kv_scales`` a separate dense array;
-* ``inline`` (what ``allocate_pool`` returns by default): one byte buffer of
-  ``P * L`` slabs, each holding per kv-head its K codes, V codes and K / V
-  scales side by side (int8: ``PS * (2 D + 8)`` bytes per kv-head; fp8:
-  ``2 PS D + 16``).  ``kv_pool`` and ``kv_scales`` are strided views of that
-  buffer with the usual shapes, so indexing them reads the same values as in
-  the plain layout.  A layer's page is one contiguous run per kv-head, and
-  at the tuned shapes the slab (33 KB at KH=8, PS=16, D=128) keeps the
-  pages of a layer off the power-of-two strides that HBM reads slower when
-  pages are scattered.  ``pool_dtype_code`` tells the kernels which layout a
-  pair of tensors has.
+* ``inline``: one byte buffer of ``P * L`` slabs, each holding per kv-head
+  its K codes, V codes and K / V scales side by side (int8: ``PS * (2 D +
+  8)`` bytes per kv-head; fp8: ``2 PS D + 128``).  ``kv_pool`` and
+  ``kv_scales`` are strided views of that buffer with the usual shapes, so
+  indexing them reads the same values as in the plain layout.  A layer's page
+  is one contiguous run per kv-head, and the slab (33 KB at KH=8, PS=16,
+  D=128) keeps the pages of a layer off the power-of-two strides that HBM
+  reads slower when pages are scattered over a pool of many layers.
+
+``allocate_pool`` makes int8 pools inline (the 14B decode over a 48-layer
+pool: 4 % faster than plain, and no slower elsewhere measured) and fp8 pools
+plain (the ragged work-item decode reads their one-float page scales faster
+from the small separate array: 1-7 % in the measured shapes).
+``pool_dtype_code`` tells the kernels which layout a pair of tensors has.
 """
 from __future__ import annotations
 
@@ -47,6 +51,7 @@ from . import _lib
 __all__ = [
     "logical_view",
     "allocate_pool",
+    "default_layout",
     "abi_dtype_code",
     "pool_dtype_code",
     "pool_layout",
@@ -72,26 +77,36 @@ LAYOUTS = ("inline", "plain")
 
 
 def _inline_geometry(num_layers: int, num_kv_heads: int, page_size: int, head_dim: int, fp8: bool):
-    """(slab bytes, kv-head record bytes, code strides, scale strides) of the
-    inline layout; strides in elements of the code / float32 views."""
+    """(slab bytes, byte offset of the scales, code strides, scale strides) of
+    the inline layout; strides in elements of the code / float32 views."""
     L, KH, PS, D = num_layers, num_kv_heads, page_size, head_dim
-    head = 2 * PS * D + 16 if fp8 else PS * (2 * D + 8)
+    # per kv-head a record of K codes, V codes, K scales, V scales (fp8: one
+    # scale each, the record padded to 128 bytes past the codes)
+    head = 2 * PS * D + 128 if fp8 else PS * (2 * D + 8)
     slab = KH * head
-    codes = (L * slab, slab, PS * D, head, D, 1)
+    scale_off = 2 * PS * D
     if fp8:
         scales = (L * slab // 4, slab // 4, 1, head // 4)
     else:
         scales = (L * slab // 4, slab // 4, PS, head // 4, 1)
-    return slab, head, codes, scales
+    codes = (L * slab, slab, PS * D, head, D, 1)
+    return slab, scale_off, codes, scales
+
+
+def default_layout(codec: str) -> str:
+    """The memory layout ``allocate_pool`` picks for a codec."""
+    _codec_dtype(codec)
+    return "inline" if codec == "int8" else "plain"
 
 
 def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, head_dim: int, codec: str,
-                  page_size: int = 16, device: Any = "cuda", layout: str = "inline") -> Tuple[Any, Any]:
-    """Zero-initialised (codes, scales) for a quantized pool, in the inline
-    layout (the default) or the plain one."""
+                  page_size: int = 16, device: Any = "cuda", layout: Optional[str] = None) -> Tuple[Any, Any]:
+    """Zero-initialised (codes, scales) for a quantized pool, in the given
+    layout ("inline" or "plain"; by default ``default_layout(codec)``)."""
     import torch
 
     dtype = _codec_dtype(codec)
+    layout = layout or default_layout(codec)
     P, L, KH, PS, D = num_pages, num_layers, num_kv_heads, page_size, head_dim
     scale_shape = (P, L, 2, KH, PS) if codec == "int8" else (P, L, 2, KH)
     if layout == "plain":
@@ -101,10 +116,10 @@ def allocate_pool(num_pages: int, num_layers: int, num_kv_heads: int, head_dim: 
         raise ValueError(f"unknown layout {layout!r}; expected one of {LAYOUTS}")
     if D % 16 or PS % 4:
         raise ValueError(f"quantized pools need head_dim % 16 == 0 and page_size % 4 == 0 (got {D}, {PS})")
-    slab, _, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, codec == "fp8")
+    slab, scale_off, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, codec == "fp8")
     buf = torch.zeros(P * L * slab, dtype=torch.uint8, device=device)
     pool = buf.view(dtype).as_strided((P, L, 2, KH, PS, D), code_strides)
-    scales = buf.view(torch.float32).as_strided(scale_shape, scale_strides, storage_offset=2 * PS * D // 4)
+    scales = buf.view(torch.float32).as_strided(scale_shape, scale_strides, storage_offset=scale_off // 4)
     return pool, scales
 
 
@@ -121,9 +136,9 @@ def pool_layout(kv_pool, kv_scales) -> Optional[str]:
         return None
     P, L, two, KH, PS, D = kv_pool.shape
     fp8 = _lib.kv_dtype_code(kv_pool.dtype) == _lib.VRM_KV_FP8E4M3
-    _, _, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, fp8)
+    _, scale_off, code_strides, scale_strides = _inline_geometry(L, KH, PS, D, fp8)
     if (_same_strides(kv_pool, code_strides) and _same_strides(kv_scales, scale_strides)
-            and kv_scales.data_ptr() == kv_pool.data_ptr() + 2 * PS * D):
+            and kv_scales.data_ptr() == kv_pool.data_ptr() + scale_off):
         return "inline"
     return None
 

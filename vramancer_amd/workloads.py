@@ -152,12 +152,14 @@ def _kv_pages(cfg: DecodeConfig, n: int, gen: torch.Generator, device, outlier_i
 
 
 def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: Sequence[int] = (0,),
-                       chunk_pages: int = 2048) -> dict:
+                       chunk_pages: int = 2048, layout: Optional[str] = None) -> dict:
     """Builds (query, kv_pool, kv_scales, page_table, context_lens) on ``device``.
 
     Only the layers in ``layers`` are filled; the others stay zero (they are
     part of the page stride, not of the attended data).  Quantized pools are
-    filled through the library's page quantizer from bf16 rows.
+    filled through the library's page quantizer from bf16 rows, in the given
+    memory layout (``kv_quant.allocate_pool``: "inline", "plain", or None for
+    the codec's default).
     """
     from . import kv_quant
 
@@ -200,7 +202,7 @@ def make_decode_inputs(cfg: DecodeConfig, device="cuda", seed: int = 0, layers: 
         dtype = None
     elif cfg.codec in ("int8", "fp8"):
         dtype = _pool_dtype(cfg.codec)
-        kv_pool, kv_scales = kv_quant.allocate_pool(P, L, KH, D, cfg.codec, PS, device)
+        kv_pool, kv_scales = kv_quant.allocate_pool(P, L, KH, D, cfg.codec, PS, device, layout=layout)
     else:
         dtype = _pool_dtype(cfg.codec)
         kv_pool = torch.zeros((P, L, 2, KH, PS, D), dtype=dtype, device=device)
