@@ -159,6 +159,10 @@ int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_sc
  * race and must be serialised by the caller.  Same arguments, results and
  * supported shapes as vrm_paged_decode otherwise.
  */
+/* The array is part of the code object that also holds the work-item and
+ * TurboQuant decode kernels: any process that runs one of them on a GPU
+ * holds these 64 MiB there until it ends, whether or not it calls this
+ * entry. */
 #define VRM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const float* kv_scales,
                              const int32_t* page_table, const int32_t* context_lens, float* out,

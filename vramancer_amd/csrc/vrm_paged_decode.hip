@@ -27,6 +27,7 @@
 
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <utility>
 
 namespace vrm {
@@ -34,27 +35,32 @@ namespace dec {
 
 // Work items one resident round of `kernel` holds: resident wavefronts (CU
 // count x workgroups per CU from the occupancy query, capped at
-// kMaxTargetWaves) over the wavefronts of one item.  Cached per kernel.
+// kMaxTargetWaves) over the wavefronts of one item.  Cached per (device,
+// kernel, workgroup size, LDS bytes): the generic kernels' LDS depends on the
+// call's head_dim or TurboQuant setting, and with it their occupancy.
 int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int units) {
+  using Key = std::tuple<int, const void*, int, size_t>;
   static std::mutex mu;
-  static std::map<std::pair<const void*, int>, int> cache;
+  static std::map<Key, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const Key key{dev, kernel, waves_per_block, lds_bytes};
   int waves = 0;
   {
     std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find({kernel, waves_per_block});
+    auto it = cache.find(key);
     if (it != cache.end()) waves = it->second;
   }
   if (waves == 0) {
-    int dev = 0, cus = 0, blocks = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    int cus = 0, blocks = 0;
+    if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64 * waves_per_block, lds_bytes) != hipSuccess ||
         blocks <= 0)
       blocks = 1;
     waves = cus * blocks * waves_per_block;
     std::lock_guard<std::mutex> lock(mu);
-    cache[{kernel, waves_per_block}] = waves;
+    cache[key] = waves;
   }
   return std::max(1, std::min(waves, kMaxTargetWaves) / units);
 }
