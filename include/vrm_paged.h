@@ -329,7 +329,9 @@ int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales, int kv_dty
  *   radius      [N] float16 bits; angles [N][padded_dim-1] uint8, level-major
  *               (level 0 first); qjl_signs [N][qjl_dim] uint8 (0/1);
  *               qjl_norms [N] float16 bits
- * Supported: padded_dim in {64, 128, 256}, 1 <= bits <= 8, qjl_dim <= 256.
+ * Supported: padded_dim a power of two from 2 to 256 (head_dim 1 .. 256, as
+ * the reference pads any head_dim to 2^ceil(log2 max(head_dim, 2)),
+ * core/kv_quantizer.py:225), 1 <= bits <= 8, qjl_dim <= 4 padded_dim.
  */
 int vrm_turboquant_compress(const void* kv, int src_dtype, int N, int head_dim,
                             int padded_dim, int n_levels, int bits, int qjl_dim,
@@ -408,8 +410,8 @@ int vrm_unpack_bits(const uint8_t* packed, long long rows, int M, int bits, uint
  * of vrm_tq_slice_bytes_ps() per (page, layer, K/V, kv-head) holding the
  * page's tokens: angle bins, fp16 radius and, for K, the QJL sign bits and the
  * fp16 residual norm.  Every compressor setting of the reference's
- * KVCacheCompressor (core/kv_quantizer.py:205-240) with head_dim 33..256
- * (padded_dim 64 / 128 / 256), 1..8 bits per angle and qjl_dim 1..256 is
+ * KVCacheCompressor (core/kv_quantizer.py:205-240) with head_dim 1..256
+ * (padded_dim 2, 4, ..., 256), 1..8 bits per angle and qjl_dim 1..256 is
  * served, at any page size.  head_dim 33..128 with the compressor's default
  * qjl_dim (padded_dim / 2: 32 or 64), 2..4 bits and 16-token pages use tuned
  * slices (angle bins in a lane-friendly order of the reference's

@@ -32,6 +32,13 @@ CASES = [
     ("d64_b8_n", 64, 8, 42, 64, "normal_f32"),
     ("d64_b2_n", 64, 2, 5, 64, "normal_f32"),
     ("d128_b4_single", 128, 4, 99, 1, "normal_f32"),
+    # head_dims below 33: padded to 32, 16, 8 and 2 (the smallest padded dim)
+    ("d32_b3_n", 32, 3, 11, 96, "normal_f32"),
+    ("d32_b4_t", 32, 4, 12, 96, "student_t_bf16"),
+    ("d16_b3_n", 16, 3, 13, 96, "normal_f32"),
+    ("d8_b3_n", 8, 3, 14, 96, "normal_f32"),
+    ("d5_b4_n", 5, 4, 15, 96, "normal_f32"),
+    ("d2_b3_n", 2, 3, 16, 96, "normal_f32"),
 ]
 
 

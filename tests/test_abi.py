@@ -233,11 +233,14 @@ def test_tq_slice_sizes():
     cases = [  # head_dim, bits, qjl_dim, page_size, padded_dim
         (96, 3, 64, 4, 128), (64, 1, 32, 16, 64), (64, 8, 33, 5, 64), (256, 5, 256, 16, 256),
         (33, 2, 1, 1, 64), (128, 4, 64, 8, 128), (128, 1, 64, 16, 128), (200, 7, 100, 3, 256),
+        # head_dims below 33 pad to 32, 16, ..., 2 (the reference's 2^ceil(log2 max(head_dim, 2)))
+        (32, 3, 16, 16, 32), (32, 3, 64, 16, 32), (17, 4, 16, 16, 32), (16, 3, 8, 16, 16), (8, 2, 4, 8, 8),
+        (5, 4, 4, 16, 8), (3, 3, 2, 16, 4), (2, 3, 1, 16, 2), (1, 8, 1, 4, 2),
     ]
     for hd, bits, qjl, ps, pd in cases:
         rec = 4 * (-(-(pd - 1) * bits // 32)) + 4 * (-(-qjl // 32)) + 4
         assert lib.vrm_tq_slice_bytes_ps(hd, bits, qjl, ps) == ps * rec, (hd, bits, qjl, ps)
-    for bad in [(32, 3, 64, 16), (257, 3, 64, 16), (96, 0, 64, 16), (96, 9, 64, 16), (96, 3, 0, 16),
+    for bad in [(0, 3, 64, 16), (257, 3, 64, 16), (96, 0, 64, 16), (96, 9, 64, 16), (96, 3, 0, 16),
                 (96, 3, 257, 16), (96, 3, 64, 0)]:
         assert lib.vrm_tq_slice_bytes_ps(*bad) == 0, bad
 

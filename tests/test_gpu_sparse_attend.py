@@ -32,7 +32,9 @@ def _say(msg):
 
 @pytest.mark.parametrize("head_dim,bits,qjl,M,N", [(128, 3, None, 5, 700), (64, 4, 96, 70, 129), (96, 2, None, 1, 33),
                                                     (256, 4, None, 3, 300), (128, 4, None, 40, 4101),
-                                                    (128, 2, None, 17, 33), (128, 3, None, 1, 1), (128, 8, None, 3, 50)])
+                                                    (128, 2, None, 17, 33), (128, 3, None, 1, 1), (128, 8, None, 3, 50),
+                                                    (32, 3, None, 5, 70), (16, 4, 24, 3, 33), (8, 3, None, 2, 17),
+                                                    (2, 3, None, 3, 9)])
 def test_native_score_matches_oracle(head_dim, bits, qjl, M, N):
     _say(f"score d{head_dim} b{bits} qjl {qjl} M{M} N{N}")
     p = TQ.make_params(head_dim, bits, qjl_dim=qjl, seed=head_dim + bits)

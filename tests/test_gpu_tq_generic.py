@@ -41,6 +41,9 @@ SETTINGS = [
     # head_dim 33 .. 64 at 32 QJL rows that of head_dim 64
     (96, 3, None, 16), (80, 4, None, 16), (65, 2, None, 16), (64, 2, None, 16), (48, 4, None, 16),
     (33, 3, None, 16),
+    # head_dim 1 .. 32: padded dims 2 .. 32, generic slices
+    (32, 3, None, 16), (32, 4, 40, 5), (17, 2, None, 16), (16, 3, None, 8), (8, 4, None, 16), (5, 3, 3, 4),
+    (2, 3, None, 16), (1, 8, None, 3),
 ]
 
 
@@ -203,6 +206,8 @@ DECODE = [  # head_dim, bits, qjl_dim, page size, H, KH
     (128, 3, 32, 16, 8, 2), (96, 3, None, 16, 40, 8), (80, 4, None, 16, 12, 4), (65, 2, None, 16, 8, 1),
     (64, 2, None, 16, 32, 4), (64, 4, None, 16, 16, 2), (48, 3, None, 16, 12, 3), (33, 4, None, 16, 8, 1),
     (64, 3, None, 16, 40, 8), (64, 3, 16, 16, 28, 4),
+    (32, 3, None, 16, 8, 2), (32, 4, None, 16, 40, 8), (24, 2, 20, 5, 6, 3), (16, 4, None, 16, 12, 4),
+    (8, 3, None, 8, 8, 2), (3, 5, None, 16, 4, 4), (2, 3, None, 16, 4, 1),
 ]
 
 
@@ -219,7 +224,7 @@ def test_generic_decode_turbo_matches_oracle(case):
 
 
 @pytest.mark.parametrize("setting", [(96, 3, None, 4), (64, 2, None, 16), (256, 4, None, 8), (64, 4, None, 16),
-                                     (56, 3, None, 16)], ids=_sid)
+                                     (56, 3, None, 16), (32, 3, None, 16), (8, 4, None, 4)], ids=_sid)
 def test_generic_decode_turbo_lse_and_no_qjl(setting):
     """The log-sum-exp output, with and without the QJL term: lse equals
     ln sum_t exp(scale score_t) of the oracle's scores, and without the QJL
@@ -323,21 +328,23 @@ def _mgr_codes_match(m, rows, layer):
     return got
 
 
-def test_manager_head_dim_96_page_4():
+@pytest.mark.parametrize("head_dim", [96, 16])
+def test_manager_head_dim_96_page_4(head_dim):
     """The reference's tests/test_turboquant_integration.py:232-252: a
     manager with head_dim 96, 4-token pages, one layer and one kv-head takes
     a token through write_kv and flush_compression, and the slot then holds
     codes; here the codes are also checked against the compressor's and the
-    request (grown to 11 tokens, three pages) is attended."""
-    _say("manager d96 ps4")
+    request (grown to 11 tokens, three pages) is attended.  The same scenario
+    at head_dim 16 (padded dim 16, 8 QJL rows)."""
+    _say(f"manager d{head_dim} ps4")
     torch.manual_seed(21)
-    m = PagedKVCacheManager(PagedKVConfig(page_size=4, num_layers=1, num_kv_heads=1, head_dim=96, max_pages=8,
+    m = PagedKVCacheManager(PagedKVConfig(page_size=4, num_layers=1, num_kv_heads=1, head_dim=head_dim, max_pages=8,
                                           device=DEV, kv_compression="turboquant"))
     assert m.kv_compression_active is True
     m.allocate("edge1")
     page_id, slot = m.append_token("edge1")
     g = torch.Generator().manual_seed(1)
-    key, value = torch.randn(1, 96, generator=g), torch.randn(1, 96, generator=g)
+    key, value = torch.randn(1, head_dim, generator=g), torch.randn(1, head_dim, generator=g)
     m.write_kv("edge1", 0, page_id, slot, key.to(DEV), value.to(DEV))
     m.flush_compression()
     torch.cuda.synchronize()
@@ -345,7 +352,7 @@ def test_manager_head_dim_96_page_4():
     rows = {(page_id, slot): (key, value)}
     for _ in range(10):
         page_id, slot = m.append_token("edge1")
-        key, value = torch.randn(1, 96, generator=g), torch.randn(1, 96, generator=g)
+        key, value = torch.randn(1, head_dim, generator=g), torch.randn(1, head_dim, generator=g)
         m.write_kv("edge1", 0, page_id, slot, key.to(DEV), value.to(DEV))
         rows[(page_id, slot)] = (key, value)
     m.flush_compression()
@@ -353,14 +360,14 @@ def test_manager_head_dim_96_page_4():
     pages = m._page_tables["edge1"].pages
     assert len(pages) == 3 and m.stats()["compressed_pages"] == 3
     codes = _mgr_codes_match(m, rows, 0)
-    q = torch.randn(2, 96, generator=g)
+    q = torch.randn(2, head_dim, generator=g)
     out = m.compute_attention_turbo(q.to(DEV), "edge1", 0)
     torch.cuda.synchronize()
     table = torch.tensor([pages], dtype=torch.int32)
     ref = PD.paged_attention_decode_turbo(_params(m._kv_compressor), q[None], codes, table,
                                           torch.tensor([11], dtype=torch.int32), head_map="mod")
-    assert out.shape == (2, 96)
-    _assert_close(out, ref[0], "manager d96 ps4")
+    assert out.shape == (2, head_dim)
+    _assert_close(out, ref[0], f"manager d{head_dim} ps4")
 
 
 def test_manager_head_dim_64_four_layers():
@@ -416,7 +423,7 @@ def test_manager_generic_lazy_bulk_compression():
     _assert_close(out, ref[0], "lazy bulk d96")
 
 
-@pytest.mark.parametrize("head_dim,bits", [(64, 3), (96, 2), (256, 5)])
+@pytest.mark.parametrize("head_dim,bits", [(64, 3), (96, 2), (256, 5), (32, 3), (16, 4), (8, 2)])
 def test_hf_cache_generic_decode_attention_matches_materialised(head_dim, bits):
     """The Hugging Face TurboQuant cache at other head dims: the paged decode
     step (TurboQuant pages + residual merged by log-sum-exp) against

@@ -127,7 +127,8 @@ def test_compress_large_student_t_bit_exact(bits):
     assert torch.equal(dec, TQ.decompress(p, ref))
 
 
-@pytest.mark.parametrize("head_dim,bits", [(96, 3), (64, 8), (256, 4), (128, 1)])
+@pytest.mark.parametrize("head_dim,bits", [(96, 3), (64, 8), (256, 4), (128, 1), (32, 3), (24, 4), (16, 3), (8, 5),
+                                           (3, 3), (2, 4), (1, 3)])
 def test_compress_other_shapes(head_dim, bits):
     _say(f"shape d{head_dim} b{bits}")
     p = TQ.make_params(head_dim, bits, seed=head_dim + bits)
@@ -140,7 +141,7 @@ def test_compress_other_shapes(head_dim, bits):
     assert torch.equal(dec, TQ.decompress(p, ref))
 
 
-@pytest.mark.parametrize("head_dim,bits", [(128, 3), (96, 2), (256, 4)])
+@pytest.mark.parametrize("head_dim,bits", [(128, 3), (96, 2), (256, 4), (32, 3), (8, 4)])
 def test_compress_bulk_launch_equals_small_launches(head_dim, bits):
     """A launch of 4,097 rows (several rows per workgroup, the last group
     partial) gives the codes of the same rows compressed 1,000 at a time."""

@@ -1,5 +1,5 @@
 // Paged decode over TurboQuant pages in the generic layout (vrm_tq_layout.h,
-// GenLayout): head_dim 33 .. 256 (padded to 64 / 128 / 256), 1 to 8 bits per
+// GenLayout): head_dim 1 .. 256 (padded to a power of two from 2 to 256), 1 to 8 bits per
 // angle, any QJL width up to 256 and any page size.  The tuned layout (head_dim
 // 128, 64 QJL rows, 2 to 4 bits, page 16) has its own kernel
 // (vrm_decode_tq.hip); this one computes the same attention,
@@ -64,7 +64,7 @@ template <int PD>
 __global__ void __launch_bounds__(64) decode_tq_gen_kernel(DecodeArgs a, TqDecodeArgs tq, tq::GenLayout gl, int D,
                                                            int G) {
   constexpr int NL = __builtin_ctz(PD);
-  constexpr int PER = PD / 64;
+  constexpr int PER = tq_per_lane(PD);  // lanes past a row of fewer than 64 dims hold nothing
   extern __shared__ __align__(16) float tg_lds[];
   const TqgLds lo = tqg_lds(gl);
   const int nb = 1 << gl.bits;
@@ -99,11 +99,12 @@ __global__ void __launch_bounds__(64) decode_tq_gen_kernel(DecodeArgs a, TqDecod
     for (int k = 0; k < PER; ++k) {
       const int e = k * 64 + lane;
       const float x = e < D ? a.query[((size_t)b * a.H + h0 + g) * D + e] : 0.f;
-      v[k] = __fmul_rn(x, tq.signs[e]);
+      v[k] = e < PD ? __fmul_rn(x, tq.signs[e]) : 0.f;
     }
     fwht<PD>(v, lane);
 #pragma unroll
-    for (int k = 0; k < PER; ++k) qrot[g * PD + k * 64 + lane] = __fdiv_rn(v[k], root);
+    for (int k = 0; k < PER; ++k)
+      if (k * 64 + lane < PD) qrot[g * PD + k * 64 + lane] = __fdiv_rn(v[k], root);
   }
   __syncthreads();
   // q_proj = q_rot JL^T (core/kv_quantizer.py:319-321)
@@ -230,6 +231,7 @@ __global__ void __launch_bounds__(64) decode_tq_gen_kernel(DecodeArgs a, TqDecod
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const int e = k * 64 + lane;
+        if (PD < 64 && e >= PD) continue;  // no element of the row
         float r = vrad;
 #pragma unroll
         for (int l = NL - 1; l >= 0; --l) {
@@ -290,6 +292,11 @@ hipError_t launch_tq_generic(const DecodeArgs& a, const TqDecodeArgs& tq, const 
                              hipStream_t st) {
   const int G = pick_group_tile(a.H / a.KH, kTqgMaxG);
   switch (gl.pd) {
+    case 2: return launch_tqg<2>(a, tq, gl, B, D, G, st);
+    case 4: return launch_tqg<4>(a, tq, gl, B, D, G, st);
+    case 8: return launch_tqg<8>(a, tq, gl, B, D, G, st);
+    case 16: return launch_tqg<16>(a, tq, gl, B, D, G, st);
+    case 32: return launch_tqg<32>(a, tq, gl, B, D, G, st);
     case 64: return launch_tqg<64>(a, tq, gl, B, D, G, st);
     case 128: return launch_tqg<128>(a, tq, gl, B, D, G, st);
     default: return launch_tqg<256>(a, tq, gl, B, D, G, st);

@@ -37,11 +37,17 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
 // several rows whose wavefronts never wait for each other.
 __device__ __forceinline__ void row_sync() { __syncwarp(); }
 
-// In-register Walsh-Hadamard transform of a PD-element row spread as element
-// e -> (lane e % 64, register e / 64); same butterfly order as the reference.
+// Registers per lane of a PD-element row spread as element e -> (lane e % 64,
+// register e / 64); below 64 elements lanes PD .. 63 hold nothing of the row.
+constexpr int tq_per_lane(int pd) { return (pd + 63) / 64; }
+
+// In-register Walsh-Hadamard transform of a PD-element row spread as above;
+// same butterfly order as the reference.  For PD < 64 the lanes past the row
+// exchange among themselves only (lane ^ h < PD for lane < PD), and their
+// values are never used.
 template <int PD>
-__device__ __forceinline__ void fwht(float (&v)[PD / 64], int lane) {
-  constexpr int PER = PD / 64;
+__device__ __forceinline__ void fwht(float (&v)[tq_per_lane(PD)], int lane) {
+  constexpr int PER = tq_per_lane(PD);
 #pragma unroll
   for (int h = 1; h < PD; h <<= 1) {
     if (h < 64) {

@@ -114,8 +114,8 @@ __host__ __device__ inline int bin_index_of(int pd, int g, int s, int bits) {
 }
 
 // ---------------------------------------------------------------------------
-// Generic page layout: every other setting of the compressor (head_dim 33 ..
-// 256, i.e. padded_dim 64 / 128 / 256, 1 to 8 bits per angle, qjl_dim 1 ..
+// Generic page layout: every other setting of the compressor (head_dim 1 ..
+// 256, i.e. padded_dim 2, 4, ..., 256, 1 to 8 bits per angle, qjl_dim 1 ..
 // 256) and any page size.  A slice holds the page's PS tokens as records of
 // record_bytes(), in token order:
 //   angle bits   [angle_dw dwords]   level-major bin b at bits
@@ -126,7 +126,7 @@ __host__ __device__ inline int bin_index_of(int pd, int g, int s, int bits) {
 //   norm         fp16                residual norm (K only; V: zero)
 // ---------------------------------------------------------------------------
 struct GenLayout {
-  int pd;        // padded dim (64, 128, 256)
+  int pd;        // padded dim (2, 4, ..., 256)
   int levels;    // log2(pd)
   int bits;      // bits per angle (1 .. 8)
   int qjl;       // QJL rows
@@ -138,11 +138,12 @@ struct GenLayout {
   __host__ __device__ size_t slice_bytes() const { return (size_t)ps * record_bytes(); }
 };
 
-// Padded dim of a head_dim: the next power of two (the reference's
-// 2^ceil(log2 head_dim), core/kv_quantizer.py:225), or 0 outside 33 .. 256.
+// Padded dim of a head_dim: the next power of two, at least 2 (the
+// reference's 2^ceil(log2 max(head_dim, 2)), core/kv_quantizer.py:225), or 0
+// outside 1 .. 256.
 __host__ __device__ inline int padded_dim_of(int head_dim) {
-  if (head_dim < 33 || head_dim > 256) return 0;
-  int pd = 64;
+  if (head_dim < 1 || head_dim > 256) return 0;
+  int pd = 2;
   while (pd < head_dim) pd <<= 1;
   return pd;
 }
@@ -150,7 +151,8 @@ __host__ __device__ inline int padded_dim_of(int head_dim) {
 __host__ __device__ inline GenLayout gen_layout(int head_dim, int bits, int qjl, int ps) {
   GenLayout g{};
   g.pd = padded_dim_of(head_dim);
-  g.levels = g.pd == 64 ? 6 : g.pd == 128 ? 7 : 8;
+  g.levels = 0;
+  while ((2 << g.levels) <= g.pd) ++g.levels;  // log2(pd)
   g.bits = bits;
   g.qjl = qjl;
   g.ps = ps;

@@ -69,7 +69,8 @@ __device__ __forceinline__ void polar_decode(float radius, const uint8_t* bins, 
                                              float* recon, int lane) {
   row_sync();
 #pragma unroll
-  for (int k = 0; k < PD / 64; ++k) recon[k * 64 + lane] = polar_element<PD>(radius, bins, lut, nb, k * 64 + lane);
+  for (int k = 0; k < tq_per_lane(PD); ++k)
+    if (k * 64 + lane < PD) recon[k * 64 + lane] = polar_element<PD>(radius, bins, lut, nb, k * 64 + lane);
   row_sync();
 }
 
@@ -85,26 +86,27 @@ struct RowLds {
 
 // Rotation and polar encoding of one row (source element e at src[e] for
 // e < head_dim, zero padding above): leaves the level-major bins in w.bins,
-// the rotated row in v (element e in lane e % 64, register e / 64) and in
-// w.rot, and returns the fp32 final radius.
+// the rotated row in v (element e in lane e % 64, register e / 64; lanes past
+// a row of fewer than 64 elements hold zeros) and in w.rot, and returns the
+// fp32 final radius.
 template <int SRC, int PD>
 __device__ __forceinline__ float encode_row(const void* src, size_t first, int head_dim, const float* signs, int bits,
-                                            float (&v)[PD / 64], RowLds<PD>& w, int lane) {
-  constexpr int PER = PD / 64;
+                                            float (&v)[tq_per_lane(PD)], RowLds<PD>& w, int lane) {
+  constexpr int PER = tq_per_lane(PD);
   constexpr int NL = __builtin_ctz(PD);
   const int nb = 1 << bits;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = k * 64 + lane;
     const float x = e < head_dim ? load_row<SRC>(src, first + e) : 0.f;
-    v[k] = __fmul_rn(x, signs[e]);
+    v[k] = e < PD ? __fmul_rn(x, signs[e]) : 0.f;
   }
   fwht<PD>(v, lane);
   const float root = (float)sqrt((double)PD);
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     v[k] = __fdiv_rn(v[k], root);
-    w.rot[k * 64 + lane] = v[k];
+    if (k * 64 + lane < PD) w.rot[k * 64 + lane] = v[k];
   }
   row_sync();
 
@@ -142,23 +144,24 @@ __device__ __forceinline__ float encode_row(const void* src, size_t first, int h
 
 // Residual against the reconstruction from the fp32 radius, its QJL signs
 // (float64 dot products; sign(j) is handed to put_sign) and the residual norm
-// (eight interleaved fused accumulators summed in order, as PyTorch's CPU
-// 2-norm reduces a 128-float row).  Returns the norm.
+// as PyTorch's CPU 2-norm reduces a row: eight interleaved fused accumulators
+// summed in order for rows of 4 floats or more, one fused chain for a row of
+// 2 (measured against torch.norm at 2 .. 256 floats).  Returns the norm.
 template <int PD, typename PutSign>
-__device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius, const float* lut, int bits,
+__device__ __forceinline__ float qjl_row(const float (&v)[tq_per_lane(PD)], float radius, const float* lut, int bits,
                                          const float* jl, int qjl_dim, RowLds<PD>& w, int lane, PutSign put_sign) {
-  constexpr int PER = PD / 64;
-  float res[PER];
+  constexpr int PER = tq_per_lane(PD);
 #pragma unroll
-  for (int k = 0; k < PER; ++k) res[k] = __fsub_rn(v[k], polar_element<PD>(radius, w.bins, lut, 1 << bits, k * 64 + lane));
-#pragma unroll
-  for (int k = 0; k < PER; ++k) w.res[k * 64 + lane] = (double)res[k];
+  for (int k = 0; k < PER; ++k) {
+    const int e = k * 64 + lane;
+    if (e < PD) w.res[e] = (double)__fsub_rn(v[k], polar_element<PD>(radius, w.bins, lut, 1 << bits, e));
+  }
   row_sync();
   // Lane j walks row j of the JL matrix.  With a 16-byte aligned matrix (every
   // row is then aligned, PD being a multiple of 4) it reads four floats per
   // load; the residual comes as doubles, two per LDS broadcast.  The
   // accumulation order is the element order either way.
-  const bool vec = (reinterpret_cast<uintptr_t>(jl) & 15) == 0;
+  const bool vec = PD >= 4 && (reinterpret_cast<uintptr_t>(jl) & 15) == 0;
   const double2* r2 = reinterpret_cast<const double2*>(w.res);
   for (int j = lane; j < qjl_dim; j += 64) {
     const float* jr = jl + (size_t)j * PD;
@@ -179,13 +182,19 @@ __device__ __forceinline__ float qjl_row(const float (&v)[PD / 64], float radius
     }
     put_sign(j, s > 0.0);
   }
+  if constexpr (PD == 2) {
+    const float x0 = (float)w.res[0], x1 = (float)w.res[1];  // exact: widened from floats
+    return sqrt_rn(fmaf(x1, x1, __fmul_rn(x0, x0)));
+  }
   if (lane < 8) {
-    float x[PD / 8];
-#pragma unroll
-    for (int m = 0; m < PD / 8; ++m) x[m] = (float)w.res[lane + 8 * m];  // exact: widened from a float
     float acc = 0.f;
 #pragma unroll
-    for (int m = 0; m < PD / 8; ++m) acc = fmaf(x[m], x[m], acc);
+    for (int m = 0; m < (PD + 7) / 8; ++m) {
+      if (lane + 8 * m < PD) {
+        const float x = (float)w.res[lane + 8 * m];  // exact: widened from a float
+        acc = fmaf(x, x, acc);
+      }
+    }
     w.norm_acc[lane] = acc;
   }
   row_sync();
@@ -215,7 +224,7 @@ __global__ void __launch_bounds__(64 * ROWS) tq_compress_kernel(TqArgs a) {
   const int row = blockIdx.x * ROWS + (int)(threadIdx.x >> 6);
   if (row >= a.N) return;
   RowLds<PD>& w = rows_lds[threadIdx.x >> 6];
-  float v[PD / 64];
+  float v[tq_per_lane(PD)];
   const float radius = encode_row<SRC, PD>(a.kv, (size_t)row * a.head_dim, a.head_dim, a.signs, a.bits, v, w, lane);
   for (int i = lane; i < PD - 1; i += 64) a.angles[(size_t)row * (PD - 1) + i] = w.bins[i];
   if (lane == 0) a.radius[row] = f32_to_f16_bits(radius);
@@ -296,7 +305,7 @@ __global__ void __launch_bounds__(64 * ROWS) tq_pool_write_kernel(TqPoolArgs a) 
     }
     return;
   }
-  float v[PD / 64];
+  float v[tq_per_lane(PD)];
   const void* src = kv ? a.value : a.key;
   const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, BITS, v, w, lane);
   // angle record: the PD slots (4 quarters of PD / 4) as one bit stream, so
@@ -368,7 +377,7 @@ __global__ void __launch_bounds__(64) tq_pool_write_gen_kernel(TqPoolArgs a, tq:
     for (int i = lane; i < g.record_bytes() / 4; i += 64) rec32[i] = 0;
     return;
   }
-  float v[PD / 64];
+  float v[tq_per_lane(PD)];
   const void* src = kv ? a.value : a.key;
   const float radius = encode_row<SRC, PD>(src, src_first, a.head_dim, a.signs, g.bits, v, w, lane);
   // angle dword k covers record bits [32 k, 32 k + 32): bins from the one holding bit 32 k
@@ -481,7 +490,7 @@ __global__ void __launch_bounds__(64) tq_pool_read_kernel(const uint8_t* pool, c
 
 template <int PD, int ROWS>
 __global__ void __launch_bounds__(64 * ROWS) tq_decompress_kernel(TqArgs a, int rotated) {
-  constexpr int PER = PD / 64;
+  constexpr int PER = tq_per_lane(PD);
   __shared__ uint8_t bins_rows[ROWS][PD];
   __shared__ float lut_lds[64];  // the angle table for up to 4 bits (4 x 16 entries)
   const int lane = threadIdx.x & 63;
@@ -496,16 +505,21 @@ __global__ void __launch_bounds__(64 * ROWS) tq_decompress_kernel(TqArgs a, int 
   const float radius = f16_bits_to_f32(a.radius[row]);
   row_sync();
   float v[PER];
+  // lanes past a row of fewer than 64 elements decode nothing (their bins
+  // would lie past the row's)
   if (lut_in_lds) {  // two copies of the loop, each with the table's address space known
 #pragma unroll
-    for (int k = 0; k < PER; ++k) v[k] = polar_element<PD>(radius, bins, lut_lds, nb, k * 64 + lane);
+    for (int k = 0; k < PER; ++k)
+      v[k] = k * 64 + lane < PD ? polar_element<PD>(radius, bins, lut_lds, nb, k * 64 + lane) : 0.f;
   } else {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) v[k] = polar_element<PD>(radius, bins, a.lut, nb, k * 64 + lane);
+    for (int k = 0; k < PER; ++k)
+      v[k] = k * 64 + lane < PD ? polar_element<PD>(radius, bins, a.lut, nb, k * 64 + lane) : 0.f;
   }
   if (rotated) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) a.out[(size_t)row * PD + k * 64 + lane] = v[k];
+    for (int k = 0; k < PER; ++k)
+      if (k * 64 + lane < PD) a.out[(size_t)row * PD + k * 64 + lane] = v[k];
     return;
   }
   fwht<PD>(v, lane);
@@ -513,8 +527,7 @@ __global__ void __launch_bounds__(64 * ROWS) tq_decompress_kernel(TqArgs a, int 
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = k * 64 + lane;
-    const float y = __fmul_rn(__fdiv_rn(v[k], root), a.signs[e]);
-    if (e < a.head_dim) a.out[(size_t)row * a.head_dim + e] = y;
+    if (e < a.head_dim) a.out[(size_t)row * a.head_dim + e] = __fmul_rn(__fdiv_rn(v[k], root), a.signs[e]);
   }
 }
 
@@ -524,7 +537,7 @@ __global__ void __launch_bounds__(64 * ROWS) tq_decompress_kernel(TqArgs a, int 
 template <int PD>
 __global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_dim, const float* signs,
                                                       const float* jl, int qjl_dim, float* ws, int permuted) {
-  constexpr int PER = PD / 64;
+  constexpr int PER = tq_per_lane(PD);
   __shared__ float rot[PD];
   const int lane = threadIdx.x;
   const int m = blockIdx.x;
@@ -533,7 +546,7 @@ __global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_d
   for (int k = 0; k < PER; ++k) {
     const int e = k * 64 + lane;
     const float x = e < head_dim ? q[(size_t)m * head_dim + e] : 0.f;
-    v[k] = __fmul_rn(x, signs[e]);
+    v[k] = e < PD ? __fmul_rn(x, signs[e]) : 0.f;
   }
   fwht<PD>(v, lane);
   const float root = (float)sqrt((double)PD);
@@ -544,8 +557,10 @@ __global__ void __launch_bounds__(64) tq_query_kernel(const float* q, int head_d
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     v[k] = __fdiv_rn(v[k], root);
-    rot[k * 64 + lane] = v[k];
-    out[at(k * 64 + lane)] = v[k];
+    if (k * 64 + lane < PD) {
+      rot[k * 64 + lane] = v[k];
+      out[at(k * 64 + lane)] = v[k];
+    }
   }
   __syncthreads();
   for (int j = lane; j < qjl_dim; j += 64) {
@@ -772,8 +787,8 @@ int check_tq(int N, int head_dim, int padded_dim, int n_levels, int bits, const 
     set_error("%s: bad sizes (N=%d head_dim=%d padded_dim=%d)", who, N, head_dim, padded_dim);
     return VRM_ERR_ARG;
   }
-  if (padded_dim != 64 && padded_dim != 128 && padded_dim != 256) {
-    set_error("%s: padded_dim %d unsupported (64, 128, 256)", who, padded_dim);
+  if (padded_dim < 2 || padded_dim > 256 || (padded_dim & (padded_dim - 1))) {
+    set_error("%s: padded_dim %d unsupported (a power of two from 2 to 256)", who, padded_dim);
     return VRM_ERR_UNSUPPORTED;
   }
   if ((1 << n_levels) != padded_dim) {
@@ -839,6 +854,11 @@ extern "C" int vrm_turboquant_compress(const void* kv, int src_dtype, int N, int
     hipLaunchKernelGGL((tq_compress_kernel<SRC, PDV, 1, false>), dim3(N), dim3(64), 0, st, a)
 #define VRM_TQ_PD(SRC)                                  \
   switch (padded_dim) {                                 \
+    case 2: VRM_TQ_LAUNCH(SRC, 2); break;               \
+    case 4: VRM_TQ_LAUNCH(SRC, 4); break;               \
+    case 8: VRM_TQ_LAUNCH(SRC, 8); break;               \
+    case 16: VRM_TQ_LAUNCH(SRC, 16); break;             \
+    case 32: VRM_TQ_LAUNCH(SRC, 32); break;             \
     case 64: VRM_TQ_LAUNCH(SRC, 64); break;             \
     case 128: VRM_TQ_LAUNCH(SRC, 128); break;           \
     default: VRM_TQ_LAUNCH(SRC, 256); break;            \
@@ -882,6 +902,11 @@ extern "C" int vrm_turboquant_decompress(const uint16_t* radius, const uint8_t* 
   else                                                                                                       \
     hipLaunchKernelGGL((tq_decompress_kernel<PDV, 1>), dim3(N), dim3(64), 0, st, a, rotated)
   switch (padded_dim) {
+    case 2: VRM_TQ_DECOMP(2); break;
+    case 4: VRM_TQ_DECOMP(4); break;
+    case 8: VRM_TQ_DECOMP(8); break;
+    case 16: VRM_TQ_DECOMP(16); break;
+    case 32: VRM_TQ_DECOMP(32); break;
     case 64: VRM_TQ_DECOMP(64); break;
     case 128: VRM_TQ_DECOMP(128); break;
     default: VRM_TQ_DECOMP(256); break;
@@ -897,7 +922,7 @@ int check_tq_pool(int KH, int D, int PS, int L, int P, int layer_idx, int bits, 
     return VRM_ERR_ARG;
   }
   if (!tq::tuned_layout(D, bits, qjl_dim, PS) && !tq::generic_ok(D, bits, qjl_dim, PS)) {
-    set_error("%s: TurboQuant pages take head_dim 33 .. 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256 and a "
+    set_error("%s: TurboQuant pages take head_dim 1 .. 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256 and a "
               "positive page size (got %d, %d, %d, %d)", who, D, bits, qjl_dim, PS);
     return VRM_ERR_UNSUPPORTED;
   }
@@ -950,11 +975,18 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
   if (!pd) {
     const tq::GenLayout g = tq::gen_layout(D, bits, qjl_dim, PS);
     const dim3 grid(rows, 2);
-#define VRM_TQ_WRITE_GEN(SRC)                                                                                  \
-  switch (g.pd) {                                                                                            \
-    case 64: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 64>), grid, dim3(64), 0, st, a, g); break;     \
-    case 128: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 128>), grid, dim3(64), 0, st, a, g); break;   \
-    default: hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, 256>), grid, dim3(64), 0, st, a, g); break;   \
+#define VRM_TQ_WRITE_GEN_PD(SRC, PDV) \
+  hipLaunchKernelGGL((tq_pool_write_gen_kernel<SRC, PDV>), grid, dim3(64), 0, st, a, g)
+#define VRM_TQ_WRITE_GEN(SRC)                                       \
+  switch (g.pd) {                                                   \
+    case 2: VRM_TQ_WRITE_GEN_PD(SRC, 2); break;                     \
+    case 4: VRM_TQ_WRITE_GEN_PD(SRC, 4); break;                     \
+    case 8: VRM_TQ_WRITE_GEN_PD(SRC, 8); break;                     \
+    case 16: VRM_TQ_WRITE_GEN_PD(SRC, 16); break;                   \
+    case 32: VRM_TQ_WRITE_GEN_PD(SRC, 32); break;                   \
+    case 64: VRM_TQ_WRITE_GEN_PD(SRC, 64); break;                   \
+    case 128: VRM_TQ_WRITE_GEN_PD(SRC, 128); break;                 \
+    default: VRM_TQ_WRITE_GEN_PD(SRC, 256); break;                  \
   }
     switch (src_dtype) {
       case VRM_SRC_F32: VRM_TQ_WRITE_GEN(VRM_SRC_F32); break;
@@ -962,6 +994,7 @@ int tq_pool_write(const void* key, const void* value, int src_dtype, const int32
       default: VRM_TQ_WRITE_GEN(VRM_SRC_BF16); break;
     }
 #undef VRM_TQ_WRITE_GEN
+#undef VRM_TQ_WRITE_GEN_PD
     return launch_status(who);
   }
   // bulk writes pack kBulkRows rows (wavefronts) per workgroup, small ones one
@@ -1102,6 +1135,11 @@ extern "C" int vrm_turboquant_score(const float* q, int M, const uint16_t* radiu
     hipLaunchKernelGGL(tq_score_kernel<PDV>, dim3(N), dim3(64), 0, st, workspace, M, qjl_dim, radius, angles,     \
                        qjl_signs, qjl_norms, N, angle_lut, bits, coef, out_scale, scores)
   switch (padded_dim) {
+    case 2: VRM_TQ_SCORE(2); break;
+    case 4: VRM_TQ_SCORE(4); break;
+    case 8: VRM_TQ_SCORE(8); break;
+    case 16: VRM_TQ_SCORE(16); break;
+    case 32: VRM_TQ_SCORE(32); break;
     case 64: VRM_TQ_SCORE(64); break;
     case 128: VRM_TQ_SCORE(128); break;
     default: VRM_TQ_SCORE(256); break;

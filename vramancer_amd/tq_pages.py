@@ -19,7 +19,7 @@ kv-head h // (H / KH), the mapping of the paged decode path.
 Head_dim 33 .. 128 with the compressor's default QJL rows (padded_dim / 2:
 32 at head_dim <= 64, 64 above), 2 to 4 bits per angle and pages of 16 tokens
 use the tuned layouts and decode kernel; every other compressor setting
-(head_dim 33 .. 256, 1 to 8 bits, QJL rows up to 256) and page size uses the
+(head_dim 1 .. 256, 1 to 8 bits, QJL rows up to 256) and page size uses the
 generic layout and kernels of the same library.
 """
 from __future__ import annotations
@@ -49,15 +49,15 @@ def slice_bytes(bits_per_angle: int, head_dim: int = 128, qjl_dim: int = 64, pag
     """Bytes of one (page, layer, K/V, kv-head) slice for these settings."""
     n = _lib.load().vrm_tq_slice_bytes_ps(head_dim, bits_per_angle, qjl_dim, page_size)
     if n == 0:
-        raise RuntimeError(f"TurboQuant pages take head_dim 33 .. 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256 "
+        raise RuntimeError(f"TurboQuant pages take head_dim 1 .. 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256 "
                            f"(got {head_dim}, {bits_per_angle}, {qjl_dim}, page {page_size})")
     return int(n)
 
 
 def _check_compressor(compressor):
-    if not (33 <= compressor.head_dim <= 256 and 1 <= compressor.bits_per_angle <= 8
+    if not (1 <= compressor.head_dim <= 256 and 1 <= compressor.bits_per_angle <= 8
             and 1 <= compressor.qjl_dim <= 256):
-        raise RuntimeError("TurboQuant pages need a KVCacheCompressor with head_dim 33 .. 256, 1 .. 8 bits per "
+        raise RuntimeError("TurboQuant pages need a KVCacheCompressor with head_dim 1 .. 256, 1 .. 8 bits per "
                            f"angle and qjl_dim 1 .. 256 (got {compressor.head_dim}, {compressor.bits_per_angle}, "
                            f"{compressor.qjl_dim})")
 

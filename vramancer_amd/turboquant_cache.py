@@ -33,7 +33,7 @@ Divergence from the reference, on purpose: a token's codes are written once.
 The reference re-compresses the decompressed older tokens at every spill
 (compress(decompress(old) ++ residual)), which quantises them again.
 
-Takes every compressor setting the TurboQuant pages serve (head_dim 33 ..
+Takes every compressor setting the TurboQuant pages serve (head_dim 1 ..
 256, 1 .. 8 bits per angle, qjl_dim 1 .. 256); a worker-GPU offloader
 (core/offloaded_compressor.py) is not supported.
 """

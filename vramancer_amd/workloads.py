@@ -255,7 +255,7 @@ def algorithmic_bytes(cfg: DecodeConfig, lens: Sequence[int]) -> Dict[str, float
         # radius; padded_dim - 1 angles of `bits` bits, padded_dim / 2 QJL rows (the compressor's
         # defaults, core/kv_quantizer.py:225-229)
         bits = int(cfg.codec[2])
-        pd = 64
+        pd = 2
         while pd < D:
             pd *= 2
         angles = ((pd - 1) * bits + 7) // 8
