@@ -33,6 +33,31 @@ def _assert_close(got, want, what):
                           f"max abs err {err.max().item():.3e}")
 
 
+def _shared_pages(dtype, D, PS):
+    """True where the int8 / fp8 decode runs on workgroups whose wavefronts
+    take page pairs as they free up (page 16, head_dim 64 .. 128): which
+    wavefront sums which pages varies from run to run, so two runs agree to
+    rounding, not bit for bit.  Every other path is deterministic."""
+    return dtype in (torch.int8, torch.float8_e4m3fn) and PS == 16 and 64 <= D <= 128
+
+
+def _assert_rerun(a, b, shared, what):
+    """Two decodes of the same logical inputs: bit-identical on the
+    deterministic paths; on the shared-page ones within rounding of the
+    output's scale, |a - b| <= 1e-5 max|b| + 1e-6.  (The decode's error
+    against the oracle is about 5e-5 wherever the x20 outlier channels make
+    outputs reach 40-50, whatever the row; two runs differ by as much.)"""
+    if shared:
+        a, b = a.float(), b.float()
+        fin = torch.isfinite(b)
+        bar = 1e-5 * b[fin].abs().max() + 1e-6 if fin.any() else 0.0
+        ok = (a == b) | (fin & ((a - b).abs() <= bar))  # equal (infinities included) or close
+        err = torch.where(fin, (a - b).abs(), torch.zeros_like(b))
+        assert ok.all(), f"{what}: {int((~ok).sum())} outside, max abs diff {err.max().item():.3e}"
+    else:
+        assert torch.equal(a, b), what
+
+
 def _oracle(inp, layer):
     pool = inp["kv_pool"].cpu()
     sc = inp["kv_scales"].cpu() if inp["kv_scales"] is not None else None
@@ -186,7 +211,7 @@ def test_partitions_then_merge_equals_fused_call():
                                     table.shape[1], s)
     _lib.check(rc, "merge")
     torch.cuda.synchronize()
-    assert torch.equal(out, out2)
+    _assert_rerun(out, out2, _shared_pages(torch.int8, D, PS), "partitions + merge")
 
 
 @pytest.mark.parametrize("H,KH,D", [(16, 4, 128), (40, 8, 128), (12, 2, 128), (14, 2, 128), (10, 2, 64),
@@ -286,7 +311,7 @@ def test_decode_full_size_int8_sampled_parity_and_relabel_invariance():
     table2 = inv[table.long()].to(torch.int32)
     out2 = paged_attention_decode(q, pool2, table2, lens, 1, kv_scales=sc2)
     torch.cuda.synchronize()
-    assert torch.equal(out, out2)
+    _assert_rerun(out, out2, _shared_pages(torch.int8, 128, 16), "relabelled pool")
 
 
 def test_decode_full_size_q4_sampled_parity_and_relabel_invariance():
@@ -548,7 +573,7 @@ def test_decode_full_size_int8_48_layer_bench_pool():
     del inp
     out2 = paged_attention_decode(q, pool2, table2, lens, 36, kv_scales=sc2)
     torch.cuda.synchronize()
-    assert torch.equal(out, out2)
+    _assert_rerun(out, out2, _shared_pages(torch.int8, 128, 16), "relabelled 48-layer pool")
 
 
 def test_wrappers_reject_bad_out_workspace_and_tables():
@@ -567,7 +592,8 @@ def test_wrappers_reject_bad_out_workspace_and_tables():
                dict(lens=lens[:1])):
         with pytest.raises(RuntimeError):
             run(**kw)
-    torch.testing.assert_close(run(out=torch.empty(2, 8, 128, device=DEV)), ref, rtol=0, atol=0)
+    _assert_rerun(run(out=torch.empty(2, 8, 128, device=DEV)), ref, _shared_pages(torch.int8, 128, 16),
+                  "caller-supplied out")
     packed = torch.zeros(pool.shape[:-1] + (64,), dtype=torch.uint8, device=DEV)
     s4 = torch.ones(pool.shape[:-1] + (4,), dtype=torch.float16, device=DEV)
     with pytest.raises(RuntimeError):
@@ -650,12 +676,12 @@ def test_balanced_decode_garbage_absent_pages_and_lse(dtype):
 @pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
 @pytest.mark.parametrize("D,PS", [(128, 16), (64, 16), (96, 16), (128, 32), (256, 16), (48, 8), (80, 4)])
 def test_inline_layout_decodes_like_the_plain_layout(dtype, D, PS):
-    """The same codes and scales copied into the inline layout give
-    bit-identical outputs and lse through the decode paths that read the
-    pool: the work-item stream kernels (pages of 16 and 32 tokens), the
-    generic kernel (other head_dims and pages) and the no-allocation entry;
-    the balanced decode (head_dim <= 128, page 16) within 1e-5; and they
-    match the oracle."""
+    """The same codes and scales copied into the inline layout give the same
+    outputs and lse through every decode path that reads the pool: the
+    work-item kernels (pages of 16 and 32 tokens), the generic kernel (other
+    head_dims and pages), the no-allocation entry and the balanced decode
+    (bit-identical where the path is deterministic, within 1e-5 where pages
+    are handed out as wavefronts free up); and they match the oracle."""
     _say(f"inline vs plain {dtype} D{D} PS{PS}")
     codec = "int8" if dtype == torch.int8 else "fp8"
     ctxs = [300, 17, 1000, 0, 129, 64]
@@ -688,14 +714,12 @@ def test_inline_layout_decodes_like_the_plain_layout(dtype, D, PS):
             got += [_balanced(d[0], pp, ss, d[3], d[4], 1, lse=lse_b), lse_b]
         outs[name] = got
     torch.cuda.synchronize()
-    # the work-item paths are deterministic: bit-identical; the balanced
-    # decode hands page pairs out as its wavefronts free up, so its summation
-    # order (and last bits) vary from run to run whatever the layout
+    # the balanced decode (outputs 3, 4) and the work items at page 16 and
+    # head_dim 64 .. 128 hand page pairs out as their wavefronts free up, so
+    # their summation order (and last bits) vary from run to run whatever the
+    # layout; the other paths are bit-identical
     for i, (a, b) in enumerate(zip(outs["plain"], outs["inline"])):
-        if i < 3:
-            assert torch.equal(a, b), f"output {i} differs between the layouts"
-        else:
-            torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
+        _assert_rerun(a, b, i >= 3 or _shared_pages(dtype, D, PS), f"output {i} of the two layouts")
     _assert_close(outs["inline"][0], PD.paged_attention_decode(q, pool, table, lens, 1, kv_scales=sc), "oracle")
 
 

@@ -1,11 +1,14 @@
 """vrm_paged_decode_noalloc: the decode entry point that takes no workspace
 (its split-K partials live in a fixed array inside the library).
 
-Parity bar: its output equals vrm_paged_decode's with a caller workspace bit
-for bit (same kernels, same work split), on consecutive calls whose second
-input is smaller than the first, so stale partials of the first call cannot
-leak into the second.  Shapes whose partials exceed the array are rejected
-on the host.
+Parity bar: its output equals vrm_paged_decode's with a caller workspace
+(same kernels, same work split) bit for bit on the deterministic bf16 path,
+and within rounding (1e-5 of the output's largest magnitude) on the int8 /
+fp8 path, whose workgroups hand page pairs to wavefronts as they free up; on
+consecutive calls whose
+second input is smaller than the first, so stale partials of the first call
+cannot leak into the second (a leak would be far outside either bar).
+Shapes whose partials exceed the array are rejected on the host.
 """
 import math
 
@@ -64,7 +67,11 @@ def test_noalloc_equals_workspace_decode_on_consecutive_calls(name, big, small):
         layer, inp = _inputs(name, seed, **kw)
         _say(f"noalloc {name} {tag} B={inp['query'].shape[0]}")
         got, ref = _both(layer, inp)
-        assert torch.equal(got, ref), f"{name} {tag}: max abs diff {(got - ref).abs().max().item():.3e}"
+        if name == "7b-bf16":  # deterministic path: bit-identical
+            assert torch.equal(got, ref), f"{name} {tag}: max abs diff {(got - ref).abs().max().item():.3e}"
+        else:  # int8 / fp8 at page 16: page pairs go to wavefronts as they free up, so the last bits vary
+            err = (got - ref).abs()
+            assert (err <= 1e-5 * ref.abs().max() + 1e-6).all(), f"{name} {tag}: max abs diff {err.max().item():.3e}"
 
 
 def test_noalloc_rejects_shapes_beyond_its_array_on_the_host():

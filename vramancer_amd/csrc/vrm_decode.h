@@ -230,6 +230,13 @@ inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
 hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st,
                                   bool loads_only = false);
 
+// The work-item partition pass with the balanced workgroups: kUnitsPerWg
+// units x 6 wavefronts share the pages of one device-sized work item through
+// LDS counters and leave its merged partials in the workspace (the merge pass
+// follows).  kind K_I8 or K_FP8, D a multiple of 16 from 64 to 128, 16-token
+// pages; hipErrorInvalidValue when the page table is too wide for the LDS copy.
+hipError_t launch_stream_shared_items(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
+
 // Paged decode over TurboQuant pages (vrm_decode_tq.hip).
 struct TqDecodeArgs {
   const float* signs;  // [padded_dim] Hadamard signs

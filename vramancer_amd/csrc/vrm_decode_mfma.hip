@@ -184,11 +184,13 @@ constexpr int kMaxWaves = 4;
 // sum l, unnormalised accumulator; lane (col, grp) holds dims 16 blk + 4 grp +
 // r of head col) are merged per unit through LDS with log-sum-exp weights
 // 2^(m_w - max m) and written to a.out[b][h0(u) .. h0(u) + G - 1] (and
-// a.lse).  Every wavefront of the workgroup must call it.
-template <int D, int NB>
+// a.lse), or, with PARTIAL, left unnormalised with their (max, sum) as work
+// item `item`'s partials for the merge pass.  Every wavefront of the
+// workgroup must call it.
+template <int D, int NB, bool PARTIAL>
 __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b,
-                                               int unit0, int units, int chunks, const v4f (&acc)[NB], float m,
-                                               float l_tot) {
+                                               int item, int unit0, int units, int chunks, const v4f (&acc)[NB],
+                                               float m, float l_tot) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   float* part = lds;
@@ -230,19 +232,35 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
       }
     }
     const int h0 = (unit / chunks) * group + (unit % chunks) * G;
-    const size_t row = (size_t)b * a.H + h0 + g;
+    if constexpr (PARTIAL) {
+      const size_t prow = (size_t)item * a.H + h0 + g;
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (lane + 64 * i < D) a.out[row * D + lane + 64 * i] = L > 0.f ? o[i] * (1.f / L) : 0.f;
-    // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
-    if (a.lse && lane == 0) a.lse[row] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+      for (int i = 0; i < PER; ++i)
+        if (lane + 64 * i < D) a.part_acc[prow * D + lane + 64 * i] = o[i];
+      if (lane == 0) {
+        a.part_ml[prow * 2] = L > 0.f ? M : -INFINITY;  // o and L are relative to 2^M
+        a.part_ml[prow * 2 + 1] = L;
+      }
+    } else {
+      const size_t row = (size_t)b * a.H + h0 + g;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (lane + 64 * i < D) a.out[row * D + lane + 64 * i] = L > 0.f ? o[i] * (1.f / L) : 0.f;
+      // ln sum_t exp(scale q.k_t) = (max + log2 L) ln 2, the maxima being in the log2 domain
+      if (a.lse && lane == 0) a.lse[row] = L > 0.f ? (M + log2f(L)) * 0.6931471805599453f : -INFINITY;
+    }
   }
 }
 
 // LOADS: a measuring build that issues exactly the kernel's loads (same
 // addresses, order, ring and page hand-out) and folds the loaded words into
 // a checksum instead of computing: the time of its access pattern alone.
-template <int KIND, int D, bool BALANCED, bool LOADS = false>
+// ITEMS (balanced builds): the workgroup's wavefronts share the pages of one
+// work item (a partition of a sequence, sized on the device as for the item
+// mode) instead of a whole sequence, and leave the item's merged partials for
+// the merge pass: the balanced mode's latency hiding for any batch, with no
+// host-side knowledge of the lengths.
+template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false>
 __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
     decode_stream_kernel(DecodeArgs a, int G) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
@@ -262,6 +280,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // the measuring build leaves its checksum in out, which only the balanced
   // entry sets (item mode writes partials to the workspace)
   static_assert(!LOADS || BALANCED, "the load-only build exists for the balanced mode only");
+  static_assert(!ITEMS || (BALANCED && !LOADS), "work items of shared pages are a balanced build that computes");
 
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -273,7 +292,11 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // mode: wave w serves unit kUnitsPerWg * blockIdx.y + w % kUnitsPerWg of
   // sequence blockIdx.x
   const int units = a.KH * chunks;
-  const int unit = BALANCED ? (int)blockIdx.y * kUnitsPerWg + wave % kUnitsPerWg
+  // grid: (work item, unit group), except ITEMS: (unit group, work item), so
+  // that the items that exist come first in dispatch order and the
+  // workgroups past the last item, which leave at once, come last
+  const int wg_units = ITEMS ? (int)blockIdx.x : (int)blockIdx.y;
+  const int unit = BALANCED ? wg_units * kUnitsPerWg + wave % kUnitsPerWg
                             : (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
   const bool unit_ok = !BALANCED || unit < units;
   const int kvh = min(unit, units - 1) / chunks;
@@ -283,21 +306,30 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // of the launch also records the partition geometry for the merge pass;
   // in balanced mode the item is the whole sequence and the wave takes page
   // pairs of it as it goes
-  const int item = blockIdx.x;
+  const int item = ITEMS ? (int)blockIdx.y : (int)blockIdx.x;
   WorkItem wi;
   int* ids_lds = nullptr;  // balanced mode: the sequence's page ids
   int* pair_ctr = nullptr;
   float* merge_lds = nullptr;
   if constexpr (BALANCED) {
     extern __shared__ __align__(16) int balanced_lds[];
-    wi.b = blockIdx.x;
-    wi.ctx = a.ctx_lens[wi.b];
-    wi.p_begin = 0;
-    wi.n_pages = seq_pages(wi.ctx, a.max_pp);
+    if constexpr (ITEMS) {
+      // every wavefront derives the same item (so the workgroup leaves as a
+      // whole, before its first barrier); wave 0 of the first workgroup
+      // records the partition geometry for the merge pass
+      if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && wg_units == 0 && wave == 0,
+                     a.header, wi))
+        return;
+    } else {
+      wi.b = blockIdx.x;
+      wi.ctx = a.ctx_lens[wi.b];
+      wi.p_begin = 0;
+      wi.n_pages = seq_pages(wi.ctx, a.max_pp);
+    }
     ids_lds = balanced_lds;
     pair_ctr = balanced_lds + a.max_pp;
     merge_lds = reinterpret_cast<float*>(reinterpret_cast<char*>(balanced_lds) + balanced_merge_offset(a.max_pp));
-    const int32_t* row = a.page_table + (size_t)wi.b * a.max_pp;
+    const int32_t* row = a.page_table + (size_t)wi.b * a.max_pp + wi.p_begin;  // an item's pages lie in one row
     for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x) ids_lds[i] = row[i];
     if (threadIdx.x < kUnitsPerWg) pair_ctr[threadIdx.x] = 0;
     __syncthreads();
@@ -676,8 +708,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   if constexpr (BALANCED) {
-    balanced_merge<D, NB>(a, merge_lds, blockDim.x >> 6, wave, G, b, blockIdx.y * kUnitsPerWg, units, chunks, acc,
-                          m_eff, l_tot);
+    balanced_merge<D, NB, ITEMS>(a, merge_lds, blockDim.x >> 6, wave, G, b, item, wg_units * kUnitsPerWg, units,
+                                 chunks, acc, m_eff, l_tot);
   } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
@@ -1401,6 +1433,36 @@ hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) 
   return hipErrorInvalidValue;
 }
 
+// Work items of shared pages: the balanced geometry (kUnitsPerWg units x 6
+// wavefronts) over the device-sized work items, one resident round of
+// workgroups covering the batch; the merge pass follows.
+template <int KIND, int D>
+hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t st) {
+  const int units = a0.KH * ((a0.H / a0.KH) / G);
+  const int wgs_y = (units + kUnitsPerWg - 1) / kUnitsPerWg;
+  const int W = kMaxBalancedWaves;
+  const size_t lds = balanced_lds_bytes(a0.max_pp, W, G, D);
+  if (lds > kMaxBalancedLds) return hipErrorInvalidValue;
+  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true>);
+  DecodeArgs a = a0;
+  a.target = items_target(fn, W, lds, wgs_y * W);  // items one resident round holds
+  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true>), dim3(wgs_y, B + 2 * a.target, 1),
+                     dim3(64 * W), lds, st, a, G);
+  return hipGetLastError();
+}
+
+template <int KIND>
+hipError_t launch_shared_items_kind(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
+  switch (D) {
+    case 64: return launch_shared_items_d<KIND, 64>(a, B, G, st);
+    case 80: return launch_shared_items_d<KIND, 80>(a, B, G, st);
+    case 96: return launch_shared_items_d<KIND, 96>(a, B, G, st);
+    case 112: return launch_shared_items_d<KIND, 112>(a, B, G, st);
+    case 128: return launch_shared_items_d<KIND, 128>(a, B, G, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int KIND, bool LOADS>
 hipError_t launch_balanced_kind(const DecodeArgs& a, int B, int D, int G, hipStream_t st) {
   switch (D) {
@@ -1433,6 +1495,15 @@ hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, i
     case K_FP8:
       return loads_only ? launch_balanced_kind<K_FP8, true>(a, B, D, G, st)
                         : launch_balanced_kind<K_FP8, false>(a, B, D, G, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_stream_shared_items(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st) {
+  if (G < 1 || G > 16) return hipErrorInvalidValue;
+  switch (kind) {
+    case K_I8: return launch_shared_items_kind<K_I8>(a, B, D, G, st);
+    case K_FP8: return launch_shared_items_kind<K_FP8>(a, B, D, G, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -599,6 +599,11 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   a.vshift = mfma ? vshift : 0;
   const int max_tile = mfma ? 16 : kind == K_Q4 ? 6 : 8;
   const int G = pick_group_tile(a.H / a.KH, max_tile);
+  // int8 / fp8 at page 16 and head_dim 64 .. 128: the work items' pages are
+  // shared by balanced workgroups (12 wavefronts, page pairs handed out in
+  // LDS), when the page table fits their LDS copy
+  const bool shared = (kind == K_I8 || kind == K_FP8) && PS == kPS && D >= 64 && D <= 128 && D % 16 == 0 &&
+                      balanced_lds_bytes(a.max_pp, kMaxBalancedWaves, G, D) <= kMaxBalancedLds;
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
   (void)units;
   a.B = B;
@@ -625,7 +630,9 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
       case K_F16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_F16>(a, B, D, G, st); break;
       case K_BF16: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_BF16>(a, B, D, G, st); break;
       case K_I8:
-      case K_FP8: e = launch_stream_mfma(a, kind, B, D, G, st); break;
+      case K_FP8:
+        e = shared ? launch_stream_shared_items(a, kind, B, D, G, st) : launch_stream_mfma(a, kind, B, D, G, st);
+        break;
       default: e = mfma ? launch_stream_mfma(a, kind, B, D, G, st) : dispatch_d<K_Q4>(a, B, D, G, st); break;
     }
     if (e != hipSuccess) {
