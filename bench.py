@@ -665,19 +665,23 @@ def main():
     # wrapper allocating out + workspace per call, and with both preallocated.
     from vramancer_amd.paged_attention_cuda import paged_attention_decode, paged_attention_decode_q4
 
-    def api(i, prealloc):
+    def api(i, prealloc, host_lens=True):
         layer = layers[i % len(layers)]
         kw = dict(out=out, workspace=ws) if prealloc else {}
         if turbo:
             tq_pages.paged_attention_decode_turbo(q, pool, table, lens, layer, comp, page_size=PS, **kw)
         elif q4:
             paged_attention_decode_q4(q, pool, sc, zp, table, lens, layer, **kw)
-        else:
+        elif host_lens:
             paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc, context_lens_host=lens_list, **kw)
+        else:
+            # the reference's own call: device lengths only, out and workspace made by the wrapper
+            paged_attention_decode(q, pool, table, lens, layer, kv_scales=sc, **kw)
 
-    for i in range(5):
+    for i in range(5):  # also loads the kernels each variant launches first
         api(i, False)
         api(i, True)
+        api(i, False, False)
     n_host = 50
     python_api = {
         "host_us_per_call": {
@@ -686,6 +690,9 @@ def main():
             "python_preallocated": round(host_us(lambda i: api(i, True), n_host), 2),
         },
         "us_per_layer_step_python_preallocated": round(time_events(lambda i: api(i, True), args.steps), 3),
+        # paged_attention_decode(query, kv_pool, page_table, context_lens, layer_idx, kv_scales=...) as the
+        # reference's callers write it: no host copy of the lengths, no preallocated buffers
+        "us_per_layer_step_reference_signature": round(time_events(lambda i: api(i, False, False), args.steps), 3),
     }
     log(f"python API: {python_api}")
 

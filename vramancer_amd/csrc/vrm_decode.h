@@ -62,6 +62,8 @@ struct DecodeArgs {
 // Workspace header (int32), written by the partition pass for the merge:
 //   [0] pps   [1] number of items   [2] number of full items
 //   [3] the sequence with the most partitions (the merge starts it first)
+//   [4] 1 when the partition pass wrote the sequences of one item to out
+//       itself (the merge pass skips them), else 0
 //   [kHeaderInts + b],         b = 0 .. B : first full item of sequence b
 //                                           (entry B = number of full items)
 //   [kHeaderInts + B + 1 + b], b < B      : tail item of sequence b, or -1
@@ -76,6 +78,7 @@ struct WorkItem {
   int p_begin;  // first logical page of the partition
   int n_pages;  // pages in the partition (>= 1)
   int ctx;      // context length of the sequence
+  int items;    // work items of the whole batch
 };
 
 // Pages of a sequence of ctx tokens (pages of ps tokens), capped by the table width.
@@ -107,10 +110,11 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 
 // Finds work item `item` of the batch.  Every wave of a launch derives the
 // same geometry from the context lengths; when `writer` is set the wave also
-// stores it in the header.  Returns false when `item` lies past the last item.
+// stores it in the header (with `direct` as header[4]).  Returns false when
+// `item` lies past the last item.
 __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, int B, int max_pp, int target,
                                           int item, bool writer, int32_t* __restrict__ header, WorkItem& w,
-                                          int ps = kPS) {
+                                          int ps = kPS, bool direct = false) {
   const int lane = __lane_id();
   int S = 0;
   for (int c = 0; c < B; c += 64) {
@@ -119,20 +123,24 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
   }
   S = wave_sum_int(S);
   auto roundup4 = [](int v) { return max(4, (v + 3) / 4 * 4); };
-  int pps = roundup4((S + target - 1) / target);
-  int tails = 0;
+  // both candidate partition sizes in one pass (three independent sums, so
+  // that their lane exchanges overlap)
+  const int pps1 = roundup4((S + target - 1) / target);
+  const int pps2 = roundup4((S + 2 * target - 1) / (2 * target));
+  int tails = 0, full1 = 0, full2 = 0;
   for (int c = 0; c < B; c += 64) {
     const int b = c + lane;
     const int pages = b < B ? seq_pages(ctx_lens[b], max_pp, ps) : 0;
-    tails += (pages % pps) != 0 ? 1 : 0;
+    tails += (pages % pps1) != 0 ? 1 : 0;
+    full1 += pages / pps1;
+    full2 += pages / pps2;
   }
-  if (wave_sum_int(tails) * 8 > target) pps = roundup4((S + 2 * target - 1) / (2 * target));
-  int n_full = 0;
-  for (int c = 0; c < B; c += 64) {
-    const int b = c + lane;
-    n_full += b < B ? seq_pages(ctx_lens[b], max_pp, ps) / pps : 0;
-  }
-  n_full = wave_sum_int(n_full);
+  tails = wave_sum_int(tails);
+  full1 = wave_sum_int(full1);
+  full2 = wave_sum_int(full2);
+  const bool halve = tails * 8 > target;
+  const int pps = halve ? pps2 : pps1;
+  const int n_full = halve ? full2 : full1;
   bool found = false;
   int carry_f = 0, carry_t = n_full;
   for (int c = 0; c < B; c += 64) {
@@ -167,6 +175,7 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
     carry_f = __builtin_amdgcn_readlane(incl_f, 63);
     carry_t = __builtin_amdgcn_readlane(incl_t, 63);
   }
+  w.items = carry_t;
   if (writer) {
     // the sequence with the most partitions (first of equals), in a pass of
     // its own so that the other waves' path stays as it is
@@ -186,6 +195,7 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
       header[1] = carry_t;
       header[2] = n_full;
       header[3] = most_b;
+      header[4] = direct ? 1 : 0;
       header[kHeaderInts + B] = n_full;
     }
   }

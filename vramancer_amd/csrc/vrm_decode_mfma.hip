@@ -184,13 +184,13 @@ constexpr int kMaxWaves = 4;
 // sum l, unnormalised accumulator; lane (col, grp) holds dims 16 blk + 4 grp +
 // r of head col) are merged per unit through LDS with log-sum-exp weights
 // 2^(m_w - max m) and written to a.out[b][h0(u) .. h0(u) + G - 1] (and
-// a.lse), or, with PARTIAL, left unnormalised with their (max, sum) as work
-// item `item`'s partials for the merge pass.  Every wavefront of the
-// workgroup must call it.
+// a.lse), or, with PARTIAL and not direct, left unnormalised with their
+// (max, sum) as work item `item`'s partials for the merge pass.  Every
+// wavefront of the workgroup must call it.
 template <int D, int NB, bool PARTIAL>
 __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b,
                                                int item, int unit0, int units, int chunks, const v4f (&acc)[NB],
-                                               float m, float l_tot) {
+                                               float m, float l_tot, bool direct = false) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   float* part = lds;
@@ -232,7 +232,7 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
       }
     }
     const int h0 = (unit / chunks) * group + (unit % chunks) * G;
-    if constexpr (PARTIAL) {
+    if (PARTIAL && !direct) {
       const size_t prow = (size_t)item * a.H + h0 + g;
 #pragma unroll
       for (int i = 0; i < PER; ++i)
@@ -260,9 +260,13 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
 // mode) instead of a whole sequence, and leave the item's merged partials for
 // the merge pass: the balanced mode's latency hiding for any batch, with no
 // host-side knowledge of the lengths.
-template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false>
-__global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
-    decode_stream_kernel(DecodeArgs a, int G) {
+//
+// stream_item computes work item `item` (balanced: sequence `item`) for the
+// unit group wg_units (item mode: the units of blockIdx.y).  It returns the
+// number of work items of the batch (1 in balanced mode), or 0, having done
+// nothing, when there is no such item.
+template <int KIND, int D, bool BALANCED, bool LOADS, bool ITEMS>
+__device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int item, const int wg_units) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
   // Pages of 16 << vshift tokens are streamed as 16-token sub-pages: work
   // items, ids and masks count sub-pages, and sub-page v of a sequence is
@@ -289,15 +293,10 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   const int chunks = group / G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // item mode: the workgroup's waves are W units of one work item; balanced
-  // mode: wave w serves unit kUnitsPerWg * blockIdx.y + w % kUnitsPerWg of
-  // sequence blockIdx.x
+  // mode: wave w serves unit kUnitsPerWg * wg_units + w % kUnitsPerWg of the
+  // item (sequence, or with ITEMS a partition of one)
   const int units = a.KH * chunks;
-  // grid: (work item, unit group), except ITEMS: (unit group, work item), so
-  // that the items that exist come first in dispatch order and the
-  // workgroups past the last item, which leave at once, come last
-  const int wg_units = ITEMS ? (int)blockIdx.x : (int)blockIdx.y;
-  const int unit = BALANCED ? wg_units * kUnitsPerWg + wave % kUnitsPerWg
-                            : (int)blockIdx.y * (int)(blockDim.x >> 6) + wave;
+  const int unit = BALANCED ? wg_units * kUnitsPerWg + wave % kUnitsPerWg : wg_units * (int)(blockDim.x >> 6) + wave;
   const bool unit_ok = !BALANCED || unit < units;
   const int kvh = min(unit, units - 1) / chunks;
   const int h0 = kvh * group + (min(unit, units - 1) % chunks) * G;
@@ -306,7 +305,6 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // of the launch also records the partition geometry for the merge pass;
   // in balanced mode the item is the whole sequence and the wave takes page
   // pairs of it as it goes
-  const int item = ITEMS ? (int)blockIdx.y : (int)blockIdx.x;
   WorkItem wi;
   int* ids_lds = nullptr;  // balanced mode: the sequence's page ids
   int* pair_ctr = nullptr;
@@ -318,13 +316,14 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       // whole, before its first barrier); wave 0 of the first workgroup
       // records the partition geometry for the merge pass
       if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && wg_units == 0 && wave == 0,
-                     a.header, wi))
-        return;
+                     a.header, wi, kPS, a.out != nullptr))
+        return 0;
     } else {
-      wi.b = blockIdx.x;
+      wi.b = item;
       wi.ctx = a.ctx_lens[wi.b];
       wi.p_begin = 0;
       wi.n_pages = seq_pages(wi.ctx, a.max_pp);
+      wi.items = 1;
     }
     ids_lds = balanced_lds;
     pair_ctr = balanced_lds + a.max_pp;
@@ -335,9 +334,10 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     __syncthreads();
   } else {
     if (!find_item(a.ctx_lens, a.B, a.max_pp << vshift, a.target, item, item == 0 && unit == 0, a.header, wi))
-      return;
+      return 0;
   }
   const int b = wi.b;
+  const int batch_items = wi.items;
   const int n_pages = wi.n_pages;
   const int last = n_pages - 1;
   const int tok_end = min(n_pages * kPS, wi.ctx - wi.p_begin * kPS);  // valid tokens of the partition
@@ -703,13 +703,16 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
   // ---------------- partition result ----------------
   if constexpr (LOADS) {
     a.out[((size_t)b * a.H + h0) * D + lane] = __uint_as_float(probe);  // lane < 64 <= D
-    return;
+    return batch_items;
   }
   float l_tot = l_run + xor_shfl<16>(l_run);
   l_tot += xor_shfl<32>(l_tot);
   if constexpr (BALANCED) {
+    // an item that is its whole sequence goes straight to out when the call
+    // has one (the merge pass then leaves that sequence alone)
+    const bool direct = ITEMS && a.out && wi.p_begin == 0 && wi.n_pages == seq_pages(wi.ctx, a.max_pp);
     balanced_merge<D, NB, ITEMS>(a, merge_lds, blockDim.x >> 6, wave, G, b, item, wg_units * kUnitsPerWg, units,
-                                 chunks, acc, m_eff, l_tot);
+                                 chunks, acc, m_eff, l_tot, direct);
   } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
@@ -721,6 +724,40 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       ml_base[col * 2] = l_tot > 0.f ? m_eff : -INFINITY;  // l and acc are relative to 2^m_eff
       ml_base[col * 2 + 1] = l_tot;
     }
+  }
+  return batch_items;
+}
+
+// grid: (work item, unit group), balanced: (sequence, unit group).  ITEMS:
+// (unit group, gridDim.y workgroups per unit group), one resident round,
+// each workgroup taking items blockIdx.y, blockIdx.y + gridDim.y, ... below
+// the batch's item count (rather than a workgroup per possible item: the
+// ones past the last item would still queue for a CU behind the working
+// ones).  Between two items every wavefront has passed the first item's
+// merge barrier, so the next item's page ids and counters overwrite nothing
+// still read.
+template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false>
+__global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
+    decode_stream_kernel(DecodeArgs a, int G) {
+  if constexpr (ITEMS) {
+    for (int item = blockIdx.y, items = item + 1; item < items; item += gridDim.y) {
+      // the arguments are read afresh for each item, from the kernarg
+      // segment through a pointer the compiler cannot follow across
+      // iterations, so that none of them stays live in registers across the
+      // loop (hoisted, they cost the body its registers)
+      using KWord = const __attribute__((address_space(4))) uint32_t;
+      KWord* kp = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();  // a is the first argument
+      asm volatile("" : "+s"(kp));
+      struct Words {
+        uint32_t w[sizeof(DecodeArgs) / 4];
+      } words;
+#pragma unroll
+      for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); ++i) words.w[i] = kp[i];
+      const DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
+      items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such item
+    }
+  } else {
+    stream_item<KIND, D, BALANCED, LOADS, ITEMS>(a, G, blockIdx.x, blockIdx.y);
   }
 }
 
@@ -1435,7 +1472,7 @@ hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) 
 
 // Work items of shared pages: the balanced geometry (kUnitsPerWg units x 6
 // wavefronts) over the device-sized work items, one resident round of
-// workgroups covering the batch; the merge pass follows.
+// workgroups per unit group looping over the items; the merge pass follows.
 template <int KIND, int D>
 hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t st) {
   const int units = a0.KH * ((a0.H / a0.KH) / G);
@@ -1446,8 +1483,8 @@ hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t
   const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true>);
   DecodeArgs a = a0;
   a.target = items_target(fn, W, lds, wgs_y * W);  // items one resident round holds
-  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true>), dim3(wgs_y, B + 2 * a.target, 1),
-                     dim3(64 * W), lds, st, a, G);
+  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true>), dim3(wgs_y, a.target, 1), dim3(64 * W), lds,
+                     st, a, G);
   return hipGetLastError();
 }
 

@@ -343,13 +343,24 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
   __shared__ float sh_res[WAVES][DMAX];
   // Workgroups start in blockIdx order: the sequence with the most partials
   // (the longest fold) takes row 0, so that its merge overlaps the others'.
+  // The entries of sequence blockIdx.y load together with header[3] and
+  // header[4]; only the two swapped rows load theirs again.
+  const int y = blockIdx.y;
   const int big = min(max(header[3], 0), B - 1);
-  const int h = blockIdx.x, b = blockIdx.y == 0 ? big : ((int)blockIdx.y == big ? 0 : (int)blockIdx.y);
+  const bool direct = header[4] != 0;
+  int first = header[kHeaderInts + y];
+  int next = header[kHeaderInts + y + 1];
+  int tail = header[kHeaderInts + B + 1 + y];
+  const int h = blockIdx.x, b = y == 0 ? big : (y == big ? 0 : y);
+  if (b != y) {
+    first = header[kHeaderInts + b];
+    next = header[kHeaderInts + b + 1];
+    tail = header[kHeaderInts + B + 1 + b];
+  }
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int first = header[kHeaderInts + b];
-  const int nf = header[kHeaderInts + b + 1] - first;
-  const int tail = header[kHeaderInts + B + 1 + b];
+  const int nf = next - first;
   const int nact = nf + (tail >= 0 ? 1 : 0);
+  if (nact == 1 && direct) return;  // the partition pass wrote this sequence's rows
   auto item_of = [&](int s) { return s < nf ? first + s : tail; };
   float M = -INFINITY, Lsum = 0.f;
   float res[PER];
@@ -617,6 +628,9 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   a.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + header_bytes(B));
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
+  // with both passes in the call, the shared-items pass writes sequences of
+  // one item to out itself
+  a.out = passes == kBoth && shared ? out : nullptr;
   hipError_t e = hipSuccess;
   if ((passes & kPartitionsOnly) && !tuned) {
     e = launch_generic(a, kind, B, D, PS, st);
