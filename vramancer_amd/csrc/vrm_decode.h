@@ -78,7 +78,8 @@ struct WorkItem {
   int p_begin;  // first logical page of the partition
   int n_pages;  // pages in the partition (>= 1)
   int ctx;      // context length of the sequence
-  int items;    // work items of the whole batch
+  int items;    // work items of the whole batch (find_piece: pieces of the row)
+  int slot;     // find_piece: the workspace row of the piece's partials
 };
 
 // Pages of a sequence of ctx tokens (pages of ps tokens), capped by the table width.
@@ -202,6 +203,96 @@ __device__ __forceinline__ bool find_item(const int32_t* __restrict__ ctx_lens, 
   return found;
 }
 
+// Pieces (the shared-items pass).  The batch's pages laid end to end,
+// sequence after sequence (S in all), are cut into `rows` runs of C =
+// max(kMinPiecePages, roundup4(ceil(S / rows))) pages: row r holds pages
+// [r C, (r + 1) C), so that every row carries the same work whatever the
+// lengths.  A row's pieces are its runs within each sequence it meets, in
+// sequence order.  Sequence b (P_b pages before it, pages_b its own) meets
+// rows P_b / C .. (P_b + pages_b - 1) / C, k_b of them; its pieces' partials
+// take workspace rows base_b .. base_b + k_b - 1 (base: the exclusive sum of
+// k), the piece of row r taking base_b + r - P_b / C.  The header takes the
+// work-item form with every piece a full item and no tails, so the merge
+// pass reads it unchanged: [kHeaderInts + b] = base_b, [kHeaderInts + B] =
+// the number of pieces, tails -1, [0] = C.
+constexpr int kMinPiecePages = 16;
+
+__device__ __forceinline__ int lane_rank(unsigned long long m) {  // set bits of m below this lane
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
+}
+
+// Finds piece j of row `row` (of `rows`); every wave of the launch derives
+// the same geometry, and the `writer` wave stores it in the header (with
+// `direct` as header[4]) whether or not the piece exists.  Returns false when
+// the row has no piece j; w.items is the row's piece count either way.
+__device__ __forceinline__ bool find_piece(const int32_t* __restrict__ ctx_lens, int B, int max_pp, int rows, int row,
+                                           int j, bool writer, bool direct, int32_t* __restrict__ header,
+                                           WorkItem& w) {
+  const int lane = __lane_id();
+  int S = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    S += b < B ? seq_pages(ctx_lens[b], max_pp) : 0;
+  }
+  S = wave_sum_int(S);
+  const int C = max(kMinPiecePages, ((S + rows - 1) / rows + 3) / 4 * 4);
+  const long long lo = (long long)row * C;
+  const long long hi = min((long long)S, lo + C);
+  int carry_p = 0, carry_k = 0, seen = 0, most = -1, most_b = 0;
+  bool found = false;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    const int ctx = b < B ? ctx_lens[b] : 0;
+    const int pages = b < B ? seq_pages(ctx, max_pp) : 0;
+    const int incl_p = wave_inclusive_scan(pages) + carry_p;
+    const int P = incl_p - pages;
+    const int k = pages > 0 ? (P + pages - 1) / C - P / C + 1 : 0;
+    const int incl_k = wave_inclusive_scan(k) + carry_k;
+    const int base = incl_k - k;
+    if (writer && b < B) {
+      header[kHeaderInts + b] = base;
+      header[kHeaderInts + B + 1 + b] = -1;
+    }
+    const bool meets = pages > 0 && P < hi && P + pages > lo;
+    const unsigned long long m = __ballot(meets);
+    const int cnt = __popcll(m);
+    if (!found && j >= seen && j < seen + cnt) {
+      const unsigned long long hit = __ballot(meets && lane_rank(m) == j - seen);
+      const int l = __builtin_ffsll(hit) - 1;
+      const int pl = __builtin_amdgcn_readlane(P, l);
+      const int nl = __builtin_amdgcn_readlane(pages, l);
+      const int first = max((int)lo, pl);
+      const int end = min((int)hi, pl + nl);
+      w.b = c + l;
+      w.p_begin = first - pl;
+      w.n_pages = end - first;
+      w.ctx = __builtin_amdgcn_readlane(ctx, l);
+      w.slot = __builtin_amdgcn_readlane(base, l) + row - pl / C;
+      found = true;
+    }
+    seen += cnt;
+    if (writer) {
+      const int kmax = wave_max_int(b < B ? k : -1);
+      if (kmax > most) {
+        most = kmax;
+        most_b = c + __builtin_ffsll(__ballot(b < B && k == kmax)) - 1;
+      }
+    }
+    carry_p = __builtin_amdgcn_readlane(incl_p, 63);
+    carry_k = __builtin_amdgcn_readlane(incl_k, 63);
+  }
+  w.items = seen;
+  if (writer && lane == 0) {
+    header[0] = C;
+    header[1] = carry_k;
+    header[2] = carry_k;
+    header[3] = most_b;
+    header[4] = direct ? 1 : 0;
+    header[kHeaderInts + B] = carry_k;
+  }
+  return found;
+}
+
 // Work items one resident round of `kernel` holds (see work items above).
 int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int units);
 
@@ -222,6 +313,10 @@ hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G
 constexpr int kMaxBalancedWaves = 12;
 constexpr int kUnitsPerWg = 2;
 constexpr size_t kMaxBalancedLds = 64 * 1024;
+// LDS one workgroup of the shared-items pass may take on the current device
+// (its 12-wavefront workgroups hold a CU each, so beyond 64 KB costs no
+// occupancy): the device's per-workgroup limit, at most 160 KB.
+size_t shared_items_max_lds();
 __host__ __device__ inline size_t balanced_merge_offset(int max_pp) {
   return ((size_t)max_pp * 4 + kUnitsPerWg * 4 + 15) / 16 * 16;
 }

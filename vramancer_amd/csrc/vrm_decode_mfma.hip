@@ -261,10 +261,11 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
 // the merge pass: the balanced mode's latency hiding for any batch, with no
 // host-side knowledge of the lengths.
 //
-// stream_item computes work item `item` (balanced: sequence `item`) for the
-// unit group wg_units (item mode: the units of blockIdx.y).  It returns the
-// number of work items of the batch (1 in balanced mode), or 0, having done
-// nothing, when there is no such item.
+// stream_item computes work item `item` (balanced: sequence `item`; ITEMS:
+// piece `item` of row blockIdx.y) for the unit group wg_units (item mode: the
+// units of blockIdx.y).  It returns the number of work items of the batch (1
+// in balanced mode, ITEMS: the row's pieces), or 0, having done nothing, when
+// there is no such item.
 template <int KIND, int D, bool BALANCED, bool LOADS, bool ITEMS>
 __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int item, const int wg_units) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
@@ -315,8 +316,8 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
       // every wavefront derives the same item (so the workgroup leaves as a
       // whole, before its first barrier); wave 0 of the first workgroup
       // records the partition geometry for the merge pass
-      if (!find_item(a.ctx_lens, a.B, a.max_pp, a.target, item, item == 0 && wg_units == 0 && wave == 0,
-                     a.header, wi, kPS, a.out != nullptr))
+      if (!find_piece(a.ctx_lens, a.B, a.max_pp, a.target, blockIdx.y, item,
+                      blockIdx.y == 0 && item == 0 && wg_units == 0 && wave == 0, a.out != nullptr, a.header, wi))
         return 0;
     } else {
       wi.b = item;
@@ -711,8 +712,8 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     // an item that is its whole sequence goes straight to out when the call
     // has one (the merge pass then leaves that sequence alone)
     const bool direct = ITEMS && a.out && wi.p_begin == 0 && wi.n_pages == seq_pages(wi.ctx, a.max_pp);
-    balanced_merge<D, NB, ITEMS>(a, merge_lds, blockDim.x >> 6, wave, G, b, item, wg_units * kUnitsPerWg, units,
-                                 chunks, acc, m_eff, l_tot, direct);
+    balanced_merge<D, NB, ITEMS>(a, merge_lds, blockDim.x >> 6, wave, G, b, ITEMS ? wi.slot : item,
+                                 wg_units * kUnitsPerWg, units, chunks, acc, m_eff, l_tot, direct);
   } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
@@ -729,18 +730,17 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
 }
 
 // grid: (work item, unit group), balanced: (sequence, unit group).  ITEMS:
-// (unit group, gridDim.y workgroups per unit group), one resident round,
-// each workgroup taking items blockIdx.y, blockIdx.y + gridDim.y, ... below
-// the batch's item count (rather than a workgroup per possible item: the
-// ones past the last item would still queue for a CU behind the working
-// ones).  Between two items every wavefront has passed the first item's
-// merge barrier, so the next item's page ids and counters overwrite nothing
+// (unit group, row), one resident round (a.target rows), each workgroup
+// taking the pieces of its row (find_piece) in turn: every row carries the
+// same number of pages, and no workgroup waits for a CU behind the working
+// ones.  Between two pieces every wavefront has passed the first piece's
+// merge barrier, so the next piece's page ids and counters overwrite nothing
 // still read.
 template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false>
 __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
     decode_stream_kernel(DecodeArgs a, int G) {
   if constexpr (ITEMS) {
-    for (int item = blockIdx.y, items = item + 1; item < items; item += gridDim.y) {
+    for (int item = 0, items = 1; item < items; ++item) {
       // the arguments are read afresh for each item, from the kernarg
       // segment through a pointer the compiler cannot follow across
       // iterations, so that none of them stays live in registers across the
@@ -754,7 +754,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
 #pragma unroll
       for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); ++i) words.w[i] = kp[i];
       const DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
-      items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such item
+      items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such piece
     }
   } else {
     stream_item<KIND, D, BALANCED, LOADS, ITEMS>(a, G, blockIdx.x, blockIdx.y);
@@ -1479,8 +1479,12 @@ hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t
   const int wgs_y = (units + kUnitsPerWg - 1) / kUnitsPerWg;
   const int W = kMaxBalancedWaves;
   const size_t lds = balanced_lds_bytes(a0.max_pp, W, G, D);
-  if (lds > kMaxBalancedLds) return hipErrorInvalidValue;
+  if (lds > shared_items_max_lds()) return hipErrorInvalidValue;
   const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true>);
+  if (lds > kMaxBalancedLds) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
   DecodeArgs a = a0;
   a.target = items_target(fn, W, lds, wgs_y * W);  // items one resident round holds
   hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true>), dim3(wgs_y, a.target, 1), dim3(64 * W), lds,

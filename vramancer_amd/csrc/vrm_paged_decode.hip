@@ -65,6 +65,22 @@ int items_target(const void* kernel, int waves_per_block, size_t lds_bytes, int 
   return std::max(1, std::min(waves, kMaxTargetWaves) / units);
 }
 
+size_t shared_items_max_lds() {
+  static std::mutex mu;
+  static std::map<int, size_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return kMaxBalancedLds;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int bytes = 0;
+  size_t lim = kMaxBalancedLds;
+  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && bytes > 0)
+    lim = std::max(kMaxBalancedLds, std::min<size_t>((size_t)bytes, 160 * 1024));
+  cache[dev] = lim;
+  return lim;
+}
+
 namespace {
 
 template <int KIND>
@@ -614,7 +630,7 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   // shared by balanced workgroups (12 wavefronts, page pairs handed out in
   // LDS), when the page table fits their LDS copy
   const bool shared = (kind == K_I8 || kind == K_FP8) && PS == kPS && D >= 64 && D <= 128 && D % 16 == 0 &&
-                      balanced_lds_bytes(a.max_pp, kMaxBalancedWaves, G, D) <= kMaxBalancedLds;
+                      balanced_lds_bytes(a.max_pp, kMaxBalancedWaves, G, D) <= shared_items_max_lds();
   const int units = a.KH * ((a.H / a.KH) / G);  // wavefronts per work item
   (void)units;
   a.B = B;
