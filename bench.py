@@ -54,8 +54,11 @@ LAYERS_FILLED = (0, 12, 24, 36)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_14b_int8.json")
 # wave64 VALU instructions per launch of the VALU-bound kernels (rocprofv3 SQ counters)
 VALU_FILE = os.path.join(ROOT, "profiles", "valu_counts.json")
-# one wave64 VALU instruction per SIMD per 4 cycles: 256 CUs x 4 SIMDs at 2.4 GHz
-PEAK_VALU_GINST = 256 * 4 * 2.4 / 4
+# one wave64 VALU instruction per SIMD per 4 cycles: 256 CUs x 4 SIMDs at 2.4 GHz (the flat
+# rate; a workload whose entry carries issue_ns_per_inst, the measured issue cost of each
+# instruction kind weighted by the kernel loop's own mix, is priced at that instead)
+N_SIMDS = 256 * 4
+PEAK_VALU_GINST = N_SIMDS * 2.4 / 4
 KV_CODE = {"f32": _lib.VRM_KV_F32, "f16": _lib.VRM_KV_F16, "bf16": _lib.VRM_KV_BF16, "int8": _lib.VRM_KV_I8,
            "fp8": _lib.VRM_KV_FP8E4M3}
 KV_NAME = {"f32": "K_F32", "f16": "K_F16", "bf16": "K_BF16", "int8": "K_I8", "fp8": "K_FP8", "q4": "K_Q4"}
@@ -820,13 +823,18 @@ def main():
         # These kernels rebuild or unpack every code on the vector ALU: the
         # binding roofline is VALU issue, the HBM figures stay as context.
         ginst = valu["valu_insts_per_launch"] / (us_part * 1e-6) / 1e9
+        ns_inst = valu.get("issue_ns_per_inst")
+        peak = N_SIMDS / ns_inst if ns_inst else PEAK_VALU_GINST
         roofline.update({
             "bound": "valu",
             "achieved": round(ginst, 1),
-            "peak": PEAK_VALU_GINST,
+            "peak": round(peak, 1),
             "unit": "Ginst/s",
-            "frac": round(ginst / PEAK_VALU_GINST, 4),
+            "frac": round(ginst / peak, 4),
             "valu_insts_per_launch": valu["valu_insts_per_launch"],
+            "issue_ns_per_inst": ns_inst,
+            "floor_us": round(valu["valu_insts_per_launch"] / peak / 1e3, 2),
+            "frac_flat_4_cycles": round(ginst / PEAK_VALU_GINST, 4),
             "hbm_achieved_gbps": round(achieved, 1),
             "hbm_frac": round(achieved / PEAK_HBM_GBPS, 4),
         })

@@ -312,7 +312,15 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
   float* merge_lds = nullptr;
   if constexpr (BALANCED) {
     extern __shared__ __align__(16) int balanced_lds[];
+    // the first piece of row r most likely starts sequence r B / rows (it
+    // does when the lengths are equal): its page ids are requested together
+    // with the lengths, and used if so
+    int spec_b = -1, spec_id = 0;
     if constexpr (ITEMS) {
+      if (item == 0) {
+        spec_b = min((int)((long long)blockIdx.y * a.B / a.target), a.B - 1);
+        if ((int)threadIdx.x < a.max_pp) spec_id = a.page_table[(size_t)spec_b * a.max_pp + threadIdx.x];
+      }
       // every wavefront derives the same item (so the workgroup leaves as a
       // whole, before its first barrier); wave 0 of the first workgroup
       // records the partition geometry for the merge pass
@@ -330,7 +338,9 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     pair_ctr = balanced_lds + a.max_pp;
     merge_lds = reinterpret_cast<float*>(reinterpret_cast<char*>(balanced_lds) + balanced_merge_offset(a.max_pp));
     const int32_t* row = a.page_table + (size_t)wi.b * a.max_pp + wi.p_begin;  // an item's pages lie in one row
-    for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x) ids_lds[i] = row[i];
+    const bool spec_hit = wi.b == spec_b && wi.p_begin == 0;
+    for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x)
+      ids_lds[i] = spec_hit && i == (int)threadIdx.x ? spec_id : row[i];
     if (threadIdx.x < kUnitsPerWg) pair_ctr[threadIdx.x] = 0;
     __syncthreads();
   } else {
@@ -729,6 +739,15 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
   return batch_items;
 }
 
+// p, rebuilt as a global-memory pointer (then cast back to a generic one,
+// which the compiler's address-space inference follows): its loads and
+// stores become global rather than flat ones.
+template <typename T>
+__device__ __forceinline__ void as_global(T*& p) {
+  using G = __attribute__((address_space(1))) T;
+  p = (T*)(G*)(uintptr_t)p;
+}
+
 // grid: (work item, unit group), balanced: (sequence, unit group).  ITEMS:
 // (unit group, row), one resident round (a.target rows), each workgroup
 // taking the pieces of its row (find_piece) in turn: every row carries the
@@ -744,7 +763,8 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       // the arguments are read afresh for each item, from the kernarg
       // segment through a pointer the compiler cannot follow across
       // iterations, so that none of them stays live in registers across the
-      // loop (hoisted, they cost the body its registers)
+      // loop (hoisted, they cost the body its registers); the pointers are
+      // then made global ones again, so that their loads stay global loads
       using KWord = const __attribute__((address_space(4))) uint32_t;
       KWord* kp = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();  // a is the first argument
       asm volatile("" : "+s"(kp));
@@ -753,7 +773,17 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
       } words;
 #pragma unroll
       for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); ++i) words.w[i] = kp[i];
-      const DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
+      DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
+      as_global(ai.query);
+      as_global(ai.pool);
+      as_global(ai.scales);
+      as_global(ai.page_table);
+      as_global(ai.ctx_lens);
+      as_global(ai.header);
+      as_global(ai.part_acc);
+      as_global(ai.part_ml);
+      as_global(ai.out);
+      as_global(ai.lse);
       items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such piece
     }
   } else {
