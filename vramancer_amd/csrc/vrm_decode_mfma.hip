@@ -748,6 +748,34 @@ __device__ __forceinline__ void as_global(T*& p) {
   p = (T*)(G*)(uintptr_t)p;
 }
 
+// The kernel's DecodeArgs (its first argument), read afresh from the
+// kernarg segment through a pointer the compiler cannot follow across the
+// iterations of a loop over work: hoisted out of such a loop, the arguments
+// stay live in registers through the whole body and cost it spills.  The
+// pointers are made global ones again, so that their loads stay global loads.
+__device__ __forceinline__ DecodeArgs kernel_args_afresh() {
+  using KWord = const __attribute__((address_space(4))) uint32_t;
+  KWord* kp = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(kp));
+  struct Words {
+    uint32_t w[sizeof(DecodeArgs) / 4];
+  } words;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); ++i) words.w[i] = kp[i];
+  DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
+  as_global(ai.query);
+  as_global(ai.pool);
+  as_global(ai.scales);
+  as_global(ai.page_table);
+  as_global(ai.ctx_lens);
+  as_global(ai.header);
+  as_global(ai.part_acc);
+  as_global(ai.part_ml);
+  as_global(ai.out);
+  as_global(ai.lse);
+  return ai;
+}
+
 // grid: (work item, unit group), balanced: (sequence, unit group).  ITEMS:
 // (unit group, row), one resident round (a.target rows), each workgroup
 // taking the pieces of its row (find_piece) in turn: every row carries the
@@ -760,30 +788,7 @@ __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves
     decode_stream_kernel(DecodeArgs a, int G) {
   if constexpr (ITEMS) {
     for (int item = 0, items = 1; item < items; ++item) {
-      // the arguments are read afresh for each item, from the kernarg
-      // segment through a pointer the compiler cannot follow across
-      // iterations, so that none of them stays live in registers across the
-      // loop (hoisted, they cost the body its registers); the pointers are
-      // then made global ones again, so that their loads stay global loads
-      using KWord = const __attribute__((address_space(4))) uint32_t;
-      KWord* kp = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();  // a is the first argument
-      asm volatile("" : "+s"(kp));
-      struct Words {
-        uint32_t w[sizeof(DecodeArgs) / 4];
-      } words;
-#pragma unroll
-      for (int i = 0; i < (int)(sizeof(DecodeArgs) / 4); ++i) words.w[i] = kp[i];
-      DecodeArgs ai = __builtin_bit_cast(DecodeArgs, words);
-      as_global(ai.query);
-      as_global(ai.pool);
-      as_global(ai.scales);
-      as_global(ai.page_table);
-      as_global(ai.ctx_lens);
-      as_global(ai.header);
-      as_global(ai.part_acc);
-      as_global(ai.part_ml);
-      as_global(ai.out);
-      as_global(ai.lse);
+      const DecodeArgs ai = kernel_args_afresh();
       items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such piece
     }
   } else {

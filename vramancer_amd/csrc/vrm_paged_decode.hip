@@ -645,7 +645,7 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
   a.part_ml = a.part_acc + (size_t)cap * a.H * D;
   a.qscale = scale * kLog2e;
   // with both passes in the call, the shared-items pass writes sequences of
-  // one item to out itself
+  // one piece to out itself
   a.out = passes == kBoth && shared ? out : nullptr;
   hipError_t e = hipSuccess;
   if ((passes & kPartitionsOnly) && !tuned) {
