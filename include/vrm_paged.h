@@ -138,7 +138,9 @@ size_t vrm_paged_decode_workspace_bytes(int B, int H, int D, int nsplit);
  * csrc/paged_attention_kernel.cu:460-466), H % KH == 0; int8 / fp8 pools
  * need D % 16 == 0 and PS % 4 == 0 (their tiled V), and other shapes return
  * VRM_ERR_UNSUPPORTED.  Page 16 with D 64 / 128 / 256 runs the tuned
- * matrix-core kernels; every other shape a generic kernel.
+ * matrix-core kernels; every other shape a generic kernel.  int8 / fp8 pools
+ * at D 64 .. 128 (multiples of 16) and page 16 hand page pairs to wavefronts
+ * dynamically, so the last bits of an output may differ between calls.
  */
 int vrm_paged_decode(const float* query, const void* kv_pool, const float* kv_scales,
                      const int32_t* page_table, const int32_t* context_lens,
