@@ -214,6 +214,44 @@ def test_partitions_then_merge_equals_fused_call():
     _assert_rerun(out, out2, _shared_pages(torch.int8, D, PS), "partitions + merge")
 
 
+@pytest.mark.parametrize("dtype", [torch.int8, torch.float8_e4m3fn], ids=["int8", "fp8"])
+@pytest.mark.parametrize("H,KH,D", [(16, 8, 128), (32, 4, 128), (24, 8, 96), (16, 4, 64)])
+def test_shared_items_many_sequences(dtype, H, KH, D):
+    """More sequences than a resident round has rows of two-unit workgroups:
+    the shared-items pass runs four kv-head units per workgroup over rows of
+    equal page runs (ragged lengths, empty sequences, one long sequence over
+    many rows); the fused call, and partitions + merge, match the oracle."""
+    _say(f"shared items, many sequences {dtype} H{H} KH{KH} D{D}")
+    g = torch.Generator().manual_seed(H * 7 + D)
+    ctxs = [int(x) for x in torch.randint(1, 400, (150,), generator=g)]
+    for i in (3, 40, 77):
+        ctxs[i] = 0
+    ctxs[100] = 6000
+    q, pool, sc, table, lens = _pool_case(dtype, len(ctxs), H, KH, D, ctxs, L=1, layer=0, seed=H + D)
+    d = [t.to(DEV) for t in (q, pool, sc, table, lens)]
+    out = paged_attention_decode(d[0], d[1], d[3], d[4], 0, kv_scales=d[2])
+    lib = _lib.load()
+    B = len(ctxs)
+    P, L, _, _, PS, _ = pool.shape
+    from vramancer_amd.paged_attention_cuda import decode_workspace
+    ws = decode_workspace(B, H, KH, D, table.shape[1], DEV)
+    out2 = torch.full_like(out, float("nan"))
+    s = _lib.stream_of(d[0])
+    code = kv_quant.abi_dtype_code(d[1], d[2])
+    rc = lib.vrm_paged_decode_partitions(d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(),
+                                         d[4].data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS, L, P,
+                                         table.shape[1], 0, 1 / math.sqrt(D), code, s)
+    _lib.check(rc, "partitions")
+    rc = lib.vrm_paged_decode_merge(d[4].data_ptr(), out2.data_ptr(), ws.data_ptr(), ws.numel(), B, H, KH, D, PS,
+                                    table.shape[1], s)
+    _lib.check(rc, "merge")
+    torch.cuda.synchronize()
+    ref = PD.paged_attention_decode(q, pool, table, lens, 0, kv_scales=sc)
+    _assert_close(out.cpu(), ref, "fused call")
+    _assert_close(out2.cpu(), ref, "partitions + merge")
+    assert not out[torch.tensor(ctxs) == 0].any(), "empty sequences give zero rows"
+
+
 @pytest.mark.parametrize("H,KH,D", [(16, 4, 128), (40, 8, 128), (12, 2, 128), (14, 2, 128), (10, 2, 64),
                                     (12, 2, 256)])
 def test_decode_q4_matches_oracle(H, KH, D):

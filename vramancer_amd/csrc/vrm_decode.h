@@ -308,17 +308,18 @@ hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G
 
 // Balanced mode geometry: workgroups of kUnitsPerWg units x (1, 2, 4 or 6)
 // wavefronts per unit.  LDS: the sequence's page ids [max_pp], the units'
-// page-pair counters [kUnitsPerWg], then (16-byte aligned) the merge area,
+// page-pair counters [kMaxUnitsPerWg], then (16-byte aligned) the merge area,
 // [W][G][D] accumulators and [W][G][2] (m, l); at most kMaxBalancedLds.
 constexpr int kMaxBalancedWaves = 12;
-constexpr int kUnitsPerWg = 2;
+constexpr int kUnitsPerWg = 2;     // the balanced mode; the shared-items pass takes 2 or 4
+constexpr int kMaxUnitsPerWg = 4;  // page-pair counters the LDS layout leaves room for
 constexpr size_t kMaxBalancedLds = 64 * 1024;
 // LDS one workgroup of the shared-items pass may take on the current device
 // (its 12-wavefront workgroups hold a CU each, so beyond 64 KB costs no
 // occupancy): the device's per-workgroup limit, at most 160 KB.
 size_t shared_items_max_lds();
 __host__ __device__ inline size_t balanced_merge_offset(int max_pp) {
-  return ((size_t)max_pp * 4 + kUnitsPerWg * 4 + 15) / 16 * 16;
+  return ((size_t)max_pp * 4 + kMaxUnitsPerWg * 4 + 15) / 16 * 16;
 }
 inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
   return balanced_merge_offset(max_pp) + (size_t)W * G * (D + 2) * sizeof(float);
@@ -335,11 +336,14 @@ inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
 hipError_t launch_stream_balanced(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st,
                                   bool loads_only = false);
 
-// The work-item partition pass with the balanced workgroups: kUnitsPerWg
-// units x 6 wavefronts share the pages of one device-sized work item through
-// LDS counters and leave its merged partials in the workspace (the merge pass
-// follows).  kind K_I8 or K_FP8, D a multiple of 16 from 64 to 128, 16-token
-// pages; hipErrorInvalidValue when the page table is too wide for the LDS copy.
+// The shared-items partition pass: balanced workgroups of 12 wavefronts (2
+// units x 6, or 4 x 3 when the batch has more sequences than a resident round
+// has rows of 2-unit workgroups) take the pieces of their row (find_piece),
+// sharing each piece's pages through LDS counters, and leave its merged
+// partials in the workspace (the merge pass follows) or, for a one-piece
+// sequence in a call with out, the output.  kind K_I8 or K_FP8, D a multiple
+// of 16 from 64 to 128, 16-token pages; hipErrorInvalidValue when the page
+// table is too wide for the LDS copy.
 hipError_t launch_stream_shared_items(const DecodeArgs& a, int kind, int B, int D, int G, hipStream_t st);
 
 // Paged decode over TurboQuant pages (vrm_decode_tq.hip).

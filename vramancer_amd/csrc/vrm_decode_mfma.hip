@@ -187,7 +187,7 @@ constexpr int kMaxWaves = 4;
 // a.lse), or, with PARTIAL and not direct, left unnormalised with their
 // (max, sum) as work item `item`'s partials for the merge pass.  Every
 // wavefront of the workgroup must call it.
-template <int D, int NB, bool PARTIAL>
+template <int D, int NB, bool PARTIAL, int UPW = kUnitsPerWg>
 __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, int W, int wave, int G, int b,
                                                int item, int unit0, int units, int chunks, const v4f (&acc)[NB],
                                                float m, float l_tot, bool direct = false) {
@@ -211,17 +211,17 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
   // lane + 64 i in the same order as the partials were written.
   const int group = a.H / a.KH;
   constexpr int PER = (D + 63) / 64;
-  for (int pr = wave; pr < kUnitsPerWg * G; pr += W) {
+  for (int pr = wave; pr < UPW * G; pr += W) {
     const int ul = pr / G, g = pr - ul * G;
     const int unit = unit0 + ul;
     if (unit >= units) continue;
     float M = -INFINITY;
-    for (int w = ul; w < W; w += kUnitsPerWg) M = fmaxf(M, ml[(w * G + g) * 2]);
+    for (int w = ul; w < W; w += UPW) M = fmaxf(M, ml[(w * G + g) * 2]);
     float L = 0.f, o[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) o[i] = 0.f;
     if (M != -INFINITY) {
-      for (int w = ul; w < W; w += kUnitsPerWg) {
+      for (int w = ul; w < W; w += UPW) {
         const float mw = ml[(w * G + g) * 2];
         const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
         L = fmaf(f, ml[(w * G + g) * 2 + 1], L);
@@ -266,7 +266,7 @@ __device__ __forceinline__ void balanced_merge(const DecodeArgs& a, float* lds, 
 // units of blockIdx.y).  It returns the number of work items of the batch (1
 // in balanced mode, ITEMS: the row's pieces), or 0, having done nothing, when
 // there is no such item.
-template <int KIND, int D, bool BALANCED, bool LOADS, bool ITEMS>
+template <int KIND, int D, bool BALANCED, bool LOADS, bool ITEMS, int UPW>
 __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int item, const int wg_units) {
   constexpr int RING = D <= 128 ? 4 : 2;  // pages in registers (two being consumed)
   // Pages of 16 << vshift tokens are streamed as 16-token sub-pages: work
@@ -294,10 +294,10 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
   const int chunks = group / G;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // item mode: the workgroup's waves are W units of one work item; balanced
-  // mode: wave w serves unit kUnitsPerWg * wg_units + w % kUnitsPerWg of the
+  // mode: wave w serves unit UPW * wg_units + w % UPW of the
   // item (sequence, or with ITEMS a partition of one)
   const int units = a.KH * chunks;
-  const int unit = BALANCED ? wg_units * kUnitsPerWg + wave % kUnitsPerWg : wg_units * (int)(blockDim.x >> 6) + wave;
+  const int unit = BALANCED ? wg_units * UPW + wave % UPW : wg_units * (int)(blockDim.x >> 6) + wave;
   const bool unit_ok = !BALANCED || unit < units;
   const int kvh = min(unit, units - 1) / chunks;
   const int h0 = kvh * group + (min(unit, units - 1) % chunks) * G;
@@ -341,7 +341,7 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     const bool spec_hit = wi.b == spec_b && wi.p_begin == 0;
     for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x)
       ids_lds[i] = spec_hit && i == (int)threadIdx.x ? spec_id : row[i];
-    if (threadIdx.x < kUnitsPerWg) pair_ctr[threadIdx.x] = 0;
+    if (threadIdx.x < UPW) pair_ctr[threadIdx.x] = 0;
     __syncthreads();
   } else {
     if (!find_item(a.ctx_lens, a.B, a.max_pp << vshift, a.target, item, item == 0 && unit == 0, a.header, wi))
@@ -422,7 +422,7 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
   // balanced mode: take the first page pair and issue its loads before the
   // query set-up, so that the set-up runs under their latency
   const int npairs = (n_pages + 1) / 2;
-  int* const pair_next = BALANCED ? pair_ctr + wave % kUnitsPerWg : nullptr;
+  int* const pair_next = BALANCED ? pair_ctr + wave % UPW : nullptr;
   auto grab = [&]() {
     int v = 0;
     if constexpr (BALANCED)
@@ -722,8 +722,8 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     // an item that is its whole sequence goes straight to out when the call
     // has one (the merge pass then leaves that sequence alone)
     const bool direct = ITEMS && a.out && wi.p_begin == 0 && wi.n_pages == seq_pages(wi.ctx, a.max_pp);
-    balanced_merge<D, NB, ITEMS>(a, merge_lds, blockDim.x >> 6, wave, G, b, ITEMS ? wi.slot : item,
-                                 wg_units * kUnitsPerWg, units, chunks, acc, m_eff, l_tot, direct);
+    balanced_merge<D, NB, ITEMS, UPW>(a, merge_lds, blockDim.x >> 6, wave, G, b, ITEMS ? wi.slot : item,
+                                      wg_units * UPW, units, chunks, acc, m_eff, l_tot, direct);
   } else if (col < G) {
     float* out = a.part_acc + ((size_t)item * a.H + h0 + col) * D;
 #pragma unroll
@@ -783,16 +783,18 @@ __device__ __forceinline__ DecodeArgs kernel_args_afresh() {
 // ones.  Between two pieces every wavefront has passed the first piece's
 // merge barrier, so the next piece's page ids and counters overwrite nothing
 // still read.
-template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false>
+template <int KIND, int D, bool BALANCED, bool LOADS = false, bool ITEMS = false, int UPW = kUnitsPerWg>
 __global__ void __launch_bounds__(64 * (BALANCED ? kMaxBalancedWaves : kMaxWaves))
     decode_stream_kernel(DecodeArgs a, int G) {
+  static_assert(UPW == kUnitsPerWg || (ITEMS && UPW <= kMaxUnitsPerWg && kMaxBalancedWaves % UPW == 0),
+                "only the shared-items pass takes other unit counts");
   if constexpr (ITEMS) {
     for (int item = 0, items = 1; item < items; ++item) {
       const DecodeArgs ai = kernel_args_afresh();
-      items = stream_item<KIND, D, BALANCED, LOADS, ITEMS>(ai, G, item, blockIdx.x);  // 0: no such piece
+      items = stream_item<KIND, D, BALANCED, LOADS, ITEMS, UPW>(ai, G, item, blockIdx.x);  // 0: no such piece
     }
   } else {
-    stream_item<KIND, D, BALANCED, LOADS, ITEMS>(a, G, blockIdx.x, blockIdx.y);
+    stream_item<KIND, D, BALANCED, LOADS, ITEMS, UPW>(a, G, blockIdx.x, blockIdx.y);
   }
 }
 
@@ -1505,26 +1507,41 @@ hipError_t launch_balanced_d(const DecodeArgs& a, int B, int G, hipStream_t st) 
   return hipErrorInvalidValue;
 }
 
-// Work items of shared pages: the balanced geometry (kUnitsPerWg units x 6
-// wavefronts) over the device-sized work items, one resident round of
-// workgroups per unit group looping over the items; the merge pass follows.
-template <int KIND, int D>
-hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t st) {
+// The shared-items pass: 12-wavefront workgroups of UPW units, one resident
+// round of rows (a.target) per unit group, each workgroup looping over its
+// row's pieces; the merge pass follows.  Four units per workgroup (3
+// wavefronts each) when the batch has more sequences than a round has rows of
+// two-unit workgroups: twice the rows, so fewer pieces per row, each of which
+// drains and refills the wavefronts' page pipeline (c5: 129 sequences over 64
+// rows, 244.4 -> 239.8 us); otherwise two (a row is then often one sequence,
+// written out directly: c3).
+template <int KIND, int D, int UPW>
+hipError_t launch_shared_items_upw(const DecodeArgs& a0, int G, size_t lds, hipStream_t st) {
   const int units = a0.KH * ((a0.H / a0.KH) / G);
-  const int wgs_y = (units + kUnitsPerWg - 1) / kUnitsPerWg;
+  const int wgs_y = (units + UPW - 1) / UPW;
   const int W = kMaxBalancedWaves;
-  const size_t lds = balanced_lds_bytes(a0.max_pp, W, G, D);
-  if (lds > shared_items_max_lds()) return hipErrorInvalidValue;
-  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true>);
+  const void* fn = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true, UPW>);
   if (lds > kMaxBalancedLds) {
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
   DecodeArgs a = a0;
-  a.target = items_target(fn, W, lds, wgs_y * W);  // items one resident round holds
-  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true>), dim3(wgs_y, a.target, 1), dim3(64 * W), lds,
-                     st, a, G);
+  a.target = items_target(fn, W, lds, wgs_y * W);  // rows: one resident round
+  hipLaunchKernelGGL((decode_stream_kernel<KIND, D, true, false, true, UPW>), dim3(wgs_y, a.target, 1), dim3(64 * W),
+                     lds, st, a, G);
   return hipGetLastError();
+}
+
+template <int KIND, int D>
+hipError_t launch_shared_items_d(const DecodeArgs& a0, int B, int G, hipStream_t st) {
+  const int units = a0.KH * ((a0.H / a0.KH) / G);
+  const size_t lds = balanced_lds_bytes(a0.max_pp, kMaxBalancedWaves, G, D);
+  if (lds > shared_items_max_lds()) return hipErrorInvalidValue;
+  const void* fn2 = reinterpret_cast<const void*>(&decode_stream_kernel<KIND, D, true, false, true, 2>);
+  const int wgs2 = (units + 1) / 2;
+  const int rows2 = items_target(fn2, kMaxBalancedWaves, lds, wgs2 * kMaxBalancedWaves);
+  if (units >= 4 && B > rows2) return launch_shared_items_upw<KIND, D, 4>(a0, G, lds, st);
+  return launch_shared_items_upw<KIND, D, 2>(a0, G, lds, st);
 }
 
 template <int KIND>
