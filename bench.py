@@ -686,16 +686,20 @@ def main():
         api(i, True)
         api(i, False, False)
     n_host = 50
+    n_api = max(args.steps, 200)
     python_api = {
         "host_us_per_call": {
             "c_abi": round(host_us(full, n_host), 2),
             "python": round(host_us(lambda i: api(i, False), n_host), 2),
             "python_preallocated": round(host_us(lambda i: api(i, True), n_host), 2),
         },
-        "us_per_layer_step_python_preallocated": round(time_events(lambda i: api(i, True), args.steps), 3),
+        # over at least 200 calls whatever --steps says: a short window would carry the cost of
+        # filling the launch queue from Python (13 us of host time per call) into the average
+        "us_per_layer_step_python_preallocated": round(time_events(lambda i: api(i, True), n_api), 3),
         # paged_attention_decode(query, kv_pool, page_table, context_lens, layer_idx, kv_scales=...) as the
         # reference's callers write it: no host copy of the lengths, no preallocated buffers
-        "us_per_layer_step_reference_signature": round(time_events(lambda i: api(i, False, False), args.steps), 3),
+        "us_per_layer_step_reference_signature": round(time_events(lambda i: api(i, False, False), n_api), 3),
+        "calls_timed": n_api,
     }
     log(f"python API: {python_api}")
 
