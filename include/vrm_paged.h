@@ -55,23 +55,26 @@ typedef enum vrm_kv_dtype {
 /*
  * Inline slab layout of the int8 / fp8 pools (VRM_KV_*_INLINE).  The codes
  * and scales of one (page, layer) share one slab of vrm_kv_slab_bytes()
- * bytes at (p L + l) slab, holding for each kv-head h in turn a record of
+ * bytes, and the slabs lie layer by layer: slab (p, l) is at (l P + p) slab,
+ * so that the P slabs of one layer form one contiguous run.  A slab holds for
+ * each kv-head h in turn a record of
  *      K codes [PS][D] | V codes [PS][D] (tiled as above)
  *      | int8: K scales [PS], V scales [PS] float32 (PS (2 D + 8) bytes)
  *      | fp8:  K scale, V scale float32, zero bytes up to 2 PS D + 128
  * Code (p, l, kv, h, t, d) of the logical kv_pool[P][L][2][KH][PS][D] is at
- * byte (p L + l) slab + h record + kv PS D + (its place in the slice), and
+ * byte (l P + p) slab + h record + kv PS D + (its place in the slice), and
  * the logical kv_scales[P][L][2][KH]([PS]) are float32s at the same slab and
  * record offsets plus kv PS (+ t) (int8) or kv (fp8) from
  * kv_scales = (char *)kv_pool + 2 PS D.  Every entry that takes a pool takes
  * these dtypes with kv_scales at exactly that address (anything else is
  * VRM_ERR_ARG).  No counterpart in the reference (whose pools are float
- * only): a page of one layer is one contiguous run per kv-head, and the slab
- * is not a power-of-two multiple of 32 KB, which HBM reads faster when the
- * pages of a pool of many layers are scattered over it (int8 14B shape, 48
- * layers: 4 % faster).  The int8 pools of the Python layer use it by default;
- * the fp8 pools do not (their few page scales read faster as a separate
- * array in the ragged work-item decode).
+ * only, one page's layers side by side): a page of one layer is one run per
+ * kv-head, and a layer's pages one run, which the balanced decodes sweep in
+ * ascending page order (int8 14B shape, 48 layers, shuffled page table:
+ * 98.0 -> 93.7 us per layer-step against the page-major float layout's
+ * order).  The int8 pools of the Python layer use it by default; the fp8
+ * pools do not (their few page scales read faster as a separate array in
+ * the ragged work-item decode).
  */
 
 /* Bytes of one (page, layer) slab of a pool of kv_dtype: 2 KH PS D times the

@@ -1,7 +1,7 @@
 """Host tests of the quantized pools' two memory layouts (no GPU): the inline
 layout's views put every code and scale at the byte the C ABI documents
-(include/vrm_paged.h: per (page, layer) slab, per kv-head a record of K
-codes, V codes, K scales, V scales), the sizes agree with the library's
+(include/vrm_paged.h: per (page, layer) slab, the slabs layer by layer, per
+kv-head a record of K codes, V codes, K scales, V scales), the sizes agree with the library's
 vrm_kv_slab_bytes, and the layout detection tells inline, plain and other
 strides apart."""
 import pytest
@@ -31,13 +31,13 @@ def test_inline_views_hit_the_documented_bytes(codec, P, L, KH, PS, D):
         t, d = int(torch.randint(PS, (1,), generator=g)), int(torch.randint(D, (1,), generator=g))
         val = int(torch.randint(1, 255, (1,), generator=g))
         raw[p, l, kv, h, t, d] = val
-        off = (p * L + l) * slab + h * head + kv * PS * D + t * D + d
+        off = (l * P + p) * slab + h * head + kv * PS * D + t * D + d
         assert int(buf[off]) == val
         raw[p, l, kv, h, t, d] = 0
         s = (torch.rand(1, generator=g) + 0.5).item()  # a float32 value
         idx = (p, l, kv, h) if fp8 else (p, l, kv, h, t)
         sc[idx] = s
-        soff = (p * L + l) * slab + h * head + 2 * PS * D + (kv * 4 if fp8 else kv * PS * 4 + t * 4)
+        soff = (l * P + p) * slab + h * head + 2 * PS * D + (kv * 4 if fp8 else kv * PS * 4 + t * 4)
         assert buf[soff:soff + 4].view(torch.float32).item() == s
         sc[idx] = 0
     assert int(buf.count_nonzero()) == 0  # nothing else was touched
@@ -69,8 +69,10 @@ def test_layout_detection():
     assert kv_quant.pool_dtype_code(pool, sc) == _lib.VRM_KV_I8
     ipool, isc = kv_quant.allocate_pool(4, 3, 2, 32, "int8", 8, device="cpu")
     assert not ipool.is_contiguous()
-    # a layer slice keeps the inline strides but not the layer count they belong to
-    assert kv_quant.pool_layout(ipool[:, :1], isc[:, :1]) is None
+    # one layer's slabs are a run of their own: a layer slice is a one-layer inline pool
+    assert kv_quant.pool_layout(ipool[:, 1:2], isc[:, 1:2]) == "inline"
+    # a page slice keeps the layer stride of all 4 pages, which 2 pages do not have
+    assert kv_quant.pool_layout(ipool[:2], isc[:2]) is None
     # views of two different buffers, or mixed layouts
     other, osc = kv_quant.allocate_pool(4, 3, 2, 32, "int8", 8, device="cpu")
     assert kv_quant.pool_layout(ipool, osc) is None

@@ -50,5 +50,5 @@ extern "C" size_t vrm_kv_slab_bytes(int kv_dtype, int KH, int PS, int D) {
       break;
     default: return 0;
   }
-  return (size_t)vrm::pool_geom(kv_dtype, KH, PS, D, row).slab;
+  return (size_t)vrm::pool_geom(kv_dtype, KH, PS, D, row, 1, 1).slab;
 }

@@ -81,20 +81,26 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 __device__ __forceinline__ float e4m3fn_to_f32(uint32_t b) { return vrm_e4m3::decode(b); }
 
 // Where a pool keeps the codes and scales of (page, layer, K/V, kv-head):
-// the codes of that slice start at pool + (page * L + layer) * slab + kvh *
-// head + kv * this->kv bytes, its scales at scales + (page * L + layer) *
-// s_slab + kvh * s_head + kv * s_kv floats (then one per token for int8).
-// Plain pools are the dense [P][L][2][KH][PS][row] arrays (and, for int8 /
-// fp8, a separate dense scale array); the inline int8 / fp8 layout keeps a
-// kv-head's codes and scales in the (page, layer) slab (inline_scale_offset
-// below), the scale pointer then pointing into the first slab.
+// the codes of that slice start at pool + page * this->page + layer *
+// this->layer + kvh * head + kv * this->kv bytes, its scales at scales + page
+// * s_page + layer * s_layer + kvh * s_head + kv * s_kv floats (then one per
+// token for int8).  Plain pools are the dense [P][L][2][KH][PS][row] arrays
+// (and, for int8 / fp8, a separate dense scale array): a page's slabs of all
+// layers lie together.  The inline int8 / fp8 layout keeps a kv-head's codes
+// and scales in the (page, layer) slab (inline_scale_offset below), the scale
+// pointer then pointing into the first slab, and lays the slabs out layer by
+// layer: the P slabs of one layer are one contiguous run.
 struct PoolGeom {
-  long long slab;    // pool bytes per (page, layer)
-  long long head;    // bytes from one kv-head's code slices to the next one's
-  long long kv;      // bytes from a kv-head's K codes to its V codes
-  long long s_slab;  // scale floats per (page, layer)
-  long long s_head;  // scale floats from one kv-head to the next
-  long long s_kv;    // scale floats from a kv-head's K scales to its V scales
+  long long slab;     // pool bytes per (page, layer)
+  long long head;     // bytes from one kv-head's code slices to the next one's
+  long long kv;       // bytes from a kv-head's K codes to its V codes
+  long long s_slab;   // scale floats per (page, layer)
+  long long s_head;   // scale floats from one kv-head to the next
+  long long s_kv;     // scale floats from a kv-head's K scales to its V scales
+  long long page;     // bytes from a (page, layer) slab to the next page's of the layer
+  long long layer;    // bytes from a (page, layer) slab to the next layer's of the page
+  long long s_page;   // the same two strides in scale floats
+  long long s_layer;
 };
 
 inline bool inline_pool(int kv_dtype) { return kv_dtype == VRM_KV_I8_INLINE || kv_dtype == VRM_KV_FP8E4M3_INLINE; }
@@ -106,9 +112,10 @@ inline bool inline_pool(int kv_dtype) { return kv_dtype == VRM_KV_I8_INLINE || k
 // pool.
 inline long long inline_scale_offset(int PS, int D) { return 2LL * PS * D; }
 
-// Geometry of a pool of kv_dtype whose token rows hold row_bytes bytes (D
-// codes, D / 2 for the 4-bit pool, D elements of a float pool).
-inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_bytes) {
+// Geometry of a pool of P pages and L layers of kv_dtype whose token rows
+// hold row_bytes bytes (D codes, D / 2 for the 4-bit pool, D elements of a
+// float pool).
+inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_bytes, int P, int L) {
   PoolGeom g{};
   const bool fp8 = kv_dtype == VRM_KV_FP8E4M3 || kv_dtype == VRM_KV_FP8E4M3_INLINE;
   const long long slice = (long long)PS * row_bytes;
@@ -126,6 +133,10 @@ inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_byt
       g.s_kv = PS;
     }
     g.s_slab = g.slab / 4;
+    g.page = g.slab;
+    g.layer = (long long)P * g.slab;
+    g.s_page = g.s_slab;
+    g.s_layer = (long long)P * g.s_slab;
   } else {
     g.head = slice;
     g.kv = KH * slice;
@@ -134,6 +145,10 @@ inline PoolGeom pool_geom(int kv_dtype, int KH, int PS, int D, long long row_byt
     g.s_head = per_head;
     g.s_kv = KH * per_head;
     g.s_slab = 2 * g.s_kv;
+    g.page = (long long)L * g.slab;
+    g.layer = g.slab;
+    g.s_page = (long long)L * g.s_slab;
+    g.s_layer = g.s_slab;
   }
   return g;
 }

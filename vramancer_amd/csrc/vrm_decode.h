@@ -308,18 +308,21 @@ hipError_t launch_stream_mfma(const DecodeArgs& a, int kind, int B, int D, int G
 
 // Balanced mode geometry: workgroups of kUnitsPerWg units x (1, 2, 4 or 6)
 // wavefronts per unit.  LDS: the sequence's page ids [max_pp], the units'
-// page-pair counters [kMaxUnitsPerWg], then (16-byte aligned) the merge area,
-// [W][G][D] accumulators and [W][G][2] (m, l); at most kMaxBalancedLds.
+// page-pair counters [kMaxUnitsPerWg], the page-id buckets' counters
+// [kIdBuckets], then (16-byte aligned) the merge area, [W][G][D]
+// accumulators and [W][G][2] (m, l); at most kMaxBalancedLds.
 constexpr int kMaxBalancedWaves = 12;
 constexpr int kUnitsPerWg = 2;     // the balanced mode; the shared-items pass takes 2 or 4
 constexpr int kMaxUnitsPerWg = 4;  // page-pair counters the LDS layout leaves room for
+constexpr int kIdBucketBits = 6;   // a work item's pages are read in 2^6 buckets of ascending page id
+constexpr int kIdBuckets = 1 << kIdBucketBits;
 constexpr size_t kMaxBalancedLds = 64 * 1024;
 // LDS one workgroup of the shared-items pass may take on the current device
 // (its 12-wavefront workgroups hold a CU each, so beyond 64 KB costs no
 // occupancy): the device's per-workgroup limit, at most 160 KB.
 size_t shared_items_max_lds();
 __host__ __device__ inline size_t balanced_merge_offset(int max_pp) {
-  return ((size_t)max_pp * 4 + kMaxUnitsPerWg * 4 + 15) / 16 * 16;
+  return ((size_t)max_pp * 4 + kMaxUnitsPerWg * 4 + kIdBuckets * 4 + 15) / 16 * 16;
 }
 inline size_t balanced_lds_bytes(int max_pp, int W, int G, int D) {
   return balanced_merge_offset(max_pp) + (size_t)W * G * (D + 2) * sizeof(float);

@@ -110,10 +110,11 @@ __global__ void __launch_bounds__(64) decode_generic_kernel(DecodeArgs a, int D,
   auto head_index = [&](int pid, int kv) { return (((size_t)pid * a.L + a.layer) * 2 + kv) * a.KH + kvh; };
   // codes of a (page, layer, K/V, kv-head) slice and, for int8 / fp8, its scales
   auto slice_of = [&](int pid, int kv) {
-    return a.pool + ((size_t)pid * a.L + a.layer) * a.g.slab + (size_t)kvh * a.g.head + (size_t)kv * a.g.kv;
+    return a.pool + (size_t)pid * a.g.page + (size_t)a.layer * a.g.layer + (size_t)kvh * a.g.head + (size_t)kv * a.g.kv;
   };
   auto scales_of = [&](int pid, int kv) {
-    return a.scales + ((size_t)pid * a.L + a.layer) * a.g.s_slab + (size_t)kvh * a.g.s_head + (size_t)kv * a.g.s_kv;
+    return a.scales + (size_t)pid * a.g.s_page + (size_t)a.layer * a.g.s_layer + (size_t)kvh * a.g.s_head +
+           (size_t)kv * a.g.s_kv;
   };
   const bool vec4 = (D & 3) == 0;
 

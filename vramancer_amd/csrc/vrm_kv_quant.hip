@@ -66,10 +66,11 @@ struct QuantArgs {
 // Codes of the (page, layer, K/V, kv-head) slice and its scales (int8: PS of
 // them, one per token; fp8: one).
 __device__ __forceinline__ uint8_t* slice_of(const QuantArgs& a, int pid, int kv, int h) {
-  return a.pool + ((size_t)pid * a.L + a.layer) * a.g.slab + (size_t)h * a.g.head + (size_t)kv * a.g.kv;
+  return a.pool + (size_t)pid * a.g.page + (size_t)a.layer * a.g.layer + (size_t)h * a.g.head + (size_t)kv * a.g.kv;
 }
 __device__ __forceinline__ float* scales_of(const QuantArgs& a, int pid, int kv, int h) {
-  return a.scales + ((size_t)pid * a.L + a.layer) * a.g.s_slab + (size_t)h * a.g.s_head + (size_t)kv * a.g.s_kv;
+  return a.scales + (size_t)pid * a.g.s_page + (size_t)a.layer * a.g.s_layer + (size_t)h * a.g.s_head +
+         (size_t)kv * a.g.s_kv;
 }
 
 // Offset of (token t, dim d) inside a slice: K token-major, V tiled.
@@ -277,7 +278,7 @@ int run_quant(const void* key, const void* value, int src_dtype, const int32_t* 
     return VRM_OK;
   }
   QuantArgs a{key, value, page_ids, slots, static_cast<uint8_t*>(pool), scales, KH, L, P, layer, D, PS,
-              pool_geom(kv_dtype, KH, PS, D, D)};
+              pool_geom(kv_dtype, KH, PS, D, D, P, L)};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (src_dtype) {
     case VRM_SRC_F32: launch_quant_d<VRM_SRC_F32>(a, n, kv_dtype, pages, D, st); break;
@@ -331,7 +332,7 @@ extern "C" int vrm_kv_dequant_pages(const void* kv_pool, const float* kv_scales,
   if (rc) return rc;
   if (NP == 0) return VRM_OK;
   QuantArgs a{nullptr, nullptr, page_ids, nullptr, const_cast<uint8_t*>(static_cast<const uint8_t*>(kv_pool)),
-              const_cast<float*>(kv_scales), KH, L, P, layer_idx, D, PS, pool_geom(kv_dtype, KH, PS, D, D)};
+              const_cast<float*>(kv_scales), KH, L, P, layer_idx, D, PS, pool_geom(kv_dtype, KH, PS, D, D, P, L)};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (fp8_pool(kv_dtype))
     hipLaunchKernelGGL(dequant_pages_kernel<true>, dim3(2 * KH, NP), dim3(256), 0, st, a, out, D);

@@ -724,9 +724,9 @@ int kind_of(int kv_dtype) {
 }
 
 // Pool geometry of a decode call (kv_dtype selects the plain or inline layout).
-PoolGeom geom_of(int kv_dtype, int kind, int KH, int PS, int D) {
+PoolGeom geom_of(int kv_dtype, int kind, int KH, int PS, int D, int P, int L) {
   const long long row = kind == K_F32 ? 4LL * D : (kind == K_F16 || kind == K_BF16) ? 2LL * D : kind == K_Q4 ? D / 2 : D;
-  return pool_geom(kv_dtype, KH, PS, D, row);
+  return pool_geom(kv_dtype, KH, PS, D, row, P, L);
 }
 
 
@@ -765,7 +765,7 @@ int decode_entry(const float* query, const void* kv_pool, const float* kv_scales
   a.max_pp = max_pp;
   a.layer = layer_idx;
   a.lse = lse;
-  a.g = geom_of(kv_dtype, kind, KH, PS, D);
+  a.g = geom_of(kv_dtype, kind, KH, PS, D, P, L);
   rc = check_kind_shape(kind, D, PS, "vrm_paged_decode");
   if (rc) return rc;
   return run_decode(a, kind, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
@@ -966,7 +966,7 @@ int balanced_entry(const float* query, const void* kv_pool, const float* kv_scal
   a.lse = lse;
   a.out = out;
   a.qscale = scale * kLog2e;
-  a.g = geom_of(kv_dtype, kind, KH, PS, D);
+  a.g = geom_of(kv_dtype, kind, KH, PS, D, P, L);
   const hipError_t e = launch_stream_balanced(a, kind, B, D, G, reinterpret_cast<hipStream_t>(stream), loads_only);
   if (e != hipSuccess) {
     set_error("%s: kernel launch failed: %s", who, hipGetErrorString(e));
@@ -1062,7 +1062,7 @@ extern "C" int vrm_paged_decode_q4(const float* query, const uint8_t* kv_pool_q4
   a.P = P;
   a.max_pp = max_pp;
   a.layer = layer_idx;
-  a.g = geom_of(VRM_KV_I8, K_Q4, KH, PS, D);  // plain layout of D / 2 bytes per row
+  a.g = geom_of(VRM_KV_I8, K_Q4, KH, PS, D, P, L);  // plain layout of D / 2 bytes per row
   return run_decode(a, K_Q4, out, workspace, workspace_bytes, B, D, PS, scale, reinterpret_cast<hipStream_t>(stream),
                     kBoth);
 }
