@@ -287,7 +287,13 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
   static_assert(!LOADS || BALANCED, "the load-only build exists for the balanced mode only");
   static_assert(!ITEMS || (BALANCED && !LOADS), "work items of shared pages are a balanced build that computes");
 
-  const int lane = threadIdx.x & 63;
+  // The shared-items pass calls this once per work item in a loop: its lane
+  // values are derived afresh per item from an opaque copy of the thread
+  // index, since hoisted out of that loop they stay live through the page
+  // loop and spill (a lane offset to scratch, compare masks to lanes).
+  int tid = threadIdx.x;
+  if constexpr (ITEMS) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int group = a.H / a.KH;
@@ -319,7 +325,7 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     if constexpr (ITEMS) {
       if (item == 0) {
         spec_b = min((int)((long long)blockIdx.y * a.B / a.target), a.B - 1);
-        if ((int)threadIdx.x < a.max_pp) spec_id = a.page_table[(size_t)spec_b * a.max_pp + threadIdx.x];
+        if (tid < a.max_pp) spec_id = a.page_table[(size_t)spec_b * a.max_pp + tid];
       }
       // every wavefront derives the same item (so the workgroup leaves as a
       // whole, before its first barrier); wave 0 of the first workgroup
@@ -348,7 +354,7 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
     // partial last page keeps its place, where the token bound masks it.
     const int n_whole = min(max(wi.ctx / kPS - wi.p_begin, 0), wi.n_pages);
     if (n_whole >= 4 && n_whole <= (int)blockDim.x) {
-      const int t = threadIdx.x;
+      const int t = tid;
       int* const bucket_ctr = pair_ctr + kMaxUnitsPerWg;
       const int shift = max(0, 32 - __clz(max(a.P - 1, 1)) - kIdBucketBits);
       int id = 0, bkt = 0, pos = 0;
@@ -380,10 +386,10 @@ __device__ __forceinline__ int stream_item(const DecodeArgs& a, int G, const int
       if (t < n_whole) ids_lds[bucket_ctr[bkt] + pos] = id;
       for (int i = n_whole + t; i < wi.n_pages; i += blockDim.x) ids_lds[i] = row[i];
     } else {
-      for (int i = threadIdx.x; i < wi.n_pages; i += blockDim.x)
-        ids_lds[i] = spec_hit && i == (int)threadIdx.x ? spec_id : row[i];
+      for (int i = tid; i < wi.n_pages; i += blockDim.x)
+        ids_lds[i] = spec_hit && i == tid ? spec_id : row[i];
     }
-    if (threadIdx.x < UPW) pair_ctr[threadIdx.x] = 0;
+    if (tid < UPW) pair_ctr[tid] = 0;
     __syncthreads();
   } else {
     if (!find_item(a.ctx_lens, a.B, a.max_pp << vshift, a.target, item, item == 0 && unit == 0, a.header, wi))

@@ -461,6 +461,93 @@ __global__ void __launch_bounds__(256) decode_reduce_kernel(const float* __restr
   }
 }
 
+// The same merge with one wavefront per (sequence, head) and the four heads
+// blockIdx.x * 4 .. + 3 of one sequence per workgroup: each wavefront folds
+// every partial of its head, BATCH at a time from two register batches, and
+// writes the row itself.  A quarter of the workgroups of
+// decode_reduce_kernel, for batches where most sequences need no merge or
+// few partials.
+template <int DMAX>
+__global__ void __launch_bounds__(256) decode_reduce_rows_kernel(const float* __restrict__ part_acc,
+                                                                 const float* __restrict__ part_ml,
+                                                                 const int32_t* __restrict__ header,
+                                                                 float* __restrict__ out, float* __restrict__ lse,
+                                                                 int H, int B, int D) {
+  constexpr int PER = DMAX / 64;
+  constexpr int BATCH = 4;
+  const int y = blockIdx.y;
+  const int big = min(max(header[3], 0), B - 1);
+  const bool direct = header[4] != 0;
+  int first = header[kHeaderInts + y];
+  int next = header[kHeaderInts + y + 1];
+  int tail = header[kHeaderInts + B + 1 + y];
+  const int b = y == 0 ? big : (y == big ? 0 : y);
+  if (b != y) {
+    first = header[kHeaderInts + b];
+    next = header[kHeaderInts + b + 1];
+    tail = header[kHeaderInts + B + 1 + b];
+  }
+  const int nf = next - first;
+  const int nact = nf + (tail >= 0 ? 1 : 0);
+  if (nact == 1 && direct) return;  // the partition pass wrote this sequence's rows
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.x * 4 + wave;
+  if (h >= H) return;
+  auto item_of = [&](int s) { return s < nf ? first + s : tail; };
+  float M = -INFINITY, Lsum = 0.f;
+  float res[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) res[i] = 0.f;
+  float m[2][BATCH], l[2][BATCH], x[2][BATCH][PER];
+  auto load_batch = [&](int buf, int s0) {
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const size_t it = (size_t)item_of(min(s0 + k, nact - 1)) * H + h;
+      m[buf][k] = part_ml[it * 2];
+      l[buf][k] = part_ml[it * 2 + 1];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) x[buf][k][i] = i * 64 + lane < D ? part_acc[it * D + i * 64 + lane] : 0.f;
+    }
+  };
+  auto fold_batch = [&](int buf, int s0) {
+    float cm = M;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k)
+      if (s0 + k < nact) cm = fmaxf(cm, m[buf][k]);
+    if (cm == -INFINITY) return;
+    const float keep = (M == -INFINITY) ? 0.f : exp2f(M - cm);
+    Lsum *= keep;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) res[i] *= keep;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const bool live = s0 + k < nact && m[buf][k] != -INFINITY;
+      const float w = live ? exp2f(m[buf][k] - cm) : 0.f;
+      Lsum = fmaf(w, l[buf][k], Lsum);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) res[i] = fmaf(w, x[buf][k][i], res[i]);
+    }
+    M = cm;
+  };
+  if (nact > 0) {
+    load_batch(0, 0);
+    int s0 = 0;
+    for (; s0 + BATCH < nact; s0 += 2 * BATCH) {
+      load_batch(1, s0 + BATCH);
+      fold_batch(0, s0);
+      load_batch(0, s0 + 2 * BATCH);  // unconditional (clamped), as above
+      fold_batch(1, s0 + BATCH);
+    }
+    if (s0 < nact) fold_batch(0, s0);
+  }
+  const float inv = Lsum > 0.f ? 1.f / Lsum : 0.f;
+  float* dst = out + ((size_t)b * H + h) * D;
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (i * 64 + lane < D) dst[i * 64 + lane] = res[i] * inv;
+  if (lse && lane == 0) lse[(size_t)b * H + h] = Lsum > 0.f ? (M + log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+}
+
 // out = (e^(lse1 - m) o1 + e^(lse2 - m) o2) / (e^(lse1 - m) + e^(lse2 - m)),
 // m = max(lse1, lse2): two attentions over disjoint token sets merged into
 // the attention over their union; lse_out (optional) gets the union's lse.
@@ -528,9 +615,27 @@ hipError_t dispatch_d(const DecodeArgs& a, int B, int D, int G, hipStream_t st) 
   }
 }
 
-hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStream_t st) {
-  dim3 grid(a.H, B);
+// rows: one wavefront per (sequence, head) (decode_reduce_rows_kernel), for
+// the shared-items pass, whose sequences mostly need no merge or a few
+// partials (c3's reference-signature call: 98.6 -> 97.7 us); otherwise four
+// per (sequence, head), for the work items' 14-16 partials per sequence
+// (c2 / c4: 0.3-1.7 us faster than one).
+hipError_t launch_reduce(const DecodeArgs& a, float* out, int B, int D, hipStream_t st, bool rows = false) {
   const dim3 block(256);
+  if (rows) {
+    const dim3 grid((a.H + 3) / 4, B);
+    if (D <= 64)
+      hipLaunchKernelGGL(decode_reduce_rows_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.lse, a.H, B, D);
+    else if (D <= 128)
+      hipLaunchKernelGGL(decode_reduce_rows_kernel<128>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.lse, a.H, B, D);
+    else
+      hipLaunchKernelGGL(decode_reduce_rows_kernel<256>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out,
+                         a.lse, a.H, B, D);
+    return hipGetLastError();
+  }
+  const dim3 grid(a.H, B);
   if (D <= 64)
     hipLaunchKernelGGL(decode_reduce_kernel<64>, grid, block, 0, st, a.part_acc, a.part_ml, a.header, out, a.lse,
                        a.H, B, D);
@@ -671,7 +776,7 @@ int run_decode(DecodeArgs a, int kind, float* out, void* workspace, size_t works
     }
   }
   if (passes & kMergeOnly) {
-    e = launch_reduce(a, out, B, D, st);
+    e = launch_reduce(a, out, B, D, st, shared);
     if (e != hipSuccess) {
       set_error("vrm_paged_decode: merge kernel launch failed: %s", hipGetErrorString(e));
       return (int)e;
