@@ -639,10 +639,15 @@ def main():
     torch.cuda.synchronize()
     settled = settle(full, args.settle)
     log(f"settle: {settled[0]} more untimed layer-steps over {settled[1]:.2f} s")
+    # int8 / fp8 at page 16 and head_dim 64 .. 128 without host lengths: the
+    # shared-items pass (rows of equal page runs, cut into pieces per sequence)
+    shared = not balanced and cfg.codec in ("int8", "fp8") and PS == 16 and D in (64, 80, 96, 112, 128)
     if balanced:
         pps, n_items = None, None
     else:
-        pps, n_items = ws[:8].view(torch.int32).tolist()  # partition geometry the kernel chose (header)
+        # partition geometry the kernel chose (header): pages per partition and
+        # work items, or for the shared-items pass pages per row and pieces
+        pps, n_items = ws[:8].view(torch.int32).tolist()
     log(f"timing {args.steps} layer-steps")
     us_step = time_events(full, args.steps)
     # TurboQuant, Q4 and the balanced decode: one kernel, whose time is the whole decode
@@ -800,6 +805,8 @@ def main():
         kname = KERNEL[cfg.codec].format(D=D)
         if balanced:
             kname = kname.replace(">", ",balanced>")
+        elif shared:
+            kname = kname.replace(">", ",shared items>")
     else:
         kname = f"decode_generic_kernel<{KV_NAME[cfg.codec]}>" + (" + merge" if q4 else "")
     G = next(g for g in range(16, 0, -1) if (H // KH) % g == 0)
@@ -860,7 +867,7 @@ def main():
             "workload": desc,
             "batch": B, "num_heads": H, "num_kv_heads": KH, "head_dim": D, "context_tokens": int(sum(lens_list)),
             "page_size": PS, "num_layers": L, "num_pages": P, "pages_per_partition": pps, "work_items": n_items,
-            "decode_mode": "balanced" if balanced else "work-items",
+            "decode_mode": "balanced" if balanced else "shared-items" if shared else "work-items",
             "layers_rotated": list(layers),
         },
         "hbm_gbps": round(overall, 1),
