@@ -667,10 +667,15 @@ def _balanced(q, pool, sc, table, lens, layer, lse=None, scale=None):
     (40, 8, 96, [700, 333, 5]),                  # head_dims between 64 and 128
     (16, 2, 80, [260, 17]),
     (24, 4, 112, [1000, 999]),
+    # 12-wavefront workgroups of 768 threads sort a sequence's whole pages
+    # when there are 4 .. 768 of them: 1000 pages (read in table order), 768
+    # whole pages and a partial one, exactly 768, and 3 pages
+    (16, 2, 128, [16000, 12289, 12288, 48]),
 ])
 def test_balanced_decode_matches_oracle(dtype, H, KH, D, ctxs):
     """The balanced decode (one workgroup per sequence and kv-head, partitions
-    merged in LDS) against the oracle, at the decode bar."""
+    merged in LDS, pages read in page order) against the oracle, at the
+    decode bar."""
     _say(f"balanced {dtype} H {H} KH {KH} D {D} B {len(ctxs)}")
     q, pool, sc, table, lens = _pool_case(dtype, len(ctxs), H, KH, D, ctxs, seed=H + D + len(ctxs))
     out = _balanced(*(t.to(DEV) for t in (q, pool, sc, table, lens)), 1)
