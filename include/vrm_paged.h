@@ -179,7 +179,10 @@ int vrm_paged_decode_noalloc(const float* query, const void* kv_pool, const floa
  * lengths (the caller knows them on the host; the page manager does).  One
  * workgroup per (sequence, kv-head or head chunk) splits the sequence's pages
  * over its wavefronts and merges their partials in LDS, writing out directly:
- * no workspace, no separate merge pass.  Correct for any lengths; its time
+ * no workspace, no separate merge pass.  A workgroup reads its sequence's
+ * whole pages in ascending page id (sorted in LDS), so that over the inline
+ * layout's layer-major slabs the workgroups sweep a layer's pages together.
+ * Correct for any lengths; its time
  * follows the longest sequence, so ragged batches belong on vrm_paged_decode,
  * which balances work items across sequences.  lse (nullable) receives
  * ln sum_t exp(scale q.k_t) per (b, h) as in vrm_paged_decode_lse.  No
